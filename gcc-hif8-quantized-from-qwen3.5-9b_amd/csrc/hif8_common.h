@@ -1,0 +1,80 @@
+// Shared host/device plumbing for the HiF8 HIP kernels: error reporting for the
+// C ABI, dtype helpers, conversions and wavefront reductions for gfx950.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hif8_format.h"
+#include "hif8_rocm.h"
+
+namespace hif8 {
+
+// ---------------------------------------------------------------- host side
+
+// Records a printf-style message as this thread's last error and returns code.
+int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+// Converts a pending launch error into a status; "what" names the operator.
+int check_launch(const char *what);
+// Clears this thread's last error (called on entry of every ABI function).
+void clear_error();
+
+inline bool is_io_dtype(int d) { return d == HIF8_DTYPE_FP16 || d == HIF8_DTYPE_BF16; }
+inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// The constexpr-built tables in device global memory (one ~9.5 KiB copy per
+// translation unit; kernels stage the part they need into LDS).
+static __device__ const Tables kDeviceTables = make_tables();
+
+// ---------------------------------------------------------------- device side
+
+constexpr int kWave = 64;
+
+template <bool kBf16>
+__device__ __forceinline__ float half_bits_to_float(uint32_t h) {
+  if constexpr (kBf16) {
+    return __uint_as_float(h << 16);
+  } else {
+    return float(__builtin_bit_cast(_Float16, uint16_t(h)));
+  }
+}
+
+// Low / high 16-bit lane of a packed pair to float.
+template <bool kBf16>
+__device__ __forceinline__ float lo_to_float(uint32_t w) {
+  if constexpr (kBf16) return __uint_as_float(w << 16);
+  return float(__builtin_bit_cast(_Float16, uint16_t(w & 0xFFFFu)));
+}
+template <bool kBf16>
+__device__ __forceinline__ float hi_to_float(uint32_t w) {
+  if constexpr (kBf16) return __uint_as_float(w & 0xFFFF0000u);
+  return float(__builtin_bit_cast(_Float16, uint16_t(w >> 16)));
+}
+
+// Round-to-nearest-even conversions (gfx950 v_cvt_pk_bf16_f32 / v_cvt_f16_f32).
+__device__ __forceinline__ uint16_t float_to_bf16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+}
+__device__ __forceinline__ uint16_t float_to_f16_bits(float f) {
+  return __builtin_bit_cast(uint16_t, static_cast<_Float16>(f));
+}
+template <bool kBf16>
+__device__ __forceinline__ uint16_t float_to_half_bits(float f) {
+  if constexpr (kBf16) return float_to_bf16_bits(f);
+  return float_to_f16_bits(f);
+}
+
+// Sum over the 64 lanes of a wavefront; every lane receives the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int offset = 32; offset >= 1; offset >>= 1) v += __shfl_xor(v, offset, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int offset = 32; offset >= 1; offset >>= 1) v = fmaxf(v, __shfl_xor(v, offset, kWave));
+  return v;
+}
+
+}  // namespace hif8

@@ -1,0 +1,33 @@
+// Internal launch interface shared by the GEMV, GEMM and C-ABI units.
+#pragma once
+
+#include "hif8_common.h"
+
+namespace hif8 {
+
+enum ActKind : int {
+  kActCodes = 0,  // uint8 HiF8 activation codes + token_scale[m]
+  kActF16 = 1,    // float16 x, statically quantised in the kernel with fixed_scale[0]
+  kActBf16 = 2,   // bfloat16 x, likewise
+};
+
+struct LinearArgs {
+  const void *act;        // [m, k] codes or fp16/bf16 x
+  int act_kind;           // ActKind
+  const float *act_scale; // token_scale[m] (codes) or fixed_scale[1] (x)
+  const uint8_t *weight;  // [n, k]
+  const float *channel_scale;  // [n]
+  const void *bias;       // [n] or nullptr
+  int bias_dtype;         // HIF8_DTYPE_*
+  void *out;              // [m, n]
+  int out_dtype;          // HIF8_DTYPE_FP16 / HIF8_DTYPE_BF16
+  int64_t m, n, k;
+  hipStream_t stream;
+};
+
+// HBM-streaming GEMV for m <= 4 (gemv.hip).  Returns a status.
+int launch_gemv(const LinearArgs &a);
+// bf16-MFMA GEMM for any m (gemm.hip).  Returns a status.
+int launch_gemm(const LinearArgs &a);
+
+}  // namespace hif8

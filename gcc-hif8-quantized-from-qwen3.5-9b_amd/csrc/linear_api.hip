@@ -1,0 +1,94 @@
+// C-ABI entry points of the soft HiF8 linear operators: validation mirrors
+// ValidateSoftLinear / SoftHif8StaticFusedGemm (hif8_native.cpp:241-316,784-861),
+// then M <= 4 goes to the GEMV kernel and larger M to the MFMA GEMM.
+#include "linear.h"
+
+using namespace hif8;
+
+namespace {
+
+int validate(const char *op, const void *act, const uint8_t *weight, const float *act_scale,
+             const float *channel_scale, const void *bias, int bias_dtype, const void *out,
+             int out_dtype, int64_t m, int64_t n, int64_t k) {
+  if (!act || !weight || !act_scale || !channel_scale || !out)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: null pointer argument", op);
+  if (m <= 0 || n <= 0 || k <= 0)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: dimensions must be positive, got M=%lld N=%lld K=%lld",
+                op, (long long)m, (long long)n, (long long)k);
+  if (m > 0x7FFFFFFFll || n > 0x7FFFFFFFll || k > 0x7FFFFFFFll)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: dimensions must fit int32", op);
+  if (!is_io_dtype(out_dtype))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "output_dtype must be torch.float16 or torch.bfloat16");
+  if (bias && !is_io_dtype(bias_dtype))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "bias must have dtype torch.float16 or torch.bfloat16");
+  if (!bias && bias_dtype != HIF8_DTYPE_NONE && !is_io_dtype(bias_dtype))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: invalid bias dtype code %d", op, bias_dtype);
+  return HIF8_OK;
+}
+
+LinearArgs codes_args(const uint8_t *activation, const uint8_t *weight, const float *token_scale,
+                      const float *channel_scale, const void *bias, int bias_dtype, void *out,
+                      int out_dtype, int64_t m, int64_t n, int64_t k, hif8_stream_t stream) {
+  LinearArgs a;
+  a.act = activation;
+  a.act_kind = kActCodes;
+  a.act_scale = token_scale;
+  a.weight = weight;
+  a.channel_scale = channel_scale;
+  a.bias = bias;
+  a.bias_dtype = bias ? bias_dtype : HIF8_DTYPE_NONE;
+  a.out = out;
+  a.out_dtype = out_dtype;
+  a.m = m;
+  a.n = n;
+  a.k = k;
+  a.stream = reinterpret_cast<hipStream_t>(stream);
+  return a;
+}
+
+}  // namespace
+
+extern "C" int soft_hif8_gemv(const uint8_t *activation, const uint8_t *weight,
+                              const float *token_scale, const float *channel_scale,
+                              const void *bias, int bias_dtype, void *out, int out_dtype,
+                              int64_t m, int64_t n, int64_t k, hif8_stream_t stream) {
+  clear_error();
+  int st = validate("soft_hif8_gemv", activation, weight, token_scale, channel_scale, bias,
+                    bias_dtype, out, out_dtype, m, n, k);
+  if (st) return st;
+  if (m > 2) return fail(HIF8_ERR_INVALID_ARGUMENT, "soft_hif8_gemv requires M <= 2");
+  return launch_gemv(codes_args(activation, weight, token_scale, channel_scale, bias, bias_dtype,
+                                out, out_dtype, m, n, k, stream));
+}
+
+extern "C" int soft_hif8_gemm(const uint8_t *activation, const uint8_t *weight,
+                              const float *token_scale, const float *channel_scale,
+                              const void *bias, int bias_dtype, void *out, int out_dtype,
+                              int64_t m, int64_t n, int64_t k, hif8_stream_t stream) {
+  clear_error();
+  int st = validate("soft_hif8_gemm", activation, weight, token_scale, channel_scale, bias,
+                    bias_dtype, out, out_dtype, m, n, k);
+  if (st) return st;
+  const LinearArgs a = codes_args(activation, weight, token_scale, channel_scale, bias, bias_dtype,
+                                  out, out_dtype, m, n, k, stream);
+  return m <= 4 ? launch_gemv(a) : launch_gemm(a);
+}
+
+extern "C" int soft_hif8_static_fused_gemm(const void *x, int x_dtype, const uint8_t *weight,
+                                           const float *fixed_scale, const float *channel_scale,
+                                           const void *bias, int bias_dtype, void *out,
+                                           int out_dtype, int64_t m, int64_t n, int64_t k,
+                                           hif8_stream_t stream) {
+  clear_error();
+  int st = validate("soft_hif8_static_fused_gemm", x, weight, fixed_scale, channel_scale, bias,
+                    bias_dtype, out, out_dtype, m, n, k);
+  if (st) return st;
+  if (!is_io_dtype(x_dtype))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "activation must have dtype torch.float16 or torch.bfloat16");
+  if (m > 4) return fail(HIF8_ERR_INVALID_ARGUMENT, "soft_hif8_static_fused_gemm requires M <= 4");
+  LinearArgs a = codes_args(nullptr, weight, fixed_scale, channel_scale, bias, bias_dtype, out,
+                            out_dtype, m, n, k, stream);
+  a.act = x;
+  a.act_kind = x_dtype == HIF8_DTYPE_BF16 ? kActBf16 : kActF16;
+  return launch_gemv(a);
+}

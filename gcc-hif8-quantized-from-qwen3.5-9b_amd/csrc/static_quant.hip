@@ -1,0 +1,236 @@
+// hif8_static_quant and hif8_scaled_decode for gfx950.
+//
+// Static quant contract (calibration.py:182-201; hif8_static_quant.cpp:67-89):
+//   q = float(x) / scale[r % S]   (IEEE round-to-nearest division)
+//   byte = static_encode(q)       (finite clamped to +-2^15, ties away, no -0)
+//
+// The vector kernel is HBM-bound (2 B in + 1 B out per element), so it spends
+// as few VALU cycles per element as possible: it multiplies by a per-row
+// reciprocal instead of dividing, and the multiply is exact enough for the
+// encode except when the product lies within a few ulps of a boundary of the
+// 13-bit (sign, exp8, mant4) encode index, where the correctly rounded
+// quotient could land on the other side.  Such lanes (and NaN lanes) redo the
+// element with a true IEEE division.  The product of x and rcp(s) is within
+// 1.5 ulp (relative) of x/s and the correctly rounded quotient within 0.5 ulp,
+// so the two fp32 bit patterns differ by at most 3; a margin of 8 covers that
+// with room to spare.  The encode itself is one LDS lookup in the 8 KiB
+// static encode table.
+#include "hif8_common.h"
+
+namespace hif8 {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr uint32_t kNearMargin = 8;
+// Below this many 16-element chunks the 8 KiB LDS table is not worth loading:
+// the launch is latency-bound and the arithmetic encoder is used instead.
+constexpr uint32_t kLutMinChunks = 2048;
+
+__device__ __forceinline__ bool near_index_boundary(float q) {
+  const uint32_t u = __float_as_uint(q);
+  return (((u + kNearMargin) & 0x7FFFFu) <= 2u * kNearMargin) || __builtin_isnan(q);
+}
+
+template <bool kBf16>
+__device__ __forceinline__ void load16(const uint16_t *p, float (&v)[16]) {
+  const uint4 a = *reinterpret_cast<const uint4 *>(p);
+  const uint4 b = *reinterpret_cast<const uint4 *>(p + 8);
+  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    v[2 * i] = lo_to_float<kBf16>(w[i]);
+    v[2 * i + 1] = hi_to_float<kBf16>(w[i]);
+  }
+}
+
+template <bool kLut>
+__device__ __forceinline__ uint32_t encode_q(float q, const uint8_t *lut) {
+  if constexpr (kLut) {
+    return lut[__float_as_uint(q) >> 19];
+  } else {
+    return static_encode_bits(__float_as_uint(q));
+  }
+}
+
+// One thread = 16 consecutive elements of one row (requires k % 16 == 0 and
+// 16-byte aligned x / data).  Grid-stride over the flattened chunks.
+template <bool kBf16, bool kLut>
+__global__ __launch_bounds__(kThreads) void static_quant_vec16(
+    const uint16_t *__restrict__ x, const float *__restrict__ fixed, uint8_t *__restrict__ out,
+    float *__restrict__ row_scale, uint32_t n_chunks, uint32_t k_chunks, uint32_t scale_count) {
+  __shared__ __attribute__((aligned(16))) uint8_t lut[kLut ? 8192 : 16];
+  if constexpr (kLut) {
+    const uint4 *src = reinterpret_cast<const uint4 *>(kDeviceTables.static_encode);
+    uint4 *dst = reinterpret_cast<uint4 *>(lut);
+    for (int i = threadIdx.x; i < 8192 / 16; i += kThreads) dst[i] = src[i];
+    __syncthreads();
+  }
+  const uint32_t stride = gridDim.x * kThreads;
+  for (uint32_t c = blockIdx.x * kThreads + threadIdx.x; c < n_chunks; c += stride) {
+    const uint32_t row = c / k_chunks;
+    const float s = fixed[row % scale_count];
+    if (c == row * k_chunks) row_scale[row] = s;
+    const float r = __builtin_amdgcn_rcpf(s);
+    float xf[16];
+    load16<kBf16>(x + size_t(c) * 16, xf);
+    float q[16];
+    bool redo = false;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      q[j] = xf[j] * r;
+      redo |= near_index_boundary(q[j]);
+    }
+    uint32_t w[4];
+    if (__builtin_expect(!redo, 1)) {
+      // No lane value is NaN or near an index boundary: the product encodes
+      // exactly like the correctly rounded quotient.
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) b[j] = encode_q<kLut>(q[4 * i + j], lut);
+        w[i] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint32_t b[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          // NaN is decided by the full mantissa, as the reference codec does.
+          const float v = xf[4 * i + j] / s;
+          b[j] = __builtin_isnan(v) ? uint32_t(kNan) : encode_q<kLut>(v, lut);
+        }
+        w[i] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+      }
+    }
+    *reinterpret_cast<uint4 *>(out + size_t(c) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// Any shape / alignment: one thread per element, true division, arithmetic encode.
+template <bool kBf16>
+__global__ __launch_bounds__(kThreads) void static_quant_scalar(
+    const uint16_t *__restrict__ x, const float *__restrict__ fixed, uint8_t *__restrict__ out,
+    float *__restrict__ row_scale, uint64_t n, uint64_t k, uint32_t scale_count) {
+  const uint64_t stride = uint64_t(gridDim.x) * kThreads;
+  for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < n; i += stride) {
+    const uint64_t row = i / k;
+    const float s = fixed[row % scale_count];
+    if (i == row * k) row_scale[row] = s;
+    const float q = half_bits_to_float<kBf16>(x[i]) / s;
+    out[i] = uint8_t(static_encode_bits(__float_as_uint(q)));
+  }
+}
+
+// ------------------------------------------------------------ scaled decode
+
+template <bool kVec>
+__global__ __launch_bounds__(kThreads) void scaled_decode_kernel(
+    const uint8_t *__restrict__ data, const float *__restrict__ scale, uint16_t *__restrict__ out,
+    uint64_t rows, uint64_t k, uint64_t stride_bytes) {
+  __shared__ uint32_t lut[256];
+  for (int i = threadIdx.x; i < 256; i += kThreads) lut[i] = kDeviceTables.decode_f32[i];
+  __syncthreads();
+  const uint64_t per_row = kVec ? k / 16 : k;
+  const uint64_t total = rows * per_row;
+  const uint64_t step = uint64_t(gridDim.x) * kThreads;
+  for (uint64_t i = uint64_t(blockIdx.x) * kThreads + threadIdx.x; i < total; i += step) {
+    const uint64_t row = i / per_row;
+    const uint64_t col = (i - row * per_row) * (kVec ? 16 : 1);
+    const float s = scale[row];
+    const uint8_t *src = data + row * stride_bytes + col;
+    uint16_t *dst = out + row * k + col;
+    if constexpr (kVec) {
+      const uint4 q = *reinterpret_cast<const uint4 *>(src);
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+      uint32_t o[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const uint32_t word = w[j >> 1] >> ((j & 1) * 16);
+        const float v0 = __uint_as_float(lut[word & 0xFFu]) * s;
+        const float v1 = __uint_as_float(lut[(word >> 8) & 0xFFu]) * s;
+        const uint32_t h0 = __builtin_isnan(v0) ? kBf16Nan : float_to_bf16_bits(v0);
+        const uint32_t h1 = __builtin_isnan(v1) ? kBf16Nan : float_to_bf16_bits(v1);
+        o[j] = h0 | (h1 << 16);
+      }
+      uint4 *d = reinterpret_cast<uint4 *>(dst);
+      d[0] = make_uint4(o[0], o[1], o[2], o[3]);
+      d[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    } else {
+      const float v = __uint_as_float(lut[*src]) * s;
+      *dst = __builtin_isnan(v) ? kBf16Nan : float_to_bf16_bits(v);
+    }
+  }
+}
+
+int grid_for(uint64_t work_items, int per_cu) {
+  uint64_t blocks = (work_items + kThreads - 1) / kThreads;
+  const uint64_t cap = uint64_t(256) * per_cu;  // 256 CUs on MI355X
+  if (blocks > cap) blocks = cap;
+  return int(blocks < 1 ? 1 : blocks);
+}
+
+}  // namespace
+}  // namespace hif8
+
+using namespace hif8;
+
+extern "C" int hif8_static_quant(const void *x, int x_dtype, int64_t rows, int64_t k,
+                                 const float *fixed_scale, int64_t scale_count, uint8_t *data,
+                                 float *row_scale, hif8_stream_t stream) {
+  clear_error();
+  if (!x || !fixed_scale || !data || !row_scale)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_static_quant: null pointer argument");
+  if (!is_io_dtype(x_dtype))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_static_quant: x must be float16 or bfloat16");
+  if (rows <= 0 || k <= 0 || scale_count <= 0)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_static_quant: dimensions must be positive");
+  if (rows % scale_count)
+    return fail(HIF8_ERR_INVALID_ARGUMENT,
+                "hif8_static_quant: fixed_scale count must divide the activation row count");
+  if (rows > 0xFFFFFFFFll || k > 0xFFFFFFFFll || scale_count > 0xFFFFFFFFll)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_static_quant: dimensions must fit uint32");
+  const bool bf16 = x_dtype == HIF8_DTYPE_BF16;
+  const uint64_t n = uint64_t(rows) * uint64_t(k);
+  const uint64_t n_chunks = n / 16;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const uint16_t *xs = static_cast<const uint16_t *>(x);
+  if (k % 16 == 0 && aligned(x, 16) && aligned(data, 16) && n_chunks <= 0xFFFFFFFFull) {
+    const bool lut = n_chunks >= kLutMinChunks;
+    const dim3 grid(grid_for(n_chunks, 8)), block(kThreads);
+    const uint32_t nc = uint32_t(n_chunks), kc = uint32_t(k / 16), sc = uint32_t(scale_count);
+    if (bf16) {
+      if (lut) static_quant_vec16<true, true><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
+      else static_quant_vec16<true, false><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
+    } else {
+      if (lut) static_quant_vec16<false, true><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
+      else static_quant_vec16<false, false><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
+    }
+  } else {
+    const dim3 grid(grid_for(n, 8)), block(kThreads);
+    if (bf16) static_quant_scalar<true><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, n, uint64_t(k), uint32_t(scale_count));
+    else static_quant_scalar<false><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, n, uint64_t(k), uint32_t(scale_count));
+  }
+  return check_launch("hif8_static_quant");
+}
+
+extern "C" int hif8_scaled_decode(const uint8_t *data, int64_t rows, int64_t k,
+                                  int64_t data_row_stride, const float *scale, uint16_t *out,
+                                  hif8_stream_t stream) {
+  clear_error();
+  if (!data || !scale || !out)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_scaled_decode: null pointer argument");
+  if (rows <= 0 || k <= 0)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_scaled_decode: dimensions must be positive");
+  if (data_row_stride < k)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_scaled_decode: row stride %lld < k %lld",
+                (long long)data_row_stride, (long long)k);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool vec = k % 16 == 0 && data_row_stride % 16 == 0 && aligned(data, 16) && aligned(out, 16);
+  const uint64_t items = uint64_t(rows) * uint64_t(vec ? k / 16 : k);
+  const dim3 grid(grid_for(items, 8)), block(kThreads);
+  if (vec) scaled_decode_kernel<true><<<grid, block, 0, s>>>(data, scale, out, rows, k, data_row_stride);
+  else scaled_decode_kernel<false><<<grid, block, 0, s>>>(data, scale, out, rows, k, data_row_stride);
+  return check_launch("hif8_scaled_decode");
+}

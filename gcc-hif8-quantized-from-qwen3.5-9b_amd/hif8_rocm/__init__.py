@@ -1,0 +1,9 @@
+"""MI355X (gfx950) HiFloat8 static W8A8KV8 hot path.
+
+Modules:
+  native    operator API (static_quant, soft_linear, soft_static_fused_linear, scaled_decode)
+  scheme    static W8A8 linear method (input_scale / weight / weight_scale)
+  _build    in-tree build of libhif8_rocm.so and the torch extension
+"""
+
+__all__ = ["native", "scheme"]

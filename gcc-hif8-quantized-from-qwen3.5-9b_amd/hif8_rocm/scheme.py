@@ -1,0 +1,112 @@
+"""Static W8A8 HiFloat8 linear method (the caller of the quant + GEMM path).
+
+Mirrors ``AscendW8A8HiFloat8StaticLinearMethod`` (scheme.py:134-211) and its
+weight processing (scheme.py:59-91) without the vLLM-Ascend registry: a layer
+holds ``weight`` uint8 [N, K], ``weight_scale`` float32 [N, 1] and
+``input_scale`` float32 [1]; ``apply`` statically quantises the activation and
+runs the soft HiF8 linear.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+from typing import Any
+
+import torch
+
+from . import native
+
+STATIC_QUANT_TYPE = "W8A8HIF8_STATIC"
+_COMPUTE_BACKEND_ENV = "HIF8_COMPUTE_BACKEND"
+_SOFT_HIF8_BACKEND = "soft_hif8"
+_STATIC_FUSED_GENERATION_ENV = "HIF8_STATIC_FUSED_GENERATION"
+_STATIC_SCALE_FACTOR_ENV = "HIF8_STATIC_SCALE_FACTOR"
+
+
+def _static_scale_factor() -> float:
+    """Optional constant multiplier for calibrated static scales (scheme.py:26-40)."""
+    raw = os.environ.get(_STATIC_SCALE_FACTOR_ENV)
+    if raw is None or raw == "":
+        return 1.0
+    try:
+        value = float(raw)
+    except ValueError as exc:
+        raise ValueError(f"{_STATIC_SCALE_FACTOR_ENV} must be a positive finite float") from exc
+    if not math.isfinite(value) or value <= 0.0:
+        raise ValueError(f"{_STATIC_SCALE_FACTOR_ENV} must be a positive finite float")
+    return value
+
+
+class W8A8HiFloat8StaticLinearMethod:
+    """Calibrated per-tensor A8 and per-channel W8 HiFloat8 Linear (scheme.py:134-211)."""
+
+    quant_type = STATIC_QUANT_TYPE
+    supports_tp_weight_switch = False
+
+    def get_weight(self, input_size: int, output_size: int, params_dtype: torch.dtype) -> dict[str, Any]:
+        return {"weight": torch.empty(output_size, input_size, dtype=torch.uint8)}
+
+    def get_perchannel_param(self, output_size: int, params_dtype: torch.dtype) -> dict[str, Any]:
+        return {"weight_scale": torch.empty(output_size, 1, dtype=torch.float32)}
+
+    def get_pertensor_param(self, params_dtype: torch.dtype, **kwargs: Any) -> dict[str, Any]:
+        del params_dtype, kwargs
+        return {"input_scale": torch.empty(1, dtype=torch.float32)}
+
+    def _process_hif8_weights(self, layer: torch.nn.Module) -> None:
+        """scheme.py:59-91 (the bf16 embedding LUT is not part of this path)."""
+        if layer.weight.dtype != torch.uint8:
+            raise TypeError(f"{self.quant_type} checkpoint weight must be torch.uint8, got {layer.weight.dtype}")
+        if layer.weight_scale.dtype != torch.float32:
+            layer.weight_scale.data = layer.weight_scale.data.to(torch.float32)
+        layer.weight.data = layer.weight.data.contiguous()
+        layer.weight_scale.data = layer.weight_scale.data.reshape(-1).contiguous()
+        backend = os.environ.get(_COMPUTE_BACKEND_ENV, _SOFT_HIF8_BACKEND)
+        if backend != _SOFT_HIF8_BACKEND:
+            raise ValueError(
+                f"unsupported {_COMPUTE_BACKEND_ENV}={backend!r}; only '{_SOFT_HIF8_BACKEND}' is supported"
+            )
+        layer._hif8_compute_backend = backend
+
+    def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+        """Validate and normalise the checkpoint tensors (scheme.py:157-172)."""
+        if not hasattr(layer, "input_scale"):
+            raise ValueError(f"{STATIC_QUANT_TYPE} checkpoint is missing input_scale")
+        scale = layer.input_scale.data.to(dtype=torch.float32).reshape(-1)
+        if scale.numel() != 1:
+            raise ValueError(
+                f"{STATIC_QUANT_TYPE} requires one input_scale value, got shape {tuple(layer.input_scale.shape)}"
+            )
+        if not bool(torch.isfinite(scale).all()) or not bool((scale > 0).all()):
+            raise ValueError(f"{STATIC_QUANT_TYPE} input_scale must be finite and greater than zero")
+        layer.input_scale.data = scale.contiguous()
+        self._process_hif8_weights(layer)
+
+    def apply(
+        self,
+        layer: torch.nn.Module,
+        x: torch.Tensor,
+        bias: torch.Tensor | None = None,
+        tp_rank: int | None = 0,
+    ) -> torch.Tensor:
+        """static_quant -> soft_linear, or the fused kernel for tiny shapes (scheme.py:174-211)."""
+        del tp_rank
+        token_rows = x.numel() // x.shape[-1]
+        use_fused = (
+            token_rows <= 4
+            and os.environ.get(_STATIC_FUSED_GENERATION_ENV) == "1"
+            and x.shape[-1] < 1024
+        )
+        scale_factor = _static_scale_factor()
+        fixed_scale = layer.input_scale
+        if scale_factor != 1.0:
+            fixed_scale = fixed_scale * scale_factor
+        if use_fused:
+            return native.soft_static_fused_linear(
+                x, layer.weight, fixed_scale, layer.weight_scale, bias, output_dtype=x.dtype
+            )
+        activation, row_scale = native.static_quant(x, fixed_scale)
+        return native.soft_linear(
+            activation, layer.weight, row_scale, layer.weight_scale, bias, output_dtype=x.dtype
+        )

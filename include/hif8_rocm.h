@@ -1,0 +1,124 @@
+/*
+ * hif8_rocm.h - C ABI of the MI355X (gfx950) HiFloat8 static W8A8KV8 hot path.
+ *
+ * Every entry point takes plain device pointers, element counts and a HIP
+ * stream, enqueues its kernels on that stream and returns without a host
+ * synchronisation.  Nothing here allocates device memory.  The return value is
+ * HIF8_OK or an error code; hif8_last_error() returns the message of the last
+ * failure on the calling thread.  Arguments are validated before any launch, so
+ * a failed call has not touched device memory.
+ *
+ * Each function cites the reference interface it replaces (paths relative to
+ * the reference repository root).  The reference reaches its Ascend kernels
+ * through ACLNN's two-phase GetWorkspaceSize + execute calls from a torch-npu
+ * bridge; here the same operators are one call each, and the single operator
+ * that needs scratch memory (paged decode attention) reports its size through
+ * a separate query so the caller owns that memory.
+ *
+ * Layout conventions (all row-major, contiguous):
+ *   HiF8 byte tensors          uint8
+ *   scales                     float32
+ *   activations / bias / out   fp16 or bf16, selected by HIF8_DTYPE_*
+ */
+#ifndef HIF8_ROCM_H
+#define HIF8_ROCM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* A hipStream_t; NULL selects the legacy default stream. */
+typedef void *hif8_stream_t;
+
+enum hif8_status {
+  HIF8_OK = 0,
+  HIF8_ERR_INVALID_ARGUMENT = 1, /* shape/dtype/pointer contract violated */
+  HIF8_ERR_UNSUPPORTED = 2,      /* valid request outside what the kernels implement */
+  HIF8_ERR_LAUNCH = 3            /* the HIP runtime rejected a launch */
+};
+
+/* Numeric codes match the reference bridge (hif8_native.cpp:32-33). */
+enum hif8_dtype {
+  HIF8_DTYPE_FP16 = 0,
+  HIF8_DTYPE_BF16 = 1,
+  HIF8_DTYPE_NONE = -1 /* "no bias" */
+};
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *hif8_last_error(void);
+
+/* Version of this ABI (bumped on any signature change). */
+int hif8_abi_version(void);
+
+/*
+ * Static activation quantisation.
+ * Replaces aclnnHif8StaticQuant as called by Hif8StaticQuant
+ * (csrc/extension/hif8_native.cpp:487-554; kernel csrc/opp/op_kernel/hif8_static_quant.cpp:37-150).
+ *   x          [rows, k] fp16/bf16
+ *   fixed_scale[scale_count] float32, finite > 0; row r uses fixed_scale[r % scale_count]
+ *   data       [rows, k] uint8  <- enc_sat(float(x) / scale)   (IEEE division)
+ *   row_scale  [rows] float32   <- fixed_scale[r % scale_count] (contiguous; the
+ *              reference returns a stride-16 view of the same values)
+ */
+int hif8_static_quant(const void *x, int x_dtype, int64_t rows, int64_t k,
+                      const float *fixed_scale, int64_t scale_count,
+                      uint8_t *data, float *row_scale, hif8_stream_t stream);
+
+/*
+ * Scaled decode to bf16.
+ * Replaces aclnnHif8ScaledDecode as called by Hif8ScaledDecode
+ * (csrc/extension/hif8_native.cpp:556-611; kernel csrc/opp/op_kernel/hif8_scaled_decode.cpp:50-125).
+ *   data  [rows, k] uint8 with row pitch data_row_stride bytes (>= k; lets the
+ *         caller decode KV rows in place, skipping the inline 4-byte scale)
+ *   scale [rows] float32
+ *   out   [rows, k] bf16 payloads <- bf16_RNE(dec(b) * scale[r]); NaN -> 0x7FC0
+ */
+int hif8_scaled_decode(const uint8_t *data, int64_t rows, int64_t k, int64_t data_row_stride,
+                       const float *scale, uint16_t *out, hif8_stream_t stream);
+
+/*
+ * Soft-decode GEMV, reference contract M <= 2.
+ * Replaces aclnnSoftHif8Gemv as called by SoftHif8Gemv
+ * (csrc/extension/hif8_native.cpp:241-316,613-631; kernel csrc/opp/op_kernel/soft_hif8_gemv.cpp:28-317).
+ *   activation [m, k] uint8, weight [n, k] uint8,
+ *   token_scale [m], channel_scale [n] float32,
+ *   bias [n] fp16/bf16 or NULL (bias_dtype HIF8_DTYPE_NONE),
+ *   out [m, n] fp16/bf16:
+ *     out = RNE((sum_k dec(a) dec(w)) * token_scale[m] * channel_scale[n] + bias[n])
+ *   with FP32 accumulation.
+ */
+int soft_hif8_gemv(const uint8_t *activation, const uint8_t *weight, const float *token_scale,
+                   const float *channel_scale, const void *bias, int bias_dtype, void *out,
+                   int out_dtype, int64_t m, int64_t n, int64_t k, hif8_stream_t stream);
+
+/*
+ * Soft-decode GEMM, any M >= 1 (same arguments and contract as soft_hif8_gemv).
+ * Replaces aclnnSoftHif8Gemm / aclnnSoftHif8PrefillGemm as routed by SoftHif8Gemm
+ * (csrc/extension/hif8_native.cpp:633-669; kernel csrc/opp/op_kernel/soft_hif8_gemm.cpp:163-2139).
+ * M <= 4 runs the HBM-streaming GEMV kernel, larger M the bf16-MFMA kernel.
+ */
+int soft_hif8_gemm(const uint8_t *activation, const uint8_t *weight, const float *token_scale,
+                   const float *channel_scale, const void *bias, int bias_dtype, void *out,
+                   int out_dtype, int64_t m, int64_t n, int64_t k, hif8_stream_t stream);
+
+/*
+ * Fixed-scale fused quant + GEMM for M <= 4.
+ * Replaces aclnnSoftHif8StaticFusedGemm as called by SoftHif8StaticFusedGemm
+ * (csrc/extension/hif8_native.cpp:784-910; kernel csrc/opp/op_kernel/soft_hif8_fused_gemm.cpp
+ * built with HIF8_FUSED_STATIC_SCALE=1).  Equal, bit for bit, to hif8_static_quant
+ * followed by soft_hif8_gemm with token_scale = fixed_scale[0].
+ *   x [m, k] fp16/bf16 (x_dtype), fixed_scale [1] float32, other arguments as above.
+ */
+int soft_hif8_static_fused_gemm(const void *x, int x_dtype, const uint8_t *weight,
+                                const float *fixed_scale, const float *channel_scale,
+                                const void *bias, int bias_dtype, void *out, int out_dtype,
+                                int64_t m, int64_t n, int64_t k, hif8_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HIF8_ROCM_H */

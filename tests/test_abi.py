@@ -1,0 +1,75 @@
+"""The C-ABI library loads without a GPU, exports every function declared in
+include/*.h and rejects invalid arguments before touching the device (CPU)."""
+
+import ctypes
+import re
+
+import pytest
+
+from conftest import PKG_ROOT, REPO
+
+LIB = PKG_ROOT / "hif8_rocm" / "libhif8_rocm.so"
+
+
+def _declared_functions():
+    names = []
+    for header in (REPO / "include").glob("*.h"):
+        text = re.sub(r"/\*.*?\*/", "", header.read_text(), flags=re.S)
+        names += re.findall(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_ ]*?\*?\s*\b([a-z][a-z0-9_]*)\s*\(", text, re.M)
+    return sorted(set(names))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not LIB.exists():
+        pytest.fail(f"{LIB} is not built; run __graft_entry__.build()")
+    lib = ctypes.CDLL(str(LIB))
+    lib.hif8_last_error.restype = ctypes.c_char_p
+    return lib
+
+
+def test_header_declares_the_operator_set():
+    names = _declared_functions()
+    for required in ("hif8_static_quant", "hif8_scaled_decode", "soft_hif8_gemv", "soft_hif8_gemm",
+                     "soft_hif8_static_fused_gemm", "hif8_last_error", "hif8_abi_version"):
+        assert required in names
+
+
+def test_every_declared_symbol_is_exported(lib):
+    missing = [n for n in _declared_functions() if not hasattr(lib, n)]
+    assert not missing, missing
+    assert lib.hif8_abi_version() >= 1
+
+
+def _p(v=1):
+    return ctypes.c_void_p(v)
+
+
+def test_static_quant_rejects_bad_arguments(lib):
+    f = lib.hif8_static_quant
+    f.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int64, ctypes.c_void_p,
+                  ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+    assert f(None, 1, 4, 8, _p(), 1, _p(), _p(), None) == 1
+    assert b"null pointer" in lib.hif8_last_error()
+    assert f(_p(), 1, 3, 8, _p(), 2, _p(), _p(), None) == 1
+    assert b"must divide" in lib.hif8_last_error()
+    assert f(_p(), 7, 4, 8, _p(), 1, _p(), _p(), None) == 1
+    assert b"float16 or bfloat16" in lib.hif8_last_error()
+
+
+def test_linear_entry_points_enforce_reference_contracts(lib):
+    args = [ctypes.c_void_p] * 5 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int] + [ctypes.c_int64] * 3 + [ctypes.c_void_p]
+    gemv = lib.soft_hif8_gemv
+    gemv.argtypes = args
+    assert gemv(_p(), _p(), _p(), _p(), None, -1, _p(), 1, 3, 8, 4, None) == 1
+    assert b"M <= 2" in lib.hif8_last_error()
+    gemm = lib.soft_hif8_gemm
+    gemm.argtypes = args
+    assert gemm(_p(), _p(), _p(), _p(), None, -1, _p(), 5, 3, 8, 4, None) == 1
+    assert b"output_dtype" in lib.hif8_last_error()
+    assert gemm(_p(), _p(), _p(), _p(), None, -1, _p(), 1, 0, 8, 4, None) == 1
+    assert b"positive" in lib.hif8_last_error()
+    fused = lib.soft_hif8_static_fused_gemm
+    fused.argtypes = [ctypes.c_void_p, ctypes.c_int] + [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int] + [ctypes.c_int64] * 3 + [ctypes.c_void_p]
+    assert fused(_p(), 1, _p(), _p(), _p(), None, -1, _p(), 1, 5, 8, 4, None) == 1
+    assert b"M <= 4" in lib.hif8_last_error()

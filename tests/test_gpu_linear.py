@@ -1,0 +1,170 @@
+"""soft_hif8_gemv / soft_hif8_gemm / soft_hif8_static_fused_gemm on the GPU
+against the oracle's linear_u8_u8 (test_npu_ops.py:179-750 shape).  Tolerance
+rtol = atol = 1e-2 on bf16/fp16 outputs with FP32 accumulation; the fused path
+must equal quant -> GEMM bit for bit."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _data import LAYER_SHAPES, bf16_activation, hif8_weight, input_scale_of, random_codes
+from oracle import hif8_oracle as o
+
+pytestmark = pytest.mark.gpu
+TOL = dict(rtol=1e-2, atol=1e-2)
+
+
+def _t(a, device, dtype=None):
+    t = torch.from_numpy(np.ascontiguousarray(a))
+    return (t.to(dtype) if dtype is not None else t).to(device)
+
+
+def _check(actual: torch.Tensor, expected: np.ndarray, **tol):
+    torch.testing.assert_close(actual.cpu().float(), torch.from_numpy(np.asarray(expected, np.float32)),
+                               **(tol or TOL), equal_nan=True)
+
+
+def test_gemv_propagates_special_codes(native_ops, device):
+    one = o.encode_scalar(1.0)
+    codes = [0x80, 0x6F, 0xEF]
+    act = torch.tensor([[c, one] for c in codes], dtype=torch.uint8, device=device)
+    weight = torch.tensor([[one, 0] for _ in codes], dtype=torch.uint8, device=device)
+    ts = torch.tensor([1.5, 0.5, 2.0], device=device)
+    cs = torch.ones(3, device=device)
+    for row, code in enumerate(codes):
+        for out_dtype in (torch.float16, torch.bfloat16):
+            y = native_ops.soft_hif8_gemv(act[row:row + 1].clone(), weight, ts[row:row + 1].clone(), cs, None, out_dtype)
+            torch.cuda.synchronize()
+            got = y.cpu().float()[0, row].item()
+            want = o.decode_scalar(code) * ts[row].item()
+            assert (math.isnan(got) and math.isnan(want)) or got == want
+
+
+@pytest.mark.parametrize("rows", [1, 2, 3, 4, 5])
+def test_soft_linear_matches_reference_small(native_ops, device, rows):
+    from hif8_rocm import native as api
+
+    w, ws = o.quantize_rows([[1.0, -2.0, 0.5, 4.0], [-0.25, 1.5, -3.0, 2.0], [2.0, 0.0, -1.0, 0.25]])
+    a, sa = o.quantize_rows([[0.5 * (r + 1), -1.0, 2.0, -0.25 * (r + 1)] for r in range(rows)])
+    for bias_dtype in (None, torch.float16, torch.bfloat16):
+        bias_vals = None if bias_dtype is None else [0.5, -1.0, 2.0]
+        bias = None if bias_dtype is None else torch.tensor(bias_vals, dtype=bias_dtype, device=device)
+        want = o.linear_u8_u8(a, sa, w, ws, bias_vals)
+        for out_dtype in (torch.float16, torch.bfloat16):
+            y = api.soft_linear(_t(a, device), _t(w, device), _t(sa, device, torch.float32),
+                                _t(ws, device, torch.float32), bias, output_dtype=out_dtype)
+            _check(y, want)
+
+
+@pytest.mark.parametrize("rows,channels,k", [
+    (1, 17, 37), (2, 17, 37), (3, 3, 4), (5, 16, 16), (3, 17, 37), (3, 256, 16),
+    (3, 2176, 16), (5, 16, 255), (1, 17, 1024), (2, 17, 1037), (1, 33, 2048),
+    (63, 16, 37), (64, 16, 64), (65, 17, 128), (129, 1024, 4097), (130, 300, 4096),
+])
+def test_gemm_shapes_and_tails(native_ops, device, rows, channels, k):
+    a = random_codes((rows, k), seed=rows * 7 + k)
+    w = random_codes((channels, k), seed=channels * 5 + k)
+    g = np.random.default_rng(rows + channels + k)
+    ts = (g.random(rows, dtype=np.float32) + 1.0) * 1e-3
+    cs = (g.random(channels, dtype=np.float32) + 1.0) * 1e-3
+    bias = (g.random(channels, dtype=np.float32) - 0.5)
+    want = o.linear_u8_u8(a, ts, w, cs, bias.astype(np.float64))
+    for out_dtype in (torch.bfloat16, torch.float16):
+        y = native_ops.soft_hif8_gemm(_t(a, device), _t(w, device), _t(ts, device), _t(cs, device),
+                                      _t(bias, device, out_dtype), out_dtype)
+        y2 = native_ops.soft_hif8_gemm(_t(a, device), _t(w, device), _t(ts, device), _t(cs, device),
+                                       _t(bias, device, out_dtype), out_dtype)
+        torch.cuda.synchronize()
+        assert torch.equal(y, y2)
+        rounded = bias.astype(np.float32)
+        rounded = (torch.from_numpy(rounded).to(out_dtype).float().numpy()).astype(np.float64)
+        _check(y, want - bias + rounded)
+
+
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("n,k", LAYER_SHAPES)
+def test_decode_gemv_config_shapes(native_ops, device, m, n, k):
+    """M in {1,4} over one layer's projection shapes."""
+    from hif8_rocm import native as api
+
+    x = bf16_activation(m, k, seed=20261201 + k)
+    s = input_scale_of(x)
+    w, ws = hif8_weight(n, k, seed=n + k)
+    xq, _ = o.static_quant_rows(x.float().numpy(), s.numpy())
+    want = o.linear_u8_u8(xq, np.repeat(s.numpy(), m), w, ws)
+    data, rs = api.static_quant(x.to(device), s.to(device))
+    y = api.soft_linear(data, _t(w, device), rs, _t(ws, device), None, output_dtype=torch.bfloat16)
+    _check(y, want)
+    fused = api.soft_static_fused_linear(x.to(device), _t(w, device), s.to(device), _t(ws, device),
+                                         None, output_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, y)
+
+
+@pytest.mark.parametrize("m", [512, 4096])
+@pytest.mark.parametrize("n,k", [(2048, 4096), (4096, 12288), (24576, 4096)])
+@pytest.mark.parametrize("heavy", [False, True])
+def test_prefill_gemm_config_shapes(native_ops, device, m, n, k, heavy):
+    """BASELINE config 3 (sampled rows checked against the oracle at full size)."""
+    from hif8_rocm import native as api
+
+    x = bf16_activation(m, k, seed=m + n + k, heavy_tail=heavy)
+    s = input_scale_of(x)
+    w, ws = hif8_weight(n, k, seed=n * 3 + k)
+    data, rs = api.static_quant(x.to(device), s.to(device))
+    y = api.soft_linear(data, _t(w, device), rs, _t(ws, device), None, output_dtype=torch.bfloat16)
+    rows = np.random.default_rng(m).choice(m, size=min(m, 48), replace=False)
+    xq = data.cpu().numpy()[rows]
+    want = o.linear_u8_u8(xq, np.repeat(s.numpy(), rows.size), w, ws)
+    _check(y[torch.from_numpy(rows).to(device)], want)
+
+
+def test_static_fused_matches_static_quant_then_gemm(native_ops, device):
+    g = torch.Generator().manual_seed(20260821)
+    for rows, channels, k, with_bias in ((1, 128, 2048, False), (2, 256, 4096, True), (4, 256, 4096, True),
+                                         (1, 128, 12288, True), (3, 77, 48, True)):
+        x = (torch.randn(rows, k, generator=g) * 3.0).to(torch.bfloat16).to(device)
+        w = torch.randint(0, 111, (channels, k), generator=g, dtype=torch.uint8).to(device)
+        fixed = torch.tensor([0.75], device=device)
+        cs = (torch.rand(channels, generator=g) + 0.01).to(device)
+        bias = torch.randn(channels, generator=g).to(torch.bfloat16).to(device) if with_bias else None
+        data, row_scale = native_ops.hif8_static_quant(x, fixed)
+        want = native_ops.soft_hif8_gemm(data, w, row_scale.contiguous(), cs, bias, torch.bfloat16)
+        got = native_ops.soft_hif8_static_fused_gemm(x, w, fixed, cs, bias, torch.bfloat16)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), (rows, channels, k)
+
+
+def test_static_fused_saturates_finite_outliers(native_ops, device):
+    k = 2048
+    x = torch.zeros((1, k), dtype=torch.bfloat16)
+    x[0, :6] = torch.tensor([1.0e20, -1.0e20, 32768.0, -32768.0, 65536.0, -65536.0], dtype=torch.bfloat16)
+    x = x.to(device)
+    w = torch.zeros((128, k), dtype=torch.uint8, device=device)
+    for c in range(6):
+        w[c, c] = o.encode_scalar(1.0)
+    fixed = torch.ones(1, device=device)
+    cs = torch.ones(128, device=device)
+    data, rs = native_ops.hif8_static_quant(x, fixed)
+    want = native_ops.soft_hif8_gemm(data, w, rs, cs, None, torch.bfloat16)
+    got = native_ops.soft_hif8_static_fused_gemm(x, w, fixed, cs, None, torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+    assert got[0, :6].float().tolist() == [32768.0, -32768.0, 32768.0, -32768.0, 32768.0, -32768.0]
+
+
+def test_operator_row_contracts_are_strict(native_ops, device):
+    act = torch.zeros((3, 4), dtype=torch.uint8, device=device)
+    w = torch.zeros((2, 4), dtype=torch.uint8, device=device)
+    with pytest.raises(RuntimeError, match="M <= 2"):
+        native_ops.soft_hif8_gemv(act, w, torch.ones(3, device=device), torch.ones(2, device=device), None, torch.float16)
+
+
+def test_nonzero_storage_offset_is_rejected(native_ops, device):
+    view = torch.zeros((3, 4), dtype=torch.uint8, device=device)[1:]
+    assert view.is_contiguous() and view.storage_offset() > 0
+    with pytest.raises(RuntimeError, match="storage_offset == 0"):
+        native_ops.soft_hif8_gemv(view, torch.zeros((2, 4), dtype=torch.uint8, device=device),
+                                  torch.ones(2, device=device), torch.ones(2, device=device), None, torch.float16)
