@@ -7,7 +7,7 @@
 // implementation validates like the reference bridge (hif8_native.cpp:131-316,
 // 487-611, 784-861), allocates outputs with the caching allocator and calls
 // the C ABI on the current HIP stream.  No host synchronisation, no fallback.
-#include <c10/hip/HIPGuard.h>
+#include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
 
@@ -96,7 +96,7 @@ at::Tensor SoftLinear(const at::Tensor &activation, const at::Tensor &weight, co
                       const at::Tensor &channel_scale, const c10::optional<at::Tensor> &bias,
                       at::ScalarType output_dtype, bool gemv, const char *op, LinearFn fn) {
   ValidateSoftLinear(activation, weight, token_scale, channel_scale, bias, output_dtype, gemv);
-  const c10::hip::HIPGuard guard(activation.device());
+  const c10::OptionalDeviceGuard guard(activation.device());
   auto out = at::empty({activation.size(0), weight.size(0)}, activation.options().dtype(output_dtype));
   const void *bias_ptr = bias.has_value() ? bias->data_ptr() : nullptr;
   const int bias_dtype = bias.has_value() ? DtypeCode(bias->scalar_type()) : HIF8_DTYPE_NONE;
@@ -124,7 +124,7 @@ std::tuple<at::Tensor, at::Tensor> Hif8StaticQuant(const at::Tensor &x, const at
   CheckFitsUint32(k, "K");
   CheckFitsUint32(fixed_scale.numel(), "fixed scale count");
   CheckSameDevice(fixed_scale, x.device(), "fixed_scale");
-  const c10::hip::HIPGuard guard(x.device());
+  const c10::OptionalDeviceGuard guard(x.device());
   auto data = at::empty(x.sizes(), x.options().dtype(at::ScalarType::Byte));
   auto row_scale = at::empty({rows}, x.options().dtype(at::ScalarType::Float));
   CheckStatus(hif8_static_quant(x.data_ptr(), DtypeCode(x.scalar_type()), rows, k, fixed_scale.data_ptr<float>(),
@@ -146,7 +146,7 @@ at::Tensor Hif8ScaledDecode(const at::Tensor &data, const at::Tensor &scale) {
   CheckFitsUint32(data.size(0), "row count");
   CheckFitsUint32(data.size(1), "K");
   CheckSameDevice(scale, data.device(), "scale");
-  const c10::hip::HIPGuard guard(data.device());
+  const c10::OptionalDeviceGuard guard(data.device());
   auto out = at::empty(data.sizes(), data.options().dtype(at::ScalarType::BFloat16));
   CheckStatus(hif8_scaled_decode(data.data_ptr<uint8_t>(), data.size(0), data.size(1), data.size(1),
                                  scale.data_ptr<float>(), reinterpret_cast<uint16_t *>(out.data_ptr()),
@@ -208,7 +208,7 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
   }
   TORCH_CHECK(output_dtype == at::ScalarType::Half || output_dtype == at::ScalarType::BFloat16,
               "output_dtype must be torch.float16 or torch.bfloat16");
-  const c10::hip::HIPGuard guard(device);
+  const c10::OptionalDeviceGuard guard(device);
   auto out = at::empty({activation.size(0), weight.size(0)}, activation.options().dtype(output_dtype));
   const void *bias_ptr = bias.has_value() ? bias->data_ptr() : nullptr;
   const int bias_dtype = bias.has_value() ? DtypeCode(bias->scalar_type()) : HIF8_DTYPE_NONE;
