@@ -1,0 +1,367 @@
+#!/usr/bin/env python3
+"""Benchmark of the HiF8 static W8A8KV8 hot path on one MI355X.
+
+Headline (``value``): the decode GEMV sweep of BASELINE configs[1] - for
+M in {1, 4}, every projection of one 9B-class decoder layer (q 4096x4096,
+fused k+v 2048x4096, o 4096x4096, fused gate+up 24576x4096, down 4096x12288)
+runs the static W8A8 linear method (hif8_rocm.scheme): hif8_static_quant of
+the bf16 activation, then soft_hif8_gemm, which runs the HBM-streaming GEMV
+kernel for M <= 4.  The fused single-launch variant (soft_hif8_static_fused_gemm)
+is reported beside it.  One step = that sweep over one layer's weights; five distinct weight copies (966 MB) are
+rotated so the 256 MB Infinity Cache cannot serve them.  Steps are captured
+in HIP graphs and replayed, so host launch overhead is not timed.
+
+``value`` = algorithmic bytes of the step (weights + activations + scales +
+outputs of every quant and GEMV launch) / wall time per step, in GB/s.
+Secondary figures (prefill GEMM TFLOP/s, static quant GB/s, KV decode
+attention) and a per-kernel table are reported in the same JSON line.
+
+Synthetic data: bf16 activations ~N(0,1) with a static scale absmax/32768;
+weights ~N(0, 0.02) with per-row scales absmax/32768, encoded on the GPU.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+PKG_ROOT = REPO / "gcc-hif8-quantized-from-qwen3.5-9b_amd"
+for _p in (str(REPO), str(PKG_ROOT)):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "HiF8 GEMV GB/s & GEMM TFLOP/s vs MI355X roofline; KV8 decode-attn μs/token"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+HIF8_MAX = 32768.0
+LAYER = [("q", 4096, 4096), ("kv", 2048, 4096), ("o", 4096, 4096), ("gate_up", 24576, 4096), ("down", 4096, 12288)]
+DECODE_M = (1, 4)
+PREFILL_M = (512, 4096)
+N_COPIES = 5
+
+
+def gemv_bytes(m: int, n: int, k: int) -> int:
+    return n * k + m * k + 4 * n + 4 * m + 2 * m * n
+
+
+def quant_bytes(m: int, k: int) -> int:
+    return 3 * m * k + 4 * m + 4
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Setup:
+    def __init__(self, torch, native, device):
+        from hif8_rocm.scheme import W8A8HiFloat8StaticLinearMethod
+
+        self.torch, self.native, self.device = torch, native, device
+        self.method = W8A8HiFloat8StaticLinearMethod()
+        g = torch.Generator(device=device).manual_seed(20261201)
+        self.x = {}
+        for m in DECODE_M + PREFILL_M:
+            for k in sorted({k for _, _, k in LAYER}):
+                x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+                s = (x.float().abs().amax() / HIF8_MAX).reshape(1).contiguous()
+                self.x[(m, k)] = (x, s)
+        self.weights = []  # [copy][name] -> (codes u8 [N,K], scale f32 [N])
+        self.layers = []   # [copy][name] -> module with weight / weight_scale / input_scale
+        for _ in range(N_COPIES):
+            ws_by_name, mods = {}, {}
+            for name, n, k in LAYER:
+                w = (torch.randn(n, k, generator=g, device=device) * 0.02).to(torch.bfloat16)
+                ws = (w.float().abs().amax(dim=1) / HIF8_MAX).contiguous()
+                codes, _ = native.static_quant(w, ws)
+                del w
+                ws_by_name[name] = (codes, ws)
+                mod = torch.nn.Module()
+                mod.weight = torch.nn.Parameter(codes, requires_grad=False)
+                mod.weight_scale = torch.nn.Parameter(ws.reshape(-1, 1).clone(), requires_grad=False)
+                mod.input_scale = torch.nn.Parameter(self.x[(1, k)][1].clone(), requires_grad=False)
+                self.method.process_weights_after_loading(mod)
+                mods[name] = mod
+            self.weights.append(ws_by_name)
+            self.layers.append(mods)
+        torch.cuda.synchronize()
+
+
+def capture(torch, fn):
+    """Capture fn() into a HIP graph after one eager warm-up run on a side stream."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        fn()
+    return graph
+
+
+def time_graphs(torch, graphs, reps: int) -> float:
+    """Average milliseconds per replay of graphs[i % len] (HIP events on the replay stream)."""
+    for g in graphs:
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(reps):
+        graphs[i % len(graphs)].replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def decode_step_fn(st: Setup, copy: int, fused: bool = False):
+    """One decode sweep through the scheme, or through the fused static-quant GEMV."""
+    native, torch = st.native, st.torch
+
+    def step():
+        for m in DECODE_M:
+            for name, n, k in LAYER:
+                x, s = st.x[(m, k)]
+                if fused:
+                    w, ws = st.weights[copy][name]
+                    native.soft_static_fused_linear(x, w, s, ws, None, output_dtype=torch.bfloat16)
+                else:
+                    st.method.apply(st.layers[copy][name], x)
+    return step
+
+
+def per_kernel_table(st: Setup, launches: int = 20) -> dict:
+    """Per-launch time of each GEMV / GEMM / quant, from graphs of back-to-back launches."""
+    torch, native = st.torch, st.native
+    table = {}
+    for m in DECODE_M + PREFILL_M:
+        for name, n, k in LAYER:
+            x, s = st.x[(m, k)]
+            q, rs = native.static_quant(x, s)
+            per = max(1, launches if m <= 4 else 5)
+
+            def fn(q=q, rs=rs, name=name):
+                for i in range(per):
+                    w, ws = st.weights[i % N_COPIES][name]
+                    native.soft_linear(q, w, rs, ws, None, output_dtype=torch.bfloat16)
+            ms = time_graphs(torch, [capture(torch, fn)], 3) / per
+            entry = {"us": round(ms * 1e3, 3)}
+            if m <= 4:
+                gbs = gemv_bytes(m, n, k) / (ms * 1e-3) / 1e9
+                entry.update(kernel="gemv", bytes=gemv_bytes(m, n, k), GBps=round(gbs, 1),
+                             frac_hbm=round(gbs / HBM_PEAK_GBS, 4))
+            else:
+                tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+                entry.update(kernel="gemm", flops=2 * m * n * k, TFLOPs=round(tf, 1),
+                             frac_bf16=round(tf / BF16_PEAK_TFLOPS, 4))
+            table[f"{name}_m{m}"] = entry
+            if m <= 4:
+                def ff(x=x, s=s, name=name):
+                    for i in range(per):
+                        w, ws = st.weights[i % N_COPIES][name]
+                        native.soft_static_fused_linear(x, w, s, ws, None, output_dtype=torch.bfloat16)
+                ms = time_graphs(torch, [capture(torch, ff)], 3) / per
+                fb = gemv_bytes(m, n, k) + m * k  # bf16 x instead of u8 codes
+                gbs = fb / (ms * 1e-3) / 1e9
+                table[f"{name}_m{m}_fused"] = {"kernel": "fused_quant_gemv", "us": round(ms * 1e3, 3), "bytes": fb,
+                                               "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    for m, k in ((4096, 4096), (512, 4096), (1, 4096), (4, 12288)):
+        x, s = st.x[(m, k)]
+
+        def fq(x=x, s=s):
+            for _ in range(10):
+                native.static_quant(x, s)
+        ms = time_graphs(torch, [capture(torch, fq)], 3) / 10
+        gbs = quant_bytes(m, k) / (ms * 1e-3) / 1e9
+        table[f"static_quant_m{m}_k{k}"] = {"kernel": "static_quant", "us": round(ms * 1e3, 3),
+                                            "bytes": quant_bytes(m, k), "GBps": round(gbs, 1),
+                                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    return table
+
+
+def cpu_baseline(budget_s: float = 20.0) -> dict:
+    """The numpy oracle's decode-GEMV sweep on the host (single-threaded numpy gather + BLAS)."""
+    import numpy as np
+
+    from oracle import hif8_oracle as o
+
+    rng = np.random.default_rng(0)
+    step_bytes = sum(quant_bytes(m, k) + gemv_bytes(m, n, k) for m in DECODE_M for _, n, k in LAYER)
+    weights = {}
+    for name, n, k in LAYER:
+        weights[name] = (rng.integers(0, 111, (n, k), dtype=np.uint8), (rng.random(n, dtype=np.float32) + 0.5) * 1e-5)
+    xs = {(m, k): rng.standard_normal((m, k)).astype(np.float32) for m in DECODE_M for k in (4096, 12288)}
+    done, t0 = 0, time.perf_counter()
+    while True:
+        for m in DECODE_M:
+            for name, n, k in LAYER:
+                x = xs[(m, k)]
+                s = np.array([np.abs(x).max() / HIF8_MAX], np.float32)
+                xq, _ = o.static_quant_rows(x, s)
+                w, ws = weights[name]
+                wd = o.DECODE_F32[w] * ws[:, None]          # decode-LUT weights x channel scale
+                _ = (o.DECODE_F32[xq] * s[0]) @ wd.T          # fp32 matmul
+        done += 1
+        if time.perf_counter() - t0 > budget_s or done >= 3:
+            break
+    elapsed = time.perf_counter() - t0
+    return {"value": round(step_bytes * done / elapsed / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"{done} full decode sweep step(s) (M in {{1,4}} x 5 projections, quant + LUT-decode + fp32 "
+                      f"matmul) of the numpy oracle, {elapsed:.1f} s, OMP/BLAS threads 1"}
+
+
+def profile_pass(st: Setup, reps: int = 3) -> None:
+    """Eager launches for counter collection (rocprofv3 --pmc ...).
+
+    Known-size calibration kernels first: a torch copy of 64 MiB (read + write)
+    and an fp32 sum over the same 64 MiB (a plain streaming read with 16-byte
+    vector loads, the load width of the GEMV).  Then every decode GEMV, static
+    quant and prefill GEMM launch `reps` times."""
+    torch, native = st.torch, st.native
+    src = torch.empty(64 << 20, dtype=torch.uint8, device=st.device).fill_(3)
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for _ in range(reps):
+        src.view(torch.float32).sum()
+    torch.cuda.synchronize()
+    for m in DECODE_M + PREFILL_M:
+        for name, n, k in LAYER:
+            x, s = st.x[(m, k)]
+            for i in range(reps):
+                q, rs = native.static_quant(x, s)
+                w, ws = st.weights[i % N_COPIES][name]
+                native.soft_linear(q, w, rs, ws, None, output_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    log("profile pass done")
+
+
+def committed_traffic(kernel_key: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/pmc_traffic.json), if present."""
+    path = REPO / "profiles" / "pmc_traffic.json"
+    if not path.exists():
+        return None
+    entry = json.loads(path.read_text()).get("kernels", {}).get(kernel_key)
+    return None if entry is None else entry.get("traffic_bytes")
+
+
+def main() -> None:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="eager launches only, for rocprofv3 counter collection; prints no JSON")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    cpu = None
+    if not args.no_cpu_baseline and not args.profile_pass:
+        for var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
+            os.environ[var] = "1"
+        log("cpu baseline (numpy oracle) ...")
+        cpu = cpu_baseline()
+        log(f"cpu baseline {cpu['value']} GB/s")
+
+    import torch
+
+    from hif8_rocm import native
+
+    native.load_extension()
+    device = torch.device("cuda:0")
+    log("generating synthetic weights ...")
+    st = Setup(torch, native, device)
+    if args.profile_pass:
+        profile_pass(st)
+        return
+
+    log("capturing decode-sweep graphs ...")
+    graphs = [capture(torch, decode_step_fn(st, c)) for c in range(N_COPIES)]
+    for i in range(args.warmup):
+        graphs[i % N_COPIES].replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(args.steps):
+        graphs[i % N_COPIES].replay()
+    e1.record()
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / args.steps
+    gpu_ms = e0.elapsed_time(e1) / args.steps
+    step_bytes = sum(quant_bytes(m, k) + gemv_bytes(m, n, k) for m in DECODE_M for _, n, k in LAYER)
+    value = step_bytes / (wall_ms * 1e-3) / 1e9
+    log(f"decode sweep: {wall_ms * 1e3:.1f} us/step wall, {gpu_ms * 1e3:.1f} us/step events, {value:.1f} GB/s")
+
+    fused = [capture(torch, decode_step_fn(st, c, fused=True)) for c in range(N_COPIES)]
+    fused_ms = time_graphs(torch, fused, args.steps)
+    fused_gbs = step_bytes / (fused_ms * 1e-3) / 1e9
+    log(f"fused single-launch sweep: {fused_ms * 1e3:.1f} us/step, {fused_gbs:.1f} GB/s")
+
+    log("per-kernel table ...")
+    table = per_kernel_table(st)
+    gemv = [v for v in table.values() if v["kernel"] == "gemv"]
+    dom = table["gate_up_m1"]
+    gemm_layer = {}
+    for m in PREFILL_M:
+        fl = sum(table[f"{n}_m{m}"]["flops"] for n, _, _ in LAYER)
+        us = sum(table[f"{n}_m{m}"]["us"] for n, _, _ in LAYER)
+        tf = fl / (us * 1e-6) / 1e12
+        gemm_layer[f"m{m}"] = {"TFLOPs": round(tf, 1), "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 4),
+                               "us_per_layer": round(us, 1)}
+    all_gemv_gbs = sum(v["bytes"] for v in gemv) / (sum(v["us"] for v in gemv) * 1e-6) / 1e9
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall_ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode GEMV sweep (BASELINE configs[1]): static W8A8 scheme apply = static_quant + "
+                        "soft_hif8_gemm, M in {1,4} x q/kv/o/gate_up/down of one 9B-class layer, 5 rotated "
+                        "weight copies, HIP-graph replay",
+            "operands": "HiF8 u8 weights/activations, bf16 dot products, fp32 accumulate, bf16 out",
+            "shapes_nk": [[n, k] for _, n, k in LAYER],
+            "m": list(DECODE_M),
+            "step_bytes": step_bytes,
+        },
+        "roofline": {
+            "kernel": "gemv_kernel (gate_up 24576x4096, M=1)",
+            "bound": "hbm",
+            "achieved": dom["GBps"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
+            "traffic": committed_traffic("gate_up_m1"),
+            "bytes_per_launch": dom["bytes"],
+            "us_per_launch": dom["us"],
+        },
+        "cpu_baseline": cpu,
+        "decode_sweep_fused_GBps": round(fused_gbs, 1),
+        "gemv_all_launches_GBps": round(all_gemv_gbs, 1),
+        "gemm_per_layer": gemm_layer,
+        "kernels": table,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

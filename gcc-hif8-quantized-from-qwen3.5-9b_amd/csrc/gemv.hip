@@ -14,6 +14,8 @@
 //     epilogue applies token scale, channel scale and bias, rounding once.
 // The fused variant takes fp16/bf16 x and statically encodes it on the fly
 // (soft_hif8_fused_gemm.cpp:449-534 with HIF8_FUSED_STATIC_SCALE).
+#include <stdlib.h>
+
 #include "linear.h"
 
 namespace hif8 {
@@ -28,31 +30,59 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
+typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+
+// Two table entries packed as one bf16 pair (compiles to one v_perm_b32).
+__device__ __forceinline__ uint32_t lut_pair(const uint16_t *lut, uint32_t lo, uint32_t hi) {
+  u16x2 v;
+  v.x = lut[lo];
+  v.y = lut[hi];
+  return __builtin_bit_cast(uint32_t, v);
+}
+
 // 16 HiF8 bytes -> 8 packed bf16 pairs through the LDS decode table.
 __device__ __forceinline__ void decode16(const uint16_t *lut, const u32x4 q, uint32_t (&p)[8]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t w = q[i];
-    p[2 * i] = uint32_t(lut[w & 0xFFu]) | (uint32_t(lut[(w >> 8) & 0xFFu]) << 16);
-    p[2 * i + 1] = uint32_t(lut[(w >> 16) & 0xFFu]) | (uint32_t(lut[w >> 24]) << 16);
+    p[2 * i] = lut_pair(lut, w & 0xFFu, (w >> 8) & 0xFFu);
+    p[2 * i + 1] = lut_pair(lut, (w >> 16) & 0xFFu, w >> 24);
   }
 }
 
-// 16 fp16/bf16 values -> static encode with scale s -> decoded bf16 pairs.
+__device__ __forceinline__ bool near_index_boundary(float q) {
+  const uint32_t u = __float_as_uint(q);
+  return (((u + 8u) & 0x7FFFFu) <= 16u) || __builtin_isnan(q);
+}
+
+// Static encode (fixed scale) + decode of 16 fp16/bf16 values into bf16 pairs.
+// Multiplies by the reciprocal and redoes the element with an IEEE division
+// when the product is within 8 ulps of an encode-index boundary or NaN (the
+// same rule as hif8_static_quant), so the codes equal the standalone quant's.
 template <bool kBf16>
-__device__ __forceinline__ void encode_decode16(const uint16_t *x, float s, const uint8_t *enc,
-                                                const uint16_t *dec, uint32_t (&p)[8]) {
-  const u32x4 a = *reinterpret_cast<const u32x4 *>(x);
-  const u32x4 b = *reinterpret_cast<const u32x4 *>(x + 8);
+__device__ __forceinline__ void fast_encode_decode16(const u32x4 a, const u32x4 b, float s, float r,
+                                                     const uint8_t *enc, const uint16_t *dec, u32x4 &lo,
+                                                     u32x4 &hi) {
+  uint32_t p[8];
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t w = i < 4 ? a[i] : b[i - 4];
-    const float q0 = lo_to_float<kBf16>(w) / s;
-    const float q1 = hi_to_float<kBf16>(w) / s;
-    const uint32_t c0 = __builtin_isnan(q0) ? uint32_t(kNan) : enc[__float_as_uint(q0) >> 19];
-    const uint32_t c1 = __builtin_isnan(q1) ? uint32_t(kNan) : enc[__float_as_uint(q1) >> 19];
+    const float x0 = lo_to_float<kBf16>(w), x1 = hi_to_float<kBf16>(w);
+    float q0 = x0 * r, q1 = x1 * r;
+    uint32_t c0, c1;
+    if (__builtin_expect(near_index_boundary(q0) || near_index_boundary(q1), 0)) {
+      q0 = x0 / s;
+      q1 = x1 / s;
+      c0 = __builtin_isnan(q0) ? uint32_t(kNan) : enc[__float_as_uint(q0) >> 19];
+      c1 = __builtin_isnan(q1) ? uint32_t(kNan) : enc[__float_as_uint(q1) >> 19];
+    } else {
+      c0 = enc[__float_as_uint(q0) >> 19];
+      c1 = enc[__float_as_uint(q1) >> 19];
+    }
     p[i] = uint32_t(dec[c0]) | (uint32_t(dec[c1]) << 16);
   }
+  lo = u32x4{p[0], p[1], p[2], p[3]};
+  hi = u32x4{p[4], p[5], p[6], p[7]};
 }
 
 constexpr int pow2_floor(int v) {
@@ -80,11 +110,39 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_kernel(
   constexpr int kV = kR * kM;
   constexpr int kPitch = kV + 4;
   constexpr bool kFused = kSrc != kActCodes;
-  __shared__ uint16_t dec_lut[256];
+  constexpr int kActWords = kFused ? 2 : 1;  // 16-byte words of activation per row per chunk
+  __shared__ __attribute__((aligned(16))) uint16_t dec_lut[256];
   __shared__ __attribute__((aligned(16))) uint8_t enc_lut[kFused ? 8192 : 16];
   __shared__ __attribute__((aligned(16))) float red[kThreads * kPitch];
 
   const int tid = threadIdx.x;
+  const int n0 = blockIdx.x * kR;
+  const int chunks = k >> 4;
+
+  // Raw operands of one 16-byte column chunk: kR weight rows + kM activation rows.
+  u32x4 wq[kR];
+  u32x4 ar[kM][kActWords];
+  auto load = [&](int c) {
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      // Rows past n re-read row n-1; their sums are never stored.
+      const int row = min(n0 + r, n - 1);
+      wq[r] = reinterpret_cast<const u32x4 *>(weight + size_t(row) * k)[c];
+    }
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+      if constexpr (kFused) {
+        const u32x4 *x = reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(act) + size_t(m) * k + 16 * c);
+        ar[m][0] = x[0];
+        ar[m][1] = x[1];
+      } else {
+        ar[m][0] = reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(act) + size_t(m) * k)[c];
+      }
+    }
+  };
+  // Loads are issued after the table barrier.  Issuing the first chunk's
+  // loads before it measured slower on MI355X (q 4096x4096 M=1: 6.65 vs
+  // 5.5 us): the table store has to wait for every earlier load to return.
   dec_lut[tid] = kDeviceTables.decode_bf16[tid];
   if constexpr (kFused) {
     const u32x4 *src = reinterpret_cast<const u32x4 *>(kDeviceTables.static_encode);
@@ -92,11 +150,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_kernel(
     dst[tid] = src[tid];
     dst[tid + kThreads] = src[tid + kThreads];
   }
-  __syncthreads();
+  lds_barrier();
 
-  const int n0 = blockIdx.x * kR;
-  const int chunks = k >> 4;
   const float fixed = kFused ? act_scale[0] : 0.f;
+  const float rcp = kFused ? __builtin_amdgcn_rcpf(fixed) : 0.f;
   float acc[kR][kM];
 #pragma unroll
   for (int r = 0; r < kR; ++r)
@@ -104,21 +161,20 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_kernel(
     for (int m = 0; m < kM; ++m) acc[r][m] = 0.f;
 
   for (int c = tid; c < chunks; c += kThreads) {
-    u32x4 wq[kR];
-#pragma unroll
-    for (int r = 0; r < kR; ++r) {
-      // Rows past n re-read row n-1; their sums are never stored.
-      const int row = min(n0 + r, n - 1);
-      wq[r] = reinterpret_cast<const u32x4 *>(weight + size_t(row) * k)[c];
-    }
+    load(c);
     uint32_t a[kM][8];
 #pragma unroll
     for (int m = 0; m < kM; ++m) {
       if constexpr (kFused) {
-        encode_decode16<kSrc == kActBf16>(static_cast<const uint16_t *>(act) + size_t(m) * k + 16 * c,
-                                          fixed, enc_lut, dec_lut, a[m]);
+        u32x4 lo, hi;
+        fast_encode_decode16<kSrc == kActBf16>(ar[m][0], ar[m][1], fixed, rcp, enc_lut, dec_lut, lo, hi);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          a[m][i] = lo[i];
+          a[m][4 + i] = hi[i];
+        }
       } else {
-        decode16(dec_lut, reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(act) + size_t(m) * k)[c], a[m]);
+        decode16(dec_lut, ar[m][0], a[m]);
       }
     }
 #pragma unroll
@@ -205,6 +261,165 @@ __global__ __launch_bounds__(64) void gemv_simple_kernel(
   }
 }
 
+// ------------------------------------------------------------------------
+// MFMA-reduced GEMV (k % 64 == 0).  A block of 8 wavefronts owns 16 weight
+// rows; wavefront w streams its share of the 64-byte k-steps.  In one step,
+// lane l loads 16 contiguous bytes of row n0 + l%16 at k offset 16*(l/16), so
+// a load instruction covers 16 rows x 64 contiguous bytes.  The 16 bytes are
+// LUT-decoded to bf16 and used as the B operand of two
+// v_mfma_f32_16x16x32_bf16 (bytes 0-7 and 8-15); the A operand holds the
+// matching activation values for rows m = l%16 < M (zeros otherwise), read
+// from a bf16 copy of the activation decoded once per block into LDS.  The
+// MFMA does the k-reduction across lanes, so the VALU work per weight byte is
+// just the table decode.  D[m][n] lands in lane n, register m.  The eight
+// wavefront partials meet in LDS and one pass applies the epilogue.
+constexpr int kMfmaWaves = 8;
+constexpr int kMfmaThreads = kMfmaWaves * kWave;
+constexpr int kMfmaUnroll = 8;  // 16-byte weight loads in flight per lane
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+template <int kM, int kSrc>
+__global__ __launch_bounds__(kMfmaThreads, 1) void gemv_mfma_kernel(
+    const void *__restrict__ act, const float *__restrict__ act_scale,
+    const uint8_t *__restrict__ weight, const float *__restrict__ cs,
+    const void *__restrict__ bias, int bias_dtype, void *__restrict__ out, int out_dtype,
+    int n, int k) {
+  constexpr bool kFused = kSrc != kActCodes;
+  // Static LDS first: the decode table sits at LDS address 0, so a table
+  // address is one SDWA shift of the weight byte.
+  __shared__ __attribute__((aligned(16))) uint16_t dec_lut[256];
+  __shared__ __attribute__((aligned(16))) uint32_t zero_block[8];
+  __shared__ __attribute__((aligned(16))) float red[kMfmaWaves * 16 * 4];
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  uint16_t *xs = reinterpret_cast<uint16_t *>(smem);                       // [kM][k] bf16
+  uint8_t *enc_lut = smem + size_t(kM) * k * 2;                             // 8 KiB (fused)
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int n0 = blockIdx.x * 16;
+  const int steps = k >> 6;
+  const int s_begin = (steps * wave) / kMfmaWaves, s_end = (steps * (wave + 1)) / kMfmaWaves;
+  const uint8_t *wptr = weight + size_t(min(n0 + (lane & 15), n - 1)) * k + ((lane >> 4) << 4);
+
+  // Weight loads go out first and stay in flight through the prologue.
+  u32x4 wq[kMfmaUnroll];
+#pragma unroll
+  for (int u = 0; u < kMfmaUnroll; ++u)
+    if (s_begin + u < s_end) wq[u] = *reinterpret_cast<const u32x4 *>(wptr + size_t(s_begin + u) * 64);
+
+  if (tid < 128) reinterpret_cast<uint32_t *>(dec_lut)[tid] = reinterpret_cast<const uint32_t *>(kDeviceTables.decode_bf16)[tid];
+  if (tid < 8) zero_block[tid] = 0u;
+  if constexpr (kFused) reinterpret_cast<u32x4 *>(enc_lut)[tid] = reinterpret_cast<const u32x4 *>(kDeviceTables.static_encode)[tid];
+  lds_barrier();
+
+  // Activation -> bf16 in LDS, once per block.
+  {
+    const int row_chunks = k >> 4;
+    const float s = kFused ? act_scale[0] : 0.f;
+    const float r = kFused ? __builtin_amdgcn_rcpf(s) : 0.f;
+    for (int c = tid; c < kM * row_chunks; c += kMfmaThreads) {
+      const int m = c / row_chunks, kc = c - m * row_chunks;
+      u32x4 lo, hi;
+      if constexpr (kFused) {
+        const u32x4 *x = reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(act) + size_t(m) * k + 16 * kc);
+        fast_encode_decode16<kSrc == kActBf16>(x[0], x[1], s, r, enc_lut, dec_lut, lo, hi);
+      } else {
+        uint32_t p[8];
+        decode16(dec_lut, reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(act) + size_t(m) * k)[kc], p);
+        lo = u32x4{p[0], p[1], p[2], p[3]};
+        hi = u32x4{p[4], p[5], p[6], p[7]};
+      }
+      u32x4 *d = reinterpret_cast<u32x4 *>(xs + size_t(m) * k + 16 * kc);
+      d[0] = lo;
+      d[1] = hi;
+    }
+  }
+  lds_barrier();
+
+  // A-operand rows m >= kM read a zero block that does not move with k.
+  const bool act_lane = (lane & 15) < kM;
+  const uint16_t *xa_base = act_lane ? xs + size_t(lane & 15) * k + ((lane >> 4) << 4)
+                                     : reinterpret_cast<const uint16_t *>(zero_block);
+  const int xa_step = act_lane ? 64 : 0;
+  f32x4_t acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+  auto step = [&](int s, const u32x4 q) {
+    uint32_t p[8];
+    decode16(dec_lut, q, p);
+    const u32x4 *xa = reinterpret_cast<const u32x4 *>(xa_base + s * xa_step);
+    const u32x4 a0 = xa[0], a1 = xa[1];
+    acc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a0),
+                                                   __builtin_bit_cast(bf16x8_t, u32x4{p[0], p[1], p[2], p[3]}),
+                                                   acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a1),
+                                                   __builtin_bit_cast(bf16x8_t, u32x4{p[4], p[5], p[6], p[7]}),
+                                                   acc1, 0, 0, 0);
+  };
+  int s0 = s_begin;
+  for (; s0 + kMfmaUnroll <= s_end; s0 += kMfmaUnroll) {
+#pragma unroll
+    for (int u = 0; u < kMfmaUnroll; ++u) {
+      const u32x4 q = wq[u];
+      if (s0 + kMfmaUnroll + u < s_end)
+        wq[u] = *reinterpret_cast<const u32x4 *>(wptr + size_t(s0 + kMfmaUnroll + u) * 64);
+      step(s0 + u, q);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kMfmaUnroll; ++u)
+    if (s0 + u < s_end) step(s0 + u, wq[u]);
+
+  if (lane < 16) {
+    float *dst = red + (wave * 16 + lane) * 4;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) dst[r] = acc0[r] + acc1[r];
+  }
+  lds_barrier();
+  if (tid < 64) {
+    const int m = tid >> 4, nl = tid & 15;
+    const int row = n0 + nl;
+    if (m < kM && row < n) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kMfmaWaves; ++w) sum += red[(w * 16 + nl) * 4 + m];
+      const float ts = kFused ? act_scale[0] : act_scale[m];
+      float y = sum * ts * cs[row];
+      if (bias) y += load_bias(bias, bias_dtype, row);
+      store_out(out, out_dtype, size_t(m) * n + row, y);
+    }
+  }
+}
+
+template <int kM, int kSrc>
+int launch_mfma(const LinearArgs &a) {
+  const size_t smem = size_t(kM) * size_t(a.k) * 2 + (kSrc != kActCodes ? 8192 : 0);
+  static size_t configured = 0;  // largest dynamic LDS size set for this instantiation
+  if (smem > configured) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_mfma_kernel<kM, kSrc>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, int(smem)) != hipSuccess)
+      return fail(HIF8_ERR_LAUNCH, "soft_hif8 GEMV: cannot reserve %zu bytes of LDS", smem);
+    configured = smem;
+  }
+  gemv_mfma_kernel<kM, kSrc><<<dim3(unsigned((a.n + 15) / 16)), kMfmaThreads, smem, a.stream>>>(
+      a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.n), int(a.k));
+  return HIF8_OK;
+}
+
+template <int kM>
+int launch_mfma_src(const LinearArgs &a) {
+  switch (a.act_kind) {
+    case kActCodes: return launch_mfma<kM, kActCodes>(a);
+    case kActF16: return launch_mfma<kM, kActF16>(a);
+    default: return launch_mfma<kM, kActBf16>(a);
+  }
+}
+
+// LDS bytes the MFMA GEMV needs, or 0 when the shape does not fit it.
+size_t mfma_gemv_smem(const LinearArgs &a) {
+  if (a.k % 64 || !aligned(a.weight, 16) || !aligned(a.act, 16)) return 0;
+  const size_t smem = 512 + 32 + 2048 + size_t(a.m) * size_t(a.k) * 2 + (a.act_kind != kActCodes ? 8192 : 0);
+  return smem <= 160 * 1024 ? smem : 0;
+}
+
 template <int kM, int kR>
 void dispatch_src(const LinearArgs &a, dim3 grid) {
   const int n = int(a.n), k = int(a.k);
@@ -235,21 +450,46 @@ void dispatch_m(const LinearArgs &a) {
   }
 }
 
+
 }  // namespace
+
+// Kernel selection knob, read once: HIF8_GEMV_KERNEL=valu|mfma (default valu),
+// HIF8_GEMV_ROWS=4|8|16 forces the VALU kernel's rows per block.
+// Measured on MI355X (gate_up 24576x4096, M=1): one-shot VALU kernel with 8
+// rows per block 20.0 us; the MFMA kernel 29.3 us (its 16-rows x 64-byte load
+// pattern alone reads ~20% slower than 1 KiB-contiguous rows); a persistent
+// double-buffered variant 24 us (2 blocks/CU keep too few bytes in flight).
+struct GemvKnobs {
+  char kernel = 'v';  // 'v' one-shot VALU (default), 'm' MFMA
+  int rows = 0;
+  GemvKnobs() {
+    if (const char *v = getenv("HIF8_GEMV_KERNEL")) kernel = v[0];
+    if (const char *v = getenv("HIF8_GEMV_ROWS")) rows = atoi(v);
+  }
+};
 
 int launch_gemv(const LinearArgs &a) {
   if (a.m < 1 || a.m > 4) return fail(HIF8_ERR_UNSUPPORTED, "GEMV kernel handles 1 <= M <= 4, got %lld", (long long)a.m);
+  static const GemvKnobs knobs;
   const bool vec = a.k % 16 == 0 && aligned(a.weight, 16) && aligned(a.act, 16);
-  if (!vec) {
+  if (knobs.kernel == 'm' && mfma_gemv_smem(a)) {
+    int st = HIF8_OK;
+    switch (a.m) {
+      case 1: st = launch_mfma_src<1>(a); break;
+      case 2: st = launch_mfma_src<2>(a); break;
+      case 3: st = launch_mfma_src<3>(a); break;
+      default: st = launch_mfma_src<4>(a); break;
+    }
+    if (st) return st;
+  } else if (!vec) {
     gemv_simple_kernel<<<dim3(unsigned(a.n)), 64, 0, a.stream>>>(
         a.act, a.act_kind, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out,
         a.out_dtype, int(a.m), int(a.n), int(a.k));
-  } else if (a.n >= 16384) {
-    dispatch_m<16>(a);
-  } else if (a.n >= 4096) {
-    dispatch_m<8>(a);
   } else {
-    dispatch_m<4>(a);
+    const int rows = knobs.rows ? knobs.rows : 8;
+    if (rows >= 16) dispatch_m<16>(a);
+    else if (rows >= 8) dispatch_m<8>(a);
+    else dispatch_m<4>(a);
   }
   return check_launch("soft_hif8 GEMV");
 }

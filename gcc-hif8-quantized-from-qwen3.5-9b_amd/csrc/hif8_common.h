@@ -64,6 +64,16 @@ __device__ __forceinline__ uint16_t float_to_half_bits(float f) {
   return float_to_f16_bits(f);
 }
 
+// Workgroup barrier that waits for this wave's LDS traffic only (lgkmcnt(0);
+// vmcnt and expcnt left at their maxima), so global loads issued before it
+// stay in flight across the barrier.  Only LDS data is exchanged through it.
+__device__ __forceinline__ void lds_barrier() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);  // no compiler motion of memory ops across
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

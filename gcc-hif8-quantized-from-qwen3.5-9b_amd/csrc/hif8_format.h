@@ -36,8 +36,10 @@ constexpr uint8_t kMaxFinite = 0x6E;
 constexpr uint16_t kBf16Nan = 0x7FC0;
 constexpr uint16_t kF16Nan = 0x7E00;
 
-// Base code of the three-mantissa-bit exponents -3..3, indexed by e+3.
-constexpr uint8_t kSmallExponentBase[7] = {0x38, 0x30, 0x18, 0x08, 0x10, 0x20, 0x28};
+// Base code of the three-mantissa-bit exponents -3..3, byte e+3 of this word
+// (0x38, 0x30, 0x18, 0x08, 0x10, 0x20, 0x28): a shift instead of a table, so
+// device code never indexes memory for it.
+constexpr uint64_t kSmallExponentBase = 0x0028201008183038ull;
 
 HIF8_HD constexpr int mantissa_bits(int e) {
   return (e <= 3 && e >= -3) ? 3 : ((e <= 7 && e >= -7) ? 2 : 1);
@@ -45,7 +47,7 @@ HIF8_HD constexpr int mantissa_bits(int e) {
 
 // 7-bit code of (1 + m / 2^mb) * 2^e for a HiF8 normal exponent -15 <= e <= 15.
 HIF8_HD constexpr uint32_t normal_code(int e, uint32_t m) {
-  if (e >= -3 && e <= 3) return kSmallExponentBase[e + 3] + m;
+  if (e >= -3 && e <= 3) return uint32_t((kSmallExponentBase >> (8 * (e + 3))) & 0xFFu) + m;
   if (e >= 4 && e <= 7) return 0x40u + uint32_t(e - 4) * 4u + m;
   if (e <= -4 && e >= -7) return 0x50u + uint32_t(-e - 4) * 4u + m;
   if (e >= 8) return 0x60u + uint32_t(e - 8) * 2u + m;
@@ -82,8 +84,10 @@ HIF8_HD constexpr uint32_t decode_magnitude_bits(uint32_t mag) {
   uint32_t m = 0;
   int mb = 3;
   if (mag < 0x40) {
-    constexpr int kGroupExponent[8] = {0, 0, 1, -1, 2, 3, -2, -3};
-    e = kGroupExponent[mag >> 3];
+    // Exponent of code groups 1..7 (mag >> 3): 0, 1, -1, 2, 3, -2, -3, as 4-bit
+    // two's-complement fields of one word.
+    const uint32_t field = (0xDE32F100u >> (4 * (mag >> 3))) & 0xFu;
+    e = int(field) - (field & 8u ? 16 : 0);
     m = mag & 7u;
   } else if (mag < 0x60) {
     const int em = 4 + int((mag >> 2) & 3u);

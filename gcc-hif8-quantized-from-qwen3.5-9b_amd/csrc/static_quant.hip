@@ -22,9 +22,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr uint32_t kNearMargin = 8;
-// Below this many 16-element chunks the 8 KiB LDS table is not worth loading:
-// the launch is latency-bound and the arithmetic encoder is used instead.
-constexpr uint32_t kLutMinChunks = 2048;
+// The vector kernel always stages the 8 KiB table: measured on MI355X, the
+// table-free arithmetic encoder is ~3x slower even for a single block
+// (M=1, K=4096: 10.2 vs 3.4 us) because of its data-dependent branches.
 
 __device__ __forceinline__ bool near_index_boundary(float q) {
   const uint32_t u = __float_as_uint(q);
@@ -43,23 +43,18 @@ __device__ __forceinline__ void load16(const uint16_t *p, float (&v)[16]) {
   }
 }
 
-template <bool kLut>
 __device__ __forceinline__ uint32_t encode_q(float q, const uint8_t *lut) {
-  if constexpr (kLut) {
-    return lut[__float_as_uint(q) >> 19];
-  } else {
-    return static_encode_bits(__float_as_uint(q));
-  }
+  return lut[__float_as_uint(q) >> 19];
 }
 
 // One thread = 16 consecutive elements of one row (requires k % 16 == 0 and
 // 16-byte aligned x / data).  Grid-stride over the flattened chunks.
-template <bool kBf16, bool kLut>
+template <bool kBf16>
 __global__ __launch_bounds__(kThreads) void static_quant_vec16(
     const uint16_t *__restrict__ x, const float *__restrict__ fixed, uint8_t *__restrict__ out,
     float *__restrict__ row_scale, uint32_t n_chunks, uint32_t k_chunks, uint32_t scale_count) {
-  __shared__ __attribute__((aligned(16))) uint8_t lut[kLut ? 8192 : 16];
-  if constexpr (kLut) {
+  __shared__ __attribute__((aligned(16))) uint8_t lut[8192];
+  {
     const uint4 *src = reinterpret_cast<const uint4 *>(kDeviceTables.static_encode);
     uint4 *dst = reinterpret_cast<uint4 *>(lut);
     for (int i = threadIdx.x; i < 8192 / 16; i += kThreads) dst[i] = src[i];
@@ -88,7 +83,7 @@ __global__ __launch_bounds__(kThreads) void static_quant_vec16(
       for (int i = 0; i < 4; ++i) {
         uint32_t b[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = encode_q<kLut>(q[4 * i + j], lut);
+        for (int j = 0; j < 4; ++j) b[j] = encode_q(q[4 * i + j], lut);
         w[i] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
       }
     } else {
@@ -99,7 +94,7 @@ __global__ __launch_bounds__(kThreads) void static_quant_vec16(
         for (int j = 0; j < 4; ++j) {
           // NaN is decided by the full mantissa, as the reference codec does.
           const float v = xf[4 * i + j] / s;
-          b[j] = __builtin_isnan(v) ? uint32_t(kNan) : encode_q<kLut>(v, lut);
+          b[j] = __builtin_isnan(v) ? uint32_t(kNan) : encode_q(v, lut);
         }
         w[i] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
       }
@@ -197,16 +192,10 @@ extern "C" int hif8_static_quant(const void *x, int x_dtype, int64_t rows, int64
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const uint16_t *xs = static_cast<const uint16_t *>(x);
   if (k % 16 == 0 && aligned(x, 16) && aligned(data, 16) && n_chunks <= 0xFFFFFFFFull) {
-    const bool lut = n_chunks >= kLutMinChunks;
     const dim3 grid(grid_for(n_chunks, 8)), block(kThreads);
     const uint32_t nc = uint32_t(n_chunks), kc = uint32_t(k / 16), sc = uint32_t(scale_count);
-    if (bf16) {
-      if (lut) static_quant_vec16<true, true><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
-      else static_quant_vec16<true, false><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
-    } else {
-      if (lut) static_quant_vec16<false, true><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
-      else static_quant_vec16<false, false><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
-    }
+    if (bf16) static_quant_vec16<true><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
+    else static_quant_vec16<false><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
   } else {
     const dim3 grid(grid_for(n, 8)), block(kThreads);
     if (bf16) static_quant_scalar<true><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, n, uint64_t(k), uint32_t(scale_count));

@@ -5,6 +5,12 @@ weight processing (scheme.py:59-91) without the vLLM-Ascend registry: a layer
 holds ``weight`` uint8 [N, K], ``weight_scale`` float32 [N, 1] and
 ``input_scale`` float32 [1]; ``apply`` statically quantises the activation and
 runs the soft HiF8 linear.
+
+Routing is the reference's (scheme.py:183-189): the fused static-quant GEMV
+is taken only when ``HIF8_STATIC_FUSED_GENERATION=1``, M <= 4 and K < 1024.
+On MI355X that is also the faster choice at model shapes: the fused kernel
+re-encodes the activation in every block (N/8 blocks x M*K encodes), which
+costs more than the separate quant launch once K reaches a few thousand.
 """
 
 from __future__ import annotations

@@ -1,0 +1,225 @@
+"""Host-side API contracts (CPU): loader without fallback, operand normalisation,
+GEMV/GEMM routing, and the static linear scheme's dispatch - the shape of the
+reference's test_native_loader.py and test_static_scheme.py."""
+
+import os
+import types
+from unittest.mock import patch
+
+import pytest
+import torch
+
+from hif8_rocm import native
+from hif8_rocm.scheme import STATIC_QUANT_TYPE, W8A8HiFloat8StaticLinearMethod
+
+
+@pytest.fixture(autouse=True)
+def _fresh_loader():
+    native.reset_extension_cache()
+    yield
+    native.reset_extension_cache()
+
+
+def test_missing_extension_raises_without_fallback():
+    with patch("importlib.import_module", side_effect=ModuleNotFoundError("missing")):
+        with pytest.raises(native.NativeExtensionUnavailable, match="no decoded-weight or floating-point fallback"):
+            native.load_extension()
+    # The failure is cached.
+    with pytest.raises(native.NativeExtensionUnavailable):
+        native.load_extension()
+
+
+def test_missing_symbol_is_rejected():
+    incomplete = types.SimpleNamespace(hif8_static_quant=lambda *a: a)
+    with patch("importlib.import_module", return_value=incomplete):
+        with pytest.raises(native.NativeExtensionUnavailable, match="soft_hif8_gemv"):
+            native.load_extension()
+
+
+def test_valid_extension_is_cached():
+    complete = types.SimpleNamespace(hif8_static_quant=lambda *a: a, soft_hif8_gemv=lambda *a: a,
+                                     soft_hif8_gemm=lambda *a: a)
+    with patch("importlib.import_module", return_value=complete) as importer:
+        assert native.load_extension() is complete
+        assert native.load_extension() is complete
+        importer.assert_called_once()
+
+
+def test_real_extension_loads_on_cpu():
+    ext = native.load_extension()
+    for name in ("hif8_static_quant", "hif8_scaled_decode", "soft_hif8_gemv", "soft_hif8_gemm",
+                 "soft_hif8_static_fused_gemm"):
+        assert callable(getattr(ext, name))
+        assert callable(getattr(torch.ops.vllm_ascend_hif8, name))
+
+
+def test_meta_shapes():
+    native.load_extension()
+    x = torch.empty(3, 2, 64, dtype=torch.bfloat16, device="meta")
+    data, scale = torch.ops.vllm_ascend_hif8.hif8_static_quant(x, torch.empty(1, device="meta"))
+    assert data.shape == x.shape and data.dtype == torch.uint8
+    assert scale.shape == (6,) and scale.dtype == torch.float32
+    y = torch.ops.vllm_ascend_hif8.soft_hif8_gemm(
+        torch.empty(5, 64, dtype=torch.uint8, device="meta"), torch.empty(7, 64, dtype=torch.uint8, device="meta"),
+        torch.empty(5, device="meta"), torch.empty(7, device="meta"), None, torch.bfloat16)
+    assert y.shape == (5, 7) and y.dtype == torch.bfloat16
+
+
+def test_offset_and_strided_views_are_materialized():
+    base = torch.arange(24, dtype=torch.uint8).reshape(6, 4)
+    for view in (base[2:], base[:, ::2]):
+        out = native._as_native_operand(view)
+        assert out.storage_offset() == 0 and out.is_contiguous() and torch.equal(out, view)
+    clean = torch.zeros((3, 4), dtype=torch.uint8)
+    assert native._as_native_operand(clean) is clean
+
+
+def test_soft_linear_feeds_clean_operands_and_reshapes():
+    seen = {}
+
+    def fake_gemm(activation, weight, token_scale, channel_scale, bias, output_dtype):
+        seen["offsets"] = [t.storage_offset() for t in (activation, token_scale, channel_scale)]
+        seen["contig"] = [t.is_contiguous() for t in (activation, token_scale, channel_scale)]
+        return torch.zeros((activation.shape[0], weight.shape[0]), dtype=output_dtype)
+
+    ext = types.SimpleNamespace(hif8_static_quant=None, soft_hif8_gemv=fake_gemm, soft_hif8_gemm=fake_gemm)
+    activation = torch.zeros((5, 2, 4), dtype=torch.uint8)[1:]
+    scale = torch.ones(10, dtype=torch.float32)[2:]
+    with patch.object(native, "load_extension", return_value=ext), \
+         patch.object(native, "_operator", lambda name, e: getattr(e, name)):
+        out = native.soft_linear(activation, torch.zeros((3, 4), dtype=torch.uint8), scale,
+                                 torch.ones(3, dtype=torch.float32), None, output_dtype=torch.float32)
+    assert seen["offsets"] == [0, 0, 0] and all(seen["contig"])
+    assert tuple(out.shape) == (4, 2, 3)
+
+
+def test_soft_linear_routes_like_the_reference():
+    calls = []
+
+    def op(kind):
+        def f(activation, weight, *rest):
+            calls.append(kind)
+            return torch.zeros((activation.shape[0], weight.shape[0]), dtype=torch.bfloat16)
+        return f
+
+    ext = types.SimpleNamespace(soft_hif8_gemv=op("gemv"), soft_hif8_gemm=op("gemm"))
+    s2 = torch.ones(2, dtype=torch.float32)
+    with patch.object(native, "load_extension", return_value=ext), \
+         patch.object(native, "_operator", lambda name, e: getattr(e, name)):
+        for m, n, k in ((1, 3, 4), (2, 3, 4), (1, 1536, 4), (1, 1664, 4), (1, 512, 8192), (1, 512, 12288)):
+            native.soft_linear(torch.zeros((m, k), dtype=torch.uint8), torch.zeros((n, k), dtype=torch.uint8),
+                               s2[:m], torch.ones(n, dtype=torch.float32), output_dtype=torch.bfloat16)
+        with patch.dict(os.environ, {"HIF8_DISABLE_GEMV": "1"}):
+            native.soft_linear(torch.zeros((1, 4), dtype=torch.uint8), torch.zeros((3, 4), dtype=torch.uint8),
+                               s2[:1], torch.ones(3, dtype=torch.float32), output_dtype=torch.bfloat16)
+    assert calls == ["gemv", "gemm", "gemv", "gemm", "gemv", "gemm", "gemm"]
+
+
+def test_static_quant_validation_messages():
+    with pytest.raises(TypeError, match="FP16/BF16"):
+        native.static_quant(torch.zeros(2, 4, dtype=torch.float32), torch.ones(1))
+    with pytest.raises(TypeError, match="1D torch.float32"):
+        native.static_quant(torch.zeros(2, 4, dtype=torch.bfloat16), torch.ones(1, dtype=torch.float64))
+    with pytest.raises(ValueError, match="must divide"):
+        native.static_quant(torch.zeros(3, 4, dtype=torch.bfloat16), torch.ones(2))
+
+
+# --------------------------------------------------------------- scheme
+
+def _layer(input_scale=0.25, k=8):
+    layer = torch.nn.Module()
+    layer.weight = torch.nn.Parameter(torch.zeros((5, k), dtype=torch.uint8), requires_grad=False)
+    layer.weight_scale = torch.nn.Parameter(torch.ones((5, 1), dtype=torch.float32), requires_grad=False)
+    layer.input_scale = torch.nn.Parameter(torch.tensor([input_scale], dtype=torch.float32), requires_grad=False)
+    return layer
+
+
+@pytest.fixture
+def clean_env():
+    with patch.dict(os.environ, {}, clear=False):
+        for var in ("HIF8_COMPUTE_BACKEND", "HIF8_STATIC_FUSED_GENERATION", "HIF8_STATIC_SCALE_FACTOR"):
+            os.environ.pop(var, None)
+        yield
+
+
+def test_declares_one_fp32_input_scale(clean_env):
+    params = W8A8HiFloat8StaticLinearMethod().get_pertensor_param(torch.bfloat16, layer_type="others")
+    assert set(params) == {"input_scale"}
+    assert params["input_scale"].dtype == torch.float32 and tuple(params["input_scale"].shape) == (1,)
+    assert STATIC_QUANT_TYPE == "W8A8HIF8_STATIC"
+
+
+@pytest.mark.parametrize("value", [0.0, -1.0, float("inf"), float("nan")])
+def test_rejects_invalid_input_scales(clean_env, value):
+    with pytest.raises(ValueError, match="finite and greater"):
+        W8A8HiFloat8StaticLinearMethod().process_weights_after_loading(_layer(value))
+
+
+def test_rejects_non_scalar_input_scale(clean_env):
+    layer = _layer()
+    layer.input_scale = torch.nn.Parameter(torch.ones(2, dtype=torch.float32), requires_grad=False)
+    with pytest.raises(ValueError, match="one input_scale"):
+        W8A8HiFloat8StaticLinearMethod().process_weights_after_loading(layer)
+
+
+def test_rejects_unsupported_backend(clean_env):
+    os.environ["HIF8_COMPUTE_BACKEND"] = "unsupported"
+    with pytest.raises(ValueError, match="unsupported"):
+        W8A8HiFloat8StaticLinearMethod().process_weights_after_loading(_layer())
+
+
+def test_apply_defaults_to_standalone_static_quant(clean_env):
+    method = W8A8HiFloat8StaticLinearMethod()
+    layer = _layer()
+    method.process_weights_after_loading(layer)
+    assert tuple(layer.weight_scale.shape) == (5,)
+    x = torch.randn((3, 8), dtype=torch.bfloat16)
+    enc, rs, out = torch.zeros_like(x, dtype=torch.uint8), torch.full((3,), 0.25), torch.randn(3, 5)
+    with patch("hif8_rocm.scheme.native.static_quant", return_value=(enc, rs)) as sq, \
+         patch("hif8_rocm.scheme.native.soft_static_fused_linear") as fused, \
+         patch("hif8_rocm.scheme.native.soft_linear", return_value=out) as lin:
+        assert method.apply(layer, x, None) is out
+    sq.assert_called_once_with(x, layer.input_scale)
+    fused.assert_not_called()
+    lin.assert_called_once_with(enc, layer.weight, rs, layer.weight_scale, None, output_dtype=x.dtype)
+
+
+def test_fused_generation_is_opt_in_and_limited_to_small_shapes(clean_env):
+    os.environ["HIF8_STATIC_FUSED_GENERATION"] = "1"
+    method = W8A8HiFloat8StaticLinearMethod()
+    layer = _layer()
+    method.process_weights_after_loading(layer)
+    out = torch.randn(2, 5)
+    with patch("hif8_rocm.scheme.native.static_quant") as sq, \
+         patch("hif8_rocm.scheme.native.soft_linear") as lin, \
+         patch("hif8_rocm.scheme.native.soft_static_fused_linear", return_value=out) as fused:
+        assert method.apply(layer, torch.randn((2, 8), dtype=torch.bfloat16)) is out
+    sq.assert_not_called()
+    lin.assert_not_called()
+    fused.assert_called_once()
+    # M = 5 and model-sized K keep the two-stage path.
+    for shape, k in (((5, 8), 8), ((1, 4096), 4096)):
+        layer = _layer(k=k)
+        method.process_weights_after_loading(layer)
+        x = torch.zeros(shape, dtype=torch.bfloat16)
+        with patch("hif8_rocm.scheme.native.static_quant", return_value=(x.to(torch.uint8), torch.ones(shape[0]))) as sq, \
+             patch("hif8_rocm.scheme.native.soft_linear", return_value=out), \
+             patch("hif8_rocm.scheme.native.soft_static_fused_linear") as fused:
+            method.apply(layer, x)
+        sq.assert_called_once()
+        fused.assert_not_called()
+
+
+def test_scale_factor_env_multiplies_the_checkpoint_scale(clean_env):
+    os.environ["HIF8_STATIC_SCALE_FACTOR"] = "2.0"
+    method = W8A8HiFloat8StaticLinearMethod()
+    layer = _layer(0.25)
+    method.process_weights_after_loading(layer)
+    x = torch.zeros((1, 8), dtype=torch.bfloat16)
+    with patch("hif8_rocm.scheme.native.static_quant", return_value=(x.to(torch.uint8), torch.ones(1))) as sq, \
+         patch("hif8_rocm.scheme.native.soft_linear", return_value=torch.zeros(1, 5)):
+        method.apply(layer, x)
+    assert float(sq.call_args[0][1]) == 0.5
+    os.environ["HIF8_STATIC_SCALE_FACTOR"] = "-1"
+    with pytest.raises(ValueError, match="positive finite"):
+        method.apply(layer, x)
