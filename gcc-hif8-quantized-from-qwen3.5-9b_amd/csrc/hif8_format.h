@@ -120,6 +120,22 @@ HIF8_HD constexpr uint32_t static_encode_bits(uint32_t u) {
   return mag ? (mag | sign) : 0u;
 }
 
+// FP16 bits of a decoded byte.  Every HiF8 value is exact in fp16: magnitudes
+// are multiples of 2^-23 (fp16 subnormal step 2^-24) with at most four
+// significant bits, and the largest finite value 1.25*2^15 is below 65504.
+HIF8_HD constexpr uint16_t decode_f16_bits(uint32_t byte) {
+  if (byte == kNan) return kF16Nan;
+  const uint32_t f = decode_magnitude_bits(byte & 0x7Fu);
+  const uint16_t sign = uint16_t((byte & 0x80u) << 8);
+  if (f == 0) return 0;
+  if (f == 0x7F800000u) return uint16_t(sign | 0x7C00u);
+  const int e = int(f >> 23) - 127;
+  const uint32_t m = f & 0x7FFFFFu;                 // at most the top 3 bits set
+  if (e >= -14) return uint16_t(sign | (uint32_t(e + 15) << 10) | (m >> 13));
+  // fp16 subnormal: the value (2^23 + m) * 2^(e-23) counted in units of 2^-24.
+  return uint16_t(sign | ((0x800000u | m) >> (-e - 1)));
+}
+
 struct alignas(16) Tables {
   // (sign, exp8, top-4 mantissa) 13-bit index -> static-encoded byte.  For
   // exponent 0xFF the entry follows the top four mantissa bits only; callers
@@ -127,6 +143,7 @@ struct alignas(16) Tables {
   uint8_t static_encode[8192];
   uint16_t decode_bf16[256];  // byte -> bf16 payload (NaN 0x7FC0)
   uint32_t decode_f32[256];   // byte -> fp32 bits (NaN 0x7FC00000)
+  uint16_t decode_f16[256];   // byte -> fp16 payload (NaN 0x7E00)
 };
 
 constexpr Tables make_tables() {
@@ -138,6 +155,7 @@ constexpr Tables make_tables() {
     const uint32_t f = decode_bits(b);
     t.decode_f32[b] = f;
     t.decode_bf16[b] = uint16_t(f >> 16);  // every finite HiF8 value is exact in bf16
+    t.decode_f16[b] = decode_f16_bits(b);
   }
   return t;
 }

@@ -5,47 +5,18 @@
 //   byte = static_encode(q)       (finite clamped to +-2^15, ties away, no -0)
 //
 // The vector kernel is HBM-bound (2 B in + 1 B out per element), so it spends
-// as few VALU cycles per element as possible: it multiplies by a per-row
-// reciprocal instead of dividing, and the multiply is exact enough for the
-// encode except when the product lies within a few ulps of a boundary of the
-// 13-bit (sign, exp8, mant4) encode index, where the correctly rounded
-// quotient could land on the other side.  Such lanes (and NaN lanes) redo the
-// element with a true IEEE division.  The product of x and rcp(s) is within
-// 1.5 ulp (relative) of x/s and the correctly rounded quotient within 0.5 ulp,
-// so the two fp32 bit patterns differ by at most 3; a margin of 8 covers that
-// with room to spare.  The encode itself is one LDS lookup in the 8 KiB
-// static encode table.
-#include "hif8_common.h"
+// as few VALU cycles per element as possible: static_encode16 multiplies by a
+// per-row reciprocal and falls back to an IEEE division only next to an
+// encode-index boundary (the argument is spelled out in quant_device.h).
+#include "quant_device.h"
 
 namespace hif8 {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr uint32_t kNearMargin = 8;
 // The vector kernel always stages the 8 KiB table: measured on MI355X, the
 // table-free arithmetic encoder is ~3x slower even for a single block
 // (M=1, K=4096: 10.2 vs 3.4 us) because of its data-dependent branches.
-
-__device__ __forceinline__ bool near_index_boundary(float q) {
-  const uint32_t u = __float_as_uint(q);
-  return (((u + kNearMargin) & 0x7FFFFu) <= 2u * kNearMargin) || __builtin_isnan(q);
-}
-
-template <bool kBf16>
-__device__ __forceinline__ void load16(const uint16_t *p, float (&v)[16]) {
-  const uint4 a = *reinterpret_cast<const uint4 *>(p);
-  const uint4 b = *reinterpret_cast<const uint4 *>(p + 8);
-  const uint32_t w[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    v[2 * i] = lo_to_float<kBf16>(w[i]);
-    v[2 * i + 1] = hi_to_float<kBf16>(w[i]);
-  }
-}
-
-__device__ __forceinline__ uint32_t encode_q(float q, const uint8_t *lut) {
-  return lut[__float_as_uint(q) >> 19];
-}
 
 // One thread = 16 consecutive elements of one row (requires k % 16 == 0 and
 // 16-byte aligned x / data).  Grid-stride over the flattened chunks.
@@ -54,51 +25,17 @@ __global__ __launch_bounds__(kThreads) void static_quant_vec16(
     const uint16_t *__restrict__ x, const float *__restrict__ fixed, uint8_t *__restrict__ out,
     float *__restrict__ row_scale, uint32_t n_chunks, uint32_t k_chunks, uint32_t scale_count) {
   __shared__ __attribute__((aligned(16))) uint8_t lut[8192];
-  {
-    const uint4 *src = reinterpret_cast<const uint4 *>(kDeviceTables.static_encode);
-    uint4 *dst = reinterpret_cast<uint4 *>(lut);
-    for (int i = threadIdx.x; i < 8192 / 16; i += kThreads) dst[i] = src[i];
-    __syncthreads();
-  }
+  stage_static_encode_table(lut, threadIdx.x, kThreads);
+  __syncthreads();
   const uint32_t stride = gridDim.x * kThreads;
   for (uint32_t c = blockIdx.x * kThreads + threadIdx.x; c < n_chunks; c += stride) {
     const uint32_t row = c / k_chunks;
     const float s = fixed[row % scale_count];
     if (c == row * k_chunks) row_scale[row] = s;
-    const float r = __builtin_amdgcn_rcpf(s);
     float xf[16];
     load16<kBf16>(x + size_t(c) * 16, xf);
-    float q[16];
-    bool redo = false;
-#pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      q[j] = xf[j] * r;
-      redo |= near_index_boundary(q[j]);
-    }
     uint32_t w[4];
-    if (__builtin_expect(!redo, 1)) {
-      // No lane value is NaN or near an index boundary: the product encodes
-      // exactly like the correctly rounded quotient.
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t b[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) b[j] = encode_q(q[4 * i + j], lut);
-        w[i] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        uint32_t b[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          // NaN is decided by the full mantissa, as the reference codec does.
-          const float v = xf[4 * i + j] / s;
-          b[j] = __builtin_isnan(v) ? uint32_t(kNan) : encode_q(v, lut);
-        }
-        w[i] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
-      }
-    }
+    static_encode16(xf, s, lut, w);
     *reinterpret_cast<uint4 *>(out + size_t(c) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }

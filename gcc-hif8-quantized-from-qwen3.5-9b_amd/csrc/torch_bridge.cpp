@@ -7,6 +7,9 @@
 // implementation validates like the reference bridge (hif8_native.cpp:131-316,
 // 487-611, 784-861), allocates outputs with the caching allocator and calls
 // the C ABI on the current HIP stream.  No host synchronisation, no fallback.
+// Two operators are new: the fused KV-cache write and the paged decode
+// attention that replace the reference's quant + pack + index_copy_ and
+// gather + decode + fused-attention sequences (kv_runtime.py:1222-1563).
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
@@ -221,6 +224,124 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
   return out;
 }
 
+
+// ---------------------------------------------------------------- KV cache
+// The KV operators take views as they come (the cache of a layer is usually a
+// view into one large allocation), so they need contiguity, not offset 0.
+
+void CheckContiguousDevice(const at::Tensor &t, const char *name) {
+  TORCH_CHECK(t.defined(), name, " must be defined");
+  TORCH_CHECK(t.is_cuda(), name, " must be a HIP device tensor, got ", t.device());
+  TORCH_CHECK(t.is_contiguous(), name, " must be contiguous");
+}
+
+int IndexCode(const at::Tensor &t, const char *name) {
+  TORCH_CHECK(t.scalar_type() == at::ScalarType::Int || t.scalar_type() == at::ScalarType::Long, name,
+              " must have dtype torch.int32 or torch.int64");
+  return t.scalar_type() == at::ScalarType::Long ? HIF8_INDEX_INT64 : HIF8_INDEX_INT32;
+}
+
+void CheckCache(const at::Tensor &cache, const char *name, int64_t heads, int64_t width) {
+  CheckContiguousDevice(cache, name);
+  TORCH_CHECK(cache.scalar_type() == at::ScalarType::Byte, name, " must have dtype torch.uint8");
+  TORCH_CHECK(cache.dim() == 4, name, " must have shape [num_blocks, block_size, num_kv_heads, head_size + 4]");
+  CheckPositiveDimensions(cache, name);
+  TORCH_CHECK(cache.size(2) == heads, name, " has ", cache.size(2), " KV heads, expected ", heads);
+  TORCH_CHECK(cache.size(3) == width, name, " row width must be ", width, ", got ", cache.size(3));
+}
+
+void Hif8KVCacheWrite(const at::Tensor &key, const at::Tensor &value, const at::Tensor &key_cache,
+                      const at::Tensor &value_cache, const at::Tensor &slot_mapping, const at::Tensor &key_scale,
+                      const at::Tensor &value_scale, const c10::optional<at::Tensor> &invalid_slots) {
+  CheckContiguousDevice(key, "key");
+  CheckContiguousDevice(value, "value");
+  TORCH_CHECK(key.scalar_type() == at::ScalarType::Half || key.scalar_type() == at::ScalarType::BFloat16,
+              "key must have dtype torch.float16 or torch.bfloat16");
+  TORCH_CHECK(value.scalar_type() == key.scalar_type(), "value must have the dtype of key");
+  TORCH_CHECK(key.dim() == 3 && value.dim() == 3, "key/value must have shape [tokens, num_kv_heads, head_size]");
+  TORCH_CHECK(value.size(0) == key.size(0) && value.size(1) == key.size(1),
+              "key and value must have the same token and head counts");
+  const int64_t tokens = key.size(0), heads = key.size(1), d = key.size(2), dv = value.size(2);
+  TORCH_CHECK(heads > 0 && d > 0 && dv > 0, "key/value dimensions must be positive");
+  TORCH_CHECK(d % 4 == 0 && dv % 4 == 0, "HIF8 KV head sizes must be divisible by four so the inline FP32 scale is aligned");
+  CheckCache(key_cache, "key_cache", heads, d + 4);
+  CheckCache(value_cache, "value_cache", heads, dv + 4);
+  TORCH_CHECK(value_cache.size(0) == key_cache.size(0) && value_cache.size(1) == key_cache.size(1),
+              "key_cache and value_cache must have the same blocks");
+  CheckContiguousDevice(slot_mapping, "slot_mapping");
+  const int slot_code = IndexCode(slot_mapping, "slot_mapping");
+  TORCH_CHECK(slot_mapping.dim() == 1 && slot_mapping.numel() == tokens, "slot_mapping must contain one slot per token");
+  for (const auto *t : {&key_scale, &value_scale}) {
+    CheckContiguousDevice(*t, "KV scale");
+    TORCH_CHECK(t->scalar_type() == at::ScalarType::Float, "KV scales must have dtype torch.float32");
+    TORCH_CHECK(t->dim() == 1 && t->numel() == heads, "KV scales must have shape [num_kv_heads]");
+  }
+  const auto device = key.device();
+  for (const auto *t : {&value, &key_cache, &value_cache, &slot_mapping, &key_scale, &value_scale})
+    CheckSameDevice(*t, device, "KV operand");
+  int32_t *invalid = nullptr;
+  if (invalid_slots.has_value()) {
+    CheckContiguousDevice(*invalid_slots, "invalid_slots");
+    TORCH_CHECK(invalid_slots->scalar_type() == at::ScalarType::Int && invalid_slots->numel() >= 1,
+                "invalid_slots must be an int32 tensor with at least one element");
+    CheckSameDevice(*invalid_slots, device, "invalid_slots");
+    invalid = invalid_slots->data_ptr<int32_t>();
+  }
+  if (tokens == 0) return;
+  const c10::OptionalDeviceGuard guard(device);
+  CheckStatus(hif8_kv_cache_write(key.data_ptr(), value.data_ptr(), DtypeCode(key.scalar_type()), tokens, heads, d, dv,
+                                  key_scale.data_ptr<float>(), value_scale.data_ptr<float>(), slot_mapping.data_ptr(),
+                                  slot_code, key_cache.data_ptr<uint8_t>(), value_cache.data_ptr<uint8_t>(),
+                                  key_cache.size(0), key_cache.size(1), invalid, CurrentStream(device)),
+              "hif8_kv_cache_write");
+}
+
+at::Tensor Hif8PagedDecodeAttention(const at::Tensor &query, const at::Tensor &key_cache, const at::Tensor &value_cache,
+                                    const at::Tensor &block_table, const at::Tensor &seq_lens, double scale,
+                                    int64_t max_seq_len) {
+  CheckContiguousDevice(query, "query");
+  TORCH_CHECK(query.scalar_type() == at::ScalarType::Half || query.scalar_type() == at::ScalarType::BFloat16,
+              "query must have dtype torch.float16 or torch.bfloat16");
+  TORCH_CHECK(query.dim() == 3, "query must have shape [batch, num_heads, head_size]");
+  const int64_t batch = query.size(0), heads = query.size(1), d = query.size(2);
+  TORCH_CHECK(heads > 0 && d > 0, "query dimensions must be positive");
+  TORCH_CHECK(key_cache.dim() == 4 && value_cache.dim() == 4, "caches must have shape [num_blocks, block_size, num_kv_heads, width]");
+  const int64_t kv_heads = key_cache.size(2), dv = value_cache.size(3) - 4;
+  CheckCache(key_cache, "key_cache", kv_heads, d + 4);
+  CheckCache(value_cache, "value_cache", kv_heads, dv + 4);
+  TORCH_CHECK(dv > 0, "value_cache rows are too short");
+  TORCH_CHECK(value_cache.size(0) == key_cache.size(0) && value_cache.size(1) == key_cache.size(1),
+              "key_cache and value_cache must have the same blocks");
+  TORCH_CHECK(heads % kv_heads == 0, "num_heads must be divisible by num_kv_heads");
+  CheckContiguousDevice(block_table, "block_table");
+  const int bt_code = IndexCode(block_table, "block_table");
+  TORCH_CHECK(block_table.dim() == 2 && block_table.size(0) >= batch && block_table.size(1) > 0,
+              "block_table must have shape [batch, max_blocks]");
+  CheckContiguousDevice(seq_lens, "seq_lens");
+  TORCH_CHECK(seq_lens.scalar_type() == at::ScalarType::Int, "seq_lens must have dtype torch.int32");
+  TORCH_CHECK(seq_lens.dim() == 1 && seq_lens.numel() >= batch, "seq_lens must contain one length per request");
+  const int64_t block_size = key_cache.size(1);
+  TORCH_CHECK(max_seq_len >= 0 && max_seq_len <= block_table.size(1) * block_size,
+              "max_seq_len must be within the block table capacity");
+  const auto device = query.device();
+  for (const auto *t : {&key_cache, &value_cache, &block_table, &seq_lens}) CheckSameDevice(*t, device, "attention operand");
+  const c10::OptionalDeviceGuard guard(device);
+  auto out = at::empty({batch, heads, dv}, query.options());
+  if (batch == 0) return out;
+  const size_t ws_bytes =
+      hif8_paged_decode_attention_workspace_size(batch, heads, kv_heads, d, dv, max_seq_len > 0 ? max_seq_len : 1);
+  at::Tensor workspace;
+  if (ws_bytes) workspace = at::empty({int64_t(ws_bytes)}, query.options().dtype(at::ScalarType::Byte));
+  CheckStatus(hif8_paged_decode_attention(query.data_ptr(), DtypeCode(query.scalar_type()), key_cache.data_ptr<uint8_t>(),
+                                          value_cache.data_ptr<uint8_t>(), key_cache.size(0), block_size, kv_heads, d, dv,
+                                          block_table.data_ptr(), bt_code, block_table.size(1),
+                                          seq_lens.data_ptr<int32_t>(), batch, heads, max_seq_len, float(scale),
+                                          out.data_ptr(), ws_bytes ? workspace.data_ptr() : nullptr, ws_bytes,
+                                          CurrentStream(device)),
+              "hif8_paged_decode_attention");
+  return out;
+}
+
 // ------------------------------------------------------------------ Meta
 
 std::tuple<at::Tensor, at::Tensor> Hif8StaticQuantMeta(const at::Tensor &x, const at::Tensor &fixed_scale) {
@@ -239,6 +360,15 @@ at::Tensor LinearMeta(const at::Tensor &activation, const at::Tensor &weight, co
   return at::empty({activation.size(0), weight.size(0)}, activation.options().dtype(output_dtype));
 }
 
+void Hif8KVCacheWriteMeta(const at::Tensor &, const at::Tensor &, const at::Tensor &, const at::Tensor &,
+                          const at::Tensor &, const at::Tensor &, const at::Tensor &,
+                          const c10::optional<at::Tensor> &) {}
+
+at::Tensor Hif8PagedDecodeAttentionMeta(const at::Tensor &query, const at::Tensor &, const at::Tensor &value_cache,
+                                        const at::Tensor &, const at::Tensor &, double, int64_t) {
+  return at::empty({query.size(0), query.size(1), value_cache.size(3) - 4}, query.options());
+}
+
 }  // namespace
 
 TORCH_LIBRARY(vllm_ascend_hif8, m) {
@@ -247,6 +377,8 @@ TORCH_LIBRARY(vllm_ascend_hif8, m) {
   m.def("soft_hif8_gemv(Tensor activation, Tensor weight, Tensor token_scale, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
   m.def("soft_hif8_gemm(Tensor activation, Tensor weight, Tensor token_scale, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
   m.def("soft_hif8_static_fused_gemm(Tensor activation, Tensor weight, Tensor fixed_scale, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
+  m.def("hif8_kv_cache_write(Tensor key, Tensor value, Tensor(a!) key_cache, Tensor(b!) value_cache, Tensor slot_mapping, Tensor key_scale, Tensor value_scale, Tensor(c!)? invalid_slots=None) -> ()");
+  m.def("hif8_paged_decode_attention(Tensor query, Tensor key_cache, Tensor value_cache, Tensor block_table, Tensor seq_lens, float scale, int max_seq_len) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
@@ -255,6 +387,8 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
   m.impl("soft_hif8_gemv", &SoftHif8Gemv);
   m.impl("soft_hif8_gemm", &SoftHif8Gemm);
   m.impl("soft_hif8_static_fused_gemm", &SoftHif8StaticFusedGemm);
+  m.impl("hif8_kv_cache_write", &Hif8KVCacheWrite);
+  m.impl("hif8_paged_decode_attention", &Hif8PagedDecodeAttention);
 }
 
 TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
@@ -263,6 +397,8 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
   m.impl("soft_hif8_gemv", &LinearMeta);
   m.impl("soft_hif8_gemm", &LinearMeta);
   m.impl("soft_hif8_static_fused_gemm", &LinearMeta);
+  m.impl("hif8_kv_cache_write", &Hif8KVCacheWriteMeta);
+  m.impl("hif8_paged_decode_attention", &Hif8PagedDecodeAttentionMeta);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
@@ -277,4 +413,10 @@ PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
   module.def("soft_hif8_static_fused_gemm", &SoftHif8StaticFusedGemm, pybind11::arg("activation"),
              pybind11::arg("weight"), pybind11::arg("fixed_scale"), pybind11::arg("channel_scale"),
              pybind11::arg("bias") = c10::nullopt, pybind11::arg("output_dtype") = at::ScalarType::Half);
+  module.def("hif8_kv_cache_write", &Hif8KVCacheWrite, pybind11::arg("key"), pybind11::arg("value"),
+             pybind11::arg("key_cache"), pybind11::arg("value_cache"), pybind11::arg("slot_mapping"),
+             pybind11::arg("key_scale"), pybind11::arg("value_scale"), pybind11::arg("invalid_slots") = c10::nullopt);
+  module.def("hif8_paged_decode_attention", &Hif8PagedDecodeAttention, pybind11::arg("query"),
+             pybind11::arg("key_cache"), pybind11::arg("value_cache"), pybind11::arg("block_table"),
+             pybind11::arg("seq_lens"), pybind11::arg("scale"), pybind11::arg("max_seq_len"));
 }

@@ -3,7 +3,8 @@
 Modules:
   native    operator API (static_quant, soft_linear, soft_static_fused_linear, scaled_decode)
   scheme    static W8A8 linear method (input_scale / weight / weight_scale)
+  kv_cache  paged HiF8 KV layout, fused static cache write, paged decode attention
   _build    in-tree build of libhif8_rocm.so and the torch extension
 """
 
-__all__ = ["native", "scheme"]
+__all__ = ["kv_cache", "native", "scheme"]

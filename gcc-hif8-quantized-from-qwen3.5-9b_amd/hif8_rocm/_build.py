@@ -26,7 +26,7 @@ LIB_NAME = "libhif8_rocm.so"
 ARCH = os.environ.get("HIF8_OFFLOAD_ARCH", "gfx950")
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
-HIP_SOURCES = ["capi.hip", "static_quant.hip", "gemv.hip", "gemm.hip", "linear_api.hip"]
+HIP_SOURCES = ["capi.hip", "static_quant.hip", "gemv.hip", "gemm.hip", "linear_api.hip", "kv_cache.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -47,6 +47,12 @@ enum hif8_dtype {
   HIF8_DTYPE_NONE = -1 /* "no bias" */
 };
 
+/* Integer index tensors (slot mappings, block tables). */
+enum hif8_index_dtype {
+  HIF8_INDEX_INT32 = 0,
+  HIF8_INDEX_INT64 = 1
+};
+
 /* Message of the last failed call on this thread ("" if none). */
 const char *hif8_last_error(void);
 
@@ -116,6 +122,69 @@ int soft_hif8_static_fused_gemm(const void *x, int x_dtype, const uint8_t *weigh
                                 const float *fixed_scale, const float *channel_scale,
                                 const void *bias, int bias_dtype, void *out, int out_dtype,
                                 int64_t m, int64_t n, int64_t k, hif8_stream_t stream);
+
+/*
+ * Fused static KV-cache write (quantise + pack + scatter in one launch).
+ * Replaces the static branch of _write_hif8_cache
+ * (src/vllm_ascend_hif8/kv_runtime.py:1222-1339): _quantize_kv with checkpoint
+ * per-head scales (kv_runtime.py:1168-1199, i.e. aclnnHif8StaticQuant on
+ * [tokens * Hkv, D] rows with S = Hkv), pack_kv_rows (kv_cache.py:151-170) and
+ * the slot index_copy_ (kv_runtime.py:1313-1316).
+ *   key [tokens, Hkv, D], value [tokens, Hkv, Dv]   fp16/bf16 (x_dtype)
+ *   key_scale, value_scale [Hkv] float32, finite > 0
+ *   slot_mapping [tokens] int32/int64 (slot_dtype): flat slot block * block_size + offset;
+ *                slot < 0 is a padding token and is skipped
+ *   key_cache [num_blocks, block_size, Hkv, D + 4], value_cache [..., Dv + 4] uint8, in place:
+ *     row = enc_sat(x / scale[h]) codes followed by scale[h] (4 bytes, little-endian)
+ *   invalid_slots  optional int32 counter (may be NULL): incremented once per token whose
+ *                  slot is >= num_blocks * block_size; such tokens are not written.  The
+ *                  caller zeroes it.  (The reference raises IndexError after a host check.)
+ * D and Dv must be divisible by 4 (kv_cache.py:48-57).
+ */
+int hif8_kv_cache_write(const void *key, const void *value, int x_dtype, int64_t tokens,
+                        int64_t num_kv_heads, int64_t head_size, int64_t head_size_v,
+                        const float *key_scale, const float *value_scale,
+                        const void *slot_mapping, int slot_dtype,
+                        uint8_t *key_cache, uint8_t *value_cache, int64_t num_blocks,
+                        int64_t block_size, int32_t *invalid_slots, hif8_stream_t stream);
+
+/*
+ * Bytes of workspace hif8_paged_decode_attention needs for these sizes (0 if none).
+ * The split plan depends only on these arguments.  Mirrors ACLNN's GetWorkspaceSize
+ * phase (csrc/extension/hif8_native.cpp:202-239).
+ */
+size_t hif8_paged_decode_attention_workspace_size(int64_t batch, int64_t num_heads,
+                                                  int64_t num_kv_heads, int64_t head_size,
+                                                  int64_t head_size_v, int64_t max_seq_len);
+
+/*
+ * Paged HiF8 decode attention, one query token per request.
+ * Replaces the decode branch of _forward_hif8_attention
+ * (src/vllm_ascend_hif8/kv_runtime.py:1470-1563): gather_kv_rows_concat
+ * (kv_cache.py:255-311) + scaled decode (kv_runtime.py:1201-1211) +
+ * torch_npu.npu_fused_infer_attention_score (kv_runtime.py:1526-1540), whose
+ * contract is paged_attention_reference (kv_cache.py:314-372).  Pages are
+ * decoded inside the kernel; nothing is materialised.
+ *   query [batch, num_heads, D] fp16/bf16 (q_dtype)
+ *   key_cache / value_cache as written by hif8_kv_cache_write
+ *   block_table [batch, max_blocks_per_seq] int32/int64
+ *   seq_lens [batch] int32 on the device; each is clamped to [0, max_seq_len]
+ *   max_seq_len <= max_blocks_per_seq * block_size, >= every seq_len
+ *   out [batch, num_heads, Dv] in the query dtype:
+ *     out[b, h] = softmax(scale * q[b, h] . K_b^T) V_b over the request's seq_lens[b]
+ *     tokens with K/V rows dec(code) * row scale and KV head h / (num_heads / Hkv);
+ *     a request with no tokens gets zeros; tokens whose block id lies outside
+ *     [0, num_blocks) are left out (the caller validates the table).
+ *   workspace  at least hif8_paged_decode_attention_workspace_size(...) bytes, 16-byte
+ *              aligned (may be NULL when that size is 0)
+ */
+int hif8_paged_decode_attention(const void *query, int q_dtype, const uint8_t *key_cache,
+                                const uint8_t *value_cache, int64_t num_blocks, int64_t block_size,
+                                int64_t num_kv_heads, int64_t head_size, int64_t head_size_v,
+                                const void *block_table, int block_table_dtype,
+                                int64_t max_blocks_per_seq, const int32_t *seq_lens, int64_t batch,
+                                int64_t num_heads, int64_t max_seq_len, float scale, void *out,
+                                void *workspace, size_t workspace_bytes, hif8_stream_t stream);
 
 #ifdef __cplusplus
 }

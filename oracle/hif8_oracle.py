@@ -459,11 +459,12 @@ def paged_attention_reference(query: np.ndarray, key_cache: np.ndarray, value_ca
     """Decode (one query token per request) paged attention (kv_cache.py:314-372).
 
     ``query`` is [B, Hq, D] float32 holding bf16 values.  K/V rows are gathered,
-    decoded as bf16_RNE(dec(b) * s_row) and repeated over the GQA group
-    (kv_cache.py:355-363).  ``rounding="bf16"`` reproduces the reference's bf16
-    intermediate roundings (logits, probabilities and output are bf16 tensors in
-    kv_cache.py:364-371); ``rounding="f64"`` keeps every intermediate in float64
-    (the textbook formula used to pin the bf16 variant).
+    decoded as bf16_RNE(dec(b) * s_row) and query head h attends KV head
+    h // (Hq / Hkv), the head ``repeat_interleave`` gives it (kv_cache.py:355-363).
+    ``rounding="bf16"`` reproduces the reference's bf16 intermediate roundings
+    (logits, probabilities and output are bf16 tensors in kv_cache.py:364-371);
+    ``rounding="f64"`` keeps every intermediate in float64.  A request with no
+    tokens yields zeros (an empty weighted sum).
     """
     q = np.asarray(query, dtype=np.float64)
     bsz, hq, d = q.shape
@@ -479,24 +480,24 @@ def paged_attention_reference(query: np.ndarray, key_cache: np.ndarray, value_ca
     for b in range(bsz):
         kd, ks = unpack_kv_rows(krows[b], kw)
         vd, vs = unpack_kv_rows(vrows[b], vw)
+        if kd.shape[0] == 0:
+            continue
         keys = round_bf16(decode_kv_rows(kd, ks)).astype(np.float64)      # [L, Hkv, D]
         vals = round_bf16(decode_kv_rows(vd, vs)).astype(np.float64)
-        if keys.shape[0] == 0:
-            continue
-        keys = np.repeat(keys, group, axis=1)
-        vals = np.repeat(vals, group, axis=1)
-        logits = np.einsum("hd,khd->hk", q[b], keys)
+        qg = q[b].reshape(hkv, group, d)                                  # head h = j * group + g
+        logits = np.einsum("jgd,kjd->jgk", qg, keys).reshape(hq, -1)      # [Hq, L]
         if rounding == "bf16":
             logits = round_bf16(logits).astype(np.float64)
             logits = round_bf16(logits * np.float32(scale)).astype(np.float64)
             mx = logits.max(axis=-1, keepdims=True)
             e = np.exp((logits - mx).astype(np.float32)).astype(np.float64)
             probs = round_bf16(e / e.sum(axis=-1, keepdims=True)).astype(np.float64)
-            out[b] = round_bf16(np.einsum("hk,khd->hd", probs, vals))
+            res = np.einsum("jgk,kjd->jgd", probs.reshape(hkv, group, -1), vals)
+            out[b] = round_bf16(res.reshape(hq, vw))
         else:
             logits = logits * scale
             mx = logits.max(axis=-1, keepdims=True)
             e = np.exp(logits - mx)
             probs = e / e.sum(axis=-1, keepdims=True)
-            out[b] = np.einsum("hk,khd->hd", probs, vals)
+            out[b] = np.einsum("jgk,kjd->jgd", probs.reshape(hkv, group, -1), vals).reshape(hq, vw)
     return out

@@ -17,8 +17,9 @@ SRC = r"""
 #include <string.h>
 #include "hif8_format.h"
 static constexpr hif8::Tables kT = hif8::make_tables();
-extern "C" void dump_tables(uint8_t *enc, uint16_t *bf16, uint32_t *f32) {
+extern "C" void dump_tables(uint8_t *enc, uint16_t *bf16, uint32_t *f32, uint16_t *f16) {
   memcpy(enc, kT.static_encode, sizeof(kT.static_encode));
+  memcpy(f16, kT.decode_f16, sizeof(kT.decode_f16));
   memcpy(bf16, kT.decode_bf16, sizeof(kT.decode_bf16));
   memcpy(f32, kT.decode_f32, sizeof(kT.decode_f32));
 }
@@ -36,7 +37,7 @@ def fmt(tmp_path_factory):
     subprocess.run(["g++", "-std=c++17", "-O1", "-fconstexpr-ops-limit=1000000000", "-shared", "-fPIC",
                     f"-I{PKG_ROOT / 'csrc'}", str(d / "fmt.cpp"), "-o", str(so)], check=True)
     lib = ctypes.CDLL(str(so))
-    lib.dump_tables.argtypes = [ctypes.c_void_p] * 3
+    lib.dump_tables.argtypes = [ctypes.c_void_p] * 4
     lib.static_encode_f32.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_long]
     return lib
 
@@ -45,13 +46,19 @@ def test_constexpr_tables_equal_oracle(fmt):
     enc = np.zeros(8192, np.uint8)
     bf = np.zeros(256, np.uint16)
     f32 = np.zeros(256, np.uint32)
-    fmt.dump_tables(enc.ctypes.data, bf.ctypes.data, f32.ctypes.data)
+    f16 = np.zeros(256, np.uint16)
+    fmt.dump_tables(enc.ctypes.data, bf.ctypes.data, f32.ctypes.data, f16.ctypes.data)
     assert np.array_equal(enc, o.STATIC_LUT)
     want_bf = np.array([o.bf16_bits_of_decode(b) for b in range(256)], np.uint16)
     assert np.array_equal(bf, want_bf)
     want_f32 = o.DECODE_F32.view(np.uint32).copy()
     want_f32[o.NAN_CODE] = 0x7FC00000
     assert np.array_equal(f32, want_f32)
+    want_f16 = np.array([o.half_bits_of_decode(b) for b in range(256)], np.uint16)
+    assert np.array_equal(f16, want_f16)
+    # Exactness: the fp16 payload converts back to the fp32 value.
+    finite = np.isfinite(o.DECODE_F32)
+    assert np.array_equal(f16.view(np.float16).astype(np.float32)[finite], o.DECODE_F32[finite])
 
 
 def test_arithmetic_static_encoder_on_all_bf16_quotients(fmt):
