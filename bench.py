@@ -43,6 +43,11 @@ LAYER = [("q", 4096, 4096), ("kv", 2048, 4096), ("o", 4096, 4096), ("gate_up", 2
 DECODE_M = (1, 4)
 PREFILL_M = (512, 4096)
 N_COPIES = 5
+# KV8 decode attention: 16 query heads, 4 KV heads, head_dim 256, 128-token pages.
+KV_HQ, KV_HKV, KV_D, KV_BS = 16, 4, 256, 128
+KV_CTX = (512, 4096, 16384)
+KV_BATCH = (1, 4)
+KV_POOL_BYTES = 1_100_000_000   # K + V page pool, > 4x the Infinity Cache
 
 
 def gemv_bytes(m: int, n: int, k: int) -> int:
@@ -51,6 +56,17 @@ def gemv_bytes(m: int, n: int, k: int) -> int:
 
 def quant_bytes(m: int, k: int) -> int:
     return 3 * m * k + 4 * m + 4
+
+
+def kv_attention_bytes(lens) -> int:
+    """K and V rows of every context token (codes + sidecar), q in, out, block-table entries."""
+    pages = sum((n + KV_BS - 1) // KV_BS for n in lens)
+    return (sum(lens) * KV_HKV * (KV_D + 4) * 2 + 2 * len(lens) * KV_HQ * KV_D * 2 + 4 * pages)
+
+
+def kv_write_bytes(tokens: int) -> int:
+    """bf16 K and V in, packed K and V rows out, 8-byte slots."""
+    return tokens * KV_HKV * (2 * KV_D * 2 + (KV_D + 4) * 2) + 8 * tokens
 
 
 def log(msg: str) -> None:
@@ -89,6 +105,120 @@ class Setup:
             self.weights.append(ws_by_name)
             self.layers.append(mods)
         torch.cuda.synchronize()
+
+
+class KVSetup:
+    """One page pool of HiF8 K/V (written by the fused write kernel) and, per
+    (batch, ctx), several block tables over disjoint random pages, rotated
+    between steps so each step reads pages no earlier step touched."""
+
+    def __init__(self, torch, device):
+        from hif8_rocm import kv_cache
+
+        self.torch, self.device = torch, device
+        page_bytes = KV_BS * KV_HKV * (KV_D + 4) * 2
+        self.num_blocks = KV_POOL_BYTES // page_bytes
+        layout = kv_cache.Hif8KVCacheLayout(self.num_blocks, KV_BS, KV_HKV, KV_D)
+        self.kc, self.vc = layout.allocate(device)
+        g = torch.Generator(device=device).manual_seed(4242)
+        chunk = 32768
+        tokens = self.num_blocks * KV_BS
+        self.ks = self.vs = None
+        for t0 in range(0, tokens, chunk):
+            n = min(chunk, tokens - t0)
+            k = torch.randn(n, KV_HKV, KV_D, generator=g, device=device).to(torch.bfloat16)
+            v = torch.randn(n, KV_HKV, KV_D, generator=g, device=device).to(torch.bfloat16)
+            if self.ks is None:   # static per-head scales from the first chunk: absmax / 32768
+                self.ks = (k.float().abs().amax(dim=(0, 2)) / HIF8_MAX).contiguous()
+                self.vs = (v.float().abs().amax(dim=(0, 2)) / HIF8_MAX).contiguous()
+            slots = torch.arange(t0, t0 + n, device=device, dtype=torch.int64)
+            kv_cache.write_kv_cache(k, v, self.kc, self.vc, slots, self.ks, self.vs, validate=False)
+        self.q = {b: torch.randn(b, KV_HQ, KV_D, generator=g, device=device).to(torch.bfloat16) for b in KV_BATCH}
+        self.perm_gen = torch.Generator().manual_seed(77)
+        torch.cuda.synchronize()
+
+    def tables(self, batch: int, ctx: int, max_tables: int = 16):
+        torch = self.torch
+        per = (ctx + KV_BS - 1) // KV_BS
+        count = max(1, min(max_tables, self.num_blocks // (batch * per)))
+        perm = torch.randperm(self.num_blocks, generator=self.perm_gen)
+        out = []
+        for r in range(count):
+            ids = perm[r * batch * per:(r + 1) * batch * per].reshape(batch, per)
+            out.append(ids.to(torch.int32).to(self.device))
+        return out
+
+
+def kv_attention_bench(kvs: KVSetup, steps: int) -> dict:
+    """µs per decode step and per token, and GB/s, of paged decode attention per config."""
+    torch = kvs.torch
+    op = torch.ops.vllm_ascend_hif8.hif8_paged_decode_attention
+    scale = KV_D ** -0.5
+    res = {}
+    for batch in KV_BATCH:
+        for ctx in KV_CTX:
+            lens = torch.full((batch,), ctx, dtype=torch.int32, device=kvs.device)
+            graphs = []
+            for table in kvs.tables(batch, ctx):
+                def fn(table=table):
+                    op(kvs.q[batch], kvs.kc, kvs.vc, table, lens, scale, ctx)
+                graphs.append(capture(torch, fn))
+            ms = time_graphs(torch, graphs, max(steps, 2 * len(graphs)))
+            nbytes = kv_attention_bytes([ctx] * batch)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            res[f"b{batch}_ctx{ctx}"] = {"us_per_step": round(ms * 1e3, 3), "us_per_token": round(ms * 1e3 / batch, 3),
+                                         "bytes": nbytes, "GBps": round(gbs, 1),
+                                         "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "tables": len(graphs)}
+            log(f"kv attention b={batch} ctx={ctx}: {ms * 1e3:.2f} us/step, {gbs:.0f} GB/s")
+    return res
+
+
+def kv_write_bench(kvs: KVSetup) -> dict:
+    """Fused KV write (quant + pack + scatter) for a decode step (4 tokens) and a 4096-token prefill."""
+    torch = kvs.torch
+    op = torch.ops.vllm_ascend_hif8.hif8_kv_cache_write
+    res = {}
+    for tokens in (4, 4096):
+        k = torch.randn(tokens, KV_HKV, KV_D, device=kvs.device).to(torch.bfloat16)
+        v = torch.randn(tokens, KV_HKV, KV_D, device=kvs.device).to(torch.bfloat16)
+        slots = torch.randperm(kvs.num_blocks * KV_BS, device=kvs.device)[:tokens].to(torch.int64)
+
+        def fn():
+            for _ in range(10):
+                op(k, v, kvs.kc, kvs.vc, slots, kvs.ks, kvs.vs, None)
+        ms = time_graphs(torch, [capture(torch, fn)], 3) / 10
+        gbs = kv_write_bytes(tokens) / (ms * 1e-3) / 1e9
+        res[f"tokens{tokens}"] = {"us": round(ms * 1e3, 3), "bytes": kv_write_bytes(tokens), "GBps": round(gbs, 1),
+                                  "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    return res
+
+
+def kv_cpu_baseline(budget_s: float = 8.0) -> dict:
+    """paged_attention_reference (numpy oracle, reference bf16 roundings) on batch 1, ctx 4096."""
+    import numpy as np
+
+    from oracle import hif8_oracle as o
+
+    rng = np.random.default_rng(1)
+    ctx, pages = 4096, 4096 // KV_BS
+    kc = np.empty((pages, KV_BS, KV_HKV, KV_D + 4), np.uint8)
+    vc = np.empty_like(kc)
+    for c in (kc, vc):
+        data, scale = o.quantize_kv_rows_static(rng.standard_normal((ctx, KV_HKV, KV_D)).astype(np.float32),
+                                                np.full(KV_HKV, 4.5 / HIF8_MAX, np.float32))
+        c[:] = o.pack_kv_rows(data, scale).reshape(c.shape)
+    q = o.round_bf16(rng.standard_normal((1, KV_HQ, KV_D)).astype(np.float32))
+    table = rng.permutation(pages)[None, :]
+    done, t0 = 0, time.perf_counter()
+    while True:
+        o.paged_attention_reference(q, kc, vc, table, [ctx], KV_BS, KV_D ** -0.5, rounding="bf16")
+        done += 1
+        if time.perf_counter() - t0 > budget_s or done >= 10:
+            break
+    elapsed = time.perf_counter() - t0
+    return {"value": round(elapsed / done * 1e6, 1), "unit": "us/token", "cores": 1, "kind": "port",
+            "sample": f"{done} decode step(s) of paged_attention_reference (numpy oracle), batch 1, ctx 4096, "
+                      f"{elapsed:.1f} s"}
 
 
 def capture(torch, fn):
@@ -265,13 +395,15 @@ def main() -> None:
               file=sys.stderr)
         sys.exit(2)
 
-    cpu = None
+    cpu = kv_cpu = None
     if not args.no_cpu_baseline and not args.profile_pass:
         for var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
             os.environ[var] = "1"
         log("cpu baseline (numpy oracle) ...")
         cpu = cpu_baseline()
         log(f"cpu baseline {cpu['value']} GB/s")
+        kv_cpu = kv_cpu_baseline()
+        log(f"kv cpu baseline {kv_cpu['value']} us/token")
 
     import torch
 
@@ -321,6 +453,12 @@ def main() -> None:
                                "us_per_layer": round(us, 1)}
     all_gemv_gbs = sum(v["bytes"] for v in gemv) / (sum(v["us"] for v in gemv) * 1e-6) / 1e9
 
+    log("KV page pool ...")
+    kvs = KVSetup(torch, device)
+    kv_attn = kv_attention_bench(kvs, args.steps)
+    kv_write = kv_write_bench(kvs)
+    kv_dom = kv_attn[f"b{KV_BATCH[-1]}_ctx{KV_CTX[-1]}"]
+
     out = {
         "metric": METRIC,
         "value": round(value, 1),
@@ -355,6 +493,17 @@ def main() -> None:
             "us_per_launch": dom["us"],
         },
         "cpu_baseline": cpu,
+        "kv_decode_attention": {
+            "workload": "BASELINE configs[3]: paged decode attention, Hq 16, Hkv 4, D 256, page 128, one query "
+                        "token per request, per-head static K/V scales, random disjoint pages from a 1.1 GB pool "
+                        "rotated per step; bytes = K+V rows (codes + sidecar) + q + out + block-table entries",
+            "configs": kv_attn,
+            "roofline": {"kernel": "paged_decode_attention_kernel + combine (batch 4, ctx 16384)", "bound": "hbm",
+                         "achieved": kv_dom["GBps"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": kv_dom["frac_hbm"], "us_per_token": kv_dom["us_per_token"]},
+            "cpu_baseline": kv_cpu,
+            "kv_cache_write": kv_write,
+        },
         "decode_sweep_fused_GBps": round(fused_gbs, 1),
         "gemv_all_launches_GBps": round(all_gemv_gbs, 1),
         "gemm_per_layer": gemm_layer,

@@ -17,22 +17,25 @@
 // request's token range (a "split") and four KV heads, one wavefront each; a
 // wavefront walks its range in 32-token tiles:
 //   * K rows go from HBM straight into VGPRs in the MFMA A-operand layout
-//     (token = lane % 16, 64 contiguous bytes per lane), are decoded through a
-//     256-entry table in LDS, and S^T = K Q^T runs on v_mfma_f32_16x16x32
-//     (B = the G query heads of the KV head, padded to 16 columns);
-//   * V rows are staged raw in LDS and read transposed (8 tokens x 4 dims per
-//     lane), decoded, and O^T += V^T P' runs on the same MFMA with the
-//     softmax weights P' rounded to bf16;
-//   * rows with the head's scale (static caches) decode through per-head tables
-//     of bf16/fp16(dec(c) * scale), i.e. rounded like the reference's decoded
-//     K/V; rows with other scales decode exactly and the K row scale and
-//     V row scale multiply the logits and softmax weights in FP32 instead;
+//     (token = lane % 16, 64 contiguous bytes per lane) and S^T = K Q^T runs
+//     on v_mfma_f32_16x16x32 (B = the G query heads of the KV head, padded to
+//     16 columns);
+//   * V rows are copied raw into LDS by DMA (global_load_lds_dwordx4) and read
+//     transposed (8 tokens x 4 dims per lane), and O^T += V^T P' runs on the
+//     same MFMA with the softmax weights P' rounded to bf16;
+//   * both operands are decoded as dtype(dec(c) * row scale) - a lookup in an
+//     fp32 table in LDS, one multiply by the row's scale, one round to
+//     nearest even - which is how the reference decodes K and V before its
+//     attention (decode_kv_rows(...).to(query dtype), kv_cache.py:355-356);
 //   * the online softmax keeps (max, sum) per query head in FP32;
 //   * the next tile's loads are in flight while the current tile computes.
 // HiF8 values are exact in bf16 and fp16, so decode adds no rounding.  With
 // more than one split per request, partial (O, max, sum) go to the caller's
 // workspace and a second kernel merges them.
+#include <stddef.h>
 #include <stdlib.h>
+
+#include <type_traits>
 
 #include "quant_device.h"
 
@@ -150,8 +153,8 @@ struct AttnParams {
   float *part_ml;             // [B, num_splits, Hq, 2]
   int64_t bt_stride;
   int64_t num_blocks;
-  int block_size, hkv, hq, group, d, dv;
-  int max_len, split_tokens, num_splits;
+  int block_size, log2_block_size, hkv, hq, group, d, dv;
+  int max_len, split_tokens, num_splits, batch;
   float scale_log2;           // softmax scale * log2(e)
 };
 
@@ -182,6 +185,18 @@ __device__ __forceinline__ u32x4 decode_column(const uint16_t *lut, const uint32
                lut_pair(lut, (w[6] >> sh) & 0xFFu, (w[7] >> sh) & 0xFFu)};
 }
 
+// Two fp32 values rounded to nearest-even and packed as the MFMA operand dtype.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+template <bool kBf16>
+__device__ __forceinline__ uint32_t pack_half2(float lo, float hi) {
+  if constexpr (kBf16) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+  } else {
+    return uint32_t(float_to_f16_bits(lo)) | (uint32_t(float_to_f16_bits(hi)) << 16);
+  }
+}
+
 template <bool kBf16>
 __device__ __forceinline__ f32x4_t mfma16(u32x4 a, u32x4 b, f32x4_t c) {
   if constexpr (kBf16) {
@@ -193,8 +208,41 @@ __device__ __forceinline__ f32x4_t mfma16(u32x4 a, u32x4 b, f32x4_t c) {
   }
 }
 
-__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
-  return uint32_t(float_to_bf16_bits(lo)) | (uint32_t(float_to_bf16_bits(hi)) << 16);
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 32-bit LDS address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_address(const void *p) {
+  return uint32_t(uintptr_t((const lds_void_t *)p));
+}
+
+// Asynchronous copy of 16 bytes per lane from global memory into LDS
+// (global_load_lds_dwordx4): lane i's bytes land at lds_base + 16 * i, the
+// LDS address being taken from M0 when the instruction issues.  Written as
+// inline assembly so that the compiler neither waits on it nor counts it:
+// every consumer of the copied data waits for it explicitly (wait_vmcnt).
+// M0 is saved and restored around the copy; one wait state separates the M0
+// write from the load.
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds_base) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(lds_base)
+      : "memory");
+}
+
+// s_waitcnt with vmcnt(n) only (lgkmcnt / expcnt left at their maxima).
+template <int kN>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(kN >= 0 && kN < 64, "vmcnt range");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt((kN & 0xF) | (0x7 << 4) | (0xF << 8) | ((kN >> 4) << 14));
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // MFMA mapping (v_mfma_f32_16x16x32: A row = lane % 16, B column = lane % 16,
@@ -206,121 +254,132 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
 //                 leave those tokens, so P' needs no data movement; A row r of
 //                 MFMA (db, q) is dim 64 db + 4 r + q, so lane (g, n) ends up with
 //                 dims 64 db + 16 g + [0, 16) of query head n contiguous.
+// V tiles reach LDS by DMA, 16-byte granule c of token t stored at granule
+// c ^ swz(t), swz(t) = 4 * ((t >> 2) % (D / 64)): the transposed reads of the
+// four lane groups (tokens 4g + j) then fall in four different bank quarters.
+//
+// A workgroup is one wavefront and owns one (request, context split, KV
+// head).  Workgroups of the Hkv heads of one split get block ids that are
+// equal modulo 8, so they run on the same XCD and the cache lines their rows
+// share are read from HBM once.
 template <int kD, bool kQBf16, bool kPaged, typename BtT>
-__global__ __launch_bounds__(kThreads, 2) void paged_decode_attention_kernel(const AttnParams p) {
-  constexpr int kRow = kD + 4;           // bytes per cache row
-  constexpr int kLaneK = kD / 4;         // K bytes per lane per 16-token block
-  constexpr int kKChunks = kD / 64;      // 16-byte K loads per lane per block
-  constexpr int kQkSteps = kD / 32;      // MFMAs per 16-token block
-  constexpr int kRowPieces = kD / 16;    // 16-byte pieces per V row
-  constexpr int kVPieces = kD / 32;      // V pieces per lane per tile
-  constexpr int kVStride = kD + 16;      // LDS bytes per staged V row (bank spread)
+__global__ __launch_bounds__(kWave, 2) void paged_decode_attention_kernel(const AttnParams p) {
+  constexpr int kRow = kD + 4;            // bytes per cache row
+  constexpr int kLaneK = kD / 4;          // K bytes per lane per 16-token block
+  constexpr int kKChunks = kD / 64;       // 16-byte K loads per lane per block
+  constexpr int kQkSteps = kD / 32;       // MFMAs per 16-token block
+  constexpr int kGranules = kD / 16;      // 16-byte granules per V row
+  constexpr int kVDma = kTile * kGranules / 64;  // DMA instructions per V tile
+  constexpr int kVBytes = kTile * kD;     // one V tile in LDS
   constexpr int kDBlocks = kD / 64;
+  static_assert(kTile * kGranules % 64 == 0, "whole DMA instructions per tile");
 
-  __shared__ __attribute__((aligned(16))) uint16_t lut_v[256];  // bf16 payloads
-  __shared__ __attribute__((aligned(16))) uint16_t lut_k[256];  // query-dtype payloads
-  // Per wavefront: dec(c) * s rounded to the operand dtype for the head's K and
-  // V scale s (the reference's decode_kv_rows(...).to(dtype), kv_cache.py:355-356).
-  __shared__ __attribute__((aligned(16))) uint16_t lut_ks[kWaves][256];
-  __shared__ __attribute__((aligned(16))) uint16_t lut_vs[kWaves][256];
-  __shared__ __attribute__((aligned(16))) uint8_t vtile[kWaves][kTile * kVStride];
-  __shared__ __attribute__((aligned(16))) float scl[kWaves][64];  // K scales | V scales
+  // One LDS block, so the decode tables sit at fixed addresses: a lookup is
+  // one SDWA shift of the code plus a ds_read_u16 with the table's offset.
+  struct Smem {
+    uint16_t k_tab[256];     // query dtype(dec(c) * k_tab_scale)
+    uint16_t v_tab[256];     // bf16(dec(c) * v_tab_scale)
+    float dec[256];          // fp32 dec(c), the source of both
+    float scl[64];           // K | V factors of the tile's tokens (0 = masked)
+    uint8_t vtile[2][kVBytes];  // double-buffered V tile
+  };
+  __shared__ __attribute__((aligned(16))) Smem smem;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-  lut_v[tid] = kDeviceTables.decode_bf16[tid];
-  lut_k[tid] = kQBf16 ? kDeviceTables.decode_bf16[tid] : kDeviceTables.decode_f16[tid];
-  __syncthreads();  // the only workgroup barrier; waves are independent after it
-
-  const int b = blockIdx.x / p.num_splits;
-  const int split = blockIdx.x - b * p.num_splits;
-  const int h = blockIdx.y * kWaves + wave;
-  if (h >= p.hkv) return;
-  const int len = clamp_len(p.seq_lens[b], p.max_len);
+  const int xcd = int(blockIdx.x) & 7, slot_id = int(blockIdx.x) >> 3;
+  const int h = slot_id % p.hkv;
+  const int bs_idx = (slot_id / p.hkv) * 8 + xcd;
+  if (bs_idx >= p.batch * p.num_splits) return;  // padding block (uniform)
+  const int b = bs_idx / p.num_splits;
+  const int split = bs_idx - b * p.num_splits;
+  const int lane = threadIdx.x;
   const int n = lane & 15, g = lane >> 4;
   const bool head_ok = n < p.group;
   const int qhead = h * p.group + (head_ok ? n : 0);
   const size_t out_row = (size_t(b) * p.hq + qhead) * kD;
   const int t_begin = split * p.split_tokens;
-  if (t_begin >= len) {
-    if (split == 0 && head_ok) {  // empty request: zero output
-      uint16_t *o = static_cast<uint16_t *>(p.out) + out_row + 16 * g;
-#pragma unroll
-      for (int db = 0; db < kDBlocks; ++db) {
-        reinterpret_cast<u32x4 *>(o + 64 * db)[0] = u32x4{0, 0, 0, 0};
-        reinterpret_cast<u32x4 *>(o + 64 * db)[1] = u32x4{0, 0, 0, 0};
-      }
-    }
-    return;
-  }
-  const int t_end = min(t_begin + p.split_tokens, len);
-  const int ntiles = (t_end - t_begin + kTile - 1) / kTile;
-  const int n_splits_b = (len + p.split_tokens - 1) / p.split_tokens;
-
-  // Q^T operand: lane (g, n) holds dims [g*D/4, (g+1)*D/4) of query head n.
-  u32x4 qf[kQkSteps];
-  {
-    const uint16_t *q = static_cast<const uint16_t *>(p.query) + out_row + kLaneK * g;
-#pragma unroll
-    for (int i = 0; i < kQkSteps; ++i)
-      qf[i] = head_ok ? reinterpret_cast<const u32x4 *>(q)[i] : u32x4{0, 0, 0, 0};
-  }
+  // The range end from max_len alone: the first loads need no length.
+  const int t_cap = min(t_begin + p.split_tokens, p.max_len);
 
   const BtT *bt = static_cast<const BtT *>(p.block_table) + size_t(b) * p.bt_stride;
   const int64_t rec = int64_t(p.hkv) * kRow;  // bytes per token record
   const int64_t head_off = int64_t(h) * kRow;
+  const int lg = p.log2_block_size;
 
-  // Byte offset of row (token t, head h) and whether its block id is valid.
+  // The block ids of this split, one per lane (a split spans at most 64
+  // blocks), loaded once so that no tile waits on a table load.
+  const int first_blk = t_begin >> lg;
+  int64_t blk_lane;
+  {
+    const int last_blk = (max(t_cap, t_begin + 1) - 1) >> lg;
+    blk_lane = int64_t(bt[min(first_blk + lane, last_blk)]);
+  }
+  const bool blk_lane_ok = blk_lane >= 0 && blk_lane < p.num_blocks;
+  const int64_t slot_lane = blk_lane_ok ? (blk_lane << lg) : int64_t(-1);  // first flat slot of the block
+
+  // Byte offset of row (token t, head h) and whether its block id is valid;
+  // rows in an invalid block read the cache's first record and are masked.
   // kPaged: a tile lies inside one block (block_size % 32 == 0), so the
-  // lookup is per tile and tokens past the end still address that block.
+  // lookup is per tile (a lane read) and tokens past the end still address
+  // that block.
+  auto tile_row = [&](int t0, bool &ok) -> int64_t {
+    const int idx = (t0 >> lg) - first_blk;
+    const int lo = __builtin_amdgcn_readlane(int(uint64_t(slot_lane)), idx);
+    const int hi = __builtin_amdgcn_readlane(int(uint64_t(slot_lane) >> 32), idx);
+    const int64_t slot0 = int64_t((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
+    ok = slot0 >= 0;
+    return ok ? (slot0 + (t0 & ((1 << lg) - 1))) * rec + head_off : head_off;
+  };
   auto token_row = [&](int t, bool &ok) -> int64_t {
-    const int64_t blk = int64_t(bt[t / p.block_size]);
-    ok = blk >= 0 && blk < p.num_blocks;
-    return ok ? (blk * p.block_size + t % p.block_size) * rec + head_off : head_off;
+    const int idx = (t >> lg) - first_blk;
+    const int lo = __shfl(int(uint64_t(slot_lane)), idx, kWave);
+    const int hi = __shfl(int(uint64_t(slot_lane) >> 32), idx, kWave);
+    const int64_t slot0 = int64_t((uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
+    ok = slot0 >= 0;
+    return ok ? (slot0 + (t & ((1 << lg) - 1))) * rec + head_off : head_off;
   };
 
-  u32x4 kr[2][kKChunks];   // K operand bytes of the tile being computed / loaded
-  u32x4 vn[kVPieces];      // next tile's V pieces
-  float sn;                // next tile's K (lanes 0-31) or V (lanes 32-63) scale
-  int nvalid_next;         // valid tokens of the next tile (0 if its block is invalid)
-  // Rows of tokens past the end are clamped to the last valid token (generic
-  // path) or stay inside the tile's block (paged path) and are masked later;
-  // rows in an invalid block read the cache's first record and are masked.
-  auto issue_v = [&](int t0) {
-    const int nv = min(kTile, t_end - t0);
+  u32x4 kr[2][kKChunks];  // K operand bytes of the tile being computed / loaded
+  float sn;               // K (lanes 0-31) or V (lanes 32-63) scale of token lane % 32
+  bool tile_ok_next;      // the next tile's block is valid (paged path)
+  uint8_t *const vbuf = &smem.vtile[0][0];
+  const uint32_t vbuf_lds = __builtin_amdgcn_readfirstlane(lds_address(vbuf));
+  // Loads of tile t0 whose tokens end at t_last: V by DMA into buffer `buf`,
+  // scales into sn, K into VGPRs.  Tokens past t_last address t_last (generic
+  // path) or stay inside the tile's block (paged path); they are masked later.
+  auto issue_v = [&](int t0, int t_last, int buf) {
+    const uint32_t dst = vbuf_lds + uint32_t(buf * kVBytes);
     if constexpr (kPaged) {
       bool ok;
-      const int64_t base = token_row(t0, ok);
-      nvalid_next = ok ? nv : 0;
+      const int64_t base = tile_row(t0, ok);
+      tile_ok_next = ok;
 #pragma unroll
-      for (int j = 0; j < kVPieces; ++j) {
-        const int piece = lane + 64 * j;
-        const int tok = piece / kRowPieces, col = piece % kRowPieces;
-        vn[j] = *reinterpret_cast<const u32x4_a4 *>(p.value_cache + base + tok * rec + 16 * col);
+      for (int j = 0; j < kVDma; ++j) {
+        const int s = lane + 64 * j, tok = s / kGranules, gl = s % kGranules;
+        const int col = gl ^ ((4 * (tok >> 2)) & (kGranules - 1));
+        dma16(p.value_cache + base + tok * rec + 16 * col, dst + 1024u * j);
       }
       sn = *reinterpret_cast<const float *>((lane < 32 ? p.key_cache : p.value_cache) + base +
                                             (lane & 31) * rec + kD);
     } else {
-      nvalid_next = nv;
-      const int last = t_end - 1;
+      tile_ok_next = true;
 #pragma unroll
-      for (int j = 0; j < kVPieces; ++j) {
-        const int piece = lane + 64 * j;
-        const int tok = piece / kRowPieces, col = piece % kRowPieces;
+      for (int j = 0; j < kVDma; ++j) {
+        const int s = lane + 64 * j, tok = s / kGranules, gl = s % kGranules;
+        const int col = gl ^ ((4 * (tok >> 2)) & (kGranules - 1));
         bool ok;
-        const int64_t off = token_row(min(t0 + tok, last), ok);
-        vn[j] = ok ? *reinterpret_cast<const u32x4_a4 *>(p.value_cache + off + 16 * col) : u32x4{0, 0, 0, 0};
+        const int64_t off = token_row(min(t0 + tok, t_last), ok);
+        dma16(p.value_cache + off + 16 * col, dst + 1024u * j);
       }
       bool ok;
-      const int64_t off = token_row(min(t0 + (lane & 31), last), ok);
+      const int64_t off = token_row(min(t0 + (lane & 31), t_last), ok);
       const float v = *reinterpret_cast<const float *>((lane < 32 ? p.key_cache : p.value_cache) + off + kD);
-      // An invalid block's tokens get a NaN marker here and are masked.
-      sn = ok ? v : __builtin_nanf("");
+      sn = ok ? v : 0.f;  // a zero scale masks the token
     }
   };
-  auto issue_k = [&](int t0) {
+  auto issue_k = [&](int t0, int t_last) {
     if constexpr (kPaged) {
       bool ok;
-      const int64_t base = token_row(t0, ok);
+      const int64_t base = tile_row(t0, ok);
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         const uint8_t *src = p.key_cache + base + (16 * s + n) * rec + kLaneK * g;
@@ -328,11 +387,10 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_attention_kernel(con
         for (int c = 0; c < kKChunks; ++c) kr[s][c] = *reinterpret_cast<const u32x4_a4 *>(src + 16 * c);
       }
     } else {
-      const int last = t_end - 1;
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
         bool ok;
-        const int64_t off = token_row(min(t0 + 16 * s + n, last), ok);
+        const int64_t off = token_row(min(t0 + 16 * s + n, t_last), ok);
         const uint8_t *src = p.key_cache + off + kLaneK * g;
 #pragma unroll
         for (int c = 0; c < kKChunks; ++c) kr[s][c] = *reinterpret_cast<const u32x4_a4 *>(src + 16 * c);
@@ -340,50 +398,49 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_attention_kernel(con
     }
   };
 
+  // Prologue, independent of the request length: the first tile, the
+  // query, the fp32 decode table.
+  const int len_raw = p.seq_lens[b];
+  issue_v(t_begin, t_cap - 1, 0);
+  issue_k(t_begin, t_cap - 1);
+  u32x4 qf[kQkSteps];
+  {
+    // Q^T operand: lane (g, n) holds dims [g*D/4, (g+1)*D/4) of query head n.
+    const uint16_t *q = static_cast<const uint16_t *>(p.query) + out_row + kLaneK * g;
+#pragma unroll
+    for (int i = 0; i < kQkSteps; ++i)
+      qf[i] = head_ok ? reinterpret_cast<const u32x4 *>(q)[i] : u32x4{0, 0, 0, 0};
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) smem.dec[lane + 64 * i] = __uint_as_float(kDeviceTables.decode_f32[lane + 64 * i]);
+  // The scales the tables currently hold (NaN: not built yet).
+  float k_tab_scale = __builtin_nanf(""), v_tab_scale = __builtin_nanf("");
+
+  const int len = clamp_len(len_raw, p.max_len);
+  if (t_begin >= len) {  // an empty split
+    wait_vmcnt<0>();     // no copy may still target LDS when the wave ends
+    if (split == 0) {    // an empty request: zero output
+      uint16_t *o = static_cast<uint16_t *>(p.out) + (size_t(b) * p.hq + h * p.group) * kD;
+      for (int i = lane; i < p.group * kD; i += kWave) o[i] = 0;
+    }
+    return;
+  }
+  const int t_end = min(t_cap, len);
+  const int n_splits_b = (len + p.split_tokens - 1) / p.split_tokens;
+  const int ntiles = (t_end - t_begin + kTile - 1) / kTile;
+
   f32x4_t oacc[kDBlocks][4];
 #pragma unroll
   for (int db = 0; db < kDBlocks; ++db)
 #pragma unroll
     for (int q = 0; q < 4; ++q) oacc[db][q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m = -__builtin_inff(), l = 0.f;
+  float *sc = smem.scl;
 
-  uint8_t *vt = vtile[wave];
-  float *sc = scl[wave];
-  issue_k(t_begin);
-  issue_v(t_begin);
-  // Scaled tables for the scales of the range's first token.  A tile whose
-  // rows all carry these scales (every tile of a cache written with static
-  // per-head scales) decodes K and V rounded exactly like the reference, with
-  // unit per-token factors; any other tile uses the plain tables and applies
-  // the row scales to the logits (K) and the softmax weights (V) in FP32.
-  const float k_lut_scale = __shfl(sn, 0, kWave), v_lut_scale = __shfl(sn, 32, kWave);
-  uint16_t *lks = lut_ks[wave], *lvs = lut_vs[wave];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int c = lane + 64 * i;
-    const float v = __uint_as_float(kDeviceTables.decode_f32[c]);
-    lks[c] = float_to_half_bits<kQBf16>(v * k_lut_scale);
-    lvs[c] = float_to_bf16_bits(v * v_lut_scale);
-  }
-  for (int it = 0; it < ntiles; ++it) {
-    const int t0 = t_begin + it * kTile;
-    const int nvalid = nvalid_next;
-    // Stage V and the scales; masked tokens get zero codes and a zero scale.
-#pragma unroll
-    for (int j = 0; j < kVPieces; ++j) {
-      const int piece = lane + 64 * j;
-      const int tok = piece / kRowPieces, col = piece % kRowPieces;
-      *reinterpret_cast<u32x4 *>(vt + tok * kVStride + 16 * col) = tok < nvalid ? vn[j] : u32x4{0, 0, 0, 0};
-    }
-    // In the generic path a NaN scale marks an invalid block (masked too).
-    const bool valid = (lane & 31) < nvalid && !__builtin_isnan(sn);
-    const bool scaled = __all(!valid || sn == (lane < 32 ? k_lut_scale : v_lut_scale));
-    sc[lane] = valid ? (scaled ? 1.f : sn) : 0.f;
-    const uint16_t *lk = scaled ? lks : lut_k;
-    const uint16_t *lv = scaled ? lvs : lut_v;
-    const bool more = it + 1 < ntiles;
-    if (more) issue_v(t0 + kTile);
-
+  // One tile.
+  auto tile = [&](const uint8_t *vt, int t0, bool more) {
+    const uint16_t *kl = smem.k_tab;
+    const uint16_t *vl = smem.v_tab;
     // S^T = K Q^T for the two 16-token blocks.
     f32x4_t sacc[2];
 #pragma unroll
@@ -392,12 +449,15 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_attention_kernel(con
 #pragma unroll
       for (int i = 0; i < kQkSteps; ++i) {
         const u32x4 w = kr[s][i >> 1];
-        const u32x4 a = (i & 1) ? decode8(lk, w[2], w[3]) : decode8(lk, w[0], w[1]);
+        const u32x4 a = (i & 1) ? decode8(kl, w[2], w[3]) : decode8(kl, w[0], w[1]);
         sacc[s] = mfma16<kQBf16>(a, qf[i], sacc[s]);
       }
     }
-
-    if (more) issue_k(t0 + kTile);  // in flight during softmax and P V
+    if (more) {  // the next tile is in flight during softmax and P V
+      const int tn = t0 + kTile;
+      issue_k(tn, t_end - 1);
+      issue_v(tn, t_end - 1, 1 - ((vt - vbuf) / kVBytes));
+    }
 
     // Online softmax over this tile (base 2).  Lane (g, n) holds tokens
     // 4g + e and 16 + 4g + e of query head n.
@@ -409,10 +469,8 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_attention_kernel(con
     float tmax = -__builtin_inff();
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const bool v0 = 4 * g + e < nvalid && ks0[e] != 0.f;
-      const bool v1 = 16 + 4 * g + e < nvalid && ks1[e] != 0.f;
-      x[e] = v0 ? sacc[0][e] * ks0[e] * p.scale_log2 : -__builtin_inff();
-      x[4 + e] = v1 ? sacc[1][e] * ks1[e] * p.scale_log2 : -__builtin_inff();
+      x[e] = ks0[e] != 0.f ? sacc[0][e] * ks0[e] * p.scale_log2 : -__builtin_inff();
+      x[4 + e] = ks1[e] != 0.f ? sacc[1][e] * ks1[e] * p.scale_log2 : -__builtin_inff();
       tmax = fmaxf(tmax, fmaxf(x[e], x[4 + e]));
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
@@ -427,13 +485,17 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_attention_kernel(con
       psum += pw[e];
     }
     l = l * alpha + psum;
+    // The output needs rescaling only when some head's running max moved
+    // from a finite value (before that the accumulators are zero).
+    if (!__all(m_new == m || m == -__builtin_inff())) {
+#pragma unroll
+      for (int db = 0; db < kDBlocks; ++db)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) oacc[db][q] *= alpha;
+    }
     m = m_new;
-#pragma unroll
-    for (int db = 0; db < kDBlocks; ++db)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) oacc[db][q] *= alpha;
-    const u32x4 pb{pack_bf16(pw[0] * vs0[0], pw[1] * vs0[1]), pack_bf16(pw[2] * vs0[2], pw[3] * vs0[3]),
-                   pack_bf16(pw[4] * vs1[0], pw[5] * vs1[1]), pack_bf16(pw[6] * vs1[2], pw[7] * vs1[3])};
+    const u32x4 pb{pack_half2<true>(pw[0] * vs0[0], pw[1] * vs0[1]), pack_half2<true>(pw[2] * vs0[2], pw[3] * vs0[3]),
+                   pack_half2<true>(pw[4] * vs1[0], pw[5] * vs1[1]), pack_half2<true>(pw[6] * vs1[2], pw[7] * vs1[3])};
 
     // O^T += V^T P'.
 #pragma unroll
@@ -442,13 +504,63 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_attention_kernel(con
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int tl = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
-        w[j] = *reinterpret_cast<const uint32_t *>(vt + tl * kVStride + 64 * db + 4 * n);
+        const int gran = (4 * db + (n >> 2)) ^ ((4 * (tl >> 2)) & (kGranules - 1));
+        w[j] = *reinterpret_cast<const uint32_t *>(vt + tl * kD + 16 * gran + 4 * (n & 3));
       }
 #pragma unroll
-      for (int q = 0; q < 4; ++q) oacc[db][q] = mfma16<true>(decode_column(lv, w, q), pb, oacc[db][q]);
+      for (int q = 0; q < 4; ++q) oacc[db][q] = mfma16<true>(decode_column(vl, w, q), pb, oacc[db][q]);
     }
-  }
+  };
 
+  // Tile k is issued during tile k - 1 (or in the prologue) and waited for
+  // at the top of iteration k.
+  for (int it = 0; it < ntiles; ++it) {
+    const int t0 = t_begin + it * kTile;
+    const int nvalid = min(kTile, t_end - t0);
+    const bool more = it + 1 < ntiles;
+    wait_vmcnt<0>();
+    const float s_cur = sn;
+    const uint8_t *vt = vbuf + (it & 1) * kVBytes;
+    // A block id outside the cache masks the whole tile.
+    const bool valid = tile_ok_next && (lane & 31) < nvalid && s_cur != 0.f;
+    // When the valid K rows (lanes 0-31) or V rows (lanes 32-63) of the tile
+    // share one scale (always, for a cache written with static per-head
+    // scales), that table holds dtype(dec(c) * scale) - the values the
+    // reference decodes K/V to (kv_cache.py:355-356) - and the rows get unit
+    // factors; otherwise it holds the exact dec(c) and the row scales multiply
+    // the logits (K) and softmax weights (V) in FP32.
+    const uint64_t vball = __ballot(valid);
+    const int k_first = __builtin_ffsll(vball & 0xFFFFFFFFull) - 1;
+    const int v_first = __builtin_ffsll(vball & 0xFFFFFFFF00000000ull) - 1;
+    const float k_one = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s_cur), max(k_first, 0)));
+    const float v_one = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s_cur), max(v_first, 32)));
+    const uint64_t same = __ballot(!valid || s_cur == (lane < 32 ? k_one : v_one));
+    const bool k_uniform = (same & 0xFFFFFFFFull) == 0xFFFFFFFFull;
+    const bool v_uniform = (same >> 32) == 0xFFFFFFFFull;
+    const float k_want = k_uniform ? k_one : 1.f, v_want = v_uniform ? v_one : 1.f;
+    if (!(k_want == k_tab_scale)) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        smem.k_tab[lane + 64 * i] = float_to_half_bits<kQBf16>(smem.dec[lane + 64 * i] * k_want);
+      k_tab_scale = k_want;
+    }
+    if (!(v_want == v_tab_scale)) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) smem.v_tab[lane + 64 * i] = float_to_bf16_bits(smem.dec[lane + 64 * i] * v_want);
+      v_tab_scale = v_want;
+    }
+    sc[lane] = valid ? ((lane < 32 ? k_uniform : v_uniform) ? 1.f : s_cur) : 0.f;
+    if (!__all(valid)) {
+      // Masked tokens: zero their V codes so that 0 * Inf / NaN cannot reach O.
+#pragma unroll
+      for (int j = 0; j < kVDma; ++j) {
+        const int s = lane + 64 * j, tok = s / kGranules;
+        if (!(tok < nvalid && sc[tok] != 0.f))
+          *reinterpret_cast<u32x4 *>(const_cast<uint8_t *>(vt) + 16 * s) = u32x4{0, 0, 0, 0};
+      }
+    }
+    tile(vt, t0, more);
+  }
   float lt = l + __shfl_xor(l, 16, kWave);
   lt += __shfl_xor(lt, 32, kWave);
   if (!head_ok) return;
@@ -463,8 +575,7 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_attention_kernel(con
         // Contiguous dim 2i (and 2i + 1) of this lane's 16 is element
         // (2i) / 4 of accumulator (2i) % 4.
         const int d0 = 2 * i, d1 = 2 * i + 1;
-        const float y0 = oacc[db][d0 & 3][d0 >> 2] * inv, y1 = oacc[db][d1 & 3][d1 >> 2] * inv;
-        packed[i] = uint32_t(float_to_half_bits<kQBf16>(y0)) | (uint32_t(float_to_half_bits<kQBf16>(y1)) << 16);
+        packed[i] = pack_half2<kQBf16>(oacc[db][d0 & 3][d0 >> 2] * inv, oacc[db][d1 & 3][d1 >> 2] * inv);
       }
       reinterpret_cast<u32x4 *>(o + 64 * db)[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
       reinterpret_cast<u32x4 *>(o + 64 * db)[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
@@ -488,44 +599,62 @@ __global__ __launch_bounds__(kThreads, 2) void paged_decode_attention_kernel(con
   }
 }
 
-// Merges the splits of each (request, query head):
+// Merges the splits of each (request, query head, 64-dim slice):
 //   M = max_s m_s, w_s = 2^(m_s - M), out = sum_s w_s O_s / sum_s w_s l_s.
+// Four groups of 64 threads take every fourth split; each thread one dim.
 template <bool kBf16>
 __global__ __launch_bounds__(kThreads) void attention_combine_kernel(const AttnParams p) {
   __shared__ float w[kMaxSplits];
-  __shared__ float red[kThreads / kWave];
+  __shared__ float red[kThreads];
   const int b = blockIdx.x / p.hq, head = blockIdx.x - b * p.hq;
   const int len = clamp_len(p.seq_lens[b], p.max_len);
   const int ns = (len + p.split_tokens - 1) / p.split_tokens;
   if (ns <= 1) return;  // written by the split kernel
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, grp = tid >> 6;
   const size_t base = size_t(b) * p.num_splits * p.hq + head;  // part index of split 0
+  const size_t stride = size_t(p.hq);                           // parts between splits
 
   float mx = -__builtin_inff();
-  for (int s = tid; s < ns; s += kThreads) mx = fmaxf(mx, p.part_ml[2 * (base + size_t(s) * p.hq)]);
+  for (int s = tid; s < ns; s += kThreads) mx = fmaxf(mx, p.part_ml[2 * (base + s * stride)]);
   mx = wave_max(mx);
-  if (lane == 0) red[wave] = mx;
+  if (lane == 0) red[grp] = mx;
   __syncthreads();
   mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
   __syncthreads();
   float lsum = 0.f;
   for (int s = tid; s < ns; s += kThreads) {
-    const float ms = p.part_ml[2 * (base + size_t(s) * p.hq)];
+    const float ms = p.part_ml[2 * (base + s * stride)];
     const float ws = ms == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
     w[s] = ws;
-    lsum += ws * p.part_ml[2 * (base + size_t(s) * p.hq) + 1];
+    lsum += ws * p.part_ml[2 * (base + s * stride) + 1];
   }
   lsum = wave_sum(lsum);
-  if (lane == 0) red[wave] = lsum;
+  if (lane == 0) red[grp] = lsum;
   __syncthreads();
   const float total = red[0] + red[1] + red[2] + red[3];
   const float inv = total > 0.f ? 1.f / total : 0.f;
-  uint16_t *o = static_cast<uint16_t *>(p.out) + (size_t(b) * p.hq + head) * p.dv;
-  for (int dim = tid; dim < p.dv; dim += kThreads) {
-    float acc = 0.f;
+  __syncthreads();
+  const int dim = int(blockIdx.y) * kWave + lane;
+  float acc = 0.f;
+  if (dim < p.dv) {
     const float *po = p.part_o + base * p.dv + dim;
-    for (int s = 0; s < ns; ++s) acc += w[s] * po[size_t(s) * p.hq * p.dv];
-    o[dim] = float_to_half_bits<kBf16>(acc * inv);
+    const size_t sstride = stride * p.dv;
+    int s = grp;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    for (; s + 12 < ns; s += 16) {
+      a0 += w[s] * po[s * sstride];
+      a1 += w[s + 4] * po[(s + 4) * sstride];
+      a2 += w[s + 8] * po[(s + 8) * sstride];
+      a3 += w[s + 12] * po[(s + 12) * sstride];
+    }
+    for (; s < ns; s += 4) a0 += w[s] * po[s * sstride];
+    acc = (a0 + a1) + (a2 + a3);
+  }
+  red[tid] = acc;
+  __syncthreads();
+  if (grp == 0 && dim < p.dv) {
+    const float y = (red[lane] + red[64 + lane]) + (red[128 + lane] + red[192 + lane]);
+    static_cast<uint16_t *>(p.out)[(size_t(b) * p.hq + head) * p.dv + dim] = float_to_half_bits<kBf16>(y * inv);
   }
 }
 
@@ -600,35 +729,55 @@ int env_int(const char *name, int fallback) {
   return x > 0 ? x : fallback;
 }
 
-// Splits a request's context so that about two workgroups per CU are in
-// flight over the batch (256 CUs), in whole 32-token tiles.
+// At most this many tiles per split: a split then spans at most 62 blocks of
+// the smallest block size the MFMA kernel takes (16), one block id per lane.
+constexpr int kMaxTilesPerSplit = 31;
+
+// Splits a request's context so that about 2048 wavefronts (eight per CU)
+// are launched over the batch and the KV heads, in whole 32-token tiles.
 SplitPlan plan_splits(int64_t batch, int64_t hkv, int64_t max_len) {
   const int64_t tiles = max_len > 0 ? (max_len + kTile - 1) / kTile : 1;
-  const int64_t head_groups = (hkv + kWaves - 1) / kWaves;
-  const int64_t wanted = 512 / (batch * head_groups);
-  const int64_t per_req = wanted < 1 ? 1 : wanted;
-  int64_t tiles_per_split = (tiles + per_req - 1) / per_req;
+  int64_t per_split = (batch * hkv * tiles + 2047) / 2048;
   static const int forced = env_int("HIF8_ATTN_SPLIT_TILES", 0);
-  if (forced > 0) tiles_per_split = forced;
-  if (tiles_per_split < 1) tiles_per_split = 1;
-  while ((tiles + tiles_per_split - 1) / tiles_per_split > kMaxSplits) tiles_per_split *= 2;
+  if (forced > 0) per_split = forced;
+  if (per_split > kMaxTilesPerSplit) per_split = kMaxTilesPerSplit;
+  if (per_split < 1) per_split = 1;
   SplitPlan plan;
-  plan.split_tokens = int(tiles_per_split * kTile);
-  plan.num_splits = int((tiles + tiles_per_split - 1) / tiles_per_split);
+  plan.split_tokens = int(per_split * kTile);
+  plan.num_splits = int((max_len + plan.split_tokens - 1) / plan.split_tokens);
+  if (plan.num_splits < 1) plan.num_splits = 1;
   return plan;
 }
 
-bool mfma_path(int64_t d, int64_t dv, int64_t group, int64_t block_size, const void *query, const void *out) {
-  return (d == 64 || d == 128 || d == 256) && dv == d && group <= 16 && aligned(query, 16) &&
-         aligned(out, 16) && block_size > 0;
+bool pow2(int64_t v) { return v > 0 && (v & (v - 1)) == 0; }
+
+int log2_of(int64_t v) {
+  int l = 0;
+  while ((int64_t(1) << l) < v) ++l;
+  return l;
+}
+
+// Shapes the MFMA kernel takes (the rest runs the one-wavefront-per-head kernel).
+bool mfma_shape(int64_t d, int64_t dv, int64_t group, int64_t block_size, int64_t max_len) {
+  return (d == 64 || d == 128 || d == 256) && dv == d && group <= 16 && pow2(block_size) && block_size >= 16 &&
+         max_len <= int64_t(kMaxSplits) * kMaxTilesPerSplit * kTile;
+}
+
+bool mfma_path(int64_t d, int64_t dv, int64_t group, int64_t block_size, int64_t max_len, const void *query,
+               const void *out) {
+  return mfma_shape(d, dv, group, block_size, max_len) && aligned(query, 16) && aligned(out, 16);
 }
 
 template <int kD, bool kQBf16, typename BtT>
 void launch_mfma(const AttnParams &p, int64_t batch, hipStream_t stream) {
-  const dim3 grid(unsigned(batch * p.num_splits), unsigned((p.hkv + kWaves - 1) / kWaves)), block(kThreads);
+  // Block id = ((request split group of 8) * Hkv + head) * 8 + position in the group.
+  const int64_t groups = (batch * p.num_splits + 7) / 8;
+  const dim3 grid(unsigned(groups * 8 * p.hkv)), block(kWave);
   if (p.block_size % kTile == 0) paged_decode_attention_kernel<kD, kQBf16, true, BtT><<<grid, block, 0, stream>>>(p);
   else paged_decode_attention_kernel<kD, kQBf16, false, BtT><<<grid, block, 0, stream>>>(p);
-  if (p.num_splits > 1) attention_combine_kernel<kQBf16><<<unsigned(batch * p.hq), kThreads, 0, stream>>>(p);
+  if (p.num_splits > 1)
+    attention_combine_kernel<kQBf16><<<dim3(unsigned(batch * p.hq), unsigned((p.dv + kWave - 1) / kWave)), kThreads, 0,
+                                       stream>>>(p);
 }
 
 template <bool kQBf16, typename BtT>
@@ -712,8 +861,8 @@ extern "C" size_t hif8_paged_decode_attention_workspace_size(int64_t batch, int6
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_size <= 0 || head_size_v <= 0 ||
       max_seq_len <= 0 || num_heads % num_kv_heads)
     return 0;
-  if (!((head_size == 64 || head_size == 128 || head_size == 256) && head_size_v == head_size &&
-        num_heads / num_kv_heads <= 16))
+  // Any power-of-two block size >= 16 qualifies; the workspace does not depend on it.
+  if (!mfma_shape(head_size, head_size_v, num_heads / num_kv_heads, 16, max_seq_len))
     return 0;  // the one-wavefront-per-head kernel needs no workspace
   const SplitPlan plan = plan_splits(batch, num_kv_heads, max_seq_len);
   if (plan.num_splits <= 1) return 0;
@@ -764,14 +913,16 @@ extern "C" int hif8_paged_decode_attention(const void *query, int q_dtype, const
   p.bt_stride = max_blocks_per_seq;
   p.num_blocks = num_blocks;
   p.block_size = int(block_size);
+  p.log2_block_size = log2_of(block_size);
   p.hkv = int(num_kv_heads);
   p.hq = int(num_heads);
   p.group = int(num_heads / num_kv_heads);
   p.d = int(head_size);
   p.dv = int(head_size_v);
   p.max_len = int(max_seq_len);
+  p.batch = int(batch);
   p.scale_log2 = scale * 1.4426950408889634f;
-  const bool mfma = mfma_path(head_size, head_size_v, p.group, block_size, query, out);
+  const bool mfma = mfma_path(head_size, head_size_v, p.group, block_size, max_seq_len, query, out);
   if (mfma) {
     const SplitPlan plan = plan_splits(batch, num_kv_heads, max_seq_len);
     p.split_tokens = plan.split_tokens;
