@@ -1,23 +1,40 @@
 // Prefill GEMM for gfx950: C[m, n] = sum_k dec(A[m,k]) dec(W[n,k]) * ts[m] * cs[n] (+ b[n]).
 //
-// Both operands are K-contiguous HiF8 bytes.  A block stages BM x 64 and
-// BN x 64 byte tiles: each thread loads 16-byte chunks from global memory into
-// VGPRs, decodes them with the 256-entry bf16 table in LDS and writes the bf16
-// tile into LDS (double buffered, 16-byte granules XOR-swizzled by row so the
-// MFMA fragment reads are bank-conflict free).  Four wavefronts in a 2 x 2
-// arrangement each own a (BM/2) x (BN/2) sub-tile and run
-// v_mfma_f32_16x16x32_bf16 with FP32 accumulation.  HiF8 values are exact in
-// bf16, so the product is exact up to FP32 summation order.  The next k-step's
-// global loads are in flight while the current step's MFMAs run.
-// The epilogue applies acc * ts[m] * cs[n] (+ bias) and rounds once.
+// Both operands are K-contiguous HiF8 bytes.  HiF8 values are exact in bf16,
+// so the operands are decoded to bf16 and multiplied on
+// v_mfma_f32_16x16x32_bf16 with FP32 accumulation: the product is exact up to
+// FP32 summation order.  The epilogue applies acc * ts[m] * cs[n] (+ bias) and
+// rounds once.
+//
+// A block computes a BM x BN tile in K steps of 64.  Each step's tiles sit in
+// LDS as bf16 (double buffered, 16-byte granules XOR-swizzled by row so that
+// the MFMA fragment reads are bank-conflict free):
+//   * W: each thread loads 16-byte code chunks into VGPRs one step ahead,
+//     decodes them with the 256-entry bf16 table in LDS and stores the bf16
+//     granules;
+//   * A, with a workspace: the activation codes are first decoded once to a
+//     bf16 matrix (decode_rows_kernel), and every step copies its A tile
+//     straight into LDS with global_load_lds_dwordx4 (no registers, no
+//     table lookups).  Without a workspace A is decoded like W.  Decoding A
+//     once instead of once per column tile halves the in-kernel table
+//     lookups, whose LDS latency bounds the decode phase of a step.
+// 256 x 256 blocks run eight wavefronts in a 2 x 4 arrangement (128 x 64
+// each, two waves per SIMD) whose two wave rows alternate between MFMA and
+// decode half a step apart; 128 x 128 blocks run four in a 2 x 2 arrangement.
+//
+// Shapes with too few output tiles to fill 256 CUs (prefill M=512, narrow N)
+// split K: block (tile, s) sums K steps [s*ksteps, (s+1)*ksteps) and stores
+// its FP32 tile to partial[s][M][N]; a second kernel adds the splits in fixed
+// order and applies the same epilogue, so results are deterministic.
 #include <stdlib.h>
+
+#include <algorithm>
 
 #include "linear.h"
 
 namespace hif8 {
 namespace {
 
-constexpr int kThreads = 256;
 constexpr int kBK = 64;  // bytes (= bf16 elements) of K per stage
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
@@ -28,6 +45,7 @@ __device__ __forceinline__ uint32_t granule_offset(int r, int g) {
   return uint32_t(r) * 128u + uint32_t((g ^ (r & 7)) * 16);
 }
 
+// 16 codes -> 16 bf16 (lo = codes 0..7, hi = codes 8..15) via the LDS table.
 __device__ __forceinline__ void decode16(const uint16_t *lut, const u32x4 q, u32x4 &lo, u32x4 &hi) {
   uint32_t p[8];
 #pragma unroll
@@ -40,21 +58,48 @@ __device__ __forceinline__ void decode16(const uint16_t *lut, const u32x4 q, u32
   hi = u32x4{p[4], p[5], p[6], p[7]};
 }
 
+// Activation codes [rows, K] -> bf16 [rows, K], 16 codes per thread and pass.
+__global__ __launch_bounds__(256) void decode_rows_kernel(const uint8_t *__restrict__ a,
+                                                          uint16_t *__restrict__ out, size_t chunks) {
+  __shared__ __attribute__((aligned(16))) uint16_t lut[256];
+  lut[threadIdx.x] = kDeviceTables.decode_bf16[threadIdx.x];
+  __syncthreads();
+  for (size_t c = size_t(blockIdx.x) * 256 + threadIdx.x; c < chunks; c += size_t(gridDim.x) * 256) {
+    u32x4 lo, hi;
+    decode16(lut, *reinterpret_cast<const u32x4 *>(a + c * 16), lo, hi);
+    u32x4 *o = reinterpret_cast<u32x4 *>(out + c * 16);
+    o[0] = lo;
+    o[1] = hi;
+  }
+}
+
 // Static LDS table at address 0 (the only static LDS object of the kernel):
 // a lookup address is then the code shifted left by one, a single SDWA op.
-template <int kBM, int kBN, int kWavesM, int kWavesN>
+//   kAPre      A is a bf16 matrix (decoded beforehand) copied into LDS by DMA
+//   kPingPong  the two wave rows alternate MFMA and decode half a step apart
+template <int kBM, int kBN, int kWavesM, int kWavesN, bool kAPre, bool kPingPong>
 __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
-    const uint8_t *__restrict__ A, const float *__restrict__ ts, const uint8_t *__restrict__ W,
+    const void *__restrict__ A, const float *__restrict__ ts, const uint8_t *__restrict__ W,
     const float *__restrict__ cs, const void *__restrict__ bias, int bias_dtype,
-    void *__restrict__ out, int out_dtype, int M, int N, int K) {
+    void *__restrict__ out, int out_dtype, int M, int N, int K, float *__restrict__ partial,
+    int splits, int ksteps) {
   constexpr int kT = kWave * kWavesM * kWavesN;         // threads per block
-  constexpr int kChunksA = kBM * (kBK / 16) / kT;        // 16-byte chunks per thread
-  constexpr int kChunksB = kBN * (kBK / 16) / kT;
-  constexpr int kRowsPass = kT / 4;                      // tile rows covered per chunk pass
+  constexpr int kWaves = kWavesM * kWavesN;
+  static_assert(!kPingPong || kWavesM == 2, "ping-pong pairs the two wave rows");
+  // Threads sharing one decode: all of them, or (ping-pong) one wave row,
+  // which decodes its half of the A rows and its half of the W rows.
+  constexpr int kDecT = kPingPong ? kT / 2 : kT;
+  constexpr int kDecA = kPingPong ? kBM / 2 : kBM, kDecB = kPingPong ? kBN / 2 : kBN;
+  constexpr int kChunksA = kAPre ? 0 : kDecA * (kBK / 16) / kDecT;  // 16-byte code chunks per thread
+  constexpr int kChunksB = kDecB * (kBK / 16) / kDecT;
+  constexpr int kRowsPass = kDecT / 4;                   // tile rows covered per chunk pass
   constexpr int kWM = kBM / kWavesM, kWN = kBN / kWavesN;  // wave sub-tile
   constexpr int kTM = kWM / 16, kTN = kWN / 16;          // 16x16 MFMA tiles per wave
   constexpr uint32_t kStageA = kBM * kBK * 2, kStageB = kBN * kBK * 2;
   constexpr int kGroupM = 4;                             // row tiles per L2 group
+  // A tile by DMA: 1 KiB (8 rows) per instruction, spread over the waves.
+  constexpr int kDmaPerWave = kBM * kBK * 2 / 1024 / kWaves;
+  static_assert(!kAPre || kDmaPerWave * kWaves * 1024 == int(kStageA), "A tile DMA split");
 
   __shared__ __attribute__((aligned(16))) uint16_t lut[256];
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -68,39 +113,71 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
   // range of tiles, walked in groups of kGroupM row tiles so that blocks
   // running together share A row panels and B column panels in that XCD's L2.
   const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
-  const int tiles = tiles_m * tiles_n;
-  const int per_xcd = (tiles + 7) / 8;
-  const int lin = (int(blockIdx.x) & 7) * per_xcd + (int(blockIdx.x) >> 3);
-  if (lin >= tiles) return;
+  // The K splits of a tile are adjacent work units, so they run on one XCD.
+  const int units = tiles_m * tiles_n * splits;
+  const int per_xcd = (units + 7) / 8;
+  const int unit = (int(blockIdx.x) & 7) * per_xcd + (int(blockIdx.x) >> 3);
+  if (unit >= units) return;
+  const int lin = unit / splits, split = unit - lin * splits;
   const int group = lin / (kGroupM * tiles_n);
   const int first_m = group * kGroupM;
   const int group_rows = min(tiles_m - first_m, kGroupM);
   const int in_group = lin - group * kGroupM * tiles_n;
   const int m0 = (first_m + in_group % group_rows) * kBM;
   const int n0 = (in_group / group_rows) * kBN;
+  const size_t k_first = size_t(split) * ksteps * kBK;
 
   const int wave = tid / kWave, lane = tid % kWave;
   const int wm = wave / kWavesN, wn = wave % kWavesN;
 
   // Global chunk coordinates: 4 threads per 64-byte tile row.
-  const int crow = tid >> 2, ccol = tid & 3;
-  const uint8_t *pa[kChunksA];
+  const int dt = tid % kDecT, crow = dt >> 2, ccol = dt & 3;
+  const int base_a = kPingPong ? wm * kDecA : 0, base_b = kPingPong ? wm * kDecB : 0;
+  const uint8_t *pa[kChunksA > 0 ? kChunksA : 1];
   const uint8_t *pb[kChunksB];
+  if constexpr (kChunksA > 0) {
 #pragma unroll
-  for (int i = 0; i < kChunksA; ++i) {
-    const int r = min(m0 + crow + kRowsPass * i, M - 1);
-    pa[i] = A + size_t(r) * K + ccol * 16;
+    for (int i = 0; i < kChunksA; ++i) {
+      const int r = min(m0 + base_a + crow + kRowsPass * i, M - 1);
+      pa[i] = static_cast<const uint8_t *>(A) + size_t(r) * K + k_first + ccol * 16;
+    }
   }
 #pragma unroll
   for (int i = 0; i < kChunksB; ++i) {
-    const int r = min(n0 + crow + kRowsPass * i, N - 1);
-    pb[i] = W + size_t(r) * K + ccol * 16;
+    const int r = min(n0 + base_b + crow + kRowsPass * i, N - 1);
+    pb[i] = W + size_t(r) * K + k_first + ccol * 16;
   }
 
-  u32x4 ra[kChunksA], rb[kChunksB];
-  auto load = [&](int kt) {
+  // DMA source of this lane for the A tile (bf16 rows of 128 bytes per step):
+  // instruction j of this wave fills LDS bytes [1024 q, 1024 q + 1024),
+  // q = wave * kDmaPerWave + j, i.e. tile rows 8q..8q+7; lane i lands at
+  // 1024 q + 16 i = row 8q + i/8, swizzled slot i%8, which holds granule
+  // (i%8) ^ (row & 7).
+  const uint8_t *pdma[kAPre ? kDmaPerWave : 1];
+  if constexpr (kAPre) {
 #pragma unroll
-    for (int i = 0; i < kChunksA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(pa[i] + kt * kBK);
+    for (int j = 0; j < kDmaPerWave; ++j) {
+      const int q = wave * kDmaPerWave + j;
+      const int r = 8 * q + (lane >> 3);
+      const int g = (lane & 7) ^ (r & 7);
+      pdma[j] = static_cast<const uint8_t *>(A) + (size_t(min(m0 + r, M - 1)) * K + k_first + g * 8) * 2;
+    }
+  }
+  auto dma_a = [&](int kt, int stage) {
+    if constexpr (kAPre) {
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_address(sa + stage * kStageA)) +
+                           uint32_t(wave * kDmaPerWave) * 1024u;
+#pragma unroll
+      for (int j = 0; j < kDmaPerWave; ++j) dma16(pdma[j] + size_t(kt) * kBK * 2, dst + 1024u * j);
+    }
+  };
+
+  u32x4 ra[kChunksA > 0 ? kChunksA : 1], rb[kChunksB];
+  auto load = [&](int kt) {
+    if constexpr (kChunksA > 0) {
+#pragma unroll
+      for (int i = 0; i < kChunksA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(pa[i] + kt * kBK);
+    }
 #pragma unroll
     for (int i = 0; i < kChunksB; ++i) rb[i] = *reinterpret_cast<const u32x4 *>(pb[i] + kt * kBK);
   };
@@ -112,10 +189,12 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
     *reinterpret_cast<u32x4 *>(d + granule_offset(r, 2 * ccol + 1)) = hi;
   };
   auto store = [&](int stage) {
+    if constexpr (kChunksA > 0) {
 #pragma unroll
-    for (int i = 0; i < kChunksA; ++i) put(sa + stage * kStageA, crow + kRowsPass * i, ra[i]);
+      for (int i = 0; i < kChunksA; ++i) put(sa + stage * kStageA, base_a + crow + kRowsPass * i, ra[i]);
+    }
 #pragma unroll
-    for (int i = 0; i < kChunksB; ++i) put(sb + stage * kStageB, crow + kRowsPass * i, rb[i]);
+    for (int i = 0; i < kChunksB; ++i) put(sb + stage * kStageB, base_b + crow + kRowsPass * i, rb[i]);
   };
 
   f32x4_t acc[kTM][kTN];
@@ -124,16 +203,8 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
 #pragma unroll
     for (int j = 0; j < kTN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  const int KT = K / kBK;
-  load(0);
-  __syncthreads();  // lut ready
-  store(0);
-  if (KT > 1) load(1);
-  __syncthreads();
-
   const int frow = lane & 15, fgrp = lane >> 4;
-  for (int kt = 0; kt < KT; ++kt) {
-    const int stage = kt & 1;
+  auto compute = [&](int stage) {
     const uint8_t *da = sa + stage * kStageA;
     const uint8_t *db = sb + stage * kStageB;
 #pragma unroll
@@ -155,16 +226,90 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
         for (int j = 0; j < kTN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[i], bfr[j], acc[i][j], 0, 0, 0);
     }
-    // The next tile (loaded during the previous step) goes to the other
-    // stage while this step's MFMAs drain; then the tile after it is loaded.
-    if (kt + 1 < KT) {
-      store(stage ^ 1);
-      if (kt + 2 < KT) load(kt + 2);
+  };
+
+  // Prologue: tile 0 in stage 0, tile 1's codes in registers.  With the DMA
+  // path the only loads in flight after the A copy are this thread's kChunksB
+  // code loads, so waiting for vmcnt <= kChunksB retires the copy.
+  const int KT = ksteps;
+  dma_a(0, 0);
+  load(0);
+  __syncthreads();  // table ready
+  store(0);
+  load(min(1, KT - 1));
+  if constexpr (kAPre) wait_vmcnt<kChunksB>();
+  __syncthreads();
+
+  if constexpr (kPingPong) {
+    // The two wave rows alternate between MFMA and decode half a step apart:
+    // while row 0 multiplies tile kt, row 1 decodes its half of tile kt+1;
+    // then row 1 multiplies tile kt while row 0 decodes its half.  Each SIMD
+    // holds one wave of each row, so the MFMA pipe is fed while the other
+    // wave decodes.  Tile kt+1 is complete (both halves) before either row
+    // multiplies it, and a stage is rewritten only after both rows read it.
+    // The A copy of tile kt+1 is issued by every wave at the top of step kt.
+    const bool second = wm == 1;
+    for (int kt = 0; kt < KT; ++kt) {
+      const int stage = kt & 1;
+      const bool more = kt + 1 < KT;
+      if (more) dma_a(kt + 1, stage ^ 1);
+      if (!second) {
+        __builtin_amdgcn_s_setprio(1);
+        compute(stage);
+        __builtin_amdgcn_s_setprio(0);
+      } else if (more) {
+        store(stage ^ 1);
+        load(min(kt + 2, KT - 1));
+      }
+      lds_barrier();
+      if (second) {
+        __builtin_amdgcn_s_setprio(1);
+        compute(stage);
+        __builtin_amdgcn_s_setprio(0);
+      } else if (more) {
+        store(stage ^ 1);
+        load(min(kt + 2, KT - 1));
+      }
+      if constexpr (kAPre) wait_vmcnt<kChunksB>();
+      lds_barrier();
     }
-    __syncthreads();
+  } else {
+    // All waves: start the A copy of the next tile, the MFMAs of this stage,
+    // then the decode of the W codes loaded during the previous step into
+    // the other stage and the loads of the tile after it (the last one is
+    // loaded again rather than branched around).  The barrier waits for LDS
+    // traffic only; the copy is retired by the vmcnt wait before it.
+    for (int kt = 0; kt + 1 < KT; ++kt) {
+      dma_a(kt + 1, (kt & 1) ^ 1);
+      compute(kt & 1);
+      store((kt & 1) ^ 1);
+      load(min(kt + 2, KT - 1));
+      if constexpr (kAPre) wait_vmcnt<kChunksB>();
+      lds_barrier();
+    }
+    compute((KT - 1) & 1);
   }
+  // No copy may still target LDS when the wave ends (the last load() above
+  // only re-reads the final tile into registers).
+  if constexpr (kAPre) wait_vmcnt<0>();
 
   // Epilogue: D[i][j] of a 16x16 tile lives in lane (i/4)*16 + j, element i%4.
+  if (partial) {
+    float *p = partial + size_t(split) * M * N;
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      const int col = n0 + wn * kWN + j * 16 + frow;
+      if (col >= N) continue;
+#pragma unroll
+      for (int i = 0; i < kTM; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = m0 + wm * kWM + i * 16 + fgrp * 4 + e;
+          if (row < M) p[size_t(row) * N + col] = acc[i][j][e];
+        }
+    }
+    return;
+  }
   uint16_t *o = static_cast<uint16_t *>(out);
   const bool obf = out_dtype == HIF8_DTYPE_BF16;
   float rs[kTM][4];
@@ -196,6 +341,37 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
   }
 }
 
+// Split-K epilogue: out = (sum over s of partial[s]) * ts[m] * cs[n] (+ b[n]),
+// four consecutive columns per thread (N % 4 == 0), splits added in order.
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(
+    const float *__restrict__ partial, int splits, const float *__restrict__ ts,
+    const float *__restrict__ cs, const void *__restrict__ bias, int bias_dtype,
+    void *__restrict__ out, int out_dtype, int M, int N) {
+  const size_t quads = size_t(M) * (N / 4);
+  const size_t plane = size_t(M) * N;
+  for (size_t q = size_t(blockIdx.x) * 256 + threadIdx.x; q < quads; q += size_t(gridDim.x) * 256) {
+    const size_t e0 = q * 4;
+    const int row = int(e0 / N), col = int(e0 - size_t(row) * N);
+    f32x4_t sum = *reinterpret_cast<const f32x4_t *>(partial + e0);
+    for (int s = 1; s < splits; ++s) sum += *reinterpret_cast<const f32x4_t *>(partial + s * plane + e0);
+    const float t = ts[row];
+    uint16_t h[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      float b = 0.f;
+      if (bias) {
+        const uint16_t hb = static_cast<const uint16_t *>(bias)[col + c];
+        b = bias_dtype == HIF8_DTYPE_BF16 ? half_bits_to_float<true>(hb) : half_bits_to_float<false>(hb);
+      }
+      const float y = sum[c] * t * cs[col + c] + b;
+      h[c] = out_dtype == HIF8_DTYPE_BF16 ? float_to_bf16_bits(y) : float_to_f16_bits(y);
+    }
+    uint16_t *o = static_cast<uint16_t *>(out) + e0;
+    *reinterpret_cast<uint2 *>(o) = make_uint2(uint32_t(h[0]) | (uint32_t(h[1]) << 16),
+                                               uint32_t(h[2]) | (uint32_t(h[3]) << 16));
+  }
+}
+
 // Any shape: one thread per output element.
 __global__ __launch_bounds__(256) void gemm_simple_kernel(
     const uint8_t *__restrict__ A, const float *__restrict__ ts, const uint8_t *__restrict__ W,
@@ -219,26 +395,90 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(
       out_dtype == HIF8_DTYPE_BF16 ? float_to_bf16_bits(y) : float_to_f16_bits(y);
 }
 
-template <int kBM, int kBN, int kWavesM, int kWavesN>
-int launch_tiled(const LinearArgs &a) {
+// Block shape, K split and workspace layout of a tiled launch.  256 x 256
+// blocks of 8 waves run at the highest rate per CU but need >= 128 tiles;
+// smaller grids use 128 x 128 blocks of 4 waves (two per CU).  When the tiles
+// still leave CUs idle, K is split in powers of two while every split keeps
+// >= 16 K steps, up to about one block per CU slot.  The workspace holds the
+// bf16 copy of A (M x K x 2 bytes, 256-byte aligned) and then the split
+// partials (splits x M x N x 4 bytes).
+struct GemmPlan {
+  int tile;          // 256 (8 waves) or 128 (4 waves)
+  int splits;        // K splits
+  size_t a_bytes;    // bf16 copy of A
+  size_t part_bytes; // FP32 partials (0 when unsplit)
+};
+
+int env_int(const char *name, int fallback) {
+  const char *v = getenv(name);
+  return v && *v ? atoi(v) : fallback;
+}
+
+GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
+  static const int tile_env = env_int("HIF8_GEMM_TILE", 0);
+  static const int split_env = env_int("HIF8_GEMM_SPLIT", 0);
+  GemmPlan p;
+  const int64_t tiles256 = ((m + 255) / 256) * ((n + 255) / 256);
+  p.tile = tile_env == 128 || tile_env == 256 ? tile_env : (m >= 256 && tiles256 >= 128 ? 256 : 128);
+  const int64_t tiles = ((m + p.tile - 1) / p.tile) * ((n + p.tile - 1) / p.tile);
+  const int64_t slots = p.tile == 256 ? 256 : 512;  // resident blocks on 256 CUs
+  const int64_t ksteps = k / kBK;
+  p.splits = 1;
+  if (n % 4 == 0 && k % kBK == 0) {
+    if (split_env > 0) {
+      while (p.splits * 2 <= split_env && ksteps % (p.splits * 2) == 0) p.splits *= 2;
+    } else {
+      while (tiles * p.splits * 2 <= slots && ksteps % (p.splits * 2) == 0 && ksteps / (p.splits * 2) >= 16)
+        p.splits *= 2;
+    }
+  }
+  p.a_bytes = (size_t(m) * size_t(k) * 2 + 255) / 256 * 256;
+  p.part_bytes = p.splits > 1 ? size_t(p.splits) * size_t(m) * size_t(n) * sizeof(float) : 0;
+  return p;
+}
+
+template <int kBM, int kBN, int kWavesM, int kWavesN, bool kAPre, bool kPingPong>
+int launch_tiled(const LinearArgs &a, const void *act, int splits, float *partial) {
   constexpr size_t kSmem = 2 * size_t(kBM + kBN) * kBK * 2;  // + 512 B of static LDS (the table)
   constexpr int kT = kWave * kWavesM * kWavesN;
   static bool configured = false;
   if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel<kBM, kBN, kWavesM, kWavesN>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kPingPong>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, int(kSmem)) != hipSuccess)
       return fail(HIF8_ERR_LAUNCH, "soft_hif8 GEMM: cannot reserve %zu bytes of LDS", kSmem);
     configured = true;
   }
   const int64_t tiles = ((a.n + kBN - 1) / kBN) * ((a.m + kBM - 1) / kBM);
-  const dim3 grid(unsigned((tiles + 7) / 8 * 8));
-  gemm_kernel<kBM, kBN, kWavesM, kWavesN><<<grid, kT, kSmem, a.stream>>>(
-      static_cast<const uint8_t *>(a.act), a.act_scale, a.weight, a.channel_scale, a.bias,
-      a.bias_dtype, a.out, a.out_dtype, int(a.m), int(a.n), int(a.k));
-  return check_launch("soft_hif8 GEMM");
+  const dim3 grid(unsigned((tiles * splits + 7) / 8 * 8));
+  gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kPingPong><<<grid, kT, kSmem, a.stream>>>(
+      act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.m),
+      int(a.n), int(a.k), partial, splits, int(a.k / kBK / splits));
+  int st = check_launch("soft_hif8 GEMM");
+  if (st || !partial) return st;
+  const size_t quads = size_t(a.m) * size_t(a.n / 4);
+  const unsigned blocks = unsigned(std::min<size_t>((quads + 255) / 256, 4096));
+  splitk_reduce_kernel<<<blocks, 256, 0, a.stream>>>(partial, splits, a.act_scale, a.channel_scale, a.bias,
+                                                   a.bias_dtype, a.out, a.out_dtype, int(a.m), int(a.n));
+  return check_launch("soft_hif8 GEMM (split-K reduce)");
+}
+
+template <bool kAPre>
+int launch_plan(const LinearArgs &a, const GemmPlan &p, const void *act, int splits, float *partial) {
+  static const int pingpong = env_int("HIF8_GEMM_PINGPONG", 1);
+  if (p.tile == 256)
+    return pingpong ? launch_tiled<256, 256, 2, 4, kAPre, true>(a, act, splits, partial)
+                    : launch_tiled<256, 256, 2, 4, kAPre, false>(a, act, splits, partial);
+  return launch_tiled<128, 128, 2, 2, kAPre, false>(a, act, splits, partial);
 }
 
 }  // namespace
+
+size_t gemm_workspace_size(int64_t m, int64_t n, int64_t k) {
+  if (m <= 4 || m > 0x7FFFFFFFll || n > 0x7FFFFFFFll || k > 0x7FFFFFFFll || n <= 0 || k <= 0 || k % kBK)
+    return 0;
+  const GemmPlan p = plan_gemm(m, n, k);
+  return p.a_bytes + p.part_bytes;
+}
 
 int launch_gemm(const LinearArgs &a) {
   if (a.act_kind != kActCodes)
@@ -251,13 +491,18 @@ int launch_gemm(const LinearArgs &a) {
         a.bias_dtype, a.out, a.out_dtype, int(a.m), int(a.n), int(a.k));
     return check_launch("soft_hif8 GEMM (generic)");
   }
-  const int64_t tiles256 = ((a.m + 255) / 256) * ((a.n + 255) / 256);
-  static const int variant = getenv("HIF8_GEMM_WAVES") ? atoi(getenv("HIF8_GEMM_WAVES")) : 8;
-  if (a.m >= 256 && tiles256 >= 128) {
-    if (variant == 4) return launch_tiled<256, 256, 2, 2>(a);
-    return launch_tiled<256, 256, 2, 4>(a);
-  }
-  return launch_tiled<128, 128, 2, 2>(a);
+  const GemmPlan p = plan_gemm(a.m, a.n, a.k);
+  const bool use_ws = a.workspace && a.workspace_bytes >= p.a_bytes + p.part_bytes && aligned(a.workspace, 256);
+  if (!use_ws) return launch_plan<false>(a, p, a.act, 1, nullptr);
+  uint8_t *ws = static_cast<uint8_t *>(a.workspace);
+  uint16_t *abf = reinterpret_cast<uint16_t *>(ws);
+  const size_t chunks = size_t(a.m) * size_t(a.k) / 16;
+  const unsigned blocks = unsigned(std::min<size_t>((chunks + 255) / 256, 2048));
+  decode_rows_kernel<<<blocks, 256, 0, a.stream>>>(static_cast<const uint8_t *>(a.act), abf, chunks);
+  int st = check_launch("soft_hif8 GEMM (activation decode)");
+  if (st) return st;
+  float *partial = p.part_bytes ? reinterpret_cast<float *>(ws + p.a_bytes) : nullptr;
+  return launch_plan<true>(a, p, abf, p.part_bytes ? p.splits : 1, partial);
 }
 
 }  // namespace hif8

@@ -74,6 +74,43 @@ __device__ __forceinline__ void lds_barrier() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// 32-bit LDS address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_address(const void *p) {
+  return uint32_t(uintptr_t((const lds_void_t *)p));
+}
+
+// Asynchronous copy of 16 bytes per lane from global memory into LDS
+// (global_load_lds_dwordx4): lane i's bytes land at lds_base + 16 * i, the
+// LDS address being taken from M0 when the instruction issues.  Written as
+// inline assembly so that the compiler neither waits on it nor counts it:
+// every consumer of the copied data waits for it explicitly (wait_vmcnt).
+// M0 is saved and restored around the copy; one wait state separates the M0
+// write from the load.
+__device__ __forceinline__ void dma16(const void *src, uint32_t lds_base) {
+  const uint32_t base = __builtin_amdgcn_readfirstlane(lds_base);  // wave-uniform: an SGPR
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(src), "s"(base)
+      : "memory");
+}
+
+// s_waitcnt with vmcnt(n) only (lgkmcnt / expcnt left at their maxima).
+template <int kN>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(kN >= 0 && kN < 64, "vmcnt range");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt((kN & 0xF) | (0x7 << 4) | (0xF << 8) | ((kN >> 4) << 14));
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Sum over the 64 lanes of a wavefront; every lane receives the total.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

@@ -209,42 +209,6 @@ __device__ __forceinline__ f32x4_t mfma16(u32x4 a, u32x4 b, f32x4_t c) {
 }
 
 
-typedef __attribute__((address_space(3))) void lds_void_t;
-
-// 32-bit LDS address of a pointer into __shared__ memory.
-__device__ __forceinline__ uint32_t lds_address(const void *p) {
-  return uint32_t(uintptr_t((const lds_void_t *)p));
-}
-
-// Asynchronous copy of 16 bytes per lane from global memory into LDS
-// (global_load_lds_dwordx4): lane i's bytes land at lds_base + 16 * i, the
-// LDS address being taken from M0 when the instruction issues.  Written as
-// inline assembly so that the compiler neither waits on it nor counts it:
-// every consumer of the copied data waits for it explicitly (wait_vmcnt).
-// M0 is saved and restored around the copy; one wait state separates the M0
-// write from the load.
-__device__ __forceinline__ void dma16(const void *src, uint32_t lds_base) {
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(src), "s"(lds_base)
-      : "memory");
-}
-
-// s_waitcnt with vmcnt(n) only (lgkmcnt / expcnt left at their maxima).
-template <int kN>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(kN >= 0 && kN < 64, "vmcnt range");
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt((kN & 0xF) | (0x7 << 4) | (0xF << 8) | ((kN >> 4) << 14));
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
 // MFMA mapping (v_mfma_f32_16x16x32: A row = lane % 16, B column = lane % 16,
 // k-slots 8 * (lane / 16) + j; D[i][j] in lane (i / 4) * 16 + j, element i % 4):
 //   S^T = K Q^T : A row = token of a 16-token block; lane group g holds dims

@@ -23,11 +23,16 @@ struct LinearArgs {
   int out_dtype;          // HIF8_DTYPE_FP16 / HIF8_DTYPE_BF16
   int64_t m, n, k;
   hipStream_t stream;
+  void *workspace = nullptr;    // split-K partials (GEMM only), may be null
+  size_t workspace_bytes = 0;
 };
 
 // HBM-streaming GEMV for m <= 4 (gemv.hip).  Returns a status.
 int launch_gemv(const LinearArgs &a);
-// bf16-MFMA GEMM for any m (gemm.hip).  Returns a status.
+// bf16-MFMA GEMM for any m (gemm.hip).  Returns a status.  With a workspace of
+// gemm_workspace_size(m, n, k) bytes, shapes with too few output tiles to fill
+// the chip split K over several blocks; without one they run unsplit.
 int launch_gemm(const LinearArgs &a);
+size_t gemm_workspace_size(int64_t m, int64_t n, int64_t k);
 
 }  // namespace hif8

@@ -61,17 +61,39 @@ extern "C" int soft_hif8_gemv(const uint8_t *activation, const uint8_t *weight,
                                 out, out_dtype, m, n, k, stream));
 }
 
-extern "C" int soft_hif8_gemm(const uint8_t *activation, const uint8_t *weight,
-                              const float *token_scale, const float *channel_scale,
-                              const void *bias, int bias_dtype, void *out, int out_dtype,
-                              int64_t m, int64_t n, int64_t k, hif8_stream_t stream) {
+extern "C" size_t soft_hif8_gemm_workspace_size(int64_t m, int64_t n, int64_t k) {
+  return gemm_workspace_size(m, n, k);
+}
+
+extern "C" int soft_hif8_gemm_with_workspace(const uint8_t *activation, const uint8_t *weight,
+                                             const float *token_scale, const float *channel_scale,
+                                             const void *bias, int bias_dtype, void *out,
+                                             int out_dtype, int64_t m, int64_t n, int64_t k,
+                                             void *workspace, size_t workspace_bytes,
+                                             hif8_stream_t stream) {
   clear_error();
   int st = validate("soft_hif8_gemm", activation, weight, token_scale, channel_scale, bias,
                     bias_dtype, out, out_dtype, m, n, k);
   if (st) return st;
-  const LinearArgs a = codes_args(activation, weight, token_scale, channel_scale, bias, bias_dtype,
-                                  out, out_dtype, m, n, k, stream);
+  const size_t need = gemm_workspace_size(m, n, k);
+  if (workspace && workspace_bytes < need)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "soft_hif8_gemm: workspace of %zu bytes, %zu required",
+                workspace_bytes, need);
+  if (workspace && !aligned(workspace, 256))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "soft_hif8_gemm: workspace must be 256-byte aligned");
+  LinearArgs a = codes_args(activation, weight, token_scale, channel_scale, bias, bias_dtype, out,
+                            out_dtype, m, n, k, stream);
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
   return m <= 4 ? launch_gemv(a) : launch_gemm(a);
+}
+
+extern "C" int soft_hif8_gemm(const uint8_t *activation, const uint8_t *weight,
+                              const float *token_scale, const float *channel_scale,
+                              const void *bias, int bias_dtype, void *out, int out_dtype,
+                              int64_t m, int64_t n, int64_t k, hif8_stream_t stream) {
+  return soft_hif8_gemm_with_workspace(activation, weight, token_scale, channel_scale, bias,
+                                       bias_dtype, out, out_dtype, m, n, k, nullptr, 0, stream);
 }
 
 extern "C" int soft_hif8_static_fused_gemm(const void *x, int x_dtype, const uint8_t *weight,

@@ -168,8 +168,23 @@ at::Tensor SoftHif8Gemv(const at::Tensor &activation, const at::Tensor &weight, 
 at::Tensor SoftHif8Gemm(const at::Tensor &activation, const at::Tensor &weight, const at::Tensor &token_scale,
                         const at::Tensor &channel_scale, const c10::optional<at::Tensor> &bias,
                         at::ScalarType output_dtype) {
-  return SoftLinear(activation, weight, token_scale, channel_scale, bias, output_dtype, false, "soft_hif8_gemm",
-                    &soft_hif8_gemm);
+  ValidateSoftLinear(activation, weight, token_scale, channel_scale, bias, output_dtype, false);
+  const c10::OptionalDeviceGuard guard(activation.device());
+  const int64_t m = activation.size(0), n = weight.size(0), k = activation.size(1);
+  auto out = at::empty({m, n}, activation.options().dtype(output_dtype));
+  // Split-K workspace from the stream-ordered caching allocator, as the
+  // reference takes its ACLNN workspace (hif8_native.cpp:202-226).
+  const size_t ws_bytes = soft_hif8_gemm_workspace_size(m, n, k);
+  at::Tensor ws;
+  if (ws_bytes) ws = at::empty({int64_t(ws_bytes)}, activation.options().dtype(at::ScalarType::Byte));
+  const void *bias_ptr = bias.has_value() ? bias->data_ptr() : nullptr;
+  const int bias_dtype = bias.has_value() ? DtypeCode(bias->scalar_type()) : HIF8_DTYPE_NONE;
+  CheckStatus(soft_hif8_gemm_with_workspace(
+                  activation.data_ptr<uint8_t>(), weight.data_ptr<uint8_t>(), token_scale.data_ptr<float>(),
+                  channel_scale.data_ptr<float>(), bias_ptr, bias_dtype, out.data_ptr(), DtypeCode(output_dtype),
+                  m, n, k, ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, CurrentStream(activation.device())),
+              "soft_hif8_gemm");
+  return out;
 }
 
 at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tensor &weight,

@@ -111,6 +111,29 @@ int soft_hif8_gemm(const uint8_t *activation, const uint8_t *weight, const float
                    int out_dtype, int64_t m, int64_t n, int64_t k, hif8_stream_t stream);
 
 /*
+ * Bytes of workspace soft_hif8_gemm_with_workspace uses for these sizes (0: none).
+ * First phase of the reference's two-phase call, aclnnSoftHif8GemmGetWorkspaceSize
+ * (csrc/extension/hif8_native.cpp:386-425).
+ */
+size_t soft_hif8_gemm_workspace_size(int64_t m, int64_t n, int64_t k);
+
+/*
+ * soft_hif8_gemm with a caller-owned workspace: the second phase,
+ * aclnnSoftHif8Gemm(workspace, size, executor, stream) (hif8_native.cpp:228-239,386-425).
+ * With workspace_bytes >= soft_hif8_gemm_workspace_size(m, n, k) (256-byte aligned)
+ * the activation codes are decoded once into the workspace (bf16) instead of once
+ * per output column tile, and shapes with too few output tiles to fill the GPU
+ * split K into FP32 partials added in a fixed order (deterministic).  With NULL
+ * the call equals soft_hif8_gemm (same results up to FP32 summation order).  A
+ * non-NULL workspace that is too small or misaligned is an error.
+ */
+int soft_hif8_gemm_with_workspace(const uint8_t *activation, const uint8_t *weight,
+                                  const float *token_scale, const float *channel_scale,
+                                  const void *bias, int bias_dtype, void *out, int out_dtype,
+                                  int64_t m, int64_t n, int64_t k, void *workspace,
+                                  size_t workspace_bytes, hif8_stream_t stream);
+
+/*
  * Fixed-scale fused quant + GEMM for M <= 4.
  * Replaces aclnnSoftHif8StaticFusedGemm as called by SoftHif8StaticFusedGemm
  * (csrc/extension/hif8_native.cpp:784-910; kernel csrc/opp/op_kernel/soft_hif8_fused_gemm.cpp

@@ -73,3 +73,28 @@ def test_linear_entry_points_enforce_reference_contracts(lib):
     fused.argtypes = [ctypes.c_void_p, ctypes.c_int] + [ctypes.c_void_p] * 4 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int] + [ctypes.c_int64] * 3 + [ctypes.c_void_p]
     assert fused(_p(), 1, _p(), _p(), _p(), None, -1, _p(), 1, 5, 8, 4, None) == 1
     assert b"M <= 4" in lib.hif8_last_error()
+
+
+def test_gemm_workspace_query_follows_the_split_plan(lib):
+    size = lib.soft_hif8_gemm_workspace_size
+    size.argtypes = [ctypes.c_int64] * 3
+    size.restype = ctypes.c_size_t
+    # The workspace is the bf16 copy of A (M*K*2 bytes, rounded to 256) plus split partials.
+    # Enough 256 x 256 tiles to fill the GPU: no split.  GEMV-sized M: no workspace.
+    assert size(4096, 24576, 4096) == 4096 * 4096 * 2
+    assert size(4, 4096, 4096) == 0
+    # Prefill M=512 over a 4096 x 4096 projection: 128 tiles of 128 x 128, K split in 4.
+    assert size(512, 4096, 4096) == 512 * 4096 * 2 + 4 * 512 * 4096 * 4
+    # Splits keep >= 16 K steps of 64 and need N % 4 == 0; K must be a multiple of 64.
+    assert size(512, 4096, 1024) == 512 * 1024 * 2
+    assert size(512, 4096, 2048) == 512 * 2048 * 2 + 2 * 512 * 4096 * 4
+    assert size(512, 4094, 4096) == 512 * 4096 * 2
+    assert size(300, 16, 100) == 0
+    assert size(0, 16, 16) == 0
+    ws = lib.soft_hif8_gemm_with_workspace
+    ws.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int] + \
+        [ctypes.c_int64] * 3 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    assert ws(_p(), _p(), _p(), _p(), None, -1, _p(), 1, 512, 4096, 4096, _p(256), 1024, None) == 1
+    assert b"workspace" in lib.hif8_last_error()
+    assert ws(_p(), _p(), _p(), _p(), None, -1, _p(), 1, 512, 4096, 4096, _p(16), 1 << 30, None) == 1
+    assert b"aligned" in lib.hif8_last_error()
