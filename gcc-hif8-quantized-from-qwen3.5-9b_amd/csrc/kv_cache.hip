@@ -13,9 +13,10 @@
 // encoder as hif8_static_quant, so the bytes equal quant -> pack -> scatter.
 //
 // Decode attention (kv_runtime.py:1470-1563 semantics, oracle kv_cache.py:314-372):
-// one query token per request, GQA group G = Hq / Hkv.  A workgroup owns one
-// request's token range (a "split") and four KV heads, one wavefront each; a
-// wavefront walks its range in 32-token tiles:
+// one query token per request, GQA group G = Hq / Hkv.  A workgroup is one
+// wavefront and owns one (request, token range = "split", KV head); the block
+// ids of the KV heads of one split are adjacent modulo 8, so they run on one
+// XCD and share its L2.  The wavefront walks its range in 32-token tiles:
 //   * K rows go from HBM straight into VGPRs in the MFMA A-operand layout
 //     (token = lane % 16, 64 contiguous bytes per lane) and S^T = K Q^T runs
 //     on v_mfma_f32_16x16x32 (B = the G query heads of the KV head, padded to
@@ -23,10 +24,14 @@
 //   * V rows are copied raw into LDS by DMA (global_load_lds_dwordx4) and read
 //     transposed (8 tokens x 4 dims per lane), and O^T += V^T P' runs on the
 //     same MFMA with the softmax weights P' rounded to bf16;
-//   * both operands are decoded as dtype(dec(c) * row scale) - a lookup in an
-//     fp32 table in LDS, one multiply by the row's scale, one round to
-//     nearest even - which is how the reference decodes K and V before its
-//     attention (decode_kv_rows(...).to(query dtype), kv_cache.py:355-356);
+//   * both operands are decoded through per-wave LDS tables that hold
+//     dtype(dec(c) * s) for the tile's row scale s - which is how the
+//     reference decodes K and V before its attention
+//     (decode_kv_rows(...).to(query dtype), kv_cache.py:355-356); static
+//     caches give every row of a head the same scale, so a table is rebuilt
+//     only when the scale changes.  A tile whose rows mix scales uses the
+//     exact decode (s = 1) and applies the FP32 row scales to the scores and
+//     the softmax weights instead (equal up to rounding);
 //   * the online softmax keeps (max, sum) per query head in FP32;
 //   * the next tile's loads are in flight while the current tile computes.
 // HiF8 values are exact in bf16 and fp16, so decode adds no rounding.  With
