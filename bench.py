@@ -321,6 +321,36 @@ def per_kernel_table(st: Setup, launches: int = 20) -> dict:
     return table
 
 
+def measured_ceilings(torch, device) -> dict:
+    """Context for the rooflines: a plain device copy (HBM read + write) and
+    torch's bf16 matmul (hipBLASLt) on the prefill shapes with bf16 operands,
+    i.e. the same GEMMs without any HiF8 decode."""
+    src = torch.empty(512 * 2 ** 20, dtype=torch.uint8, device=device)
+    dst = torch.empty_like(src)
+
+    def cp():
+        for _ in range(5):
+            dst.copy_(src)
+    ms = time_graphs(torch, [capture(torch, cp)], 3) / 5
+    copy_gbs = 2 * src.numel() / (ms * 1e-3) / 1e9
+    del src, dst
+    gemm = {}
+    for m in PREFILL_M:
+        for name, n, k in LAYER:
+            a = torch.randn(m, k, device=device).to(torch.bfloat16)
+            w = torch.randn(n, k, device=device).to(torch.bfloat16)
+
+            def mm(a=a, w=w):
+                for _ in range(3):
+                    torch.matmul(a, w.t())
+            ms = time_graphs(torch, [capture(torch, mm)], 5) / 3
+            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            gemm[f"{name}_m{m}"] = {"us": round(ms * 1e3, 2), "TFLOPs": round(tf, 1),
+                                    "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 4)}
+    return {"hbm_copy_GBps": round(copy_gbs, 1), "hbm_copy_frac": round(copy_gbs / HBM_PEAK_GBS, 4),
+            "hipblaslt_bf16_gemm": gemm}
+
+
 def cpu_baseline(budget_s: float = 20.0) -> dict:
     """The numpy oracle's decode-GEMV sweep on the host (single-threaded numpy gather + BLAS)."""
     import numpy as np
@@ -465,6 +495,9 @@ def main() -> None:
                               "us_per_launch": gdom["us"]}
     all_gemv_gbs = sum(v["bytes"] for v in gemv) / (sum(v["us"] for v in gemv) * 1e-6) / 1e9
 
+    log("ceilings (plain copy, hipBLASLt bf16 GEMM) ...")
+    ceilings = measured_ceilings(torch, device)
+
     log("KV page pool ...")
     kvs = KVSetup(torch, device)
     kv_attn = kv_attention_bench(kvs, args.steps)
@@ -519,6 +552,7 @@ def main() -> None:
         "decode_sweep_fused_GBps": round(fused_gbs, 1),
         "gemv_all_launches_GBps": round(all_gemv_gbs, 1),
         "gemm_per_layer": gemm_layer,
+        "ceilings": ceilings,
         "kernels": table,
     }
     print(json.dumps(out), flush=True)

@@ -17,7 +17,10 @@
 //     straight into LDS with global_load_lds_dwordx4 (no registers, no
 //     table lookups).  Without a workspace A is decoded like W.  Decoding A
 //     once instead of once per column tile halves the in-kernel table
-//     lookups, whose LDS latency bounds the decode phase of a step.
+//     lookups, whose LDS latency bounds the decode phase of a step;
+//   * W, with a workspace and M >= 2048: decoded once per call the same way
+//     (the in-kernel decode would repeat it for every 256-row tile of M) and
+//     copied by DMA like A, so the K loop is MFMA, fragment reads and copies.
 // 256 x 256 blocks run eight wavefronts in a 2 x 4 arrangement (128 x 64
 // each, two waves per SIMD) whose two wave rows alternate between MFMA and
 // decode half a step apart; 128 x 128 blocks run four in a 2 x 2 arrangement.
@@ -77,29 +80,32 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(const uint8_t *__restr
 // a lookup address is then the code shifted left by one, a single SDWA op.
 //   kAPre      A is a bf16 matrix (decoded beforehand) copied into LDS by DMA
 //   kPingPong  the two wave rows alternate MFMA and decode half a step apart
-template <int kBM, int kBN, int kWavesM, int kWavesN, bool kAPre, bool kPingPong>
+template <int kBM, int kBN, int kWavesM, int kWavesN, bool kAPre, bool kBPre, bool kPingPong>
 __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
-    const void *__restrict__ A, const float *__restrict__ ts, const uint8_t *__restrict__ W,
+    const void *__restrict__ A, const float *__restrict__ ts, const void *__restrict__ W,
     const float *__restrict__ cs, const void *__restrict__ bias, int bias_dtype,
     void *__restrict__ out, int out_dtype, int M, int N, int K, float *__restrict__ partial,
     int splits, int ksteps) {
   constexpr int kT = kWave * kWavesM * kWavesN;         // threads per block
   constexpr int kWaves = kWavesM * kWavesN;
   static_assert(!kPingPong || kWavesM == 2, "ping-pong pairs the two wave rows");
+  static_assert(!kBPre || (kAPre && !kPingPong), "W by DMA needs A by DMA and no decode phase");
   // Threads sharing one decode: all of them, or (ping-pong) one wave row,
   // which decodes its half of the A rows and its half of the W rows.
   constexpr int kDecT = kPingPong ? kT / 2 : kT;
   constexpr int kDecA = kPingPong ? kBM / 2 : kBM, kDecB = kPingPong ? kBN / 2 : kBN;
   constexpr int kChunksA = kAPre ? 0 : kDecA * (kBK / 16) / kDecT;  // 16-byte code chunks per thread
-  constexpr int kChunksB = kDecB * (kBK / 16) / kDecT;
+  constexpr int kChunksB = kBPre ? 0 : kDecB * (kBK / 16) / kDecT;
   constexpr int kRowsPass = kDecT / 4;                   // tile rows covered per chunk pass
   constexpr int kWM = kBM / kWavesM, kWN = kBN / kWavesN;  // wave sub-tile
   constexpr int kTM = kWM / 16, kTN = kWN / 16;          // 16x16 MFMA tiles per wave
   constexpr uint32_t kStageA = kBM * kBK * 2, kStageB = kBN * kBK * 2;
   constexpr int kGroupM = 4;                             // row tiles per L2 group
-  // A tile by DMA: 1 KiB (8 rows) per instruction, spread over the waves.
+  // Tiles by DMA: 1 KiB (8 rows) per instruction, spread over the waves.
   constexpr int kDmaPerWave = kBM * kBK * 2 / 1024 / kWaves;
+  constexpr int kDmaPerWaveB = kBN * kBK * 2 / 1024 / kWaves;
   static_assert(!kAPre || kDmaPerWave * kWaves * 1024 == int(kStageA), "A tile DMA split");
+  static_assert(!kBPre || kDmaPerWaveB * kWaves * 1024 == int(kStageB), "W tile DMA split");
 
   __shared__ __attribute__((aligned(16))) uint16_t lut[256];
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -134,7 +140,7 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
   const int dt = tid % kDecT, crow = dt >> 2, ccol = dt & 3;
   const int base_a = kPingPong ? wm * kDecA : 0, base_b = kPingPong ? wm * kDecB : 0;
   const uint8_t *pa[kChunksA > 0 ? kChunksA : 1];
-  const uint8_t *pb[kChunksB];
+  const uint8_t *pb[kChunksB > 0 ? kChunksB : 1];
   if constexpr (kChunksA > 0) {
 #pragma unroll
     for (int i = 0; i < kChunksA; ++i) {
@@ -142,10 +148,12 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
       pa[i] = static_cast<const uint8_t *>(A) + size_t(r) * K + k_first + ccol * 16;
     }
   }
+  if constexpr (kChunksB > 0) {
 #pragma unroll
-  for (int i = 0; i < kChunksB; ++i) {
-    const int r = min(n0 + base_b + crow + kRowsPass * i, N - 1);
-    pb[i] = W + size_t(r) * K + k_first + ccol * 16;
+    for (int i = 0; i < kChunksB; ++i) {
+      const int r = min(n0 + base_b + crow + kRowsPass * i, N - 1);
+      pb[i] = static_cast<const uint8_t *>(W) + size_t(r) * K + k_first + ccol * 16;
+    }
   }
 
   // DMA source of this lane for the A tile (bf16 rows of 128 bytes per step):
@@ -163,6 +171,16 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
       pdma[j] = static_cast<const uint8_t *>(A) + (size_t(min(m0 + r, M - 1)) * K + k_first + g * 8) * 2;
     }
   }
+  const uint8_t *pdmb[kBPre ? kDmaPerWaveB : 1];
+  if constexpr (kBPre) {
+#pragma unroll
+    for (int j = 0; j < kDmaPerWaveB; ++j) {
+      const int q = wave * kDmaPerWaveB + j;
+      const int r = 8 * q + (lane >> 3);
+      const int g = (lane & 7) ^ (r & 7);
+      pdmb[j] = static_cast<const uint8_t *>(W) + (size_t(min(n0 + r, N - 1)) * K + k_first + g * 8) * 2;
+    }
+  }
   auto dma_a = [&](int kt, int stage) {
     if constexpr (kAPre) {
       const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_address(sa + stage * kStageA)) +
@@ -170,16 +188,24 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
 #pragma unroll
       for (int j = 0; j < kDmaPerWave; ++j) dma16(pdma[j] + size_t(kt) * kBK * 2, dst + 1024u * j);
     }
+    if constexpr (kBPre) {
+      const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_address(sb + stage * kStageB)) +
+                           uint32_t(wave * kDmaPerWaveB) * 1024u;
+#pragma unroll
+      for (int j = 0; j < kDmaPerWaveB; ++j) dma16(pdmb[j] + size_t(kt) * kBK * 2, dst + 1024u * j);
+    }
   };
 
-  u32x4 ra[kChunksA > 0 ? kChunksA : 1], rb[kChunksB];
+  u32x4 ra[kChunksA > 0 ? kChunksA : 1], rb[kChunksB > 0 ? kChunksB : 1];
   auto load = [&](int kt) {
     if constexpr (kChunksA > 0) {
 #pragma unroll
       for (int i = 0; i < kChunksA; ++i) ra[i] = *reinterpret_cast<const u32x4 *>(pa[i] + kt * kBK);
     }
+    if constexpr (kChunksB > 0) {
 #pragma unroll
-    for (int i = 0; i < kChunksB; ++i) rb[i] = *reinterpret_cast<const u32x4 *>(pb[i] + kt * kBK);
+      for (int i = 0; i < kChunksB; ++i) rb[i] = *reinterpret_cast<const u32x4 *>(pb[i] + kt * kBK);
+    }
   };
   // Decode one 16-byte chunk and store its two bf16 granules.
   auto put = [&](uint8_t *d, int r, const u32x4 q) {
@@ -193,8 +219,10 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
 #pragma unroll
       for (int i = 0; i < kChunksA; ++i) put(sa + stage * kStageA, base_a + crow + kRowsPass * i, ra[i]);
     }
+    if constexpr (kChunksB > 0) {
 #pragma unroll
-    for (int i = 0; i < kChunksB; ++i) put(sb + stage * kStageB, base_b + crow + kRowsPass * i, rb[i]);
+      for (int i = 0; i < kChunksB; ++i) put(sb + stage * kStageB, base_b + crow + kRowsPass * i, rb[i]);
+    }
   };
 
   f32x4_t acc[kTM][kTN];
@@ -405,7 +433,9 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(
 struct GemmPlan {
   int tile;          // 256 (8 waves) or 128 (4 waves)
   int splits;        // K splits
+  bool w_pre;        // W decoded once per call too (large M)
   size_t a_bytes;    // bf16 copy of A
+  size_t w_bytes;    // bf16 copy of W (0 unless w_pre)
   size_t part_bytes; // FP32 partials (0 when unsplit)
 };
 
@@ -417,6 +447,7 @@ int env_int(const char *name, int fallback) {
 GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
   static const int tile_env = env_int("HIF8_GEMM_TILE", 0);
   static const int split_env = env_int("HIF8_GEMM_SPLIT", 0);
+  static const int wpre_env = env_int("HIF8_GEMM_WPRE", -1);
   GemmPlan p;
   const int64_t tiles256 = ((m + 255) / 256) * ((n + 255) / 256);
   p.tile = tile_env == 128 || tile_env == 256 ? tile_env : (m >= 256 && tiles256 >= 128 ? 256 : 128);
@@ -432,26 +463,31 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
         p.splits *= 2;
     }
   }
+  // Decoding W once costs ~3 bytes of HBM traffic per weight; the in-kernel
+  // decode repeats it once per 256-row tile of M, so from M = 2048 on the
+  // one-pass decode wins and the kernel streams both operands by DMA.
+  p.w_pre = p.tile == 256 && p.splits == 1 && (wpre_env >= 0 ? wpre_env > 0 : m >= 2048);
   p.a_bytes = (size_t(m) * size_t(k) * 2 + 255) / 256 * 256;
+  p.w_bytes = p.w_pre ? (size_t(n) * size_t(k) * 2 + 255) / 256 * 256 : 0;
   p.part_bytes = p.splits > 1 ? size_t(p.splits) * size_t(m) * size_t(n) * sizeof(float) : 0;
   return p;
 }
 
-template <int kBM, int kBN, int kWavesM, int kWavesN, bool kAPre, bool kPingPong>
-int launch_tiled(const LinearArgs &a, const void *act, int splits, float *partial) {
+template <int kBM, int kBN, int kWavesM, int kWavesN, bool kAPre, bool kBPre, bool kPingPong>
+int launch_tiled(const LinearArgs &a, const void *act, const void *wt, int splits, float *partial) {
   constexpr size_t kSmem = 2 * size_t(kBM + kBN) * kBK * 2;  // + 512 B of static LDS (the table)
   constexpr int kT = kWave * kWavesM * kWavesN;
   static bool configured = false;
   if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kPingPong>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kBPre, kPingPong>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, int(kSmem)) != hipSuccess)
       return fail(HIF8_ERR_LAUNCH, "soft_hif8 GEMM: cannot reserve %zu bytes of LDS", kSmem);
     configured = true;
   }
   const int64_t tiles = ((a.n + kBN - 1) / kBN) * ((a.m + kBM - 1) / kBM);
   const dim3 grid(unsigned((tiles * splits + 7) / 8 * 8));
-  gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kPingPong><<<grid, kT, kSmem, a.stream>>>(
-      act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.m),
+  gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kBPre, kPingPong><<<grid, kT, kSmem, a.stream>>>(
+      act, a.act_scale, wt, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.m),
       int(a.n), int(a.k), partial, splits, int(a.k / kBK / splits));
   int st = check_launch("soft_hif8 GEMM");
   if (st || !partial) return st;
@@ -466,9 +502,9 @@ template <bool kAPre>
 int launch_plan(const LinearArgs &a, const GemmPlan &p, const void *act, int splits, float *partial) {
   static const int pingpong = env_int("HIF8_GEMM_PINGPONG", 1);
   if (p.tile == 256)
-    return pingpong ? launch_tiled<256, 256, 2, 4, kAPre, true>(a, act, splits, partial)
-                    : launch_tiled<256, 256, 2, 4, kAPre, false>(a, act, splits, partial);
-  return launch_tiled<128, 128, 2, 2, kAPre, false>(a, act, splits, partial);
+    return pingpong ? launch_tiled<256, 256, 2, 4, kAPre, false, true>(a, act, a.weight, splits, partial)
+                    : launch_tiled<256, 256, 2, 4, kAPre, false, false>(a, act, a.weight, splits, partial);
+  return launch_tiled<128, 128, 2, 2, kAPre, false, false>(a, act, a.weight, splits, partial);
 }
 
 }  // namespace
@@ -477,7 +513,7 @@ size_t gemm_workspace_size(int64_t m, int64_t n, int64_t k) {
   if (m <= 4 || m > 0x7FFFFFFFll || n > 0x7FFFFFFFll || k > 0x7FFFFFFFll || n <= 0 || k <= 0 || k % kBK)
     return 0;
   const GemmPlan p = plan_gemm(m, n, k);
-  return p.a_bytes + p.part_bytes;
+  return p.a_bytes + p.w_bytes + p.part_bytes;
 }
 
 int launch_gemm(const LinearArgs &a) {
@@ -492,7 +528,8 @@ int launch_gemm(const LinearArgs &a) {
     return check_launch("soft_hif8 GEMM (generic)");
   }
   const GemmPlan p = plan_gemm(a.m, a.n, a.k);
-  const bool use_ws = a.workspace && a.workspace_bytes >= p.a_bytes + p.part_bytes && aligned(a.workspace, 256);
+  const bool use_ws = a.workspace && a.workspace_bytes >= p.a_bytes + p.w_bytes + p.part_bytes &&
+                      aligned(a.workspace, 256);
   if (!use_ws) return launch_plan<false>(a, p, a.act, 1, nullptr);
   uint8_t *ws = static_cast<uint8_t *>(a.workspace);
   uint16_t *abf = reinterpret_cast<uint16_t *>(ws);
@@ -501,7 +538,16 @@ int launch_gemm(const LinearArgs &a) {
   decode_rows_kernel<<<blocks, 256, 0, a.stream>>>(static_cast<const uint8_t *>(a.act), abf, chunks);
   int st = check_launch("soft_hif8 GEMM (activation decode)");
   if (st) return st;
-  float *partial = p.part_bytes ? reinterpret_cast<float *>(ws + p.a_bytes) : nullptr;
+  if (p.w_pre) {
+    uint16_t *wbf = reinterpret_cast<uint16_t *>(ws + p.a_bytes);
+    const size_t wchunks = size_t(a.n) * size_t(a.k) / 16;
+    decode_rows_kernel<<<unsigned(std::min<size_t>((wchunks + 255) / 256, 4096)), 256, 0, a.stream>>>(
+        a.weight, wbf, wchunks);
+    st = check_launch("soft_hif8 GEMM (weight decode)");
+    if (st) return st;
+    return launch_tiled<256, 256, 2, 4, true, true, false>(a, abf, wbf, 1, nullptr);
+  }
+  float *partial = p.part_bytes ? reinterpret_cast<float *>(ws + p.a_bytes + p.w_bytes) : nullptr;
   return launch_plan<true>(a, p, abf, p.part_bytes ? p.splits : 1, partial);
 }
 

@@ -571,6 +571,8 @@ __global__ __launch_bounds__(kWave, 2) void paged_decode_attention_kernel(const 
 // Merges the splits of each (request, query head, 64-dim slice):
 //   M = max_s m_s, w_s = 2^(m_s - M), out = sum_s w_s O_s / sum_s w_s l_s.
 // Four groups of 64 threads take every fourth split; each thread one dim.
+constexpr int kCombineDims = 16;  // output dims per combine block
+
 template <bool kBf16>
 __global__ __launch_bounds__(kThreads) void attention_combine_kernel(const AttnParams p) {
   __shared__ float w[kMaxSplits];
@@ -603,26 +605,29 @@ __global__ __launch_bounds__(kThreads) void attention_combine_kernel(const AttnP
   const float total = red[0] + red[1] + red[2] + red[3];
   const float inv = total > 0.f ? 1.f / total : 0.f;
   __syncthreads();
-  const int dim = int(blockIdx.y) * kWave + lane;
+  // 16 dims per block, 16 split groups: thread (d, g) sums splits s = g mod 16
+  // of dim blockIdx.y * 16 + d, so every CU gets work even for one request.
+  const int d = tid & 15, g = tid >> 4;
+  const int dim = int(blockIdx.y) * kCombineDims + d;
   float acc = 0.f;
   if (dim < p.dv) {
     const float *po = p.part_o + base * p.dv + dim;
     const size_t sstride = stride * p.dv;
-    int s = grp;
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    for (; s + 12 < ns; s += 16) {
+    int s = g;
+    float a0 = 0.f, a1 = 0.f;
+    for (; s + 16 < ns; s += 32) {
       a0 += w[s] * po[s * sstride];
-      a1 += w[s + 4] * po[(s + 4) * sstride];
-      a2 += w[s + 8] * po[(s + 8) * sstride];
-      a3 += w[s + 12] * po[(s + 12) * sstride];
+      a1 += w[s + 16] * po[(s + 16) * sstride];
     }
-    for (; s < ns; s += 4) a0 += w[s] * po[s * sstride];
-    acc = (a0 + a1) + (a2 + a3);
+    for (; s < ns; s += 16) a0 += w[s] * po[s * sstride];
+    acc = a0 + a1;
   }
   red[tid] = acc;
   __syncthreads();
-  if (grp == 0 && dim < p.dv) {
-    const float y = (red[lane] + red[64 + lane]) + (red[128 + lane] + red[192 + lane]);
+  if (tid < kCombineDims && dim < p.dv) {
+    float y = 0.f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) y += red[16 * j + tid];
     static_cast<uint16_t *>(p.out)[(size_t(b) * p.hq + head) * p.dv + dim] = float_to_half_bits<kBf16>(y * inv);
   }
 }
@@ -702,11 +707,17 @@ int env_int(const char *name, int fallback) {
 // the smallest block size the MFMA kernel takes (16), one block id per lane.
 constexpr int kMaxTilesPerSplit = 31;
 
-// Splits a request's context so that about 2048 wavefronts (eight per CU)
-// are launched over the batch and the KV heads, in whole 32-token tiles.
+// Splits a request's context in whole 32-token tiles: as many tiles per
+// split as keep at least ~1024 wavefronts (four per CU) over the batch and
+// the KV heads, at most 4 (longer splits leave too few waves in flight per
+// tile; measured on MI355X, B=1/4 x ctx 512..16384), and enough that the
+// split count fits the combine kernel.
 SplitPlan plan_splits(int64_t batch, int64_t hkv, int64_t max_len) {
   const int64_t tiles = max_len > 0 ? (max_len + kTile - 1) / kTile : 1;
-  int64_t per_split = (batch * hkv * tiles + 2047) / 2048;
+  int64_t per_split = (batch * hkv * tiles) / 1024;
+  if (per_split > 4) per_split = 4;
+  const int64_t fit = (tiles + kMaxSplits - 1) / kMaxSplits;
+  if (per_split < fit) per_split = fit;
   static const int forced = env_int("HIF8_ATTN_SPLIT_TILES", 0);
   if (forced > 0) per_split = forced;
   if (per_split > kMaxTilesPerSplit) per_split = kMaxTilesPerSplit;
@@ -745,8 +756,8 @@ void launch_mfma(const AttnParams &p, int64_t batch, hipStream_t stream) {
   if (p.block_size % kTile == 0) paged_decode_attention_kernel<kD, kQBf16, true, BtT><<<grid, block, 0, stream>>>(p);
   else paged_decode_attention_kernel<kD, kQBf16, false, BtT><<<grid, block, 0, stream>>>(p);
   if (p.num_splits > 1)
-    attention_combine_kernel<kQBf16><<<dim3(unsigned(batch * p.hq), unsigned((p.dv + kWave - 1) / kWave)), kThreads, 0,
-                                       stream>>>(p);
+    attention_combine_kernel<kQBf16><<<dim3(unsigned(batch * p.hq), unsigned((p.dv + kCombineDims - 1) / kCombineDims)),
+                                       kThreads, 0, stream>>>(p);
 }
 
 template <bool kQBf16, typename BtT>

@@ -79,9 +79,11 @@ def test_gemm_workspace_query_follows_the_split_plan(lib):
     size = lib.soft_hif8_gemm_workspace_size
     size.argtypes = [ctypes.c_int64] * 3
     size.restype = ctypes.c_size_t
-    # The workspace is the bf16 copy of A (M*K*2 bytes, rounded to 256) plus split partials.
+    # The workspace is the bf16 copy of A (M*K*2 bytes, rounded to 256), from M = 2048 on
+    # also the bf16 copy of W (N*K*2), plus split partials.
     # Enough 256 x 256 tiles to fill the GPU: no split.  GEMV-sized M: no workspace.
-    assert size(4096, 24576, 4096) == 4096 * 4096 * 2
+    assert size(4096, 24576, 4096) == 4096 * 4096 * 2 + 24576 * 4096 * 2
+    assert size(1024, 24576, 4096) == 1024 * 4096 * 2
     assert size(4, 4096, 4096) == 0
     # Prefill M=512 over a 4096 x 4096 projection: 128 tiles of 128 x 128, K split in 4.
     assert size(512, 4096, 4096) == 512 * 4096 * 2 + 4 * 512 * 4096 * 4

@@ -37,8 +37,8 @@ def _ptr(t):
 
 
 @pytest.mark.parametrize("m,n,k", [(512, 4096, 4096), (512, 2048, 4096), (300, 1000, 2048), (4096, 2048, 2048),
-                                   (600, 4096, 12288)])
-def test_split_k_gemm_matches_unsplit_and_oracle(lib, device, m, n, k):
+                                   (600, 4096, 12288), (2048, 4096, 1024), (2100, 4000, 1024)])
+def test_workspace_gemm_matches_plain_and_oracle(lib, device, m, n, k):
     a = random_codes((m, k), seed=m + k)
     w = random_codes((n, k), seed=n + 3 * k)
     g = np.random.default_rng(m * n)
@@ -49,7 +49,7 @@ def test_split_k_gemm_matches_unsplit_and_oracle(lib, device, m, n, k):
     tb = torch.from_numpy(bias).to(torch.bfloat16).to(device)
     need = lib.soft_hif8_gemm_workspace_size(m, n, k)
     print(f"split-K case m={m} n={n} k={k} workspace={need}", flush=True)
-    assert need > m * k * 2, "these shapes are chosen to take the split path"
+    assert need > m * k * 2, "these shapes take the split or the weight-decode path"
     ws = torch.empty(need, dtype=torch.uint8, device=device)
     outs = []
     for workspace in (None, ws, ws):
