@@ -466,7 +466,7 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
   // Decoding W once costs ~3 bytes of HBM traffic per weight; the in-kernel
   // decode repeats it once per 256-row tile of M, so from M = 2048 on the
   // one-pass decode wins and the kernel streams both operands by DMA.
-  p.w_pre = p.tile == 256 && p.splits == 1 && (wpre_env >= 0 ? wpre_env > 0 : m >= 2048);
+  p.w_pre = wpre_env >= 0 ? wpre_env > 0 : (p.tile == 256 && p.splits == 1 && m >= 2048);
   p.a_bytes = (size_t(m) * size_t(k) * 2 + 255) / 256 * 256;
   p.w_bytes = p.w_pre ? (size_t(n) * size_t(k) * 2 + 255) / 256 * 256 : 0;
   p.part_bytes = p.splits > 1 ? size_t(p.splits) * size_t(m) * size_t(n) * sizeof(float) : 0;
@@ -545,9 +545,14 @@ int launch_gemm(const LinearArgs &a) {
         a.weight, wbf, wchunks);
     st = check_launch("soft_hif8 GEMM (weight decode)");
     if (st) return st;
-    return launch_tiled<256, 256, 2, 4, true, true, false>(a, abf, wbf, 1, nullptr);
   }
   float *partial = p.part_bytes ? reinterpret_cast<float *>(ws + p.a_bytes + p.w_bytes) : nullptr;
+  if (p.w_pre) {
+    const void *wbf = ws + p.a_bytes;
+    const int splits = p.part_bytes ? p.splits : 1;
+    if (p.tile == 256) return launch_tiled<256, 256, 2, 4, true, true, false>(a, abf, wbf, splits, partial);
+    return launch_tiled<128, 128, 2, 2, true, true, false>(a, abf, wbf, splits, partial);
+  }
   return launch_plan<true>(a, p, abf, p.part_bytes ? p.splits : 1, partial);
 }
 
