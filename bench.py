@@ -321,6 +321,41 @@ def per_kernel_table(st: Setup, launches: int = 20) -> dict:
     return table
 
 
+def aux_kernels(torch, native, device) -> dict:
+    """The decode ops beside the fused path: hif8_scaled_decode of KV rows
+    (16384 rows x 256 codes -> bf16) and the embedding gather-decode (vocab
+    151936 x 4096 table; 4 decode tokens and a 512-token prompt).  Bytes:
+    codes + scales read, bf16 written (+ ids)."""
+    res = {}
+    g = torch.Generator(device=device).manual_seed(5)
+    rows, k = 16384, 256
+    data = torch.randint(0, 111, (rows, k), generator=g, device=device, dtype=torch.uint8)
+    scale = torch.rand(rows, generator=g, device=device)
+
+    def dec():
+        for _ in range(10):
+            native.scaled_decode(data, scale)
+    ms = time_graphs(torch, [capture(torch, dec)], 3) / 10
+    nbytes = rows * k * 3 + rows * 4
+    res["scaled_decode_16384x256"] = {"us": round(ms * 1e3, 3), "bytes": nbytes,
+                                      "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    vocab, dim = 151936, 4096
+    table = torch.randint(0, 111, (vocab, dim), generator=g, device=device, dtype=torch.uint8)
+    tscale = torch.rand(vocab, generator=g, device=device)
+    for tokens in (4, 512):
+        ids = torch.randint(0, vocab, (tokens,), generator=g, device=device)
+
+        def emb(ids=ids):
+            for _ in range(10):
+                native.embedding_lookup(table, tscale, ids, validate=False)
+        ms = time_graphs(torch, [capture(torch, emb)], 3) / 10
+        nbytes = tokens * (dim * 3 + 4 + 8)
+        res[f"embedding_{tokens}tok_x{dim}"] = {"us": round(ms * 1e3, 3), "bytes": nbytes,
+                                                "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+    del table
+    return res
+
+
 def measured_ceilings(torch, device) -> dict:
     """Context for the rooflines: a plain device copy (HBM read + write) and
     torch's bf16 matmul (hipBLASLt) on the prefill shapes with bf16 operands,
@@ -497,6 +532,8 @@ def main() -> None:
 
     log("ceilings (plain copy, hipBLASLt bf16 GEMM) ...")
     ceilings = measured_ceilings(torch, device)
+    log("scaled decode and embedding ...")
+    aux = aux_kernels(torch, native, device)
 
     log("KV page pool ...")
     kvs = KVSetup(torch, device)
@@ -553,6 +590,7 @@ def main() -> None:
         "gemv_all_launches_GBps": round(all_gemv_gbs, 1),
         "gemm_per_layer": gemm_layer,
         "ceilings": ceilings,
+        "decode_ops": aux,
         "kernels": table,
     }
     print(json.dumps(out), flush=True)

@@ -357,6 +357,39 @@ at::Tensor Hif8PagedDecodeAttention(const at::Tensor &query, const at::Tensor &k
   return out;
 }
 
+// Token-embedding gather-decode (scheme.py:121-131): ids of any shape -> [*ids.shape, dim] bf16.
+at::Tensor Hif8EmbeddingLookup(const at::Tensor &ids, const at::Tensor &weight, const at::Tensor &weight_scale,
+                               const c10::optional<at::Tensor> &invalid_ids) {
+  CheckContiguousDevice(ids, "input_ids");
+  CheckContiguousDevice(weight, "weight");
+  CheckContiguousDevice(weight_scale, "weight_scale");
+  const int id_code = IndexCode(ids, "input_ids");
+  TORCH_CHECK(weight.scalar_type() == at::ScalarType::Byte, "weight must have dtype torch.uint8");
+  TORCH_CHECK(weight.dim() == 2, "weight must have shape [vocab, dim]");
+  TORCH_CHECK(weight_scale.scalar_type() == at::ScalarType::Float, "weight_scale must have dtype torch.float32");
+  TORCH_CHECK(weight_scale.numel() == weight.size(0), "weight_scale must contain one value per vocabulary row");
+  CheckSameDevice(weight, ids.device(), "weight");
+  CheckSameDevice(weight_scale, ids.device(), "weight_scale");
+  std::vector<int64_t> shape(ids.sizes().begin(), ids.sizes().end());
+  shape.push_back(weight.size(1));
+  const c10::OptionalDeviceGuard guard(ids.device());
+  auto out = at::empty(shape, weight.options().dtype(at::ScalarType::BFloat16));
+  if (ids.numel() == 0) return out;
+  int32_t *invalid = nullptr;
+  if (invalid_ids.has_value()) {
+    CheckContiguousDevice(*invalid_ids, "invalid_ids");
+    TORCH_CHECK(invalid_ids->scalar_type() == at::ScalarType::Int && invalid_ids->numel() >= 1,
+                "invalid_ids must be an int32 tensor with at least one element");
+    invalid = invalid_ids->data_ptr<int32_t>();
+  }
+  CheckStatus(hif8_embedding_lookup(ids.data_ptr(), id_code, ids.numel(), weight.data_ptr<uint8_t>(),
+                                    weight_scale.data_ptr<float>(), weight.size(0), weight.size(1),
+                                    reinterpret_cast<uint16_t *>(out.data_ptr()), invalid,
+                                    CurrentStream(ids.device())),
+              "hif8_embedding_lookup");
+  return out;
+}
+
 // ------------------------------------------------------------------ Meta
 
 std::tuple<at::Tensor, at::Tensor> Hif8StaticQuantMeta(const at::Tensor &x, const at::Tensor &fixed_scale) {
@@ -384,6 +417,13 @@ at::Tensor Hif8PagedDecodeAttentionMeta(const at::Tensor &query, const at::Tenso
   return at::empty({query.size(0), query.size(1), value_cache.size(3) - 4}, query.options());
 }
 
+at::Tensor Hif8EmbeddingLookupMeta(const at::Tensor &ids, const at::Tensor &weight, const at::Tensor &,
+                                   const c10::optional<at::Tensor> &) {
+  std::vector<int64_t> shape(ids.sizes().begin(), ids.sizes().end());
+  shape.push_back(weight.size(1));
+  return at::empty(shape, weight.options().dtype(at::kBFloat16));
+}
+
 }  // namespace
 
 TORCH_LIBRARY(vllm_ascend_hif8, m) {
@@ -394,6 +434,7 @@ TORCH_LIBRARY(vllm_ascend_hif8, m) {
   m.def("soft_hif8_static_fused_gemm(Tensor activation, Tensor weight, Tensor fixed_scale, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
   m.def("hif8_kv_cache_write(Tensor key, Tensor value, Tensor(a!) key_cache, Tensor(b!) value_cache, Tensor slot_mapping, Tensor key_scale, Tensor value_scale, Tensor(c!)? invalid_slots=None) -> ()");
   m.def("hif8_paged_decode_attention(Tensor query, Tensor key_cache, Tensor value_cache, Tensor block_table, Tensor seq_lens, float scale, int max_seq_len) -> Tensor");
+  m.def("hif8_embedding_lookup(Tensor input_ids, Tensor weight, Tensor weight_scale, Tensor(a!)? invalid_ids=None) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
@@ -404,6 +445,7 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
   m.impl("soft_hif8_static_fused_gemm", &SoftHif8StaticFusedGemm);
   m.impl("hif8_kv_cache_write", &Hif8KVCacheWrite);
   m.impl("hif8_paged_decode_attention", &Hif8PagedDecodeAttention);
+  m.impl("hif8_embedding_lookup", &Hif8EmbeddingLookup);
 }
 
 TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
@@ -414,6 +456,7 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
   m.impl("soft_hif8_static_fused_gemm", &LinearMeta);
   m.impl("hif8_kv_cache_write", &Hif8KVCacheWriteMeta);
   m.impl("hif8_paged_decode_attention", &Hif8PagedDecodeAttentionMeta);
+  m.impl("hif8_embedding_lookup", &Hif8EmbeddingLookupMeta);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {

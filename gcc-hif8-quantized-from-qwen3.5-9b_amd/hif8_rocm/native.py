@@ -140,6 +140,36 @@ def scaled_decode(data: "torch.Tensor", scale: "torch.Tensor") -> "torch.Tensor"
     return _operator("hif8_scaled_decode", extension)(data, scale)
 
 
+def embedding_lookup(
+    weight: "torch.Tensor",
+    weight_scale: "torch.Tensor",
+    input_ids: "torch.Tensor",
+    *,
+    validate: bool = True,
+) -> "torch.Tensor":
+    """Gather and decode token-embedding rows into BF16 (scheme.py:121-131).
+
+    ``out[..., :] = bf16(decode(weight[id]) * bf16(weight_scale[id]))`` with the
+    shape ``[*input_ids.shape, dim]``.  With ``validate`` an id outside the
+    vocabulary raises IndexError (one host synchronisation, as index_select
+    would); without it such rows are zeros.
+    """
+    import torch
+
+    if weight.dtype != torch.uint8 or weight.ndim != 2:
+        raise TypeError("embedding weight must be a 2-D torch.uint8 tensor")
+    if input_ids.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"input_ids must be int32 or int64, got {input_ids.dtype}")
+    extension = load_extension()
+    ids = _as_native_operand(input_ids.to(weight.device))
+    scale = _as_native_operand(weight_scale.reshape(-1).to(torch.float32))
+    invalid = torch.zeros(1, dtype=torch.int32, device=weight.device) if validate else None
+    out = _operator("hif8_embedding_lookup", extension)(ids, _as_native_operand(weight), scale, invalid)
+    if validate and int(invalid.item()):
+        raise IndexError("embedding input_ids reference rows outside the vocabulary")
+    return out
+
+
 def _as_native_operand(tensor: "torch.Tensor") -> "torch.Tensor":
     """Return a contiguous, zero-offset tensor (native.py:148-157)."""
     if tensor.is_contiguous() and tensor.storage_offset() == 0:

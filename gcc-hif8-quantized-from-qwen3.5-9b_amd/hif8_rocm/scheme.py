@@ -116,3 +116,41 @@ class W8A8HiFloat8StaticLinearMethod:
         return native.soft_linear(
             activation, layer.weight, row_scale, layer.weight_scale, bias, output_dtype=x.dtype
         )
+
+
+SOFT_QUANT_TYPE = "W8A8HIF8_SOFT"
+
+
+class W8A8HiFloat8SoftEmbeddingMethod:
+    """Token embedding stored as HiF8 rows with per-row FP32 scales.
+
+    The exporter writes the embedding with the ``W8A8HIF8_SOFT`` load interface
+    (no activation quantisation); the lookup gathers only the requested rows
+    and decodes them (``AscendW8A8HiFloat8SoftLinearMethod.get_weight``,
+    ``_process_hif8_weights`` and ``embedding``, scheme.py:43-131).
+    """
+
+    quant_type = SOFT_QUANT_TYPE
+
+    def get_weight(self, input_size: int, output_size: int, params_dtype: torch.dtype) -> dict[str, Any]:
+        return {"weight": torch.empty(output_size, input_size, dtype=torch.uint8)}
+
+    def get_perchannel_param(self, output_size: int, params_dtype: torch.dtype) -> dict[str, Any]:
+        return {"weight_scale": torch.empty(output_size, 1, dtype=torch.float32)}
+
+    def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+        if layer.weight.dtype != torch.uint8:
+            raise TypeError(f"{self.quant_type} checkpoint weight must be torch.uint8, got {layer.weight.dtype}")
+        if layer.weight_scale.dtype != torch.float32:
+            layer.weight_scale.data = layer.weight_scale.data.to(torch.float32)
+        layer.weight.data = layer.weight.data.contiguous()
+        layer.weight_scale.data = layer.weight_scale.data.reshape(-1).contiguous()
+        backend = os.environ.get(_COMPUTE_BACKEND_ENV, _SOFT_HIF8_BACKEND)
+        if backend != _SOFT_HIF8_BACKEND:
+            raise ValueError(
+                f"unsupported {_COMPUTE_BACKEND_ENV}={backend!r}; only '{_SOFT_HIF8_BACKEND}' is supported"
+            )
+
+    def embedding(self, layer: torch.nn.Module, input_ids: torch.Tensor) -> torch.Tensor:
+        """Gather and dequantize only the requested token embedding rows (scheme.py:121-131)."""
+        return native.embedding_lookup(layer.weight, layer.weight_scale, input_ids)

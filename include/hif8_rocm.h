@@ -86,6 +86,21 @@ int hif8_scaled_decode(const uint8_t *data, int64_t rows, int64_t k, int64_t dat
                        const float *scale, uint16_t *out, hif8_stream_t stream);
 
 /*
+ * HiF8 token-embedding gather-decode.
+ * Replaces AscendW8A8HiFloat8SoftLinearMethod.embedding
+ * (src/vllm_ascend_hif8/scheme.py:121-131: index_select of weight rows and
+ * weight_scale, bf16 decode table, product with bf16(scale)).
+ *   ids [tokens] int32/int64 (ids_dtype HIF8_INDEX_*), table [vocab, dim] uint8,
+ *   table_scale [vocab] float32, out [tokens, dim] bf16:
+ *     out[t] = bf16(decode_bf16(table[ids[t]]) * bf16(table_scale[ids[t]]))
+ *   ids outside [0, vocab) give zero rows and, if invalid_ids is not NULL, add
+ *   one each to *invalid_ids (the caller raises, as index_select would).
+ */
+int hif8_embedding_lookup(const void *ids, int ids_dtype, int64_t tokens, const uint8_t *table,
+                          const float *table_scale, int64_t vocab, int64_t dim, uint16_t *out,
+                          int32_t *invalid_ids, hif8_stream_t stream);
+
+/*
  * Soft-decode GEMV, reference contract M <= 2.
  * Replaces aclnnSoftHif8Gemv as called by SoftHif8Gemv
  * (csrc/extension/hif8_native.cpp:241-316,613-631; kernel csrc/opp/op_kernel/soft_hif8_gemv.cpp:28-317).

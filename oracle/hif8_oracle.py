@@ -22,6 +22,9 @@ function) is listed per function:
                                       checked against torch's own conversion
 * KV pack/unpack/scatter/gather      - reference known answers (byte layout)
 * paged attention                    - textbook softmax attention in float64
+* embedding gather-decode            - the reference formula executed by torch on the
+                                      CPU (bf16 table, bf16 scale, bf16 product) and
+                                      closed-form products
 """
 
 from __future__ import annotations
@@ -501,3 +504,20 @@ def paged_attention_reference(query: np.ndarray, key_cache: np.ndarray, value_ca
             probs = e / e.sum(axis=-1, keepdims=True)
             out[b] = np.einsum("jgk,kjd->jgd", probs.reshape(hkv, group, -1), vals).reshape(hq, vw)
     return out
+
+
+def embedding_reference(weight: np.ndarray, weight_scale: np.ndarray, ids: np.ndarray) -> np.ndarray:
+    """Token-embedding gather-decode, as float32 holding bf16 values (scheme.py:121-131).
+
+    rows = weight[ids], decoded through the bf16 table (exact: HiF8 is a subset of
+    bf16); the row scale is rounded to bf16 first; the product of two bf16 values
+    is exact in float32 and is rounded once to bf16 (torch's bf16 multiply).
+    """
+    weight = np.asarray(weight, np.uint8)
+    ids = np.asarray(ids).reshape(-1)
+    if ids.size and (ids.min() < 0 or ids.max() >= weight.shape[0]):
+        raise IndexError("embedding ids outside the vocabulary")
+    rows = DECODE_F32[weight[ids].astype(np.int64)]
+    scale = round_bf16(np.asarray(weight_scale, np.float32).reshape(-1)[ids])
+    with np.errstate(all="ignore"):
+        return round_bf16((rows * scale[:, None]).astype(np.float32))

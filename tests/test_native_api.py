@@ -51,6 +51,8 @@ def test_real_extension_loads_on_cpu():
                  "soft_hif8_static_fused_gemm"):
         assert callable(getattr(ext, name))
         assert callable(getattr(torch.ops.vllm_ascend_hif8, name))
+    for name in ("hif8_kv_cache_write", "hif8_paged_decode_attention", "hif8_embedding_lookup"):
+        assert callable(getattr(torch.ops.vllm_ascend_hif8, name))
 
 
 def test_meta_shapes():
@@ -63,6 +65,27 @@ def test_meta_shapes():
         torch.empty(5, 64, dtype=torch.uint8, device="meta"), torch.empty(7, 64, dtype=torch.uint8, device="meta"),
         torch.empty(5, device="meta"), torch.empty(7, device="meta"), None, torch.bfloat16)
     assert y.shape == (5, 7) and y.dtype == torch.bfloat16
+    e = torch.ops.vllm_ascend_hif8.hif8_embedding_lookup(
+        torch.empty(2, 3, dtype=torch.int64, device="meta"), torch.empty(50, 64, dtype=torch.uint8, device="meta"),
+        torch.empty(50, device="meta"))
+    assert e.shape == (2, 3, 64) and e.dtype == torch.bfloat16
+
+
+def test_embedding_method_validates_weights_without_a_gpu(monkeypatch):
+    from hif8_rocm import scheme
+
+    layer = torch.nn.Module()
+    layer.weight = torch.nn.Parameter(torch.zeros(4, 8), requires_grad=False)
+    layer.weight_scale = torch.nn.Parameter(torch.ones(4, 1), requires_grad=False)
+    method = scheme.W8A8HiFloat8SoftEmbeddingMethod()
+    with pytest.raises(TypeError, match="torch.uint8"):
+        method.process_weights_after_loading(layer)
+    layer.weight = torch.nn.Parameter(torch.zeros(4, 8, dtype=torch.uint8), requires_grad=False)
+    method.process_weights_after_loading(layer)
+    assert layer.weight_scale.shape == (4,)
+    monkeypatch.setenv("HIF8_COMPUTE_BACKEND", "other")
+    with pytest.raises(ValueError, match="soft_hif8"):
+        method.process_weights_after_loading(layer)
 
 
 def test_offset_and_strided_views_are_materialized():

@@ -273,3 +273,32 @@ def test_scaled_decode_rounds_like_torch():
     nan = np.isnan(ref.float().numpy())
     assert np.array_equal(got[~nan], ref_bits[~nan])
     assert np.all(got[nan] == 0x7FC0)
+
+
+def test_embedding_reference_matches_torch_running_the_reference_formula():
+    """scheme.py:121-131 executed literally by torch on the CPU: index_select,
+    bf16 decode table, bf16(scale), bf16 product."""
+    import torch
+
+    rng = np.random.default_rng(11)
+    vocab, dim = 300, 48
+    weight = rng.integers(0, 256, (vocab, dim), dtype=np.uint8)
+    scale = (rng.random(vocab, dtype=np.float32) * 3 + 1e-3).astype(np.float32)
+    scale[:4] = [1.0, 0.5, 3.0e-7, 1234.5]
+    ids = rng.integers(0, vocab, (5, 7))
+    ids[0, :4] = [0, 1, 2, 3]
+    want = o.embedding_reference(weight, scale, ids)
+    lut = torch.tensor(o.DECODE, dtype=torch.bfloat16)
+    flat = torch.from_numpy(ids.reshape(-1))
+    rows = lut[torch.index_select(torch.from_numpy(weight), 0, flat).long()]
+    ref = rows * torch.index_select(torch.from_numpy(scale), 0, flat).to(torch.bfloat16).unsqueeze(-1)
+    got = torch.from_numpy(want)
+    both_nan = torch.isnan(got) & torch.isnan(ref.float())
+    assert torch.equal(got[~both_nan], ref.float()[~both_nan])
+    # Closed forms: code of 1.5 times scale 2 is 3; NaN and Inf codes propagate.
+    one5 = o.encode_scalar(1.5)
+    w = np.array([[one5, o.NAN_CODE, 0x6F, 0x00]], np.uint8)
+    out = o.embedding_reference(w, np.array([2.0], np.float32), np.array([0]))
+    assert out[0, 0] == 3.0 and np.isnan(out[0, 1]) and out[0, 2] == np.inf and out[0, 3] == 0.0
+    with pytest.raises(IndexError):
+        o.embedding_reference(w, np.array([2.0], np.float32), np.array([1]))
