@@ -24,6 +24,8 @@
 // 256 x 256 blocks run eight wavefronts in a 2 x 4 arrangement (128 x 64
 // each, two waves per SIMD) whose two wave rows alternate between MFMA and
 // decode half a step apart; 128 x 128 blocks run four in a 2 x 2 arrangement.
+// The epilogue scales and rounds each wave's outputs into LDS and stores
+// them as 16-byte row chunks (full 128-byte row segments per 8 lanes).
 //
 // Shapes with too few output tiles to fill 256 CUs (prefill M=512, narrow N)
 // split K: block (tile, s) sums K steps [s*ksteps, (s+1)*ksteps) and stores
@@ -76,6 +78,159 @@ __global__ __launch_bounds__(256) void decode_rows_kernel(const uint8_t *__restr
   }
 }
 
+// Tile order: the blocks of one XCD (block id modulo 8) take a contiguous
+// range of tiles, walked in groups of 4 row tiles so that blocks running
+// together share A row panels and B column panels in that XCD's L2.  The K
+// splits of a tile are adjacent work units, so they run on one XCD.  Returns
+// false for the padding blocks of the grid.
+template <int kBM, int kBN>
+__device__ __forceinline__ bool tile_of(int M, int N, int splits, int &m0, int &n0, int &split) {
+  constexpr int kGroupM = 4;
+  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
+  const int units = tiles_m * tiles_n * splits;
+  const int per_xcd = (units + 7) / 8;
+  const int unit = (int(blockIdx.x) & 7) * per_xcd + (int(blockIdx.x) >> 3);
+  if (unit >= units) return false;
+  const int lin = unit / splits;
+  split = unit - lin * splits;
+  const int group = lin / (kGroupM * tiles_n);
+  const int first_m = group * kGroupM;
+  const int group_rows = min(tiles_m - first_m, kGroupM);
+  const int in_group = lin - group * kGroupM * tiles_n;
+  m0 = (first_m + in_group % group_rows) * kBM;
+  n0 = (in_group / group_rows) * kBN;
+  return true;
+}
+
+// Epilogue of a wave's kTM x kTN grid of 16x16 MFMA tiles whose top-left
+// output is (r0, c0).  D[i][j] of a 16x16 tile lives in lane (i/4)*16 + j,
+// element i%4.  With split-K partials the raw FP32 sums go to
+// partial[split][M][N]; otherwise out = acc * ts[row] * cs[col] (+ bias),
+// rounded once.
+template <int kTM, int kTN>
+__device__ __forceinline__ void store_tile(const f32x4_t (&acc)[kTM][kTN], int r0, int c0, int frow, int fgrp,
+                                           const float *__restrict__ ts, const float *__restrict__ cs,
+                                           const void *__restrict__ bias, int bias_dtype,
+                                           void *__restrict__ out, int out_dtype, int M, int N,
+                                           float *__restrict__ partial, int split) {
+  if (partial) {
+    float *p = partial + size_t(split) * M * N;
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) {
+      const int col = c0 + j * 16 + frow;
+      if (col >= N) continue;
+#pragma unroll
+      for (int i = 0; i < kTM; ++i)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int row = r0 + i * 16 + fgrp * 4 + e;
+          if (row < M) p[size_t(row) * N + col] = acc[i][j][e];
+        }
+    }
+    return;
+  }
+  uint16_t *o = static_cast<uint16_t *>(out);
+  const bool obf = out_dtype == HIF8_DTYPE_BF16;
+  float rs[kTM][4];
+#pragma unroll
+  for (int i = 0; i < kTM; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rs[i][e] = ts[min(r0 + i * 16 + fgrp * 4 + e, M - 1)];
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    const int col = c0 + j * 16 + frow;
+    if (col >= N) continue;
+    const float c = cs[col];
+    float b = 0.f;
+    if (bias) {
+      const uint16_t h = static_cast<const uint16_t *>(bias)[col];
+      b = bias_dtype == HIF8_DTYPE_BF16 ? half_bits_to_float<true>(h) : half_bits_to_float<false>(h);
+    }
+#pragma unroll
+    for (int i = 0; i < kTM; ++i) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int row = r0 + i * 16 + fgrp * 4 + e;
+        if (row < M) {
+          const float y = acc[i][j][e] * rs[i][e] * c + b;
+          o[size_t(row) * N + col] = obf ? float_to_bf16_bits(y) : float_to_f16_bits(y);
+        }
+      }
+    }
+  }
+}
+
+// Epilogue through LDS for 16-bit outputs: the wave's outputs, scaled and
+// rounded, go to its own LDS region (row pitch kWN * 2 + 16 bytes, so the
+// four 4-row groups of a 16x16 tile fall in different banks) and come back
+// as 16-byte row chunks, each stored with one 16-byte store: 8 lanes write a
+// 128-byte row segment instead of 16 lanes writing 32 bytes with 2-byte
+// stores.  The caller has retired every read of the LDS stages.
+template <int kTM, int kTN>
+constexpr int epilogue_region_bytes() {
+  return kTM * 16 * (kTN * 16 * 2 + 16);
+}
+
+template <int kTM, int kTN>
+__device__ __forceinline__ void store_tile_lds(const f32x4_t (&acc)[kTM][kTN], uint8_t *region, int r0, int c0,
+                                               int lane, const float *__restrict__ ts, const float *__restrict__ cs,
+                                               const void *__restrict__ bias, int bias_dtype,
+                                               void *__restrict__ out, int out_dtype, int M, int N) {
+  constexpr int kWM = kTM * 16, kWN = kTN * 16, kPitch = kWN * 2 + 16;
+  const int frow = lane & 15, fgrp = lane >> 4;
+  const bool obf = out_dtype == HIF8_DTYPE_BF16;
+  float rs[kTM][4];
+#pragma unroll
+  for (int i = 0; i < kTM; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) rs[i][e] = ts[min(r0 + i * 16 + fgrp * 4 + e, M - 1)];
+#pragma unroll
+  for (int j = 0; j < kTN; ++j) {
+    const int cl = j * 16 + frow;
+    const int col = min(c0 + cl, N - 1);
+    const float c = cs[col];
+    float b = 0.f;
+    if (bias) {
+      const uint16_t h = static_cast<const uint16_t *>(bias)[col];
+      b = bias_dtype == HIF8_DTYPE_BF16 ? half_bits_to_float<true>(h) : half_bits_to_float<false>(h);
+    }
+#pragma unroll
+    for (int i = 0; i < kTM; ++i)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float y = acc[i][j][e] * rs[i][e] * c + b;
+        *reinterpret_cast<uint16_t *>(region + (i * 16 + fgrp * 4 + e) * kPitch + cl * 2) =
+            obf ? float_to_bf16_bits(y) : float_to_f16_bits(y);
+      }
+  }
+  // LDS operations of one wave complete in order; the wait and the fences
+  // keep the compiler from moving the reads above the writes.
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_wave_barrier();
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  constexpr int kRowChunks = kWN / 8;
+  constexpr int kPerLane = kWM * kRowChunks / kWave;
+  uint16_t *o = static_cast<uint16_t *>(out);
+  const bool vec = (N % 8 == 0) && (reinterpret_cast<uintptr_t>(out) & 15) == 0;
+#pragma unroll
+  for (int t = 0; t < kPerLane; ++t) {
+    const int ch = lane + kWave * t;
+    const int rl = ch / kRowChunks, cc = (ch % kRowChunks) * 8;
+    const u32x4 v = *reinterpret_cast<const u32x4 *>(region + rl * kPitch + cc * 2);
+    const int row = r0 + rl, col = c0 + cc;
+    if (row >= M || col >= N) continue;
+    uint16_t *dst = o + size_t(row) * N + col;
+    if (vec && col + 8 <= N) {
+      *reinterpret_cast<u32x4 *>(dst) = v;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (col + e < N) dst[e] = uint16_t(v[e >> 1] >> ((e & 1) * 16));
+    }
+  }
+}
+
 // Static LDS table at address 0 (the only static LDS object of the kernel):
 // a lookup address is then the code shifted left by one, a single SDWA op.
 //   kAPre      A is a bf16 matrix (decoded beforehand) copied into LDS by DMA
@@ -100,7 +255,6 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
   constexpr int kWM = kBM / kWavesM, kWN = kBN / kWavesN;  // wave sub-tile
   constexpr int kTM = kWM / 16, kTN = kWN / 16;          // 16x16 MFMA tiles per wave
   constexpr uint32_t kStageA = kBM * kBK * 2, kStageB = kBN * kBK * 2;
-  constexpr int kGroupM = 4;                             // row tiles per L2 group
   // Tiles by DMA: 1 KiB (8 rows) per instruction, spread over the waves.
   constexpr int kDmaPerWave = kBM * kBK * 2 / 1024 / kWaves;
   constexpr int kDmaPerWaveB = kBN * kBK * 2 / 1024 / kWaves;
@@ -115,22 +269,8 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
   const int tid = threadIdx.x;
   if (tid < 256) lut[tid] = kDeviceTables.decode_bf16[tid];
 
-  // Tile order: the blocks of one XCD (block id modulo 8) take a contiguous
-  // range of tiles, walked in groups of kGroupM row tiles so that blocks
-  // running together share A row panels and B column panels in that XCD's L2.
-  const int tiles_m = (M + kBM - 1) / kBM, tiles_n = (N + kBN - 1) / kBN;
-  // The K splits of a tile are adjacent work units, so they run on one XCD.
-  const int units = tiles_m * tiles_n * splits;
-  const int per_xcd = (units + 7) / 8;
-  const int unit = (int(blockIdx.x) & 7) * per_xcd + (int(blockIdx.x) >> 3);
-  if (unit >= units) return;
-  const int lin = unit / splits, split = unit - lin * splits;
-  const int group = lin / (kGroupM * tiles_n);
-  const int first_m = group * kGroupM;
-  const int group_rows = min(tiles_m - first_m, kGroupM);
-  const int in_group = lin - group * kGroupM * tiles_n;
-  const int m0 = (first_m + in_group % group_rows) * kBM;
-  const int n0 = (in_group / group_rows) * kBN;
+  int m0, n0, split;
+  if (!tile_of<kBM, kBN>(M, N, splits, m0, n0, split)) return;
   const size_t k_first = size_t(split) * ksteps * kBK;
 
   const int wave = tid / kWave, lane = tid % kWave;
@@ -321,52 +461,14 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
   // only re-reads the final tile into registers).
   if constexpr (kAPre) wait_vmcnt<0>();
 
-  // Epilogue: D[i][j] of a 16x16 tile lives in lane (i/4)*16 + j, element i%4.
   if (partial) {
-    float *p = partial + size_t(split) * M * N;
-#pragma unroll
-    for (int j = 0; j < kTN; ++j) {
-      const int col = n0 + wn * kWN + j * 16 + frow;
-      if (col >= N) continue;
-#pragma unroll
-      for (int i = 0; i < kTM; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int row = m0 + wm * kWM + i * 16 + fgrp * 4 + e;
-          if (row < M) p[size_t(row) * N + col] = acc[i][j][e];
-        }
-    }
+    store_tile<kTM, kTN>(acc, m0 + wm * kWM, n0 + wn * kWN, frow, fgrp, ts, cs, bias, bias_dtype, out, out_dtype,
+                         M, N, partial, split);
     return;
   }
-  uint16_t *o = static_cast<uint16_t *>(out);
-  const bool obf = out_dtype == HIF8_DTYPE_BF16;
-  float rs[kTM][4];
-#pragma unroll
-  for (int i = 0; i < kTM; ++i)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) rs[i][e] = ts[min(m0 + wm * kWM + i * 16 + fgrp * 4 + e, M - 1)];
-#pragma unroll
-  for (int j = 0; j < kTN; ++j) {
-    const int col = n0 + wn * kWN + j * 16 + frow;
-    if (col >= N) continue;
-    const float c = cs[col];
-    float b = 0.f;
-    if (bias) {
-      const uint16_t h = static_cast<const uint16_t *>(bias)[col];
-      b = bias_dtype == HIF8_DTYPE_BF16 ? half_bits_to_float<true>(h) : half_bits_to_float<false>(h);
-    }
-#pragma unroll
-    for (int i = 0; i < kTM; ++i) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int row = m0 + wm * kWM + i * 16 + fgrp * 4 + e;
-        if (row < M) {
-          const float y = acc[i][j][e] * rs[i][e] * c + b;
-          o[size_t(row) * N + col] = obf ? float_to_bf16_bits(y) : float_to_f16_bits(y);
-        }
-      }
-    }
-  }
+  lds_barrier();  // every wave is done reading the stages
+  store_tile_lds<kTM, kTN>(acc, smem + wave * epilogue_region_bytes<kTM, kTN>(), m0 + wm * kWM, n0 + wn * kWN, lane,
+                           ts, cs, bias, bias_dtype, out, out_dtype, M, N);
 }
 
 // Split-K epilogue: out = (sum over s of partial[s]) * ts[m] * cs[n] (+ b[n]),
@@ -475,7 +577,10 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
 
 template <int kBM, int kBN, int kWavesM, int kWavesN, bool kAPre, bool kBPre, bool kPingPong>
 int launch_tiled(const LinearArgs &a, const void *act, const void *wt, int splits, float *partial) {
-  constexpr size_t kSmem = 2 * size_t(kBM + kBN) * kBK * 2;  // + 512 B of static LDS (the table)
+  // K-step stages, or the epilogue regions if larger; + 512 B of static LDS (the table).
+  constexpr size_t kSmem = std::max<size_t>(2 * size_t(kBM + kBN) * kBK * 2,
+                                            size_t(kWavesM * kWavesN) *
+                                                epilogue_region_bytes<kBM / kWavesM / 16, kBN / kWavesN / 16>());
   constexpr int kT = kWave * kWavesM * kWavesN;
   static bool configured = false;
   if (!configured) {
