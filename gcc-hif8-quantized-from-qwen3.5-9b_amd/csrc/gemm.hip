@@ -552,14 +552,25 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
   static const int wpre_env = env_int("HIF8_GEMM_WPRE", -1);
   GemmPlan p;
   const int64_t tiles256 = ((m + 255) / 256) * ((n + 255) / 256);
-  p.tile = tile_env == 128 || tile_env == 256 ? tile_env : (m >= 256 && tiles256 >= 128 ? 256 : 128);
+  const int64_t ksteps = k / kBK;
+  const bool splittable = n % 4 == 0 && k % kBK == 0;
+  // 256-tiles also when a K split of >= 24 steps each fills all 256 CUs
+  // exactly (long K, e.g. the down projection at M = 512): their 8-wave
+  // blocks run faster per step than two 4-wave 128-tile blocks.
+  int64_t s256 = 1;
+  while (splittable && tiles256 * s256 * 2 <= 256 && ksteps % (s256 * 2) == 0 && ksteps / (s256 * 2) >= 24)
+    s256 *= 2;
+  const bool long_k_fill = m >= 256 && tiles256 * s256 == 256;
+  p.tile = tile_env == 128 || tile_env == 256 ? tile_env
+                                              : (m >= 256 && (tiles256 >= 128 || long_k_fill) ? 256 : 128);
   const int64_t tiles = ((m + p.tile - 1) / p.tile) * ((n + p.tile - 1) / p.tile);
   const int64_t slots = p.tile == 256 ? 256 : 512;  // resident blocks on 256 CUs
-  const int64_t ksteps = k / kBK;
   p.splits = 1;
-  if (n % 4 == 0 && k % kBK == 0) {
+  if (splittable) {
     if (split_env > 0) {
       while (p.splits * 2 <= split_env && ksteps % (p.splits * 2) == 0) p.splits *= 2;
+    } else if (p.tile == 256 && tiles256 < 128) {
+      p.splits = int(s256);
     } else {
       while (tiles * p.splits * 2 <= slots && ksteps % (p.splits * 2) == 0 && ksteps / (p.splits * 2) >= 16)
         p.splits *= 2;

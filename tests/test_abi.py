@@ -90,6 +90,8 @@ def test_gemm_workspace_query_follows_the_split_plan(lib):
     # Splits keep >= 16 K steps of 64 and need N % 4 == 0; K must be a multiple of 64.
     assert size(512, 4096, 1024) == 512 * 1024 * 2
     assert size(512, 4096, 2048) == 512 * 2048 * 2 + 2 * 512 * 4096 * 4
+    # Long K: 32 tiles of 256 x 256 split 8 ways (24 steps each) fill the 256 CUs.
+    assert size(512, 4096, 12288) == 512 * 12288 * 2 + 8 * 512 * 4096 * 4
     assert size(512, 4094, 4096) == 512 * 4096 * 2
     assert size(300, 16, 100) == 0
     assert size(0, 16, 16) == 0
