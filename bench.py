@@ -323,9 +323,10 @@ def per_kernel_table(st: Setup, launches: int = 20) -> dict:
 
 def aux_kernels(torch, native, device) -> dict:
     """The decode ops beside the fused path: hif8_scaled_decode of KV rows
-    (16384 rows x 256 codes -> bf16) and the embedding gather-decode (vocab
-    151936 x 4096 table; 4 decode tokens and a 512-token prompt).  Bytes:
-    codes + scales read, bf16 written (+ ids)."""
+    (16384 rows x 256 codes -> bf16), the embedding gather-decode (vocab
+    151936 x 4096 table; 4 decode tokens and a 512-token prompt) and the
+    legacy dynamic quant (M in {1, 4096}, K 4096).  Bytes: codes + scales
+    read, bf16 written (+ ids); dynamic quant: bf16 in, codes + scales out."""
     res = {}
     g = torch.Generator(device=device).manual_seed(5)
     rows, k = 16384, 256
@@ -353,6 +354,18 @@ def aux_kernels(torch, native, device) -> dict:
         res[f"embedding_{tokens}tok_x{dim}"] = {"us": round(ms * 1e3, 3), "bytes": nbytes,
                                                 "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
     del table
+    # The legacy dynamic-scale path: per-row amax + encode (bf16 in, codes and
+    # row scales out; the row is read twice, the second time from cache).
+    for m, kk in ((1, 4096), (4096, 4096)):
+        x = torch.randn(m, kk, generator=g, device=device).to(torch.bfloat16)
+
+        def dq(x=x):
+            for _ in range(10):
+                native.dynamic_quant(x)
+        ms = time_graphs(torch, [capture(torch, dq)], 3) / 10
+        nbytes = m * kk * 3 + m * 4
+        res[f"dynamic_quant_m{m}_k{kk}"] = {"us": round(ms * 1e3, 3), "bytes": nbytes,
+                                            "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
     return res
 
 

@@ -12,8 +12,10 @@
 //     FP32 accumulation;
 //   * partial sums are reduced through LDS (thread-major, padded rows) and the
 //     epilogue applies token scale, channel scale and bias, rounding once.
-// The fused variant takes fp16/bf16 x and statically encodes it on the fly
-// (soft_hif8_fused_gemm.cpp:449-534 with HIF8_FUSED_STATIC_SCALE).
+// The fused variants take fp16/bf16 x and encode it on the fly: with the
+// fixed scale (soft_hif8_fused_gemm.cpp:449-534 with HIF8_FUSED_STATIC_SCALE)
+// or with each row's dynamic scale max(finite amax, 1e-12), which every block
+// reduces from the whole row first (soft_hif8_fused_gemm.cpp:536-571).
 #include <stdlib.h>
 
 #include "linear.h"
@@ -110,6 +112,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_kernel(
   constexpr int kV = kR * kM;
   constexpr int kPitch = kV + 4;
   constexpr bool kFused = kSrc != kActCodes;
+  constexpr bool kDynamic = kSrc == kActF16Dyn || kSrc == kActBf16Dyn;
+  constexpr bool kInBf16 = kSrc == kActBf16 || kSrc == kActBf16Dyn;
   constexpr int kActWords = kFused ? 2 : 1;  // 16-byte words of activation per row per chunk
   __shared__ __attribute__((aligned(16))) uint16_t dec_lut[256];
   __shared__ __attribute__((aligned(16))) uint8_t enc_lut[kFused ? 8192 : 16];
@@ -152,8 +156,51 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_kernel(
   }
   lds_barrier();
 
-  const float fixed = kFused ? act_scale[0] : 0.f;
-  const float rcp = kFused ? __builtin_amdgcn_rcpf(fixed) : 0.f;
+  // Activation scale of each row: the fixed one, or (dynamic) the row's
+  // finite amax floored at 1e-12, reduced over the whole row by the block.
+  float row_s[kM], row_r[kM];
+  if constexpr (kDynamic) {
+    __shared__ float amax_red[kM][kThreads / kWave];
+    float m_loc[kM];
+#pragma unroll
+    for (int m = 0; m < kM; ++m) m_loc[m] = 0.f;
+    for (int c = tid; c < chunks; c += kThreads) {
+#pragma unroll
+      for (int m = 0; m < kM; ++m) {
+        const u32x4 *xp = reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(act) + size_t(m) * k + 16 * c);
+        const u32x4 h[2] = {xp[0], xp[1]};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const uint32_t w = h[i >> 2][i & 3];
+          const float v0 = lo_to_float<kInBf16>(w), v1 = hi_to_float<kInBf16>(w);
+          if (__builtin_isfinite(v0)) m_loc[m] = fmaxf(m_loc[m], fabsf(v0));
+          if (__builtin_isfinite(v1)) m_loc[m] = fmaxf(m_loc[m], fabsf(v1));
+        }
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+      const float w = wave_max(m_loc[m]);
+      if (tid % kWave == 0) amax_red[m][tid / kWave] = w;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+      float a = amax_red[m][0];
+#pragma unroll
+      for (int w = 1; w < kThreads / kWave; ++w) a = fmaxf(a, amax_red[m][w]);
+      row_s[m] = fmaxf(a, 1.0e-12f);
+      row_r[m] = __builtin_amdgcn_rcpf(row_s[m]);
+    }
+  } else {
+    const float fixed = kFused ? act_scale[0] : 0.f;
+    const float rcp = kFused ? __builtin_amdgcn_rcpf(fixed) : 0.f;
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+      row_s[m] = fixed;
+      row_r[m] = rcp;
+    }
+  }
   float acc[kR][kM];
 #pragma unroll
   for (int r = 0; r < kR; ++r)
@@ -167,7 +214,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_kernel(
     for (int m = 0; m < kM; ++m) {
       if constexpr (kFused) {
         u32x4 lo, hi;
-        fast_encode_decode16<kSrc == kActBf16>(ar[m][0], ar[m][1], fixed, rcp, enc_lut, dec_lut, lo, hi);
+        fast_encode_decode16<kInBf16>(ar[m][0], ar[m][1], row_s[m], row_r[m], enc_lut, dec_lut, lo, hi);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           a[m][i] = lo[i];
@@ -214,7 +261,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_kernel(
     const int r = v / kM, m = v % kM;
     const int row = n0 + r;
     if (row < n) {
-      const float ts = kFused ? fixed : act_scale[m];
+      float ts = kFused ? row_s[0] : act_scale[m];
+      if constexpr (kFused) {
+#pragma unroll
+        for (int mm = 1; mm < kM; ++mm)
+          if (m == mm) ts = row_s[mm];
+      }
       float y = s * ts * cs[row];
       if (bias) y += load_bias(bias, bias_dtype, row);
       store_out(out, out_dtype, size_t(m) * n + row, y);
@@ -231,7 +283,24 @@ __global__ __launch_bounds__(64) void gemv_simple_kernel(
   const int row = blockIdx.x;
   const int lane = threadIdx.x;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  const float fixed = act_kind == kActCodes ? 0.f : act_scale[0];
+  const bool dyn = act_kind == kActF16Dyn || act_kind == kActBf16Dyn;
+  const bool in_bf16 = act_kind == kActBf16 || act_kind == kActBf16Dyn;
+  const float fixed = act_kind == kActCodes || dyn ? 1.f : act_scale[0];
+  float scale[4] = {fixed, fixed, fixed, fixed};  // activation scale of each row
+  if (dyn) {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      if (m < m_rows) {
+        float amax = 0.f;
+        for (int kk = lane; kk < k; kk += kWave) {
+          const uint16_t h = static_cast<const uint16_t *>(act)[size_t(m) * k + kk];
+          const float xv = in_bf16 ? half_bits_to_float<true>(h) : half_bits_to_float<false>(h);
+          if (__builtin_isfinite(xv)) amax = fmaxf(amax, fabsf(xv));
+        }
+        scale[m] = fmaxf(wave_max(amax), 1.0e-12f);
+      }
+    }
+  }
   for (int kk = lane; kk < k; kk += kWave) {
     const float wv = __uint_as_float(kDeviceTables.decode_f32[weight[size_t(row) * k + kk]]);
 #pragma unroll
@@ -242,8 +311,8 @@ __global__ __launch_bounds__(64) void gemv_simple_kernel(
           code = static_cast<const uint8_t *>(act)[size_t(m) * k + kk];
         } else {
           const uint16_t h = static_cast<const uint16_t *>(act)[size_t(m) * k + kk];
-          const float xv = act_kind == kActBf16 ? half_bits_to_float<true>(h) : half_bits_to_float<false>(h);
-          code = static_encode_bits(__float_as_uint(xv / fixed));
+          const float xv = in_bf16 ? half_bits_to_float<true>(h) : half_bits_to_float<false>(h);
+          code = static_encode_bits(__float_as_uint(xv / scale[m]));
         }
         acc[m] = fmaf(__uint_as_float(kDeviceTables.decode_f32[code]), wv, acc[m]);
       }
@@ -254,7 +323,8 @@ __global__ __launch_bounds__(64) void gemv_simple_kernel(
   if (lane < m_rows) {
     const int m = lane;
     const float a = m == 0 ? acc[0] : (m == 1 ? acc[1] : (m == 2 ? acc[2] : acc[3]));
-    const float ts = act_kind == kActCodes ? act_scale[m] : fixed;
+    const float sm = m == 0 ? scale[0] : (m == 1 ? scale[1] : (m == 2 ? scale[2] : scale[3]));
+    const float ts = act_kind == kActCodes ? act_scale[m] : sm;
     float y = a * ts * cs[row];
     if (bias) y += load_bias(bias, bias_dtype, row);
     store_out(out, out_dtype, size_t(m) * n + row, y);
@@ -432,8 +502,16 @@ void dispatch_src(const LinearArgs &a, dim3 grid) {
       gemv_kernel<kM, kR, kActF16><<<grid, kThreads, 0, a.stream>>>(
           a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
       break;
-    default:
+    case kActBf16:
       gemv_kernel<kM, kR, kActBf16><<<grid, kThreads, 0, a.stream>>>(
+          a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
+      break;
+    case kActF16Dyn:
+      gemv_kernel<kM, kR, kActF16Dyn><<<grid, kThreads, 0, a.stream>>>(
+          a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
+      break;
+    default:
+      gemv_kernel<kM, kR, kActBf16Dyn><<<grid, kThreads, 0, a.stream>>>(
           a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
       break;
   }
@@ -472,7 +550,8 @@ int launch_gemv(const LinearArgs &a) {
   if (a.m < 1 || a.m > 4) return fail(HIF8_ERR_UNSUPPORTED, "GEMV kernel handles 1 <= M <= 4, got %lld", (long long)a.m);
   static const GemvKnobs knobs;
   const bool vec = a.k % 16 == 0 && aligned(a.weight, 16) && aligned(a.act, 16);
-  if (knobs.kernel == 'm' && mfma_gemv_smem(a)) {
+  const bool dynamic = a.act_kind == kActF16Dyn || a.act_kind == kActBf16Dyn;
+  if (knobs.kernel == 'm' && !dynamic && mfma_gemv_smem(a)) {
     int st = HIF8_OK;
     switch (a.m) {
       case 1: st = launch_mfma_src<1>(a); break;

@@ -9,6 +9,8 @@ enum ActKind : int {
   kActCodes = 0,  // uint8 HiF8 activation codes + token_scale[m]
   kActF16 = 1,    // float16 x, statically quantised in the kernel with fixed_scale[0]
   kActBf16 = 2,   // bfloat16 x, likewise
+  kActF16Dyn = 3,   // float16 x, quantised in the kernel with its per-row dynamic scale
+  kActBf16Dyn = 4,  // bfloat16 x, likewise
 };
 
 struct LinearArgs {

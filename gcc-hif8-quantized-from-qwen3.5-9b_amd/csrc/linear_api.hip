@@ -114,3 +114,21 @@ extern "C" int soft_hif8_static_fused_gemm(const void *x, int x_dtype, const uin
   a.act_kind = x_dtype == HIF8_DTYPE_BF16 ? kActBf16 : kActF16;
   return launch_gemv(a);
 }
+
+extern "C" int soft_hif8_fused_gemm(const void *x, int x_dtype, const uint8_t *weight,
+                                    const float *channel_scale, const void *bias, int bias_dtype, void *out,
+                                    int out_dtype, int64_t m, int64_t n, int64_t k, hif8_stream_t stream) {
+  clear_error();
+  // No activation-scale argument: every row's scale is its own finite amax.
+  int st = validate("soft_hif8_fused_gemm", x, weight, channel_scale, channel_scale, bias, bias_dtype, out,
+                    out_dtype, m, n, k);
+  if (st) return st;
+  if (!is_io_dtype(x_dtype))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "activation must have dtype torch.float16 or torch.bfloat16");
+  if (m > 2) return fail(HIF8_ERR_INVALID_ARGUMENT, "soft_hif8_fused_gemm requires M <= 2");
+  LinearArgs a = codes_args(nullptr, weight, nullptr, channel_scale, bias, bias_dtype, out, out_dtype, m, n, k,
+                            stream);
+  a.act = x;
+  a.act_kind = x_dtype == HIF8_DTYPE_BF16 ? kActBf16Dyn : kActF16Dyn;
+  return launch_gemv(a);
+}

@@ -8,6 +8,8 @@
 // as few VALU cycles per element as possible: static_encode16 multiplies by a
 // per-row reciprocal and falls back to an IEEE division only next to an
 // encode-index boundary (the argument is spelled out in quant_device.h).
+#include <algorithm>
+
 #include "quant_device.h"
 
 namespace hif8 {
@@ -96,6 +98,74 @@ __global__ __launch_bounds__(kThreads) void scaled_decode_kernel(
   }
 }
 
+// Dynamic per-row quantisation (the legacy W8A8HIF8_SOFT activations;
+// hif8_dynamic_quant.cpp:35-200):
+//   scale[r] = max(max |x[r, :]| over the finite values, 1e-12)
+//   q = x * RN(1 / scale)   when k % 32 == 0 (the reference's vector path),
+//       x / scale           otherwise (its scalar path)
+//   data = encode(q): NaN -> 0x80, Inf kept, zero magnitude unsigned.
+// |q| <= 1 + 1 ulp for finite x, far below the static table's saturation
+// point (1.25 * 2^15), so the static table gives the plain signed encode.
+// One block per row (grid-stride), 16 elements per thread and pass when
+// k % 16 == 0 and the row is 16-byte aligned.
+template <bool kBf16, bool kVec>
+__global__ __launch_bounds__(kThreads) void dynamic_quant_kernel(const uint16_t *__restrict__ x,
+                                                                 uint8_t *__restrict__ out,
+                                                                 float *__restrict__ row_scale, uint32_t rows,
+                                                                 uint32_t k) {
+  __shared__ __attribute__((aligned(16))) uint8_t lut[8192];
+  __shared__ float red[kThreads / kWave];
+  stage_static_encode_table(lut, threadIdx.x, kThreads);
+  __syncthreads();
+  const bool by_reciprocal = k % 32 == 0;
+  const uint32_t chunks = kVec ? k / 16 : k;
+  for (uint32_t row = blockIdx.x; row < rows; row += gridDim.x) {
+    const uint16_t *xr = x + size_t(row) * k;
+    float m = 0.f;
+    for (uint32_t c = threadIdx.x; c < chunks; c += kThreads) {
+      if constexpr (kVec) {
+        float v[16];
+        load16<kBf16>(xr + size_t(c) * 16, v);
+#pragma unroll
+        for (int j = 0; j < 16; ++j)
+          if (__builtin_isfinite(v[j])) m = fmaxf(m, fabsf(v[j]));
+      } else {
+        const float v = half_bits_to_float<kBf16>(xr[c]);
+        if (__builtin_isfinite(v)) m = fmaxf(m, fabsf(v));
+      }
+    }
+    m = wave_max(m);
+    if (threadIdx.x % kWave == 0) red[threadIdx.x / kWave] = m;
+    __syncthreads();
+    float amax = red[0];
+#pragma unroll
+    for (int w = 1; w < kThreads / kWave; ++w) amax = fmaxf(amax, red[w]);
+    const float s = fmaxf(amax, 1.0e-12f);
+    const float r = 1.0f / s;  // IEEE division (built with correctly rounded division)
+    auto encode = [&](float v) -> uint32_t {
+      const float q = by_reciprocal ? v * r : v / s;
+      return __builtin_isnan(q) ? uint32_t(kNan) : uint32_t(lut[__float_as_uint(q) >> 19]);
+    };
+    uint8_t *orow = out + size_t(row) * k;
+    for (uint32_t c = threadIdx.x; c < chunks; c += kThreads) {
+      if constexpr (kVec) {
+        float v[16];
+        load16<kBf16>(xr + size_t(c) * 16, v);
+        uint32_t w[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          w[i] = encode(v[4 * i]) | (encode(v[4 * i + 1]) << 8) | (encode(v[4 * i + 2]) << 16) |
+                 (encode(v[4 * i + 3]) << 24);
+        *reinterpret_cast<uint4 *>(orow + size_t(c) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+      } else {
+        orow[c] = uint8_t(encode(half_bits_to_float<kBf16>(xr[c])));
+      }
+    }
+    if (threadIdx.x == 0) row_scale[row] = s;
+    __syncthreads();  // red is reused by the next row
+  }
+}
+
 int grid_for(uint64_t work_items, int per_cu) {
   uint64_t blocks = (work_items + kThreads - 1) / kThreads;
   const uint64_t cap = uint64_t(256) * per_cu;  // 256 CUs on MI355X
@@ -139,6 +209,31 @@ extern "C" int hif8_static_quant(const void *x, int x_dtype, int64_t rows, int64
     else static_quant_scalar<false><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, n, uint64_t(k), uint32_t(scale_count));
   }
   return check_launch("hif8_static_quant");
+}
+
+extern "C" int hif8_dynamic_quant(const void *x, int x_dtype, int64_t rows, int64_t k, uint8_t *data,
+                                  float *row_scale, hif8_stream_t stream) {
+  clear_error();
+  if (!x || !data || !row_scale) return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_dynamic_quant: null pointer argument");
+  if (!is_io_dtype(x_dtype))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_dynamic_quant: x must be float16 or bfloat16");
+  if (rows <= 0 || k <= 0) return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_dynamic_quant: dimensions must be positive");
+  if (rows > 0xFFFFFFFFll || k > 0xFFFFFFFFll)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_dynamic_quant: dimensions must fit uint32");
+  const bool bf16 = x_dtype == HIF8_DTYPE_BF16;
+  const bool vec = k % 16 == 0 && aligned(x, 16) && aligned(data, 16);
+  const dim3 grid(unsigned(std::min<int64_t>(rows, 2048))), block(kThreads);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const uint16_t *xs = static_cast<const uint16_t *>(x);
+  const uint32_t r = uint32_t(rows), kk = uint32_t(k);
+  if (bf16) {
+    if (vec) dynamic_quant_kernel<true, true><<<grid, block, 0, s>>>(xs, data, row_scale, r, kk);
+    else dynamic_quant_kernel<true, false><<<grid, block, 0, s>>>(xs, data, row_scale, r, kk);
+  } else {
+    if (vec) dynamic_quant_kernel<false, true><<<grid, block, 0, s>>>(xs, data, row_scale, r, kk);
+    else dynamic_quant_kernel<false, false><<<grid, block, 0, s>>>(xs, data, row_scale, r, kk);
+  }
+  return check_launch("hif8_dynamic_quant");
 }
 
 extern "C" int hif8_scaled_decode(const uint8_t *data, int64_t rows, int64_t k,

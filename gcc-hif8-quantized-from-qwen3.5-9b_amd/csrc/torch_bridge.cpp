@@ -137,6 +137,27 @@ std::tuple<at::Tensor, at::Tensor> Hif8StaticQuant(const at::Tensor &x, const at
   return {data, row_scale};
 }
 
+// hif8_native.cpp:433-485 (Hif8DynamicQuant): row scales are returned
+// contiguous [rows] rather than as a stride-16 view.
+std::tuple<at::Tensor, at::Tensor> Hif8DynamicQuant(const at::Tensor &x) {
+  CheckDeviceTensor(x, "x");
+  TORCH_CHECK(x.scalar_type() == at::ScalarType::Half || x.scalar_type() == at::ScalarType::BFloat16,
+              "x must have dtype torch.float16 or torch.bfloat16");
+  TORCH_CHECK(x.dim() >= 1, "x must have at least one dimension");
+  CheckPositiveDimensions(x, "x");
+  const int64_t k = x.size(-1);
+  const int64_t rows = x.numel() / k;
+  CheckFitsUint32(rows, "activation row count");
+  CheckFitsUint32(k, "K");
+  const c10::OptionalDeviceGuard guard(x.device());
+  auto data = at::empty(x.sizes(), x.options().dtype(at::ScalarType::Byte));
+  auto row_scale = at::empty({rows}, x.options().dtype(at::ScalarType::Float));
+  CheckStatus(hif8_dynamic_quant(x.data_ptr(), DtypeCode(x.scalar_type()), rows, k, data.data_ptr<uint8_t>(),
+                                 row_scale.data_ptr<float>(), CurrentStream(x.device())),
+              "hif8_dynamic_quant");
+  return {data, row_scale};
+}
+
 at::Tensor Hif8ScaledDecode(const at::Tensor &data, const at::Tensor &scale) {
   CheckDeviceTensor(data, "data");
   CheckDeviceTensor(scale, "scale");
@@ -236,6 +257,54 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
                                           DtypeCode(output_dtype), activation.size(0), weight.size(0),
                                           activation.size(1), CurrentStream(device)),
               "soft_hif8_static_fused_gemm");
+  return out;
+}
+
+// hif8_native.cpp:671-782 (SoftHif8FusedGemm): dynamic per-row scale, M <= 2.
+at::Tensor SoftHif8FusedGemm(const at::Tensor &activation, const at::Tensor &weight,
+                             const at::Tensor &channel_scale, const c10::optional<at::Tensor> &bias,
+                             at::ScalarType output_dtype) {
+  CheckDeviceTensor(activation, "activation");
+  CheckDeviceTensor(weight, "weight");
+  CheckDeviceTensor(channel_scale, "channel_scale");
+  TORCH_CHECK(activation.scalar_type() == at::ScalarType::Half || activation.scalar_type() == at::ScalarType::BFloat16,
+              "activation must have dtype torch.float16 or torch.bfloat16");
+  TORCH_CHECK(weight.scalar_type() == at::ScalarType::Byte, "weight must have dtype torch.uint8");
+  TORCH_CHECK(channel_scale.scalar_type() == at::ScalarType::Float, "channel_scale must have dtype torch.float32");
+  TORCH_CHECK(activation.dim() == 2, "activation must have shape [M, K]");
+  TORCH_CHECK(weight.dim() == 2, "weight must have shape [N, K]");
+  TORCH_CHECK(channel_scale.dim() == 1, "channel_scale must have shape [N]");
+  CheckPositiveDimensions(activation, "activation");
+  CheckPositiveDimensions(weight, "weight");
+  TORCH_CHECK(activation.size(0) <= 2, "soft_hif8_fused_gemm requires M <= 2");
+  TORCH_CHECK(activation.size(1) == weight.size(1), "activation and weight K dimensions differ: ",
+              activation.size(1), " != ", weight.size(1));
+  TORCH_CHECK(channel_scale.numel() == weight.size(0), "channel_scale must contain one value per output channel");
+  CheckFitsUint32(activation.size(0), "M");
+  CheckFitsUint32(weight.size(0), "N");
+  CheckFitsUint32(activation.size(1), "K");
+  const auto device = activation.device();
+  CheckSameDevice(weight, device, "weight");
+  CheckSameDevice(channel_scale, device, "channel_scale");
+  if (bias.has_value()) {
+    CheckDeviceTensor(*bias, "bias");
+    CheckSameDevice(*bias, device, "bias");
+    TORCH_CHECK(bias->dim() == 1, "bias must have shape [N]");
+    TORCH_CHECK(bias->numel() == weight.size(0), "bias must contain N values");
+    TORCH_CHECK(bias->scalar_type() == at::ScalarType::Half || bias->scalar_type() == at::ScalarType::BFloat16,
+                "bias must have dtype torch.float16 or torch.bfloat16");
+  }
+  TORCH_CHECK(output_dtype == at::ScalarType::Half || output_dtype == at::ScalarType::BFloat16,
+              "output_dtype must be torch.float16 or torch.bfloat16");
+  const c10::OptionalDeviceGuard guard(device);
+  auto out = at::empty({activation.size(0), weight.size(0)}, activation.options().dtype(output_dtype));
+  const void *bias_ptr = bias.has_value() ? bias->data_ptr() : nullptr;
+  const int bias_dtype = bias.has_value() ? DtypeCode(bias->scalar_type()) : HIF8_DTYPE_NONE;
+  CheckStatus(soft_hif8_fused_gemm(activation.data_ptr(), DtypeCode(activation.scalar_type()),
+                                   weight.data_ptr<uint8_t>(), channel_scale.data_ptr<float>(), bias_ptr, bias_dtype,
+                                   out.data_ptr(), DtypeCode(output_dtype), activation.size(0), weight.size(0),
+                                   activation.size(1), CurrentStream(device)),
+              "soft_hif8_fused_gemm");
   return out;
 }
 
@@ -399,6 +468,17 @@ std::tuple<at::Tensor, at::Tensor> Hif8StaticQuantMeta(const at::Tensor &x, cons
   return {data, at::empty({rows}, x.options().dtype(at::kFloat))};
 }
 
+std::tuple<at::Tensor, at::Tensor> Hif8DynamicQuantMeta(const at::Tensor &x) {
+  auto data = at::empty_like(x, x.options().dtype(at::kByte));
+  const int64_t rows = x.dim() ? x.numel() / x.size(-1) : 1;
+  return {data, at::empty({rows}, x.options().dtype(at::kFloat))};
+}
+
+at::Tensor FusedLinearMeta(const at::Tensor &activation, const at::Tensor &weight, const at::Tensor &,
+                           const c10::optional<at::Tensor> &, at::ScalarType output_dtype) {
+  return at::empty({activation.size(0), weight.size(0)}, activation.options().dtype(output_dtype));
+}
+
 at::Tensor Hif8ScaledDecodeMeta(const at::Tensor &data, const at::Tensor &) {
   return at::empty_like(data, data.options().dtype(at::kBFloat16));
 }
@@ -435,6 +515,8 @@ TORCH_LIBRARY(vllm_ascend_hif8, m) {
   m.def("hif8_kv_cache_write(Tensor key, Tensor value, Tensor(a!) key_cache, Tensor(b!) value_cache, Tensor slot_mapping, Tensor key_scale, Tensor value_scale, Tensor(c!)? invalid_slots=None) -> ()");
   m.def("hif8_paged_decode_attention(Tensor query, Tensor key_cache, Tensor value_cache, Tensor block_table, Tensor seq_lens, float scale, int max_seq_len) -> Tensor");
   m.def("hif8_embedding_lookup(Tensor input_ids, Tensor weight, Tensor weight_scale, Tensor(a!)? invalid_ids=None) -> Tensor");
+  m.def("hif8_dynamic_quant(Tensor x) -> (Tensor, Tensor)");
+  m.def("soft_hif8_fused_gemm(Tensor activation, Tensor weight, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
@@ -446,6 +528,8 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
   m.impl("hif8_kv_cache_write", &Hif8KVCacheWrite);
   m.impl("hif8_paged_decode_attention", &Hif8PagedDecodeAttention);
   m.impl("hif8_embedding_lookup", &Hif8EmbeddingLookup);
+  m.impl("hif8_dynamic_quant", &Hif8DynamicQuant);
+  m.impl("soft_hif8_fused_gemm", &SoftHif8FusedGemm);
 }
 
 TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
@@ -457,10 +541,16 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
   m.impl("hif8_kv_cache_write", &Hif8KVCacheWriteMeta);
   m.impl("hif8_paged_decode_attention", &Hif8PagedDecodeAttentionMeta);
   m.impl("hif8_embedding_lookup", &Hif8EmbeddingLookupMeta);
+  m.impl("hif8_dynamic_quant", &Hif8DynamicQuantMeta);
+  m.impl("soft_hif8_fused_gemm", &FusedLinearMeta);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {
   module.def("hif8_static_quant", &Hif8StaticQuant, pybind11::arg("x"), pybind11::arg("fixed_scale"));
+  module.def("hif8_dynamic_quant", &Hif8DynamicQuant, pybind11::arg("x"));
+  module.def("soft_hif8_fused_gemm", &SoftHif8FusedGemm, pybind11::arg("activation"), pybind11::arg("weight"),
+             pybind11::arg("channel_scale"), pybind11::arg("bias") = c10::nullopt,
+             pybind11::arg("output_dtype") = at::ScalarType::Half);
   module.def("hif8_scaled_decode", &Hif8ScaledDecode, pybind11::arg("data"), pybind11::arg("scale"));
   module.def("soft_hif8_gemv", &SoftHif8Gemv, pybind11::arg("activation"), pybind11::arg("weight"),
              pybind11::arg("token_scale"), pybind11::arg("channel_scale"), pybind11::arg("bias") = c10::nullopt,

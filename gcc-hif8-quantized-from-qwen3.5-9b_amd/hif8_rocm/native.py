@@ -20,6 +20,7 @@ if TYPE_CHECKING:
 
 _EXTENSION_MODULE = "hif8_rocm._C"
 _REQUIRED_SYMBOLS = (
+    "hif8_dynamic_quant",
     "hif8_static_quant",
     "soft_hif8_gemv",
     "soft_hif8_gemm",
@@ -94,6 +95,19 @@ def _operator(name: str, extension: ModuleType):
     if not callable(op):
         raise NativeExtensionUnavailable(f"the native extension has no {name} operator; rebuild it")
     return op
+
+
+def dynamic_quant(x: "torch.Tensor") -> tuple["torch.Tensor", "torch.Tensor"]:
+    """Quantize BF16/FP16 activations into U8 HiFloat8 with FP32 token scales (native.py:77-87).
+
+    Row r's scale is max(finite amax of the row, 1e-12); the row scales come
+    back contiguous ``[rows]``.
+    """
+    extension = load_extension()
+    x = _as_native_operand(x)
+    data, scale = _operator("hif8_dynamic_quant", extension)(x)
+    _validate_quantized_activation(x, data, scale, operation="hif8_dynamic_quant")
+    return data, scale
 
 
 def static_quant(x: "torch.Tensor", fixed_scale: "torch.Tensor") -> tuple["torch.Tensor", "torch.Tensor"]:
@@ -218,6 +232,36 @@ def soft_linear(
     operator = _operator("soft_hif8_gemv" if use_gemv else "soft_hif8_gemm", extension)
     output = operator(flattened, weight, token_scale, channel_scale, bias, output_dtype)
     return output.reshape(*activation.shape[:-1], weight.shape[0])
+
+
+def soft_fused_linear(
+    x: "torch.Tensor",
+    weight: "torch.Tensor",
+    weight_scale: "torch.Tensor",
+    bias: "torch.Tensor | None" = None,
+    *,
+    output_dtype: "torch.dtype",
+) -> "torch.Tensor":
+    """Fused dynamic activation quant/decode with U8-weight GEMV, M <= 2 (native.py:205-238)."""
+    import torch
+
+    if x.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError(f"fused soft HiFP8 linear requires FP16/BF16 activation, got {x.dtype}")
+    if weight.dtype != torch.uint8 or weight.ndim != 2:
+        raise TypeError("fused soft HiFP8 linear requires a 2D uint8 weight tensor")
+    if x.ndim < 2 or x.shape[-1] != weight.shape[-1]:
+        raise ValueError("activation and weight must have compatible final K dimensions")
+    if weight_scale.dtype != torch.float32 or weight_scale.numel() != weight.shape[0]:
+        raise TypeError("fused soft HiFP8 linear requires one float32 scale per output channel")
+
+    flattened = _as_native_operand(x.reshape(-1, x.shape[-1]))
+    if flattened.shape[0] > 2:
+        raise ValueError("fused soft HiFP8 linear supports M <= 2")
+    channel_scale = _as_native_operand(weight_scale.reshape(-1))
+    extension = load_extension()
+    operator = _operator("soft_hif8_fused_gemm", extension)
+    output = operator(flattened, weight, channel_scale, bias, output_dtype)
+    return output.reshape(*x.shape[:-1], weight.shape[0])
 
 
 def soft_static_fused_linear(

@@ -119,18 +119,22 @@ class W8A8HiFloat8StaticLinearMethod:
 
 
 SOFT_QUANT_TYPE = "W8A8HIF8_SOFT"
+_SOFT_FUSED_GENERATION_ENV = "HIF8_SOFT_FUSED_GENERATION"
 
 
-class W8A8HiFloat8SoftEmbeddingMethod:
-    """Token embedding stored as HiF8 rows with per-row FP32 scales.
+class W8A8HiFloat8SoftLinearMethod:
+    """Dynamic per-token A8 and per-channel W8 HiFloat8 (the W8A8HIF8_SOFT type, scheme.py:43-131).
 
-    The exporter writes the embedding with the ``W8A8HIF8_SOFT`` load interface
-    (no activation quantisation); the lookup gathers only the requested rows
-    and decodes them (``AscendW8A8HiFloat8SoftLinearMethod.get_weight``,
-    ``_process_hif8_weights`` and ``embedding``, scheme.py:43-131).
+    The legacy scheme: each activation row is quantised with its own scale
+    (``hif8_dynamic_quant``) before the soft GEMM; with
+    ``HIF8_SOFT_FUSED_GENERATION=1`` and at most two token rows the fused
+    dynamic-scale GEMV runs instead.  Exported checkpoints also load their
+    token embedding through this type; :meth:`embedding` gathers and decodes
+    only the requested rows.
     """
 
     quant_type = SOFT_QUANT_TYPE
+    supports_tp_weight_switch = False
 
     def get_weight(self, input_size: int, output_size: int, params_dtype: torch.dtype) -> dict[str, Any]:
         return {"weight": torch.empty(output_size, input_size, dtype=torch.uint8)}
@@ -139,6 +143,7 @@ class W8A8HiFloat8SoftEmbeddingMethod:
         return {"weight_scale": torch.empty(output_size, 1, dtype=torch.float32)}
 
     def process_weights_after_loading(self, layer: torch.nn.Module) -> None:
+        """scheme.py:59-91 (the decode table lives in the kernels, not in a buffer)."""
         if layer.weight.dtype != torch.uint8:
             raise TypeError(f"{self.quant_type} checkpoint weight must be torch.uint8, got {layer.weight.dtype}")
         if layer.weight_scale.dtype != torch.float32:
@@ -150,7 +155,29 @@ class W8A8HiFloat8SoftEmbeddingMethod:
             raise ValueError(
                 f"unsupported {_COMPUTE_BACKEND_ENV}={backend!r}; only '{_SOFT_HIF8_BACKEND}' is supported"
             )
+        layer._hif8_compute_backend = backend
+
+    def apply(
+        self,
+        layer: torch.nn.Module,
+        x: torch.Tensor,
+        bias: torch.Tensor | None = None,
+        tp_rank: int | None = 0,
+    ) -> torch.Tensor:
+        """dynamic_quant -> soft_linear, or the fused kernel for one or two rows (scheme.py:93-118)."""
+        del tp_rank
+        token_rows = x.numel() // x.shape[-1]
+        if token_rows <= 2 and os.environ.get(_SOFT_FUSED_GENERATION_ENV) == "1":
+            return native.soft_fused_linear(x, layer.weight, layer.weight_scale, bias, output_dtype=x.dtype)
+        activation, activation_scale = native.dynamic_quant(x)
+        return native.soft_linear(
+            activation, layer.weight, activation_scale, layer.weight_scale, bias, output_dtype=x.dtype
+        )
 
     def embedding(self, layer: torch.nn.Module, input_ids: torch.Tensor) -> torch.Tensor:
         """Gather and dequantize only the requested token embedding rows (scheme.py:121-131)."""
         return native.embedding_lookup(layer.weight, layer.weight_scale, input_ids)
+
+
+# The token embedding of an exported checkpoint loads through the same type.
+W8A8HiFloat8SoftEmbeddingMethod = W8A8HiFloat8SoftLinearMethod

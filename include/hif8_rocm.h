@@ -74,6 +74,20 @@ int hif8_static_quant(const void *x, int x_dtype, int64_t rows, int64_t k,
                       uint8_t *data, float *row_scale, hif8_stream_t stream);
 
 /*
+ * Dynamic per-row activation quantisation (the legacy W8A8HIF8_SOFT scheme).
+ * Replaces aclnnHif8DynamicQuant as called by Hif8DynamicQuant
+ * (csrc/extension/hif8_native.cpp:433-485; kernel csrc/opp/op_kernel/hif8_dynamic_quant.cpp:35-200).
+ *   x         [rows, k] fp16/bf16
+ *   row_scale [rows] float32 <- max(max |x[r, :]| over finite values, 1e-12)
+ *             (contiguous; the reference returns a stride-16 view)
+ *   data      [rows, k] uint8 <- enc(float(x) * RN(1 / row_scale)) when k % 32 == 0,
+ *             enc(float(x) / row_scale) otherwise (the reference's vector and
+ *             scalar paths); NaN -> 0x80, Inf kept, zero magnitude unsigned
+ */
+int hif8_dynamic_quant(const void *x, int x_dtype, int64_t rows, int64_t k, uint8_t *data,
+                       float *row_scale, hif8_stream_t stream);
+
+/*
  * Scaled decode to bf16.
  * Replaces aclnnHif8ScaledDecode as called by Hif8ScaledDecode
  * (csrc/extension/hif8_native.cpp:556-611; kernel csrc/opp/op_kernel/hif8_scaled_decode.cpp:50-125).
@@ -160,6 +174,20 @@ int soft_hif8_static_fused_gemm(const void *x, int x_dtype, const uint8_t *weigh
                                 const float *fixed_scale, const float *channel_scale,
                                 const void *bias, int bias_dtype, void *out, int out_dtype,
                                 int64_t m, int64_t n, int64_t k, hif8_stream_t stream);
+
+/*
+ * Dynamic-scale fused quant + GEMM for M <= 2 (the legacy soft scheme's
+ * HIF8_SOFT_FUSED_GENERATION path).
+ * Replaces aclnnSoftHif8FusedGemm as called by SoftHif8FusedGemm
+ * (csrc/extension/hif8_native.cpp:671-782; kernel csrc/opp/op_kernel/soft_hif8_fused_gemm.cpp
+ * with the dynamic scale, lines 445-571 and 720-745):
+ *   s[m] = max(finite amax of x[m, :], 1e-12);  a = dec(enc(float(x) / s[m]))  (IEEE division)
+ *   out[m, n] = sum_k a[m, k] dec(w[n, k]) * s[m] * channel_scale[n] (+ bias[n])
+ *   x [m, k] fp16/bf16 (x_dtype); other arguments as soft_hif8_gemm.
+ */
+int soft_hif8_fused_gemm(const void *x, int x_dtype, const uint8_t *weight, const float *channel_scale,
+                         const void *bias, int bias_dtype, void *out, int out_dtype, int64_t m, int64_t n,
+                         int64_t k, hif8_stream_t stream);
 
 /*
  * Fused static KV-cache write (quantise + pack + scatter in one launch).

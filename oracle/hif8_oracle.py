@@ -25,6 +25,12 @@ function) is listed per function:
 * embedding gather-decode            - the reference formula executed by torch on the
                                       CPU (bf16 table, bf16 scale, bf16 product) and
                                       closed-form products
+* dynamic quant                      - the reference's known-answer rows (test_npu_ops.py:
+                                      30-50), scale = finite amax exactly, and the
+                                      reciprocal path equal to the float64 division encode
+                                      except within 2 ulp of a rounding midpoint
+* dynamic fused linear               - fp64 brute force (division encode, decode, dot)
+                                      and equality with dynamic quant on exact rows
 """
 
 from __future__ import annotations
@@ -324,6 +330,48 @@ def linear_u8_u8(a: np.ndarray, a_scale, w: np.ndarray, w_scale, bias=None) -> n
         if bias is not None:
             y = y + np.asarray(bias, dtype=np.float64).reshape(1, -1)
     return y
+
+
+def dynamic_quant_rows(x: np.ndarray) -> tuple[np.ndarray, np.ndarray]:
+    """The ``hif8_dynamic_quant`` contract on [rows, K] input.
+
+    scale[r] = max(max |x[r, :]| over finite values, 1e-12) in float32
+    (hif8_dynamic_quant.cpp:64-78 and 112-135: ReduceMax, non-finite values
+    ignored, kScaleEpsilon = 1e-12 from hif8_codec.h:20).  For K % 32 == 0
+    the kernel multiplies by the float32 reciprocal (Muls(normalized, 1/scale),
+    hif8_dynamic_quant.cpp:137) and encodes through the signed table or the
+    scalar encoder (:138-171); other K take the scalar path with a true
+    division (:64-79).  Returns (u8 [rows, K], f32 scale [rows]).
+    """
+    x = np.asarray(x, dtype=np.float32)
+    k = x.shape[-1]
+    rows = x.size // k if k else 0
+    x2 = x.reshape(rows, k)
+    finite = np.isfinite(x2)
+    amax = np.where(finite, np.abs(x2), np.float32(0)).max(axis=1).astype(np.float32)
+    scale = np.maximum(amax, np.float32(1.0e-12)).astype(np.float32)
+    with np.errstate(all="ignore"):
+        if k % 32 == 0:
+            q = x2 * (np.float32(1.0) / scale)[:, None]
+        else:
+            q = x2 / scale[:, None]
+    return encode_array(q.astype(np.float32)).reshape(x.shape), scale
+
+
+def soft_fused_linear_reference(x: np.ndarray, w: np.ndarray, w_scale, bias=None) -> np.ndarray:
+    """``soft_hif8_fused_gemm`` with the dynamic scale, float64 accumulation.
+
+    s[m] = max(finite amax of row m, 1e-12) (soft_hif8_fused_gemm.cpp:536-566);
+    the activation is encoded with a true float32 division and decoded
+    (:506-516); out = dot(dec(a), dec(w)) * channel_scale * s (+ bias) (:730-745).
+    """
+    x = np.asarray(x, dtype=np.float32)
+    finite = np.isfinite(x)
+    amax = np.where(finite, np.abs(x), np.float32(0)).max(axis=1).astype(np.float32)
+    s = np.maximum(amax, np.float32(1.0e-12)).astype(np.float32)
+    with np.errstate(all="ignore"):
+        codes = encode_array((x / s[:, None]).astype(np.float32))
+    return linear_u8_u8(codes, s.astype(np.float64), w, w_scale, bias)
 
 
 def linear_u8_u8_pure(a, a_scale, w, w_scale, bias=None):

@@ -30,15 +30,15 @@ def test_missing_extension_raises_without_fallback():
 
 
 def test_missing_symbol_is_rejected():
-    incomplete = types.SimpleNamespace(hif8_static_quant=lambda *a: a)
+    incomplete = types.SimpleNamespace(hif8_dynamic_quant=lambda *a: a, hif8_static_quant=lambda *a: a)
     with patch("importlib.import_module", return_value=incomplete):
         with pytest.raises(native.NativeExtensionUnavailable, match="soft_hif8_gemv"):
             native.load_extension()
 
 
 def test_valid_extension_is_cached():
-    complete = types.SimpleNamespace(hif8_static_quant=lambda *a: a, soft_hif8_gemv=lambda *a: a,
-                                     soft_hif8_gemm=lambda *a: a)
+    complete = types.SimpleNamespace(hif8_dynamic_quant=lambda *a: a, hif8_static_quant=lambda *a: a,
+                                     soft_hif8_gemv=lambda *a: a, soft_hif8_gemm=lambda *a: a)
     with patch("importlib.import_module", return_value=complete) as importer:
         assert native.load_extension() is complete
         assert native.load_extension() is complete
@@ -47,8 +47,8 @@ def test_valid_extension_is_cached():
 
 def test_real_extension_loads_on_cpu():
     ext = native.load_extension()
-    for name in ("hif8_static_quant", "hif8_scaled_decode", "soft_hif8_gemv", "soft_hif8_gemm",
-                 "soft_hif8_static_fused_gemm"):
+    for name in ("hif8_dynamic_quant", "hif8_static_quant", "hif8_scaled_decode", "soft_hif8_gemv",
+                 "soft_hif8_gemm", "soft_hif8_static_fused_gemm", "soft_hif8_fused_gemm"):
         assert callable(getattr(ext, name))
         assert callable(getattr(torch.ops.vllm_ascend_hif8, name))
     for name in ("hif8_kv_cache_write", "hif8_paged_decode_attention", "hif8_embedding_lookup"):
@@ -65,6 +65,12 @@ def test_meta_shapes():
         torch.empty(5, 64, dtype=torch.uint8, device="meta"), torch.empty(7, 64, dtype=torch.uint8, device="meta"),
         torch.empty(5, device="meta"), torch.empty(7, device="meta"), None, torch.bfloat16)
     assert y.shape == (5, 7) and y.dtype == torch.bfloat16
+    d, ds = torch.ops.vllm_ascend_hif8.hif8_dynamic_quant(x)
+    assert d.shape == x.shape and d.dtype == torch.uint8 and ds.shape == (6,) and ds.dtype == torch.float32
+    f = torch.ops.vllm_ascend_hif8.soft_hif8_fused_gemm(
+        torch.empty(2, 64, dtype=torch.float16, device="meta"), torch.empty(7, 64, dtype=torch.uint8, device="meta"),
+        torch.empty(7, device="meta"), None, torch.float16)
+    assert f.shape == (2, 7) and f.dtype == torch.float16
     e = torch.ops.vllm_ascend_hif8.hif8_embedding_lookup(
         torch.empty(2, 3, dtype=torch.int64, device="meta"), torch.empty(50, 64, dtype=torch.uint8, device="meta"),
         torch.empty(50, device="meta"))
@@ -246,3 +252,60 @@ def test_scale_factor_env_multiplies_the_checkpoint_scale(clean_env):
     os.environ["HIF8_STATIC_SCALE_FACTOR"] = "-1"
     with pytest.raises(ValueError, match="positive finite"):
         method.apply(layer, x)
+
+
+def test_soft_method_defaults_to_dynamic_quant_then_soft_linear(clean_env):
+    from hif8_rocm.scheme import SOFT_QUANT_TYPE, W8A8HiFloat8SoftLinearMethod
+
+    os.environ.pop("HIF8_SOFT_FUSED_GENERATION", None)
+    method = W8A8HiFloat8SoftLinearMethod()
+    assert method.quant_type == SOFT_QUANT_TYPE == "W8A8HIF8_SOFT"
+    layer = _layer()
+    del layer.input_scale
+    method.process_weights_after_loading(layer)
+    x = torch.randn((2, 8), dtype=torch.bfloat16)
+    enc, ts, out = torch.zeros_like(x, dtype=torch.uint8), torch.full((2,), 3.0), torch.randn(2, 5)
+    with patch("hif8_rocm.scheme.native.dynamic_quant", return_value=(enc, ts)) as dq, \
+         patch("hif8_rocm.scheme.native.soft_fused_linear") as fused, \
+         patch("hif8_rocm.scheme.native.soft_linear", return_value=out) as lin:
+        assert method.apply(layer, x, None) is out
+    dq.assert_called_once_with(x)
+    fused.assert_not_called()
+    lin.assert_called_once_with(enc, layer.weight, ts, layer.weight_scale, None, output_dtype=x.dtype)
+
+
+def test_soft_fused_generation_is_opt_in_for_two_rows(clean_env):
+    from hif8_rocm.scheme import W8A8HiFloat8SoftLinearMethod
+
+    os.environ["HIF8_SOFT_FUSED_GENERATION"] = "1"
+    try:
+        method = W8A8HiFloat8SoftLinearMethod()
+        layer = _layer()
+        method.process_weights_after_loading(layer)
+        out = torch.randn(2, 5)
+        with patch("hif8_rocm.scheme.native.dynamic_quant") as dq, \
+             patch("hif8_rocm.scheme.native.soft_fused_linear", return_value=out) as fused:
+            assert method.apply(layer, torch.randn((2, 8), dtype=torch.bfloat16)) is out
+        dq.assert_not_called()
+        fused.assert_called_once()
+        x = torch.zeros((3, 8), dtype=torch.bfloat16)
+        with patch("hif8_rocm.scheme.native.dynamic_quant", return_value=(x.to(torch.uint8), torch.ones(3))) as dq, \
+             patch("hif8_rocm.scheme.native.soft_linear", return_value=out), \
+             patch("hif8_rocm.scheme.native.soft_fused_linear") as fused:
+            method.apply(layer, x)
+        dq.assert_called_once()
+        fused.assert_not_called()
+    finally:
+        os.environ.pop("HIF8_SOFT_FUSED_GENERATION", None)
+
+
+def test_soft_fused_linear_validates_like_the_reference():
+    w = torch.zeros(4, 8, dtype=torch.uint8)
+    with pytest.raises(TypeError, match="FP16/BF16 activation"):
+        native.soft_fused_linear(torch.zeros(1, 8), w, torch.ones(4), output_dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="compatible final K"):
+        native.soft_fused_linear(torch.zeros(1, 7, dtype=torch.bfloat16), w, torch.ones(4), output_dtype=torch.bfloat16)
+    with pytest.raises(TypeError, match="one float32 scale per output channel"):
+        native.soft_fused_linear(torch.zeros(1, 8, dtype=torch.bfloat16), w, torch.ones(3), output_dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="M <= 2"):
+        native.soft_fused_linear(torch.zeros(3, 8, dtype=torch.bfloat16), w, torch.ones(4), output_dtype=torch.bfloat16)
