@@ -466,12 +466,53 @@ def committed_traffic(kernel_key: str):
     return None if entry is None else entry.get("traffic_bytes")
 
 
+E2E_PROMPT, E2E_NEW = 512, 256
+
+
+def e2e_decode(torch, device) -> dict:
+    """greedy decode through the static scheme of a
+    random-init Qwen3.5-9B-shaped hybrid (hif8_rocm.synthetic_model), random
+    prompt ids, 512 prompt + 256 new tokens at batch 1 and 4.  Output tok/s
+    = batch x 256 / (prefill + 255 decode steps at the graph-replay rate);
+    the first decode step and the graph recording (done once per process by a
+    server) are reported apart."""
+    from hif8_rocm.synthetic_model import HybridConfig, HybridModel, generate
+
+    cfg = HybridConfig()
+    t0 = time.perf_counter()
+    model = HybridModel(cfg, device, seed=0)
+    model.calibrate(batch=1, tokens=128)
+    torch.cuda.synchronize()
+    res = {"workload": "BASELINE configs[4]: random-init Qwen3.5-9B-shaped hybrid (32 layers, hidden 4096, "
+                       "full attention every 4th layer with HiF8 KV, gated-delta-rule layers, intermediate "
+                       "12288, vocab 151936); every projection W8A8 HiF8 static through the scheme, embedding "
+                       "HiF8 SOFT, norms / conv / recurrence / LM head in bf16-fp32 torch; greedy, random ids",
+           "prompt_tokens": E2E_PROMPT, "new_tokens": E2E_NEW, "build_and_calibrate_s": round(time.perf_counter() - t0, 2)}
+    g = torch.Generator(device=device).manual_seed(9)
+    for b in (1, 4):
+        prompt = torch.randint(0, cfg.vocab, (b, E2E_PROMPT), generator=g, device=device)
+        generate(model, prompt[:, :64], 4)  # warm-up: allocator, kernels, graph capture path
+        _, tm = generate(model, prompt, E2E_NEW)
+        step_s = tm["decode"] / tm["decode_steps"]
+        total = tm["prefill"] + step_s * (E2E_NEW - 1)
+        res[f"b{b}"] = {"prefill_ms": round(tm["prefill"] * 1e3, 2), "ms_per_decode_step": round(step_s * 1e3, 3),
+                        "first_step_and_graph_record_ms": round(tm["setup"] * 1e3, 1),
+                        "decode_tok_per_s": round(b / step_s, 1),
+                        "output_tok_per_s": round(b * E2E_NEW / total, 1)}
+        log(f"e2e b{b}: prefill {tm['prefill'] * 1e3:.1f} ms, {step_s * 1e3:.3f} ms/step, "
+            f"{res[f'b{b}']['output_tok_per_s']} output tok/s")
+    del model
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the synthetic end-to-end decode (config 5)")
     ap.add_argument("--profile-pass", action="store_true",
                     help="eager launches only, for rocprofv3 counter collection; prints no JSON")
     args = ap.parse_args()
@@ -553,6 +594,11 @@ def main() -> None:
     kv_attn = kv_attention_bench(kvs, args.steps)
     kv_write = kv_write_bench(kvs)
     kv_dom = kv_attn[f"b{KV_BATCH[-1]}_ctx{KV_CTX[-1]}"]
+    e2e = None
+    if not args.no_e2e:
+        del kvs
+        log("end-to-end synthetic decode ...")
+        e2e = e2e_decode(torch, device)
 
     out = {
         "metric": METRIC,
@@ -604,6 +650,7 @@ def main() -> None:
         "gemm_per_layer": gemm_layer,
         "ceilings": ceilings,
         "decode_ops": aux,
+        "e2e_decode": e2e,
         "kernels": table,
     }
     print(json.dumps(out), flush=True)
