@@ -1,0 +1,268 @@
+// Decode-step glue of the synthetic hybrid model (the config-5 workload),
+// fused so that one decode step is a few launches per layer instead of tens
+// of elementwise ones.  None of these is a HiF8 operator; they are the bf16 /
+// fp32 parts the reference leaves to the model (norms, the MLP activation,
+// the linear-attention conv and recurrence).
+//
+//   hif8_add_rms_norm     h <- bf16(h + delta) (optional), out = bf16(h * rsqrt(mean(h^2) + eps) * w)
+//   hif8_silu_mul         out[r, i] = bf16(silu(gu[r, i]) * gu[r, n + i])
+//   hif8_gdn_decode_step  one token of the gated delta rule per request and value head:
+//       causal depthwise conv over the q|k|v channels with the carried state, SiLU;
+//       q, k L2-normalised (q also / sqrt(dk)), k/q heads shared by v_heads / k_heads
+//       value heads; beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias);
+//       S <- e^g S;  S <- S + k (beta (v - S^T k))^T;  o = S^T q;
+//       out = bf16(rms_norm(o) * w_out * silu(z)).
+//   hif8_qk_norm_rope     per-head RMSNorm of q and k, rotary embedding on the
+//       first rotary_dim dims (neox halves), v split off, cache slots.
+#include <math.h>
+
+#include <algorithm>
+
+#include "hif8_common.h"
+#include "hif8_rocm.h"
+
+namespace hif8 {
+namespace {
+
+__device__ __forceinline__ float bf(uint16_t h) { return __uint_as_float(uint32_t(h) << 16); }
+__device__ __forceinline__ uint16_t to_bf(float f) { return float_to_bf16_bits(f); }
+
+template <int kThreads>
+__device__ __forceinline__ float block_sum(float v, float *red) {
+  v = wave_sum(v);
+  const int w = threadIdx.x / kWave;
+  __syncthreads();  // red may still be read by a previous reduction
+  if (threadIdx.x % kWave == 0) red[w] = v;
+  __syncthreads();
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < kThreads / kWave; ++i) s += red[i];
+  return s;
+}
+
+constexpr int kNormThreads = 256;
+
+template <bool kResidual>
+__global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(uint16_t *__restrict__ h,
+                                                                    const uint16_t *__restrict__ delta,
+                                                                    const uint16_t *__restrict__ w,
+                                                                    uint16_t *__restrict__ out, int n, float eps) {
+  __shared__ float red[kNormThreads / kWave];
+  uint16_t *hr = h + size_t(blockIdx.x) * n;
+  const uint16_t *dr = kResidual ? delta + size_t(blockIdx.x) * n : nullptr;
+  uint16_t *orow = out + size_t(blockIdx.x) * n;
+  float ss = 0.f;
+  for (int i = threadIdx.x; i < n; i += kNormThreads) {
+    float v = bf(hr[i]);
+    if constexpr (kResidual) {
+      const uint16_t s = to_bf(v + bf(dr[i]));  // the residual stream is bf16
+      hr[i] = s;
+      v = bf(s);
+    }
+    ss += v * v;
+  }
+  const float r = rsqrtf(block_sum<kNormThreads>(ss, red) / float(n) + eps);
+  for (int i = threadIdx.x; i < n; i += kNormThreads) orow[i] = to_bf(bf(hr[i]) * r * bf(w[i]));
+}
+
+__global__ __launch_bounds__(256) void silu_mul_kernel(const uint16_t *__restrict__ gu, uint16_t *__restrict__ out,
+                                                       int64_t rows, int n) {
+  const int64_t total = rows * n;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
+    const int64_t r = i / n, c = i - r * n;
+    const float g = bf(gu[r * 2 * n + c]), u = bf(gu[r * 2 * n + n + c]);
+    out[i] = to_bf(g / (1.f + expf(-g)) * u);
+  }
+}
+
+// Conv over channel c of request b: out = silu(sum_j w[c, j] seq[j]),
+// seq = (state[b, c, 0 .. K-2], x); the state shifts by one.
+__global__ __launch_bounds__(256) void gdn_conv_kernel(const uint16_t *__restrict__ mixed, int64_t ld, int channels,
+                                                       const uint16_t *__restrict__ w, uint16_t *__restrict__ state,
+                                                       float *__restrict__ out, int batch, int kw) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= batch * channels) return;
+  const int b = idx / channels, c = idx - b * channels;
+  uint16_t *st = state + size_t(idx) * (kw - 1);
+  const uint16_t x = mixed[size_t(b) * ld + c];
+  float acc = 0.f;
+  for (int j = 0; j < kw - 1; ++j) acc += bf(st[j]) * bf(w[size_t(c) * kw + j]);
+  acc += bf(x) * bf(w[size_t(c) * kw + kw - 1]);
+  for (int j = 0; j + 1 < kw - 1; ++j) st[j] = st[j + 1];
+  st[kw - 2] = x;
+  out[idx] = acc / (1.f + expf(-acc));
+}
+
+constexpr int kGdnThreads = 128;
+
+// One block per (request, value head); thread j owns column j of the
+// [dk, dv] state (dk, dv <= 128).
+__global__ __launch_bounds__(kGdnThreads) void gdn_delta_kernel(
+    const float *__restrict__ conv, int channels, const uint16_t *__restrict__ mixed, int64_t ld,
+    const uint16_t *__restrict__ ba, const float *__restrict__ a_log, const float *__restrict__ dt_bias,
+    float *__restrict__ state, const uint16_t *__restrict__ w_out, uint16_t *__restrict__ out, int k_heads,
+    int v_heads, int dk, int dv, float eps) {
+  __shared__ float qs[kGdnThreads], ks[kGdnThreads];
+  __shared__ float red[kGdnThreads / kWave];
+  const int b = blockIdx.x / v_heads, hv = blockIdx.x - b * v_heads;
+  const int hk = hv / (v_heads / k_heads);
+  const int qk_width = k_heads * dk;
+  const int j = threadIdx.x;
+  const float *cr = conv + size_t(b) * channels;
+  const float qi = j < dk ? cr[hk * dk + j] : 0.f;
+  const float ki = j < dk ? cr[qk_width + hk * dk + j] : 0.f;
+  const float vj = j < dv ? cr[2 * qk_width + hv * dv + j] : 0.f;
+  // F.normalize: x / max(||x||, 1e-12); q also scaled by 1 / sqrt(dk).
+  const float qn = fmaxf(sqrtf(block_sum<kGdnThreads>(qi * qi, red)), 1e-12f);
+  const float kn = fmaxf(sqrtf(block_sum<kGdnThreads>(ki * ki, red)), 1e-12f);
+  const float qv = qi / qn / sqrtf(float(dk)), kv = ki / kn;
+  qs[j] = qv;
+  ks[j] = kv;
+  const float kq = block_sum<kGdnThreads>(kv * qv, red);  // also orders the qs / ks stores
+  const float braw = bf(ba[size_t(b) * 2 * v_heads + hv]);
+  const float araw = bf(ba[size_t(b) * 2 * v_heads + v_heads + hv]) + dt_bias[hv];
+  const float beta = 1.f / (1.f + expf(-braw));
+  const float softplus = araw > 20.f ? araw : log1pf(expf(araw));
+  const float decay = expf(-expf(a_log[hv]) * softplus);
+  float *S = state + (size_t(b) * v_heads + hv) * dk * dv;
+  float o = 0.f;
+  if (j < dv) {
+    float a = 0.f, c = 0.f;
+    for (int i = 0; i < dk; ++i) {
+      const float s = S[size_t(i) * dv + j];
+      a += s * ks[i];
+      c += s * qs[i];
+    }
+    const float delta = beta * (vj - decay * a);
+    o = decay * c + delta * kq;
+    for (int i = 0; i < dk; ++i) {
+      float *p = S + size_t(i) * dv + j;
+      *p = decay * *p + ks[i] * delta;
+    }
+  }
+  const float r = rsqrtf(block_sum<kGdnThreads>(j < dv ? o * o : 0.f, red) / float(dv) + eps);
+  if (j < dv) {
+    const float z = bf(mixed[size_t(b) * ld + 2 * qk_width + v_heads * dv + hv * dv + j]);
+    out[(size_t(b) * v_heads + hv) * dv + j] = to_bf(o * r * bf(w_out[j]) * (z / (1.f + expf(-z))));
+  }
+}
+
+constexpr int kHeadThreads = 256;
+
+// One block per (request, head of q | k | v) of a decode token: q and k heads
+// RMS-normalised (weight w_q / w_k) and rotated on their first rot dims
+// (halves i, i + rot/2, angle pos * inv_freq[i]); v heads copied.  Block
+// (b, 0) also writes the cache slot of position pos[b].
+__global__ __launch_bounds__(kHeadThreads) void qk_norm_rope_kernel(
+    const uint16_t *__restrict__ qkv, const uint16_t *__restrict__ w_q, const uint16_t *__restrict__ w_k,
+    const int64_t *__restrict__ pos, const float *__restrict__ inv_freq, const int32_t *__restrict__ block_table,
+    int64_t max_blocks, int block_size, uint16_t *__restrict__ q_out, uint16_t *__restrict__ k_out,
+    uint16_t *__restrict__ v_out, int64_t *__restrict__ slots, int hq, int hkv, int d, int rot, float eps) {
+  __shared__ float y[kHeadThreads];
+  __shared__ float red[kHeadThreads / kWave];
+  const int heads = hq + 2 * hkv;
+  const int b = blockIdx.x / heads, h = blockIdx.x - b * heads;
+  const int j = threadIdx.x;
+  const float x = j < d ? bf(qkv[(size_t(b) * heads + h) * d + j]) : 0.f;
+  const int64_t p = pos[b];
+  if (h == 0 && j == 0 && slots) {
+    const int64_t blk = block_table[size_t(b) * max_blocks + p / block_size];
+    slots[b] = blk * block_size + p % block_size;
+  }
+  if (h >= hq + hkv) {
+    if (j < d) v_out[(size_t(b) * hkv + (h - hq - hkv)) * d + j] = qkv[(size_t(b) * heads + h) * d + j];
+    return;
+  }
+  const bool is_q = h < hq;
+  const float r = rsqrtf(block_sum<kHeadThreads>(x * x, red) / float(d) + eps);
+  const float yn = j < d ? bf(to_bf(x * r * bf((is_q ? w_q : w_k)[j]))) : 0.f;  // the normed head is bf16
+  y[j] = yn;
+  __syncthreads();
+  float out = yn;
+  if (j < rot) {
+    const int half = rot / 2, i = j < half ? j : j - half;
+    const float ang = float(p) * inv_freq[i];
+    const float c = cosf(ang), s = sinf(ang);
+    out = j < half ? y[j] * c - y[j + half] * s : y[j] * c + y[j - half] * s;
+  }
+  if (j < d) {
+    uint16_t *dst = is_q ? q_out + (size_t(b) * hq + h) * d : k_out + (size_t(b) * hkv + (h - hq)) * d;
+    dst[j] = to_bf(out);
+  }
+}
+
+}  // namespace
+}  // namespace hif8
+
+using namespace hif8;
+
+extern "C" int hif8_qk_norm_rope(const uint16_t *qkv, const uint16_t *q_norm, const uint16_t *k_norm,
+                                 const int64_t *pos, const float *inv_freq, const int32_t *block_table,
+                                 int64_t max_blocks, int64_t block_size, uint16_t *q_out, uint16_t *k_out,
+                                 uint16_t *v_out, int64_t *slots, int64_t batch, int64_t num_heads,
+                                 int64_t num_kv_heads, int64_t head_size, int64_t rotary_dim, float eps,
+                                 hif8_stream_t stream) {
+  clear_error();
+  if (!qkv || !q_norm || !k_norm || !pos || !inv_freq || !q_out || !k_out || !v_out || (slots && !block_table))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_qk_norm_rope: null pointer argument");
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_size <= 0 || head_size > kHeadThreads ||
+      rotary_dim < 0 || rotary_dim > head_size || rotary_dim % 2 || block_size <= 0 || batch > 65536)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_qk_norm_rope: unsupported dimensions");
+  qk_norm_rope_kernel<<<unsigned(batch * (num_heads + 2 * num_kv_heads)), kHeadThreads, 0,
+                        reinterpret_cast<hipStream_t>(stream)>>>(
+      qkv, q_norm, k_norm, pos, inv_freq, block_table, max_blocks, int(block_size), q_out, k_out, v_out, slots,
+      int(num_heads), int(num_kv_heads), int(head_size), int(rotary_dim), eps);
+  return check_launch("hif8_qk_norm_rope");
+}
+
+extern "C" int hif8_add_rms_norm(uint16_t *h, const uint16_t *delta, const uint16_t *weight, uint16_t *out,
+                                 int64_t rows, int64_t n, float eps, hif8_stream_t stream) {
+  clear_error();
+  if (!h || !weight || !out) return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_add_rms_norm: null pointer argument");
+  if (rows <= 0 || n <= 0 || rows > 0x7FFFFFFFll || n > 0x7FFFFFFFll)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_add_rms_norm: invalid dimensions");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (delta)
+    add_rms_norm_kernel<true><<<unsigned(rows), kNormThreads, 0, s>>>(h, delta, weight, out, int(n), eps);
+  else
+    add_rms_norm_kernel<false><<<unsigned(rows), kNormThreads, 0, s>>>(h, nullptr, weight, out, int(n), eps);
+  return check_launch("hif8_add_rms_norm");
+}
+
+extern "C" int hif8_silu_mul(const uint16_t *gate_up, uint16_t *out, int64_t rows, int64_t n, hif8_stream_t stream) {
+  clear_error();
+  if (!gate_up || !out) return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_silu_mul: null pointer argument");
+  if (rows <= 0 || n <= 0 || n > 0x7FFFFFFFll) return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_silu_mul: invalid dimensions");
+  const int64_t blocks = std::min<int64_t>((rows * n + 255) / 256, 4096);
+  silu_mul_kernel<<<unsigned(blocks), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(gate_up, out, rows, int(n));
+  return check_launch("hif8_silu_mul");
+}
+
+extern "C" int hif8_gdn_decode_step(const uint16_t *mixed_qkvz, int64_t ld, const uint16_t *ba,
+                                    const uint16_t *conv_weight, uint16_t *conv_state, const float *a_log,
+                                    const float *dt_bias, float *rec_state, const uint16_t *out_norm,
+                                    uint16_t *out, float *conv_scratch, int64_t batch, int64_t k_heads,
+                                    int64_t v_heads, int64_t k_dim, int64_t v_dim, int64_t conv_width, float eps,
+                                    hif8_stream_t stream) {
+  clear_error();
+  if (!mixed_qkvz || !ba || !conv_weight || !conv_state || !a_log || !dt_bias || !rec_state || !out_norm || !out ||
+      !conv_scratch)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gdn_decode_step: null pointer argument");
+  if (batch <= 0 || k_heads <= 0 || v_heads <= 0 || v_heads % k_heads || k_dim <= 0 || v_dim <= 0 ||
+      k_dim > kGdnThreads || v_dim > kGdnThreads || conv_width < 2 || conv_width > 16 || batch > 65536)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gdn_decode_step: unsupported dimensions");
+  const int64_t channels = 2 * k_heads * k_dim + v_heads * v_dim;
+  if (ld < channels + v_heads * v_dim)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gdn_decode_step: mixed_qkvz row too short");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const int64_t items = batch * channels;
+  gdn_conv_kernel<<<unsigned((items + 255) / 256), 256, 0, s>>>(mixed_qkvz, ld, int(channels), conv_weight,
+                                                                conv_state, conv_scratch, int(batch),
+                                                                int(conv_width));
+  int st = check_launch("hif8_gdn_decode_step (conv)");
+  if (st) return st;
+  gdn_delta_kernel<<<unsigned(batch * v_heads), kGdnThreads, 0, s>>>(
+      conv_scratch, int(channels), mixed_qkvz, ld, ba, a_log, dt_bias, rec_state, out_norm, out, int(k_heads),
+      int(v_heads), int(k_dim), int(v_dim), eps);
+  return check_launch("hif8_gdn_decode_step (delta rule)");
+}

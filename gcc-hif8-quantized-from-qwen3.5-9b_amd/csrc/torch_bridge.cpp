@@ -459,6 +459,116 @@ at::Tensor Hif8EmbeddingLookup(const at::Tensor &ids, const at::Tensor &weight, 
   return out;
 }
 
+// ------------------------------------------------- synthetic-model glue
+
+at::Tensor Hif8AddRmsNorm(at::Tensor &h, const c10::optional<at::Tensor> &delta, const at::Tensor &weight,
+                          double eps) {
+  CheckContiguousDevice(h, "h");
+  CheckContiguousDevice(weight, "weight");
+  TORCH_CHECK(h.scalar_type() == at::kBFloat16 && weight.scalar_type() == at::kBFloat16,
+              "hif8_add_rms_norm takes bfloat16 tensors");
+  const int64_t n = h.size(-1);
+  TORCH_CHECK(weight.numel() == n, "weight must have the row width");
+  if (delta.has_value()) {
+    CheckContiguousDevice(*delta, "delta");
+    TORCH_CHECK(delta->scalar_type() == at::kBFloat16 && delta->sizes() == h.sizes(), "delta must match h");
+  }
+  const c10::OptionalDeviceGuard guard(h.device());
+  auto out = at::empty_like(h);
+  CheckStatus(hif8_add_rms_norm(reinterpret_cast<uint16_t *>(h.data_ptr()),
+                                delta.has_value() ? reinterpret_cast<const uint16_t *>(delta->data_ptr()) : nullptr,
+                                reinterpret_cast<const uint16_t *>(weight.data_ptr()),
+                                reinterpret_cast<uint16_t *>(out.data_ptr()), h.numel() / n, n, float(eps),
+                                CurrentStream(h.device())),
+              "hif8_add_rms_norm");
+  return out;
+}
+
+at::Tensor Hif8SiluMul(const at::Tensor &gate_up) {
+  CheckContiguousDevice(gate_up, "gate_up");
+  TORCH_CHECK(gate_up.scalar_type() == at::kBFloat16, "hif8_silu_mul takes bfloat16");
+  TORCH_CHECK(gate_up.size(-1) % 2 == 0, "gate_up width must be even");
+  const int64_t n = gate_up.size(-1) / 2;
+  std::vector<int64_t> shape(gate_up.sizes().begin(), gate_up.sizes().end());
+  shape.back() = n;
+  const c10::OptionalDeviceGuard guard(gate_up.device());
+  auto out = at::empty(shape, gate_up.options());
+  CheckStatus(hif8_silu_mul(reinterpret_cast<const uint16_t *>(gate_up.data_ptr()),
+                            reinterpret_cast<uint16_t *>(out.data_ptr()), gate_up.numel() / (2 * n), n,
+                            CurrentStream(gate_up.device())),
+              "hif8_silu_mul");
+  return out;
+}
+
+at::Tensor Hif8GdnDecodeStep(const at::Tensor &mixed, const at::Tensor &ba, const at::Tensor &conv_weight,
+                             at::Tensor &conv_state, const at::Tensor &a_log, const at::Tensor &dt_bias,
+                             at::Tensor &rec_state, const at::Tensor &out_norm, int64_t k_heads, int64_t v_heads,
+                             int64_t k_dim, int64_t v_dim, double eps) {
+  for (auto *t : {&mixed, &ba, &conv_weight, &a_log, &dt_bias, &out_norm}) CheckContiguousDevice(*t, "operand");
+  CheckContiguousDevice(conv_state, "conv_state");
+  CheckContiguousDevice(rec_state, "rec_state");
+  TORCH_CHECK(mixed.dim() == 2 && ba.dim() == 2 && conv_weight.dim() == 2 && conv_state.dim() == 3 &&
+                  rec_state.dim() == 4, "hif8_gdn_decode_step: operand ranks");
+  const int64_t batch = mixed.size(0);
+  const int64_t channels = 2 * k_heads * k_dim + v_heads * v_dim;
+  TORCH_CHECK(mixed.scalar_type() == at::kBFloat16 && ba.scalar_type() == at::kBFloat16 &&
+                  conv_weight.scalar_type() == at::kBFloat16 && conv_state.scalar_type() == at::kBFloat16 &&
+                  out_norm.scalar_type() == at::kBFloat16,
+              "hif8_gdn_decode_step: bf16 operands expected");
+  TORCH_CHECK(a_log.scalar_type() == at::kFloat && dt_bias.scalar_type() == at::kFloat &&
+                  rec_state.scalar_type() == at::kFloat, "hif8_gdn_decode_step: float32 a_log / dt_bias / state");
+  TORCH_CHECK(ba.size(0) == batch && ba.size(1) == 2 * v_heads, "ba must be [batch, 2 v_heads]");
+  TORCH_CHECK(conv_weight.size(0) == channels && conv_state.size(0) == batch && conv_state.size(1) == channels &&
+                  conv_state.size(2) == conv_weight.size(1) - 1, "conv weight / state shapes");
+  TORCH_CHECK(rec_state.size(0) == batch && rec_state.size(1) == v_heads && rec_state.size(2) == k_dim &&
+                  rec_state.size(3) == v_dim, "rec_state must be [batch, v_heads, k_dim, v_dim]");
+  TORCH_CHECK(a_log.numel() == v_heads && dt_bias.numel() == v_heads && out_norm.numel() == v_dim,
+              "per-head parameters");
+  const c10::OptionalDeviceGuard guard(mixed.device());
+  auto out = at::empty({batch, v_heads * v_dim}, mixed.options());
+  auto scratch = at::empty({batch, channels}, mixed.options().dtype(at::kFloat));
+  CheckStatus(hif8_gdn_decode_step(
+                  reinterpret_cast<const uint16_t *>(mixed.data_ptr()), mixed.size(1),
+                  reinterpret_cast<const uint16_t *>(ba.data_ptr()),
+                  reinterpret_cast<const uint16_t *>(conv_weight.data_ptr()),
+                  reinterpret_cast<uint16_t *>(conv_state.data_ptr()), a_log.data_ptr<float>(),
+                  dt_bias.data_ptr<float>(), rec_state.data_ptr<float>(),
+                  reinterpret_cast<const uint16_t *>(out_norm.data_ptr()), reinterpret_cast<uint16_t *>(out.data_ptr()),
+                  scratch.data_ptr<float>(), batch, k_heads, v_heads, k_dim, v_dim, conv_weight.size(1), float(eps),
+                  CurrentStream(mixed.device())),
+              "hif8_gdn_decode_step");
+  return out;
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> Hif8QkNormRope(
+    const at::Tensor &qkv, const at::Tensor &q_norm, const at::Tensor &k_norm, const at::Tensor &pos,
+    const at::Tensor &inv_freq, const at::Tensor &block_table, int64_t block_size, int64_t num_heads,
+    int64_t num_kv_heads, int64_t head_size, double eps) {
+  for (auto *t : {&qkv, &q_norm, &k_norm, &pos, &inv_freq, &block_table}) CheckContiguousDevice(*t, "operand");
+  TORCH_CHECK(qkv.scalar_type() == at::kBFloat16 && q_norm.scalar_type() == at::kBFloat16 &&
+                  k_norm.scalar_type() == at::kBFloat16, "hif8_qk_norm_rope: bf16 qkv and norms");
+  TORCH_CHECK(pos.scalar_type() == at::kLong && inv_freq.scalar_type() == at::kFloat &&
+                  block_table.scalar_type() == at::kInt, "hif8_qk_norm_rope: int64 pos, float32 inv_freq, int32 table");
+  const int64_t batch = qkv.size(0);
+  TORCH_CHECK(qkv.numel() == batch * (num_heads + 2 * num_kv_heads) * head_size, "qkv width");
+  TORCH_CHECK(pos.numel() == batch && block_table.dim() == 2 && block_table.size(0) >= batch, "pos / block_table");
+  const c10::OptionalDeviceGuard guard(qkv.device());
+  auto q = at::empty({batch, num_heads, head_size}, qkv.options());
+  auto k = at::empty({batch, num_kv_heads, head_size}, qkv.options());
+  auto v = at::empty({batch, num_kv_heads, head_size}, qkv.options());
+  auto slots = at::empty({batch}, qkv.options().dtype(at::kLong));
+  CheckStatus(hif8_qk_norm_rope(reinterpret_cast<const uint16_t *>(qkv.data_ptr()),
+                                reinterpret_cast<const uint16_t *>(q_norm.data_ptr()),
+                                reinterpret_cast<const uint16_t *>(k_norm.data_ptr()), pos.data_ptr<int64_t>(),
+                                inv_freq.data_ptr<float>(), block_table.data_ptr<int32_t>(), block_table.size(1),
+                                block_size, reinterpret_cast<uint16_t *>(q.data_ptr()),
+                                reinterpret_cast<uint16_t *>(k.data_ptr()), reinterpret_cast<uint16_t *>(v.data_ptr()),
+                                slots.data_ptr<int64_t>(), batch, num_heads, num_kv_heads, head_size,
+                                2 * inv_freq.numel(), float(eps), CurrentStream(qkv.device())),
+              "hif8_qk_norm_rope");
+  return {q, k, v, slots};
+}
+
 // ------------------------------------------------------------------ Meta
 
 std::tuple<at::Tensor, at::Tensor> Hif8StaticQuantMeta(const at::Tensor &x, const at::Tensor &fixed_scale) {
@@ -517,6 +627,10 @@ TORCH_LIBRARY(vllm_ascend_hif8, m) {
   m.def("hif8_embedding_lookup(Tensor input_ids, Tensor weight, Tensor weight_scale, Tensor(a!)? invalid_ids=None) -> Tensor");
   m.def("hif8_dynamic_quant(Tensor x) -> (Tensor, Tensor)");
   m.def("soft_hif8_fused_gemm(Tensor activation, Tensor weight, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
+  m.def("hif8_add_rms_norm(Tensor(a!) h, Tensor? delta, Tensor weight, float eps) -> Tensor");
+  m.def("hif8_silu_mul(Tensor gate_up) -> Tensor");
+  m.def("hif8_qk_norm_rope(Tensor qkv, Tensor q_norm, Tensor k_norm, Tensor pos, Tensor inv_freq, Tensor block_table, int block_size, int num_heads, int num_kv_heads, int head_size, float eps) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("hif8_gdn_decode_step(Tensor mixed_qkvz, Tensor ba, Tensor conv_weight, Tensor(a!) conv_state, Tensor a_log, Tensor dt_bias, Tensor(b!) rec_state, Tensor out_norm, int k_heads, int v_heads, int k_dim, int v_dim, float eps) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
@@ -530,6 +644,10 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
   m.impl("hif8_embedding_lookup", &Hif8EmbeddingLookup);
   m.impl("hif8_dynamic_quant", &Hif8DynamicQuant);
   m.impl("soft_hif8_fused_gemm", &SoftHif8FusedGemm);
+  m.impl("hif8_add_rms_norm", &Hif8AddRmsNorm);
+  m.impl("hif8_silu_mul", &Hif8SiluMul);
+  m.impl("hif8_qk_norm_rope", &Hif8QkNormRope);
+  m.impl("hif8_gdn_decode_step", &Hif8GdnDecodeStep);
 }
 
 TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {

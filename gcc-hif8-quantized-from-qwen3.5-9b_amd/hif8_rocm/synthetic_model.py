@@ -283,6 +283,21 @@ class HybridModel:
         blk = torch.gather(st.block_table.long(), 1, (pos // bs).long())
         return (blk * bs + pos % bs).reshape(-1)
 
+    def _attention_decode(self, L, idx: int, st: RequestState, x: torch.Tensor, pos: torch.Tensor):
+        """One decode token of full attention: fused q/k norm + rotary + slots,
+        fused KV write, paged HiF8 decode attention; x [B, H], pos [B, 1]."""
+        c = self.cfg
+        b = x.shape[0]
+        qkv = L["qkv"](x)
+        q, k, v, slots = torch.ops.vllm_ascend_hif8.hif8_qk_norm_rope(
+            qkv, L["q_norm"], L["k_norm"], pos.reshape(b), self.inv_freq, st.block_table, c.block_size, c.heads,
+            c.kv_heads, c.head_dim, c.rms_eps)
+        kc, vc = st.key_caches[idx], st.value_caches[idx]
+        kv_cache.write_kv_cache(k, v, kc, vc, slots, L["k_scale"], L["v_scale"], validate=False)
+        o = kv_cache.paged_decode_attention(q, kc, vc, st.block_table, st.seq_lens, scale=1.0 / math.sqrt(c.head_dim),
+                                            max_seq_len=st.max_len, validate=False)
+        return L["o"](o.reshape(b, c.heads * c.head_dim))
+
     def _attention(self, L, idx: int, st: RequestState, h: torch.Tensor, pos: torch.Tensor, decode: bool):
         c = self.cfg
         b, t, _ = h.shape
@@ -359,6 +374,40 @@ class HybridModel:
         o = o.to(h.dtype).reshape(b * t, c.lin_v_width)
         return L["out"](o).reshape(b, t, -1)
 
+    def _linear_attention_decode(self, L, idx: int, st: RequestState, x: torch.Tensor) -> torch.Tensor:
+        """One decode token of the linear-attention mixer with the fused glue
+        kernel (conv + recurrence + gated norm in two launches); x [B, H]."""
+        c = self.cfg
+        qkvz = L["qkvz"](x)
+        ba = torch.nn.functional.linear(x, L["ba"])
+        o = torch.ops.vllm_ascend_hif8.hif8_gdn_decode_step(
+            qkvz, ba, L["conv"], st.conv_states[idx], L["A_log"], L["dt_bias"], st.rec_states[idx], L["out_norm"],
+            c.lin_k_heads, c.lin_v_heads, c.lin_k_dim, c.lin_v_dim, c.rms_eps)
+        return L["out"](o)
+
+    def _forward_decode(self, st: RequestState, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """The decode step with fused glue: residual add + RMSNorm in one
+        kernel, SiLU-mul in one, the linear-attention token in two."""
+        c = self.cfg
+        ops = torch.ops.vllm_ascend_hif8
+        b = ids.shape[0]
+        h = native.embedding_lookup(self.embed.weight, self.embed.weight_scale, ids.reshape(b),
+                                    validate=False).reshape(b, c.hidden)
+        pending = None
+        attn_i = lin_i = 0
+        for i, L in enumerate(self.layers):
+            x = ops.hif8_add_rms_norm(h, pending, L["input_norm"], c.rms_eps)
+            if c.is_full_attention(i):
+                mix = self._attention_decode(L, attn_i, st, x, pos)
+                attn_i += 1
+            else:
+                mix = self._linear_attention_decode(L, lin_i, st, x)
+                lin_i += 1
+            x2 = ops.hif8_add_rms_norm(h, mix, L["post_norm"], c.rms_eps)
+            pending = L["down"](ops.hif8_silu_mul(L["gate_up"](x2)))
+        last = ops.hif8_add_rms_norm(h, pending, self.final_norm, c.rms_eps)
+        return torch.nn.functional.linear(last, self.lm_head).float()
+
     def _mlp(self, L, h: torch.Tensor) -> torch.Tensor:
         c = self.cfg
         b, t, _ = h.shape
@@ -374,8 +423,9 @@ class HybridModel:
         The caller sets ``st.seq_lens`` to the lengths including these tokens
         before a decode step (the decode attention reads them)."""
         c = self.cfg
-        h = self.embed_method.embedding(self.embed, ids) if not decode else native.embedding_lookup(
-            self.embed.weight, self.embed.weight_scale, ids, validate=False)
+        if decode:
+            return self._forward_decode(st, ids, pos)
+        h = self.embed_method.embedding(self.embed, ids)
         attn_i = lin_i = 0
         for i, L in enumerate(self.layers):
             x = rms_norm(h, L["input_norm"], c.rms_eps)

@@ -252,6 +252,44 @@ int hif8_paged_decode_attention(const void *query, int q_dtype, const uint8_t *k
                                 int64_t num_heads, int64_t max_seq_len, float scale, void *out,
                                 void *workspace, size_t workspace_bytes, hif8_stream_t stream);
 
+/*
+ * Decode-step glue of the synthetic hybrid model (the end-to-end workload).
+ * These have no counterpart among the reference's operators: they fuse the
+ * bf16 / fp32 model parts that the reference leaves to vLLM (norms, the MLP
+ * activation, the linear-attention conv and recurrence), so that a decode
+ * step is a few launches per layer.  All tensors bf16 unless stated.
+ *
+ * hif8_add_rms_norm: per row of h [rows, n]: if delta is not NULL,
+ *   h <- bf16(h + delta) in place; out = bf16(h * rsqrt(mean(h^2) + eps) * weight).
+ * hif8_silu_mul: gate_up [rows, 2n] -> out [rows, n] = bf16(silu(gate) * up).
+ * hif8_qk_norm_rope: one decode token of full attention: qkv [batch, (Hq + 2 Hkv) D] ->
+ *   q_out [batch, Hq, D], k_out / v_out [batch, Hkv, D]; q and k heads RMS-normalised
+ *   (q_norm / k_norm [D]) then rotated on the first rotary_dim dims (halves i, i + r/2,
+ *   angle pos[b] * inv_freq[i], float32 inv_freq [r/2], int64 pos [batch]); if slots is
+ *   not NULL, slots[b] = block_table[b, pos / block_size] * block_size + pos % block_size
+ *   (int32 block_table [batch, max_blocks]).  D <= 256.
+ * hif8_gdn_decode_step: one token of the gated delta rule for batch requests.
+ *   mixed_qkvz [batch, ld]: q | k (k_heads x k_dim each) | v | z (v_heads x v_dim each)
+ *   ba [batch, 2 v_heads]: b | a;  conv_weight [C, conv_width], C = 2 k_heads k_dim + v_heads v_dim;
+ *   conv_state [batch, C, conv_width - 1] (updated); a_log, dt_bias [v_heads] float32;
+ *   rec_state [batch, v_heads, k_dim, v_dim] float32 (updated); out_norm [v_dim];
+ *   out [batch, v_heads * v_dim]; conv_scratch [batch, C] float32 workspace.
+ *   k_dim, v_dim <= 128; v_heads a multiple of k_heads.
+ */
+int hif8_add_rms_norm(uint16_t *h, const uint16_t *delta, const uint16_t *weight, uint16_t *out,
+                      int64_t rows, int64_t n, float eps, hif8_stream_t stream);
+int hif8_silu_mul(const uint16_t *gate_up, uint16_t *out, int64_t rows, int64_t n, hif8_stream_t stream);
+int hif8_qk_norm_rope(const uint16_t *qkv, const uint16_t *q_norm, const uint16_t *k_norm, const int64_t *pos,
+                      const float *inv_freq, const int32_t *block_table, int64_t max_blocks, int64_t block_size,
+                      uint16_t *q_out, uint16_t *k_out, uint16_t *v_out, int64_t *slots, int64_t batch,
+                      int64_t num_heads, int64_t num_kv_heads, int64_t head_size, int64_t rotary_dim, float eps,
+                      hif8_stream_t stream);
+int hif8_gdn_decode_step(const uint16_t *mixed_qkvz, int64_t ld, const uint16_t *ba,
+                         const uint16_t *conv_weight, uint16_t *conv_state, const float *a_log,
+                         const float *dt_bias, float *rec_state, const uint16_t *out_norm, uint16_t *out,
+                         float *conv_scratch, int64_t batch, int64_t k_heads, int64_t v_heads, int64_t k_dim,
+                         int64_t v_dim, int64_t conv_width, float eps, hif8_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

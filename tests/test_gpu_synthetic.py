@@ -65,3 +65,71 @@ def test_graph_replay_matches_eager_decode(model, device):
     graphed, timings = generate(model, prompt, 8, graph=True)
     assert torch.equal(eager, graphed)
     assert timings["prefill"] > 0 and timings["decode"] > 0 and timings["decode_steps"] == 6
+
+
+def test_fused_add_rms_norm_and_silu_mul_match_torch(native_ops, device):
+    from hif8_rocm.synthetic_model import rms_norm
+
+    g = torch.Generator(device=device).manual_seed(7)
+    h = torch.randn(3, 4096, generator=g, device=device).to(torch.bfloat16)
+    d = torch.randn(3, 4096, generator=g, device=device).to(torch.bfloat16)
+    w = (torch.rand(4096, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    want_h = h + d
+    want = rms_norm(want_h, w, 1e-6)
+    got_h = h.clone()
+    got = torch.ops.vllm_ascend_hif8.hif8_add_rms_norm(got_h, d, w, 1e-6)
+    assert torch.equal(got_h, want_h)
+    torch.testing.assert_close(got.float(), want.float(), rtol=1e-2, atol=1e-2)
+    plain = torch.ops.vllm_ascend_hif8.hif8_add_rms_norm(h.clone(), None, w, 1e-6)
+    torch.testing.assert_close(plain.float(), rms_norm(h, w, 1e-6).float(), rtol=1e-2, atol=1e-2)
+    gu = torch.randn(5, 600, generator=g, device=device).to(torch.bfloat16)
+    act = torch.ops.vllm_ascend_hif8.hif8_silu_mul(gu)
+    ref = (torch.nn.functional.silu(gu[:, :300].float()) * gu[:, 300:].float()).to(torch.bfloat16)
+    torch.testing.assert_close(act.float(), ref.float(), rtol=1e-2, atol=1e-2)
+
+
+def test_fused_linear_attention_step_matches_torch_step(model, device):
+    import copy
+
+    c = model.cfg
+    idx = 0
+    L = model.layers[0]
+    assert not c.is_full_attention(0)
+    b = 3
+    st_a = model.new_state(b, 8)
+    g = torch.Generator(device=device).manual_seed(11)
+    st_a.conv_states[idx].copy_(torch.randn(st_a.conv_states[idx].shape, generator=g, device=device))
+    st_a.rec_states[idx].copy_(torch.randn(st_a.rec_states[idx].shape, generator=g, device=device) * 0.1)
+    st_b = copy.copy(st_a)
+    st_b.conv_states = [t.clone() for t in st_a.conv_states]
+    st_b.rec_states = [t.clone() for t in st_a.rec_states]
+    for step in range(3):
+        x = torch.randn(b, c.hidden, generator=g, device=device).to(torch.bfloat16)
+        fused = model._linear_attention_decode(L, idx, st_a, x)
+        ref = model._linear_attention(L, idx, st_b, x[:, None], decode=True)[:, 0]
+        torch.testing.assert_close(fused.float(), ref.float(), rtol=2e-2, atol=2e-2)
+        torch.testing.assert_close(st_a.conv_states[idx], st_b.conv_states[idx])
+        torch.testing.assert_close(st_a.rec_states[idx], st_b.rec_states[idx], rtol=1e-4, atol=1e-5)
+
+
+def test_fused_attention_step_matches_torch_step(model, device):
+    import copy
+
+    c = model.cfg
+    L = model.layers[3]
+    assert c.is_full_attention(3)
+    b, t = 2, 5
+    g = torch.Generator(device=device).manual_seed(13)
+    st_a = model.new_state(b, 40)
+    st_b = copy.copy(st_a)
+    st_b.key_caches = [kc.clone() for kc in st_a.key_caches]
+    st_b.value_caches = [vc.clone() for vc in st_a.value_caches]
+    for step in range(3):
+        x = torch.randn(b, c.hidden, generator=g, device=device).to(torch.bfloat16)
+        pos = torch.full((b, 1), t + step, dtype=torch.int64, device=device)
+        st_a.seq_lens.fill_(t + step + 1)
+        fused = model._attention_decode(L, 0, st_a, x, pos)
+        ref = model._attention(L, 0, st_b, x[:, None], pos, True)[:, 0]
+        torch.testing.assert_close(st_a.key_caches[0], st_b.key_caches[0], rtol=0, atol=0)
+        torch.testing.assert_close(st_a.value_caches[0], st_b.value_caches[0], rtol=0, atol=0)
+        torch.testing.assert_close(fused.float(), ref.float(), rtol=2e-2, atol=2e-2)
