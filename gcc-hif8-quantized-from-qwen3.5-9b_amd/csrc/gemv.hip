@@ -10,8 +10,10 @@
 //   * weight bytes are decoded with a 256-entry bf16 table in LDS (HiF8 is a
 //     subset of bf16, so decode is exact) and multiplied with v_dot2_f32_bf16,
 //     FP32 accumulation;
-//   * partial sums are reduced through LDS (thread-major, padded rows) and the
-//     epilogue applies token scale, channel scale and bias, rounding once.
+//   * each wavefront sums its kR*kM partials over its 64 lanes in registers
+//     (permlane swaps and DPP, halving the values per lane at each level),
+//     the four wavefront totals meet in LDS, and the epilogue applies token
+//     scale, channel scale and bias, rounding once.
 // The fused variants take fp16/bf16 x and encode it on the fly: with the
 // fixed scale (soft_hif8_fused_gemm.cpp:449-534 with HIF8_FUSED_STATIC_SCALE)
 // or with each row's dynamic scale max(finite amax, 1e-12), which every block
@@ -61,6 +63,10 @@ __device__ __forceinline__ bool near_index_boundary(float q) {
 // Multiplies by the reciprocal and redoes the element with an IEEE division
 // when the product is within 8 ulps of an encode-index boundary or NaN (the
 // same rule as hif8_static_quant), so the codes equal the standalone quant's.
+// Two LDS lookups per element (encode table, decode table): measured on
+// MI355X, rounding the quotient's bits arithmetically instead (about 20 VALU
+// operations per element) made the fused GEMV 20-30 % slower, since every
+// block re-encodes its activation chunk.
 template <bool kBf16>
 __device__ __forceinline__ void fast_encode_decode16(const u32x4 a, const u32x4 b, float s, float r,
                                                      const uint8_t *enc, const uint16_t *dec, u32x4 &lo,
@@ -93,6 +99,72 @@ constexpr int pow2_floor(int v) {
   return p;
 }
 
+constexpr int pow2_ceil(int v) {
+  int p = 1;
+  while (p < v) p *= 2;
+  return p;
+}
+
+constexpr int log2_exact(int v) { return v <= 1 ? 0 : 1 + log2_exact(v / 2); }
+
+// One exchange level of the in-register transpose-reduce, on lane bit kBit
+// (5 = lanes l and l^32, 4 = 16-lane rows, 3..0 = DPP partners inside a row:
+// mirror, half mirror, quad reverse, quad swap).  Every partner differs from
+// its lane in bit kBit, so lanes whose bit is 0 end with lo + the partner's lo
+// and lanes whose bit is 1 with hi + the partner's hi; called with lo == hi,
+// every lane ends with the sum over the pair.
+template <int kBit>
+__device__ __forceinline__ float exchange_add(float lo, float hi, int lane) {
+  if constexpr (kBit >= 4) {
+    const auto s = kBit == 5 ? __builtin_amdgcn_permlane32_swap(__float_as_uint(lo), __float_as_uint(hi), false, false)
+                             : __builtin_amdgcn_permlane16_swap(__float_as_uint(lo), __float_as_uint(hi), false, false);
+    return __uint_as_float(s[0]) + __uint_as_float(s[1]);
+  } else {
+    constexpr int kCtrl = kBit == 3 ? 0x140 : kBit == 2 ? 0x141 : kBit == 1 ? 0x1B : 0xB1;
+    const bool up = (lane >> kBit) & 1;
+    const float keep = up ? hi : lo, send = up ? lo : hi;
+    return keep + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(send), kCtrl, 0xF, 0xF, false));
+  }
+}
+
+// Sums v[0..kV) (kV a power of two <= 64) over the 64 lanes of a wavefront
+// in log2(kV) halving levels plus 6 - log2(kV) full levels: 2 kV - 2 + 6 -
+// log2(kV) lane exchanges instead of a round trip through LDS.  Afterwards
+// lane l holds the total of index l >> (6 - log2(kV)).
+template <int kV>
+__device__ __forceinline__ float wave_transpose_sum(float (&v)[kV], int lane) {
+  constexpr int kLevels = log2_exact(kV);
+  static_assert((1 << kLevels) == kV && kV <= 64, "value count must be a power of two <= 64");
+#pragma unroll
+  for (int level = 0; level < kLevels; ++level) {
+    const int half = kV >> (level + 1);
+#pragma unroll
+    for (int i = 0; i < half; ++i) {
+      switch (5 - level) {
+        case 5: v[i] = exchange_add<5>(v[i], v[i + half], lane); break;
+        case 4: v[i] = exchange_add<4>(v[i], v[i + half], lane); break;
+        case 3: v[i] = exchange_add<3>(v[i], v[i + half], lane); break;
+        case 2: v[i] = exchange_add<2>(v[i], v[i + half], lane); break;
+        case 1: v[i] = exchange_add<1>(v[i], v[i + half], lane); break;
+        default: v[i] = exchange_add<0>(v[i], v[i + half], lane); break;
+      }
+    }
+  }
+  float s = v[0];
+#pragma unroll
+  for (int bit = 5 - kLevels; bit >= 0; --bit) {
+    switch (bit) {
+      case 5: s = exchange_add<5>(s, s, lane); break;
+      case 4: s = exchange_add<4>(s, s, lane); break;
+      case 3: s = exchange_add<3>(s, s, lane); break;
+      case 2: s = exchange_add<2>(s, s, lane); break;
+      case 1: s = exchange_add<1>(s, s, lane); break;
+      default: s = exchange_add<0>(s, s, lane); break;
+    }
+  }
+  return s;
+}
+
 __device__ __forceinline__ float load_bias(const void *bias, int dtype, int i) {
   const uint16_t h = static_cast<const uint16_t *>(bias)[i];
   return dtype == HIF8_DTYPE_BF16 ? half_bits_to_float<true>(h) : half_bits_to_float<false>(h);
@@ -103,21 +175,28 @@ __device__ __forceinline__ void store_out(void *out, int dtype, size_t i, float 
       dtype == HIF8_DTYPE_BF16 ? float_to_bf16_bits(y) : float_to_f16_bits(y);
 }
 
-template <int kM, int kR, int kSrc>
-__global__ __launch_bounds__(kThreads, 2) void gemv_kernel(
+// Waves per SIMD the register allocation must allow.  Tighter bounds than
+// these make the compiler spill (M = 2 at 5 waves, M = 4 at 4 waves).
+constexpr int gemv_min_waves(int m, int rows) { return rows > 8 ? 2 : m == 1 ? 6 : m == 2 ? 4 : 2; }
+
+// kOneChunk: k <= 16 * kThreads, so each thread owns at most one 16-byte
+// column chunk per row (code activations only).
+template <int kM, int kR, int kSrc, bool kOneChunk>
+__global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
     const void *__restrict__ act, const float *__restrict__ act_scale,
     const uint8_t *__restrict__ weight, const float *__restrict__ cs,
     const void *__restrict__ bias, int bias_dtype, void *__restrict__ out, int out_dtype,
     int n, int k) {
   constexpr int kV = kR * kM;
-  constexpr int kPitch = kV + 4;
+  constexpr int kVp = pow2_ceil(kV);  // partial sums per lane, zero-padded
+  constexpr int kWaves = kThreads / kWave;
   constexpr bool kFused = kSrc != kActCodes;
   constexpr bool kDynamic = kSrc == kActF16Dyn || kSrc == kActBf16Dyn;
   constexpr bool kInBf16 = kSrc == kActBf16 || kSrc == kActBf16Dyn;
   constexpr int kActWords = kFused ? 2 : 1;  // 16-byte words of activation per row per chunk
   __shared__ __attribute__((aligned(16))) uint16_t dec_lut[256];
   __shared__ __attribute__((aligned(16))) uint8_t enc_lut[kFused ? 8192 : 16];
-  __shared__ __attribute__((aligned(16))) float red[kThreads * kPitch];
+  __shared__ __attribute__((aligned(16))) float red[kWaves][kVp];
 
   const int tid = threadIdx.x;
   const int n0 = blockIdx.x * kR;
@@ -126,13 +205,9 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_kernel(
   // Raw operands of one 16-byte column chunk: kR weight rows + kM activation rows.
   u32x4 wq[kR];
   u32x4 ar[kM][kActWords];
+  // Activation loads go first: their decode then waits only for them while
+  // the weight loads are still in flight.
   auto load = [&](int c) {
-#pragma unroll
-    for (int r = 0; r < kR; ++r) {
-      // Rows past n re-read row n-1; their sums are never stored.
-      const int row = min(n0 + r, n - 1);
-      wq[r] = reinterpret_cast<const u32x4 *>(weight + size_t(row) * k)[c];
-    }
 #pragma unroll
     for (int m = 0; m < kM; ++m) {
       if constexpr (kFused) {
@@ -143,11 +218,26 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_kernel(
         ar[m][0] = reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(act) + size_t(m) * k)[c];
       }
     }
+#pragma unroll
+    for (int r = 0; r < kR; ++r) {
+      // Rows past n re-read row n-1; their sums are never stored.
+      const int row = min(n0 + r, n - 1);
+      wq[r] = reinterpret_cast<const u32x4 *>(weight + size_t(row) * k)[c];
+    }
   };
-  // Loads are issued after the table barrier.  Issuing the first chunk's
-  // loads before it measured slower on MI355X (q 4096x4096 M=1: 6.65 vs
-  // 5.5 us): the table store has to wait for every earlier load to return.
-  dec_lut[tid] = kDeviceTables.decode_bf16[tid];
+  // The decode table is computed, one entry per thread, rather than copied
+  // from global memory, so in the one-chunk kernel the chunk's loads go out
+  // before it and stay in flight across the LDS barrier: the kernel pays one
+  // memory round trip before its first products, not two.  (A copied table
+  // would have to wait for those loads: global loads return in order.  That
+  // is why the fused kinds, which copy the 8 KiB encode table, load after
+  // the barrier: loading first measured slower for them at M = 1.)  In a
+  // loop the preloaded registers stay live across the loop and the kernel
+  // spills, hence the separate one-chunk kernel.
+  static_assert(!kOneChunk || !kFused, "the one-chunk kernel takes code activations");
+  const uint16_t entry = uint16_t(decode_bits(uint32_t(tid)) >> 16);
+  if (kOneChunk && tid < chunks) load(tid);
+  dec_lut[tid] = entry;
   if constexpr (kFused) {
     const u32x4 *src = reinterpret_cast<const u32x4 *>(kDeviceTables.static_encode);
     u32x4 *dst = reinterpret_cast<u32x4 *>(enc_lut);
@@ -207,8 +297,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_kernel(
 #pragma unroll
     for (int m = 0; m < kM; ++m) acc[r][m] = 0.f;
 
-  for (int c = tid; c < chunks; c += kThreads) {
-    load(c);
+  // Products of the chunk whose operands are in wq / ar.
+  auto compute = [&]() {
     uint32_t a[kM][8];
 #pragma unroll
     for (int m = 0; m < kM; ++m) {
@@ -233,31 +323,33 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_kernel(
 #pragma unroll
         for (int m = 0; m < kM; ++m) acc[r][m] = dot2(a[m][j], p[j], acc[r][m]);
     }
+  };
+  if constexpr (kOneChunk) {
+    if (tid < chunks) compute();
+  } else {
+    for (int c = tid; c < chunks; c += kThreads) {
+      load(c);
+      compute();
+    }
   }
 
-  // Thread-major partials, then column sums by kTpo threads per output.
-  float *mine = red + tid * kPitch;
+  // Each wavefront sums its partials in registers; the kWaves wavefront
+  // totals of each output meet in LDS.
+  const int lane = tid % kWave;
+  float vals[kVp];
 #pragma unroll
-  for (int v = 0; v < kV; v += 4) {
-    float4 f;
-    f.x = acc[(v + 0) / kM][(v + 0) % kM];
-    f.y = acc[(v + 1) / kM][(v + 1) % kM];
-    f.z = acc[(v + 2) / kM][(v + 2) % kM];
-    f.w = acc[(v + 3) / kM][(v + 3) % kM];
-    *reinterpret_cast<float4 *>(mine + v) = f;
-  }
+  for (int v = 0; v < kVp; ++v) vals[v] = v < kV ? acc[v / kM][v % kM] : 0.f;
+  const float wsum = wave_transpose_sum<kVp>(vals, lane);
+  constexpr int kGroup = kWave / kVp;  // lanes holding one total
+  if (lane % kGroup == 0) red[tid / kWave][lane / kGroup] = wsum;
   __syncthreads();
-  constexpr int kTpo = pow2_floor(kThreads / kV) > 64 ? 64 : pow2_floor(kThreads / kV);
-  const int v = tid / kTpo;
-  const int part = tid % kTpo;
+  const int v = tid;
   float s = 0.f;
   if (v < kV) {
-#pragma unroll 4
-    for (int t = part; t < kThreads; t += kTpo) s += red[t * kPitch + v];
-  }
 #pragma unroll
-  for (int off = kTpo / 2; off > 0; off >>= 1) s += __shfl_xor(s, off, kWave);
-  if (v < kV && part == 0) {
+    for (int w = 0; w < kWaves; ++w) s += red[w][v];
+  }
+  if (v < kV) {
     const int r = v / kM, m = v % kM;
     const int row = n0 + r;
     if (row < n) {
@@ -495,23 +587,27 @@ void dispatch_src(const LinearArgs &a, dim3 grid) {
   const int n = int(a.n), k = int(a.k);
   switch (a.act_kind) {
     case kActCodes:
-      gemv_kernel<kM, kR, kActCodes><<<grid, kThreads, 0, a.stream>>>(
-          a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
+      if (k <= 16 * kThreads)
+        gemv_kernel<kM, kR, kActCodes, true><<<grid, kThreads, 0, a.stream>>>(
+            a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
+      else
+        gemv_kernel<kM, kR, kActCodes, false><<<grid, kThreads, 0, a.stream>>>(
+            a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
       break;
     case kActF16:
-      gemv_kernel<kM, kR, kActF16><<<grid, kThreads, 0, a.stream>>>(
+      gemv_kernel<kM, kR, kActF16, false><<<grid, kThreads, 0, a.stream>>>(
           a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
       break;
     case kActBf16:
-      gemv_kernel<kM, kR, kActBf16><<<grid, kThreads, 0, a.stream>>>(
+      gemv_kernel<kM, kR, kActBf16, false><<<grid, kThreads, 0, a.stream>>>(
           a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
       break;
     case kActF16Dyn:
-      gemv_kernel<kM, kR, kActF16Dyn><<<grid, kThreads, 0, a.stream>>>(
+      gemv_kernel<kM, kR, kActF16Dyn, false><<<grid, kThreads, 0, a.stream>>>(
           a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
       break;
     default:
-      gemv_kernel<kM, kR, kActBf16Dyn><<<grid, kThreads, 0, a.stream>>>(
+      gemv_kernel<kM, kR, kActBf16Dyn, false><<<grid, kThreads, 0, a.stream>>>(
           a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
       break;
   }
