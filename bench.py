@@ -489,18 +489,25 @@ def e2e_decode(torch, device) -> dict:
                        "HiF8 SOFT, norms / conv / recurrence / LM head in bf16-fp32 torch; greedy, random ids",
            "prompt_tokens": E2E_PROMPT, "new_tokens": E2E_NEW, "build_and_calibrate_s": round(time.perf_counter() - t0, 2)}
     g = torch.Generator(device=device).manual_seed(9)
-    for b in (1, 4):
+    # b1_single_row_fusion: batch 1 again with HIF8_STATIC_FUSED_SINGLE_ROW=1
+    # (one-row projections with K <= 4096 in one fused launch; same tokens).
+    for b, key, single in ((1, "b1", False), (4, "b4", False), (1, "b1_single_row_fusion", True)):
         prompt = torch.randint(0, cfg.vocab, (b, E2E_PROMPT), generator=g, device=device)
-        generate(model, prompt[:, :64], 4)  # warm-up: allocator, kernels, graph capture path
-        _, tm = generate(model, prompt, E2E_NEW)
+        if single:
+            os.environ["HIF8_STATIC_FUSED_SINGLE_ROW"] = "1"
+        try:
+            generate(model, prompt[:, :64], 4)  # warm-up: allocator, kernels, graph capture path
+            _, tm = generate(model, prompt, E2E_NEW)
+        finally:
+            os.environ.pop("HIF8_STATIC_FUSED_SINGLE_ROW", None)
         step_s = tm["decode"] / tm["decode_steps"]
         total = tm["prefill"] + step_s * (E2E_NEW - 1)
-        res[f"b{b}"] = {"prefill_ms": round(tm["prefill"] * 1e3, 2), "ms_per_decode_step": round(step_s * 1e3, 3),
-                        "first_step_and_graph_record_ms": round(tm["setup"] * 1e3, 1),
-                        "decode_tok_per_s": round(b / step_s, 1),
-                        "output_tok_per_s": round(b * E2E_NEW / total, 1)}
-        log(f"e2e b{b}: prefill {tm['prefill'] * 1e3:.1f} ms, {step_s * 1e3:.3f} ms/step, "
-            f"{res[f'b{b}']['output_tok_per_s']} output tok/s")
+        res[key] = {"prefill_ms": round(tm["prefill"] * 1e3, 2), "ms_per_decode_step": round(step_s * 1e3, 3),
+                    "first_step_and_graph_record_ms": round(tm["setup"] * 1e3, 1),
+                    "decode_tok_per_s": round(b / step_s, 1),
+                    "output_tok_per_s": round(b * E2E_NEW / total, 1)}
+        log(f"e2e {key}: prefill {tm['prefill'] * 1e3:.1f} ms, {step_s * 1e3:.3f} ms/step, "
+            f"{res[key]['output_tok_per_s']} output tok/s")
     del model
     torch.cuda.empty_cache()
     return res
@@ -565,6 +572,16 @@ def main() -> None:
     fused_ms = time_graphs(torch, fused, args.steps)
     fused_gbs = step_bytes / (fused_ms * 1e-3) / 1e9
     log(f"fused single-launch sweep: {fused_ms * 1e3:.1f} us/step, {fused_gbs:.1f} GB/s")
+
+    # The scheme with the MI355X opt-in HIF8_STATIC_FUSED_SINGLE_ROW=1 (one token
+    # row, K <= 4096 fused; equal outputs).  apply() routes at capture time.
+    os.environ["HIF8_STATIC_FUSED_SINGLE_ROW"] = "1"
+    single = [capture(torch, decode_step_fn(st, c)) for c in range(N_COPIES)]
+    del os.environ["HIF8_STATIC_FUSED_SINGLE_ROW"]
+    single_ms = time_graphs(torch, single, args.steps)
+    single_gbs = step_bytes / (single_ms * 1e-3) / 1e9
+    del single
+    log(f"sweep with single-row fusion: {single_ms * 1e3:.1f} us/step, {single_gbs:.1f} GB/s")
 
     log("per-kernel table ...")
     table = per_kernel_table(st)
@@ -646,6 +663,10 @@ def main() -> None:
             "kv_cache_write": kv_write,
         },
         "decode_sweep_fused_GBps": round(fused_gbs, 1),
+        "decode_sweep_single_row_fusion": {"GBps": round(single_gbs, 1), "us_per_step": round(single_ms * 1e3, 1),
+                                           "routing": "scheme apply with HIF8_STATIC_FUSED_SINGLE_ROW=1: M=1 "
+                                                      "and K <= 4096 fused (one launch), other shapes as the "
+                                                      "headline; outputs equal"},
         "gemv_all_launches_GBps": round(all_gemv_gbs, 1),
         "gemm_per_layer": gemm_layer,
         "ceilings": ceilings,

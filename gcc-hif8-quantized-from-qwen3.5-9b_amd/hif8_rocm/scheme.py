@@ -6,11 +6,18 @@ holds ``weight`` uint8 [N, K], ``weight_scale`` float32 [N, 1] and
 ``input_scale`` float32 [1]; ``apply`` statically quantises the activation and
 runs the soft HiF8 linear.
 
-Routing is the reference's (scheme.py:183-189): the fused static-quant GEMV
-is taken only when ``HIF8_STATIC_FUSED_GENERATION=1``, M <= 4 and K < 1024.
-On MI355X that is also the faster choice at model shapes: the fused kernel
-re-encodes the activation in every block (N/8 blocks x M*K encodes), which
-costs more than the separate quant launch once K reaches a few thousand.
+Routing is the reference's by default (scheme.py:181-189): the fused
+static-quant GEMV only when ``HIF8_STATIC_FUSED_GENERATION=1``, M <= 4 and
+K < 1024, because on its hardware the fused kernel pays a global barrier.
+The MI355X fused kernel has none (every block encodes its own activation
+chunk) and its outputs equal quant -> GEMM bit for bit.  Measured on
+MI355X, one token row with K <= 4096 is faster fused (q 6.9 vs 9.0 us,
+fused k/v 5.3 vs 7.9, o 7.2 vs 8.5, gate_up 21.9 vs 23.4: the separate
+quant launch costs about 4 us of launch and cold-cache latency), while
+K = 12288 (down 15.3 vs 14.4) and two or more rows at the large shapes are
+faster separate (each block re-encodes M*K values).
+``HIF8_STATIC_FUSED_SINGLE_ROW=1`` opts into fusing one token row with
+K <= 4096 as well; it changes which kernels run, not the outputs.
 """
 
 from __future__ import annotations
@@ -28,6 +35,9 @@ _COMPUTE_BACKEND_ENV = "HIF8_COMPUTE_BACKEND"
 _SOFT_HIF8_BACKEND = "soft_hif8"
 _STATIC_FUSED_GENERATION_ENV = "HIF8_STATIC_FUSED_GENERATION"
 _STATIC_SCALE_FACTOR_ENV = "HIF8_STATIC_SCALE_FACTOR"
+# MI355X opt-in: fuse one token row up to this K (measured; see the module text).
+_STATIC_FUSED_SINGLE_ROW_ENV = "HIF8_STATIC_FUSED_SINGLE_ROW"
+_FUSED_SINGLE_ROW_MAX_K = 4096
 
 
 def _static_scale_factor() -> float:
@@ -96,13 +106,20 @@ class W8A8HiFloat8StaticLinearMethod:
         bias: torch.Tensor | None = None,
         tp_rank: int | None = 0,
     ) -> torch.Tensor:
-        """static_quant -> soft_linear, or the fused kernel for tiny shapes (scheme.py:174-211)."""
+        """static_quant -> soft_linear, or the fused kernel (scheme.py:174-211).
+
+        Fused when the reference would fuse (``HIF8_STATIC_FUSED_GENERATION=1``,
+        M <= 4, K < 1024) and, with ``HIF8_STATIC_FUSED_SINGLE_ROW=1``, for
+        one token row with K <= 4096; the two routes give equal outputs."""
         del tp_rank
         token_rows = x.numel() // x.shape[-1]
+        k = x.shape[-1]
         use_fused = (
-            token_rows <= 4
-            and os.environ.get(_STATIC_FUSED_GENERATION_ENV) == "1"
-            and x.shape[-1] < 1024
+            token_rows <= 4 and os.environ.get(_STATIC_FUSED_GENERATION_ENV) == "1" and k < 1024
+        ) or (
+            token_rows == 1
+            and k <= _FUSED_SINGLE_ROW_MAX_K
+            and os.environ.get(_STATIC_FUSED_SINGLE_ROW_ENV) == "1"
         )
         scale_factor = _static_scale_factor()
         fixed_scale = layer.input_scale

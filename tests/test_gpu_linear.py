@@ -169,3 +169,27 @@ def test_nonzero_storage_offset_is_rejected(native_ops, device):
     with pytest.raises(RuntimeError, match="storage_offset == 0"):
         native_ops.soft_hif8_gemv(view, torch.zeros((2, 4), dtype=torch.uint8, device=device),
                                   torch.ones(2, device=device), torch.ones(2, device=device), None, torch.float16)
+
+
+@pytest.mark.parametrize("n,k", LAYER_SHAPES)
+def test_single_row_fusion_equals_the_two_stage_apply(native_ops, device, monkeypatch, n, k):
+    """The scheme's HIF8_STATIC_FUSED_SINGLE_ROW route gives the two-stage
+    route's outputs bit for bit at every decode projection shape."""
+    import torch.nn as nn
+
+    from hif8_rocm import scheme
+
+    w, ws = hif8_weight(n, k, seed=n * 3 + k)
+    x = bf16_activation(1, k, seed=k + 11)
+    layer = nn.Module()
+    layer.weight = nn.Parameter(_t(w, device), requires_grad=False)
+    layer.weight_scale = nn.Parameter(_t(ws, device).reshape(-1, 1), requires_grad=False)
+    layer.input_scale = nn.Parameter(input_scale_of(x).to(device), requires_grad=False)
+    method = scheme.W8A8HiFloat8StaticLinearMethod()
+    method.process_weights_after_loading(layer)
+    monkeypatch.delenv("HIF8_STATIC_FUSED_SINGLE_ROW", raising=False)
+    two_stage = method.apply(layer, x.to(device))
+    monkeypatch.setenv("HIF8_STATIC_FUSED_SINGLE_ROW", "1")
+    fused = method.apply(layer, x.to(device))
+    torch.cuda.synchronize()
+    assert torch.equal(fused, two_stage)

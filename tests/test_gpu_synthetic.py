@@ -67,6 +67,19 @@ def test_graph_replay_matches_eager_decode(model, device):
     assert timings["prefill"] > 0 and timings["decode"] > 0 and timings["decode_steps"] == 6
 
 
+def test_single_row_fusion_generates_the_same_tokens(model, device, monkeypatch):
+    """HIF8_STATIC_FUSED_SINGLE_ROW=1 swaps quant -> GEMV for the fused kernel
+    on one-row projections; the logits, hence the tokens, are unchanged."""
+    from hif8_rocm.synthetic_model import generate
+
+    g = torch.Generator(device=device).manual_seed(21)
+    prompt = torch.randint(0, model.cfg.vocab, (1, 12), generator=g, device=device)
+    plain, _ = generate(model, prompt, 6, graph=True)
+    monkeypatch.setenv("HIF8_STATIC_FUSED_SINGLE_ROW", "1")
+    fused, _ = generate(model, prompt, 6, graph=True)
+    assert torch.equal(plain, fused)
+
+
 def test_fused_add_rms_norm_and_silu_mul_match_torch(native_ops, device):
     from hif8_rocm.synthetic_model import rms_norm
 

@@ -166,7 +166,8 @@ def _layer(input_scale=0.25, k=8):
 @pytest.fixture
 def clean_env():
     with patch.dict(os.environ, {}, clear=False):
-        for var in ("HIF8_COMPUTE_BACKEND", "HIF8_STATIC_FUSED_GENERATION", "HIF8_STATIC_SCALE_FACTOR"):
+        for var in ("HIF8_COMPUTE_BACKEND", "HIF8_STATIC_FUSED_GENERATION", "HIF8_STATIC_SCALE_FACTOR",
+                    "HIF8_STATIC_FUSED_SINGLE_ROW"):
             os.environ.pop(var, None)
         yield
 
@@ -237,6 +238,32 @@ def test_fused_generation_is_opt_in_and_limited_to_small_shapes(clean_env):
             method.apply(layer, x)
         sq.assert_called_once()
         fused.assert_not_called()
+
+
+def test_single_row_fusion_is_an_opt_in(clean_env):
+    """HIF8_STATIC_FUSED_SINGLE_ROW=1 fuses one token row with K <= 4096 and
+    nothing else; unset, routing is the reference's."""
+    method = W8A8HiFloat8StaticLinearMethod()
+    out = torch.randn(1, 5)
+    cases = [(None, (1, 4096), False), ("1", (1, 4096), True), ("1", (1, 8), True), ("1", (2, 4096), False),
+             ("1", (1, 4112), False), ("0", (1, 64), False)]
+    for flag, shape, want_fused in cases:
+        if flag is None:
+            os.environ.pop("HIF8_STATIC_FUSED_SINGLE_ROW", None)
+        else:
+            os.environ["HIF8_STATIC_FUSED_SINGLE_ROW"] = flag
+        layer = _layer(k=shape[1])
+        method.process_weights_after_loading(layer)
+        x = torch.zeros(shape, dtype=torch.bfloat16)
+        with patch("hif8_rocm.scheme.native.static_quant",
+                   return_value=(x.to(torch.uint8), torch.ones(shape[0]))) as sq, \
+             patch("hif8_rocm.scheme.native.soft_linear", return_value=out), \
+             patch("hif8_rocm.scheme.native.soft_static_fused_linear", return_value=out) as fused:
+            method.apply(layer, x)
+        assert fused.called == want_fused and sq.called != want_fused, (flag, shape)
+        if want_fused:
+            fused.assert_called_once_with(x, layer.weight, layer.input_scale, layer.weight_scale, None,
+                                          output_dtype=x.dtype)
 
 
 def test_scale_factor_env_multiplies_the_checkpoint_scale(clean_env):
