@@ -321,6 +321,41 @@ def per_kernel_table(st: Setup, launches: int = 20) -> dict:
     return table
 
 
+def decoded_weight_gemm(st: Setup) -> dict:
+    """Prefill GEMMs with the weight kept decoded to bf16 (the opt-in
+    HIF8_PREFILL_BF16_WEIGHTS=1 route, soft_hif8_gemm_decoded_weight): per
+    shape and per layer at M in PREFILL_M, same graphs of 5 launches over the
+    rotated copies as the code-weight table.  The one-time decodes are made
+    before timing (they happen once per model load)."""
+    torch, native = st.torch, st.native
+    decoded = [{name: native.decode_weight(st.weights[c][name][0]) for name, _, _ in LAYER} for c in range(N_COPIES)]
+    res = {}
+    for m in PREFILL_M:
+        fl_total = us_total = 0.0
+        for name, n, k in LAYER:
+            x, s = st.x[(m, k)]
+            q, rs = native.static_quant(x, s)
+            per = 5
+
+            def fn(q=q, rs=rs, name=name):
+                for i in range(per):
+                    ws = st.weights[i % N_COPIES][name][1]
+                    native.soft_linear_decoded_weight(q, decoded[i % N_COPIES][name], rs, ws, None,
+                                                      output_dtype=torch.bfloat16)
+            ms = time_graphs(torch, [capture(torch, fn)], 3) / per
+            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+            res[f"{name}_m{m}"] = {"us": round(ms * 1e3, 3), "TFLOPs": round(tf, 1),
+                                   "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 4)}
+            fl_total += 2.0 * m * n * k
+            us_total += ms * 1e3
+        tf = fl_total / (us_total * 1e-6) / 1e12
+        res[f"layer_m{m}"] = {"TFLOPs": round(tf, 1), "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 4),
+                              "us_per_layer": round(us_total, 1)}
+    del decoded
+    torch.cuda.empty_cache()
+    return res
+
+
 def aux_kernels(torch, native, device) -> dict:
     """The decode ops beside the fused path: hif8_scaled_decode of KV rows
     (16384 rows x 256 codes -> bf16), the embedding gather-decode (vocab
@@ -585,6 +620,10 @@ def main() -> None:
 
     log("per-kernel table ...")
     table = per_kernel_table(st)
+    log("prefill GEMMs over decoded weights ...")
+    gemm_decoded = decoded_weight_gemm(st)
+    log(f"decoded-weight layer: m512 {gemm_decoded['layer_m512']['us_per_layer']} us, "
+        f"m4096 {gemm_decoded['layer_m4096']['us_per_layer']} us")
     gemv = [v for v in table.values() if v["kernel"] == "gemv"]
     dom = table["gate_up_m1"]
     gemm_layer = {}
@@ -669,6 +708,9 @@ def main() -> None:
                                                       "headline; outputs equal"},
         "gemv_all_launches_GBps": round(all_gemv_gbs, 1),
         "gemm_per_layer": gemm_layer,
+        "gemm_decoded_weights": {"routing": "HIF8_PREFILL_BF16_WEIGHTS=1: weights kept decoded to bf16 "
+                                            "(2 B/element), soft_hif8_gemm_decoded_weight",
+                                 **gemm_decoded},
         "ceilings": ceilings,
         "decode_ops": aux,
         "e2e_decode": e2e,

@@ -21,6 +21,8 @@
 //   * W, with a workspace and M >= 2048: decoded once per call the same way
 //     (the in-kernel decode would repeat it for every 256-row tile of M) and
 //     copied by DMA like A, so the K loop is MFMA, fragment reads and copies.
+//     A caller that keeps the weight decoded (soft_hif8_gemm_decoded_weight)
+//     gets that kernel at every M without the per-call weight decode.
 // 256 x 256 blocks run eight wavefronts in a 2 x 4 arrangement (128 x 64
 // each, two waves per SIMD) whose two wave rows alternate between MFMA and
 // decode half a step apart; 128 x 128 blocks run four in a 2 x 2 arrangement.
@@ -546,7 +548,12 @@ int env_int(const char *name, int fallback) {
   return v && *v ? atoi(v) : fallback;
 }
 
-GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
+// decoded_weight: the plan of soft_hif8_gemm_decoded_weight, whose kernel
+// reads W by DMA at every M.  There, from M = 2048 on, a grid of at most 128
+// 256-tiles (half the CUs) runs faster as unsplit 128-tiles than as 256-tiles
+// split in two (4096 x 2048 x 4096: 88 vs 99.5 us on MI355X); with 192 tiles
+// (M = 512 gate_up) 256-tiles win.
+GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k, bool decoded_weight = false) {
   static const int tile_env = env_int("HIF8_GEMM_TILE", 0);
   static const int split_env = env_int("HIF8_GEMM_SPLIT", 0);
   static const int wpre_env = env_int("HIF8_GEMM_WPRE", -1);
@@ -563,6 +570,7 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k) {
   const bool long_k_fill = m >= 256 && tiles256 * s256 == 256;
   p.tile = tile_env == 128 || tile_env == 256 ? tile_env
                                               : (m >= 256 && (tiles256 >= 128 || long_k_fill) ? 256 : 128);
+  if (decoded_weight && tile_env == 0 && m >= 2048 && tiles256 <= 128) p.tile = 128;
   const int64_t tiles = ((m + p.tile - 1) / p.tile) * ((n + p.tile - 1) / p.tile);
   const int64_t slots = p.tile == 256 ? 256 : 512;  // resident blocks on 256 CUs
   p.splits = 1;
@@ -670,6 +678,35 @@ int launch_gemm(const LinearArgs &a) {
     return launch_tiled<128, 128, 2, 2, true, true, false>(a, abf, wbf, splits, partial);
   }
   return launch_plan<true>(a, p, abf, p.part_bytes ? p.splits : 1, partial);
+}
+
+size_t gemm_decoded_weight_workspace_size(int64_t m, int64_t n, int64_t k) {
+  if (m <= 0 || n <= 0 || k <= 0 || m > 0x7FFFFFFFll || n > 0x7FFFFFFFll || k > 0x7FFFFFFFll || k % kBK)
+    return 0;
+  const GemmPlan p = plan_gemm(m, n, k, true);
+  return p.a_bytes + p.part_bytes;
+}
+
+int launch_gemm_decoded_weight(const LinearArgs &a) {
+  const GemmPlan p = plan_gemm(a.m, a.n, a.k, true);
+  uint8_t *ws = static_cast<uint8_t *>(a.workspace);
+  uint16_t *abf = reinterpret_cast<uint16_t *>(ws);
+  const size_t chunks = size_t(a.m) * size_t(a.k) / 16;
+  decode_rows_kernel<<<unsigned(std::min<size_t>((chunks + 255) / 256, 2048)), 256, 0, a.stream>>>(
+      static_cast<const uint8_t *>(a.act), abf, chunks);
+  const int st = check_launch("soft_hif8 GEMM (activation decode)");
+  if (st) return st;
+  float *partial = p.part_bytes ? reinterpret_cast<float *>(ws + p.a_bytes) : nullptr;
+  const int splits = p.part_bytes ? p.splits : 1;
+  if (p.tile == 256) return launch_tiled<256, 256, 2, 4, true, true, false>(a, abf, a.weight_bf16, splits, partial);
+  return launch_tiled<128, 128, 2, 2, true, true, false>(a, abf, a.weight_bf16, splits, partial);
+}
+
+int launch_decode_bf16(const uint8_t *codes, uint16_t *out, size_t elements, hipStream_t stream) {
+  const size_t chunks = elements / 16;
+  decode_rows_kernel<<<unsigned(std::min<size_t>((chunks + 255) / 256, 4096)), 256, 0, stream>>>(codes, out,
+                                                                                                  chunks);
+  return check_launch("hif8_decode_bf16");
 }
 
 }  // namespace hif8

@@ -27,6 +27,7 @@ struct LinearArgs {
   hipStream_t stream;
   void *workspace = nullptr;    // split-K partials (GEMM only), may be null
   size_t workspace_bytes = 0;
+  const uint16_t *weight_bf16 = nullptr;  // [n, k] weight decoded beforehand (GEMM), else null
 };
 
 // HBM-streaming GEMV for m <= 4 (gemv.hip).  Returns a status.
@@ -36,5 +37,14 @@ int launch_gemv(const LinearArgs &a);
 // the chip split K over several blocks; without one they run unsplit.
 int launch_gemm(const LinearArgs &a);
 size_t gemm_workspace_size(int64_t m, int64_t n, int64_t k);
+// The GEMM with the weight already decoded to bf16 (a.weight_bf16; a.weight is
+// not read): the activation codes are decoded into the workspace and both
+// operands stream into LDS by DMA.  Needs k % 64 == 0, 16-byte aligned
+// operands and a 256-byte aligned workspace of
+// gemm_decoded_weight_workspace_size(m, n, k) bytes (checked by the caller).
+int launch_gemm_decoded_weight(const LinearArgs &a);
+size_t gemm_decoded_weight_workspace_size(int64_t m, int64_t n, int64_t k);
+// HiF8 codes -> bf16 (elements % 16 == 0, 16-byte aligned buffers).
+int launch_decode_bf16(const uint8_t *codes, uint16_t *out, size_t elements, hipStream_t stream);
 
 }  // namespace hif8

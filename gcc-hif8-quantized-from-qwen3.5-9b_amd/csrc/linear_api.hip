@@ -96,6 +96,47 @@ extern "C" int soft_hif8_gemm(const uint8_t *activation, const uint8_t *weight,
                                        bias_dtype, out, out_dtype, m, n, k, nullptr, 0, stream);
 }
 
+extern "C" int hif8_decode_bf16(const uint8_t *codes, uint16_t *out, int64_t elements, hif8_stream_t stream) {
+  clear_error();
+  if (!codes || !out) return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_decode_bf16: null pointer argument");
+  if (elements < 0 || elements % 16)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_decode_bf16: element count must be a non-negative multiple of 16, got %lld",
+                (long long)elements);
+  if (!aligned(codes, 16) || !aligned(out, 16))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_decode_bf16: buffers must be 16-byte aligned");
+  if (elements == 0) return HIF8_OK;
+  return launch_decode_bf16(codes, out, size_t(elements), reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" size_t soft_hif8_gemm_decoded_weight_workspace_size(int64_t m, int64_t n, int64_t k) {
+  return gemm_decoded_weight_workspace_size(m, n, k);
+}
+
+extern "C" int soft_hif8_gemm_decoded_weight(const uint8_t *activation, const uint16_t *weight_bf16,
+                                             const float *token_scale, const float *channel_scale,
+                                             const void *bias, int bias_dtype, void *out, int out_dtype,
+                                             int64_t m, int64_t n, int64_t k, void *workspace,
+                                             size_t workspace_bytes, hif8_stream_t stream) {
+  clear_error();
+  const char *op = "soft_hif8_gemm_decoded_weight";
+  int st = validate(op, activation, reinterpret_cast<const uint8_t *>(weight_bf16), token_scale, channel_scale,
+                    bias, bias_dtype, out, out_dtype, m, n, k);
+  if (st) return st;
+  if (k % 64) return fail(HIF8_ERR_UNSUPPORTED, "%s: K must be a multiple of 64, got %lld", op, (long long)k);
+  if (!aligned(activation, 16) || !aligned(weight_bf16, 16))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: activation and weight must be 16-byte aligned", op);
+  const size_t need = gemm_decoded_weight_workspace_size(m, n, k);
+  if (!workspace || workspace_bytes < need)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: workspace of %zu bytes, %zu required", op, workspace_bytes, need);
+  if (!aligned(workspace, 256)) return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: workspace must be 256-byte aligned", op);
+  LinearArgs a = codes_args(activation, nullptr, token_scale, channel_scale, bias, bias_dtype, out, out_dtype, m,
+                            n, k, stream);
+  a.weight_bf16 = weight_bf16;
+  a.workspace = workspace;
+  a.workspace_bytes = workspace_bytes;
+  return launch_gemm_decoded_weight(a);
+}
+
 extern "C" int soft_hif8_static_fused_gemm(const void *x, int x_dtype, const uint8_t *weight,
                                            const float *fixed_scale, const float *channel_scale,
                                            const void *bias, int bias_dtype, void *out,

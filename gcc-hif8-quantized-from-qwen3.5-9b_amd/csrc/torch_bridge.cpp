@@ -53,13 +53,15 @@ void CheckStatus(int status, const char *op) {
 void ValidateSoftLinear(const at::Tensor &activation, const at::Tensor &weight,
                         const at::Tensor &token_scale, const at::Tensor &channel_scale,
                         const c10::optional<at::Tensor> &bias, at::ScalarType output_dtype,
-                        bool gemv) {
+                        bool gemv, at::ScalarType weight_dtype = at::ScalarType::Byte) {
   CheckDeviceTensor(activation, "activation");
   CheckDeviceTensor(weight, "weight");
   CheckDeviceTensor(token_scale, "token_scale");
   CheckDeviceTensor(channel_scale, "channel_scale");
   TORCH_CHECK(activation.scalar_type() == at::ScalarType::Byte, "activation must have dtype torch.uint8");
-  TORCH_CHECK(weight.scalar_type() == at::ScalarType::Byte, "weight must have dtype torch.uint8");
+  TORCH_CHECK(weight.scalar_type() == weight_dtype, weight_dtype == at::ScalarType::Byte
+                                                       ? "weight must have dtype torch.uint8"
+                                                       : "weight must have dtype torch.bfloat16 (decoded HiF8)");
   TORCH_CHECK(token_scale.scalar_type() == at::ScalarType::Float, "token_scale must have dtype torch.float32");
   TORCH_CHECK(channel_scale.scalar_type() == at::ScalarType::Float, "channel_scale must have dtype torch.float32");
   TORCH_CHECK(activation.dim() == 2, "activation must have shape [M, K]");
@@ -205,6 +207,41 @@ at::Tensor SoftHif8Gemm(const at::Tensor &activation, const at::Tensor &weight, 
                   channel_scale.data_ptr<float>(), bias_ptr, bias_dtype, out.data_ptr(), DtypeCode(output_dtype),
                   m, n, k, ws_bytes ? ws.data_ptr() : nullptr, ws_bytes, CurrentStream(activation.device())),
               "soft_hif8_gemm");
+  return out;
+}
+
+// Prefill GEMM over a weight kept decoded to bf16 (no reference counterpart).
+at::Tensor SoftHif8GemmDecodedWeight(const at::Tensor &activation, const at::Tensor &weight_bf16,
+                                     const at::Tensor &token_scale, const at::Tensor &channel_scale,
+                                     const c10::optional<at::Tensor> &bias, at::ScalarType output_dtype) {
+  ValidateSoftLinear(activation, weight_bf16, token_scale, channel_scale, bias, output_dtype, false,
+                     at::ScalarType::BFloat16);
+  const c10::OptionalDeviceGuard guard(activation.device());
+  const int64_t m = activation.size(0), n = weight_bf16.size(0), k = activation.size(1);
+  TORCH_CHECK(k % 64 == 0, "soft_hif8_gemm_decoded_weight requires K % 64 == 0, got ", k);
+  auto out = at::empty({m, n}, activation.options().dtype(output_dtype));
+  const size_t ws_bytes = soft_hif8_gemm_decoded_weight_workspace_size(m, n, k);
+  at::Tensor ws = at::empty({int64_t(ws_bytes)}, activation.options().dtype(at::ScalarType::Byte));
+  const void *bias_ptr = bias.has_value() ? bias->data_ptr() : nullptr;
+  const int bias_dtype = bias.has_value() ? DtypeCode(bias->scalar_type()) : HIF8_DTYPE_NONE;
+  CheckStatus(soft_hif8_gemm_decoded_weight(
+                  activation.data_ptr<uint8_t>(), reinterpret_cast<const uint16_t *>(weight_bf16.data_ptr()),
+                  token_scale.data_ptr<float>(), channel_scale.data_ptr<float>(), bias_ptr, bias_dtype,
+                  out.data_ptr(), DtypeCode(output_dtype), m, n, k, ws.data_ptr(), ws_bytes,
+                  CurrentStream(activation.device())),
+              "soft_hif8_gemm_decoded_weight");
+  return out;
+}
+
+at::Tensor Hif8DecodeBf16(const at::Tensor &codes) {
+  CheckDeviceTensor(codes, "codes");
+  TORCH_CHECK(codes.scalar_type() == at::ScalarType::Byte, "codes must have dtype torch.uint8");
+  TORCH_CHECK(codes.numel() % 16 == 0, "hif8_decode_bf16 requires a multiple of 16 elements, got ", codes.numel());
+  const c10::OptionalDeviceGuard guard(codes.device());
+  auto out = at::empty(codes.sizes(), codes.options().dtype(at::ScalarType::BFloat16));
+  CheckStatus(hif8_decode_bf16(codes.data_ptr<uint8_t>(), reinterpret_cast<uint16_t *>(out.data_ptr()),
+                               codes.numel(), CurrentStream(codes.device())),
+              "hif8_decode_bf16");
   return out;
 }
 
@@ -589,6 +626,10 @@ at::Tensor FusedLinearMeta(const at::Tensor &activation, const at::Tensor &weigh
   return at::empty({activation.size(0), weight.size(0)}, activation.options().dtype(output_dtype));
 }
 
+at::Tensor Hif8DecodeBf16Meta(const at::Tensor &codes) {
+  return at::empty_like(codes, codes.options().dtype(at::kBFloat16));
+}
+
 at::Tensor Hif8ScaledDecodeMeta(const at::Tensor &data, const at::Tensor &) {
   return at::empty_like(data, data.options().dtype(at::kBFloat16));
 }
@@ -630,6 +671,8 @@ TORCH_LIBRARY(vllm_ascend_hif8, m) {
   m.def("hif8_add_rms_norm(Tensor(a!) h, Tensor? delta, Tensor weight, float eps) -> Tensor");
   m.def("hif8_silu_mul(Tensor gate_up) -> Tensor");
   m.def("hif8_qk_norm_rope(Tensor qkv, Tensor q_norm, Tensor k_norm, Tensor pos, Tensor inv_freq, Tensor block_table, int block_size, int num_heads, int num_kv_heads, int head_size, float eps) -> (Tensor, Tensor, Tensor, Tensor)");
+  m.def("soft_hif8_gemm_decoded_weight(Tensor activation, Tensor weight_bf16, Tensor token_scale, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
+  m.def("hif8_decode_bf16(Tensor codes) -> Tensor");
   m.def("hif8_gdn_decode_step(Tensor mixed_qkvz, Tensor ba, Tensor conv_weight, Tensor(a!) conv_state, Tensor a_log, Tensor dt_bias, Tensor(b!) rec_state, Tensor out_norm, int k_heads, int v_heads, int k_dim, int v_dim, float eps) -> Tensor");
 }
 
@@ -648,6 +691,8 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
   m.impl("hif8_silu_mul", &Hif8SiluMul);
   m.impl("hif8_qk_norm_rope", &Hif8QkNormRope);
   m.impl("hif8_gdn_decode_step", &Hif8GdnDecodeStep);
+  m.impl("soft_hif8_gemm_decoded_weight", &SoftHif8GemmDecodedWeight);
+  m.impl("hif8_decode_bf16", &Hif8DecodeBf16);
 }
 
 TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
@@ -661,6 +706,8 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
   m.impl("hif8_embedding_lookup", &Hif8EmbeddingLookupMeta);
   m.impl("hif8_dynamic_quant", &Hif8DynamicQuantMeta);
   m.impl("soft_hif8_fused_gemm", &FusedLinearMeta);
+  m.impl("soft_hif8_gemm_decoded_weight", &LinearMeta);
+  m.impl("hif8_decode_bf16", &Hif8DecodeBf16Meta);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {

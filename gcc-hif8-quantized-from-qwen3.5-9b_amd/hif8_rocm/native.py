@@ -234,6 +234,56 @@ def soft_linear(
     return output.reshape(*activation.shape[:-1], weight.shape[0])
 
 
+def decode_weight(weight: "torch.Tensor") -> "torch.Tensor":
+    """HiF8 codes -> bf16 (exact; no counterpart in the reference): the weight
+    that ``soft_linear_decoded_weight`` reads, 2 bytes per element."""
+    import torch
+
+    if weight.dtype != torch.uint8:
+        raise TypeError(f"decode_weight requires a uint8 tensor, got {weight.dtype}")
+    if weight.numel() % 16:
+        raise ValueError(f"decode_weight requires a multiple of 16 elements, got {weight.numel()}")
+    extension = load_extension()
+    return _operator("hif8_decode_bf16", extension)(_as_native_operand(weight))
+
+
+def soft_linear_decoded_weight(
+    activation: "torch.Tensor",
+    weight_bf16: "torch.Tensor",
+    activation_scale: "torch.Tensor",
+    weight_scale: "torch.Tensor",
+    bias: "torch.Tensor | None" = None,
+    *,
+    output_dtype: "torch.dtype",
+) -> "torch.Tensor":
+    """``soft_linear`` for prefill with the weight kept decoded (``decode_weight``):
+    the same results (FP32 summation order aside) with no per-call weight
+    decode; requires K % 64 == 0.  No counterpart in the reference."""
+    import torch
+
+    if activation.dtype != torch.uint8 or weight_bf16.dtype != torch.bfloat16:
+        raise TypeError("soft_linear_decoded_weight requires uint8 activation codes and a bfloat16 weight")
+    if activation.ndim < 2 or weight_bf16.ndim != 2:
+        raise ValueError("activation must be at least 2D and weight must be 2D")
+    if activation.shape[-1] != weight_bf16.shape[-1]:
+        raise ValueError(
+            f"incompatible K dimensions: activation={activation.shape[-1]}, weight={weight_bf16.shape[-1]}"
+        )
+    if activation_scale.dtype != torch.float32 or weight_scale.dtype != torch.float32:
+        raise TypeError("soft HiFloat8 linear requires float32 activation and weight scales")
+    extension = load_extension()
+    flattened = _as_native_operand(activation.reshape(-1, activation.shape[-1]))
+    token_scale = _as_native_operand(activation_scale.reshape(-1))
+    channel_scale = _as_native_operand(weight_scale.reshape(-1))
+    if token_scale.numel() != flattened.shape[0]:
+        raise ValueError("activation_scale must contain one value per token row")
+    if channel_scale.numel() != weight_bf16.shape[0]:
+        raise ValueError("weight_scale must contain one value per output channel")
+    operator = _operator("soft_hif8_gemm_decoded_weight", extension)
+    output = operator(flattened, _as_native_operand(weight_bf16), token_scale, channel_scale, bias, output_dtype)
+    return output.reshape(*activation.shape[:-1], weight_bf16.shape[0])
+
+
 def soft_fused_linear(
     x: "torch.Tensor",
     weight: "torch.Tensor",

@@ -18,6 +18,12 @@ K = 12288 (down 15.3 vs 14.4) and two or more rows at the large shapes are
 faster separate (each block re-encodes M*K values).
 ``HIF8_STATIC_FUSED_SINGLE_ROW=1`` opts into fusing one token row with
 K <= 4096 as well; it changes which kernels run, not the outputs.
+
+``HIF8_PREFILL_BF16_WEIGHTS=1`` (read in ``process_weights_after_loading``)
+keeps each weight decoded to bf16 beside its codes (2 bytes per element;
+HBM is 288 GB per MI355X) and runs GEMMs of more than four rows on it,
+without the per-call weight decode; results equal the code path's up to
+FP32 summation order.
 """
 
 from __future__ import annotations
@@ -38,6 +44,8 @@ _STATIC_SCALE_FACTOR_ENV = "HIF8_STATIC_SCALE_FACTOR"
 # MI355X opt-in: fuse one token row up to this K (measured; see the module text).
 _STATIC_FUSED_SINGLE_ROW_ENV = "HIF8_STATIC_FUSED_SINGLE_ROW"
 _FUSED_SINGLE_ROW_MAX_K = 4096
+# MI355X opt-in: keep each static weight decoded to bf16 for prefill GEMMs.
+_PREFILL_BF16_WEIGHTS_ENV = "HIF8_PREFILL_BF16_WEIGHTS"
 
 
 def _static_scale_factor() -> float:
@@ -98,6 +106,15 @@ class W8A8HiFloat8StaticLinearMethod:
             raise ValueError(f"{STATIC_QUANT_TYPE} input_scale must be finite and greater than zero")
         layer.input_scale.data = scale.contiguous()
         self._process_hif8_weights(layer)
+        # MI355X opt-in: keep the weight decoded to bf16 as well (2 bytes per
+        # element) so prefill GEMMs skip the per-call weight decode.
+        layer._hif8_weight_bf16 = None
+        if (
+            os.environ.get(_PREFILL_BF16_WEIGHTS_ENV) == "1"
+            and layer.weight.is_cuda
+            and layer.weight.shape[-1] % 64 == 0
+        ):
+            layer._hif8_weight_bf16 = native.decode_weight(layer.weight.data)
 
     def apply(
         self,
@@ -130,6 +147,11 @@ class W8A8HiFloat8StaticLinearMethod:
                 x, layer.weight, fixed_scale, layer.weight_scale, bias, output_dtype=x.dtype
             )
         activation, row_scale = native.static_quant(x, fixed_scale)
+        decoded = getattr(layer, "_hif8_weight_bf16", None)
+        if decoded is not None and token_rows > 4:
+            return native.soft_linear_decoded_weight(
+                activation, decoded, row_scale, layer.weight_scale, bias, output_dtype=x.dtype
+            )
         return native.soft_linear(
             activation, layer.weight, row_scale, layer.weight_scale, bias, output_dtype=x.dtype
         )

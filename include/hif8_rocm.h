@@ -163,6 +163,32 @@ int soft_hif8_gemm_with_workspace(const uint8_t *activation, const uint8_t *weig
                                   size_t workspace_bytes, hif8_stream_t stream);
 
 /*
+ * Prefill GEMM over a weight kept decoded to bf16.  No counterpart in the
+ * reference (its GEMM reads the uint8 weight every call): for callers that
+ * trade memory for speed (2 bytes per weight element, 18 GB for a 9B model,
+ * on 288 GB of HBM) and keep hif8_decode_bf16(weight) next to the codes.
+ * Same arguments and results as soft_hif8_gemm_with_workspace (within FP32
+ * summation order) for any M >= 1, with weight_bf16 [n, k] in place of the
+ * codes; requires K % 64 == 0, 16-byte aligned activation and weight, and a
+ * 256-byte aligned workspace of soft_hif8_gemm_decoded_weight_workspace_size
+ * bytes (the decoded activation and split-K partials).
+ */
+size_t soft_hif8_gemm_decoded_weight_workspace_size(int64_t m, int64_t n, int64_t k);
+int soft_hif8_gemm_decoded_weight(const uint8_t *activation, const uint16_t *weight_bf16,
+                                  const float *token_scale, const float *channel_scale,
+                                  const void *bias, int bias_dtype, void *out, int out_dtype,
+                                  int64_t m, int64_t n, int64_t k, void *workspace,
+                                  size_t workspace_bytes, hif8_stream_t stream);
+
+/*
+ * Plain decode of HiF8 codes to bf16 payloads (exact: every HiF8 value is a
+ * bf16 value; NaN 0x80 -> 0x7FC0), elements % 16 == 0, 16-byte aligned
+ * buffers.  No counterpart in the reference; builds the weight that
+ * soft_hif8_gemm_decoded_weight reads.
+ */
+int hif8_decode_bf16(const uint8_t *codes, uint16_t *out, int64_t elements, hif8_stream_t stream);
+
+/*
  * Fixed-scale fused quant + GEMM for M <= 4.
  * Replaces aclnnSoftHif8StaticFusedGemm as called by SoftHif8StaticFusedGemm
  * (csrc/extension/hif8_native.cpp:784-910; kernel csrc/opp/op_kernel/soft_hif8_fused_gemm.cpp

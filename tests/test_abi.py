@@ -75,6 +75,35 @@ def test_linear_entry_points_enforce_reference_contracts(lib):
     assert b"M <= 4" in lib.hif8_last_error()
 
 
+def test_decoded_weight_entry_points_check_their_contracts(lib):
+    """The prefill GEMM over a bf16-decoded weight needs K % 64 == 0, aligned
+    operands and a workspace (the decoded activation + split partials, no
+    weight copy); the plain decode needs a multiple of 16 elements."""
+    size = lib.soft_hif8_gemm_decoded_weight_workspace_size
+    size.argtypes = [ctypes.c_int64] * 3
+    size.restype = ctypes.c_size_t
+    assert size(4096, 24576, 4096) == 4096 * 4096 * 2
+    assert size(512, 4096, 4096) == 512 * 4096 * 2 + 4 * 512 * 4096 * 4
+    assert size(5, 16, 64) > 0 and size(5, 16, 100) == 0 and size(0, 16, 64) == 0
+    f = lib.soft_hif8_gemm_decoded_weight
+    f.argtypes = [ctypes.c_void_p] * 5 + [ctypes.c_int, ctypes.c_void_p, ctypes.c_int] + \
+        [ctypes.c_int64] * 3 + [ctypes.c_void_p, ctypes.c_size_t, ctypes.c_void_p]
+    a16 = _p(256)
+    assert f(a16, a16, a16, a16, None, -1, a16, 1, 8, 16, 100, a16, 1 << 20, None) == 2
+    assert b"multiple of 64" in lib.hif8_last_error()
+    assert f(a16, a16, a16, a16, None, -1, a16, 1, 8, 16, 64, None, 0, None) == 1
+    assert b"workspace" in lib.hif8_last_error()
+    assert f(a16, _p(258), a16, a16, None, -1, a16, 1, 8, 16, 64, a16, 1 << 20, None) == 1
+    assert b"16-byte aligned" in lib.hif8_last_error()
+    assert f(a16, None, a16, a16, None, -1, a16, 1, 8, 16, 64, a16, 1 << 20, None) == 1
+    assert b"null pointer" in lib.hif8_last_error()
+    dec = lib.hif8_decode_bf16
+    dec.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_void_p]
+    assert dec(a16, a16, 24, None) == 1 and b"multiple of 16" in lib.hif8_last_error()
+    assert dec(_p(8), a16, 32, None) == 1 and b"aligned" in lib.hif8_last_error()
+    assert dec(a16, a16, 0, None) == 0
+
+
 def test_gemm_workspace_query_follows_the_split_plan(lib):
     size = lib.soft_hif8_gemm_workspace_size
     size.argtypes = [ctypes.c_int64] * 3

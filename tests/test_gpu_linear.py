@@ -193,3 +193,78 @@ def test_single_row_fusion_equals_the_two_stage_apply(native_ops, device, monkey
     fused = method.apply(layer, x.to(device))
     torch.cuda.synchronize()
     assert torch.equal(fused, two_stage)
+
+
+def test_decode_bf16_gives_every_code_exactly(native_ops, device):
+    """hif8_decode_bf16 on all 256 codes (NaN 0x80 -> 0x7FC0) against the oracle's bf16 bits."""
+    from hif8_rocm import native as api
+
+    codes = np.tile(np.arange(256, dtype=np.uint8), 3).reshape(6, 128)
+    got = api.decode_weight(_t(codes, device))
+    torch.cuda.synchronize()
+    bits = got.cpu().view(torch.int16).numpy().astype(np.uint16)
+    want = np.array([o.bf16_bits_of_decode(int(c)) for c in codes.reshape(-1)], np.uint16).reshape(codes.shape)
+    np.testing.assert_array_equal(bits, want)
+
+
+@pytest.mark.parametrize("m,n,k", [(5, 16, 64), (129, 33, 128), (300, 1000, 2048), (512, 4096, 4096),
+                                   (512, 4096, 12288), (2048, 24576, 256), (4096, 2048, 4096)])
+def test_decoded_weight_gemm_matches_oracle_and_codes_path(native_ops, device, m, n, k):
+    """soft_hif8_gemm_decoded_weight over hif8_decode_bf16(weight): within 1e-2 of the
+    float64 oracle and within FP32 summation order of soft_hif8_gemm on the codes
+    (split-K plans at M = 512, 128- and 256-tiles, ragged M and N)."""
+    from hif8_rocm import native as api
+
+    a = random_codes((m, k), seed=m + k)
+    w, ws = hif8_weight(n, k, seed=n * 7 + k)
+    g = np.random.default_rng(m * 3 + n)
+    ts = (g.random(m, dtype=np.float32) + 0.5) * 1e-2
+    bias = (g.random(n, dtype=np.float32) - 0.5)
+    want = o.linear_u8_u8(a, ts, w, ws, bias.astype(np.float64))
+    wd = api.decode_weight(_t(w, device))
+    bias_t = _t(bias, device, torch.bfloat16)
+    y = api.soft_linear_decoded_weight(_t(a, device), wd, _t(ts, device), _t(ws, device), bias_t,
+                                       output_dtype=torch.bfloat16)
+    y_codes = native_ops.soft_hif8_gemm(_t(a, device), _t(w, device), _t(ts, device), _t(ws, device), bias_t,
+                                        torch.bfloat16)
+    torch.cuda.synchronize()
+    rounded = torch.from_numpy(bias).to(torch.bfloat16).float().numpy().astype(np.float64)
+    _check(y, want - bias + rounded)
+    torch.testing.assert_close(y.float(), y_codes.float(), rtol=1e-2, atol=1e-3)
+
+
+def test_prefill_bf16_weights_scheme_equals_the_codes_scheme(native_ops, device, monkeypatch):
+    """HIF8_PREFILL_BF16_WEIGHTS=1: the layer keeps a decoded weight; M > 4 runs on it
+    (within FP32 summation order of the default), M <= 4 is unchanged bit for bit."""
+    import torch.nn as nn
+
+    from hif8_rocm import scheme
+
+    n, k = 1000, 4096
+    w, ws = hif8_weight(n, k, seed=5)
+
+    def layer_with(flag):
+        if flag:
+            monkeypatch.setenv("HIF8_PREFILL_BF16_WEIGHTS", "1")
+        else:
+            monkeypatch.delenv("HIF8_PREFILL_BF16_WEIGHTS", raising=False)
+        layer = nn.Module()
+        layer.weight = nn.Parameter(_t(w, device), requires_grad=False)
+        layer.weight_scale = nn.Parameter(_t(ws, device).reshape(-1, 1), requires_grad=False)
+        layer.input_scale = nn.Parameter(torch.tensor([2e-4], device=device), requires_grad=False)
+        method = scheme.W8A8HiFloat8StaticLinearMethod()
+        method.process_weights_after_loading(layer)
+        return method, layer
+
+    m0, plain = layer_with(False)
+    m1, cached = layer_with(True)
+    assert plain._hif8_weight_bf16 is None and cached._hif8_weight_bf16.dtype == torch.bfloat16
+    for rows in (3, 300):
+        x = bf16_activation(rows, k, seed=rows).to(device)
+        a, b = m0.apply(plain, x), m1.apply(cached, x)
+        torch.cuda.synchronize()
+        if rows <= 4:
+            assert torch.equal(a, b)
+        else:
+            torch.testing.assert_close(b.float(), a.float(), rtol=1e-2, atol=1e-3)
+

@@ -65,6 +65,12 @@ def test_meta_shapes():
         torch.empty(5, 64, dtype=torch.uint8, device="meta"), torch.empty(7, 64, dtype=torch.uint8, device="meta"),
         torch.empty(5, device="meta"), torch.empty(7, device="meta"), None, torch.bfloat16)
     assert y.shape == (5, 7) and y.dtype == torch.bfloat16
+    yd = torch.ops.vllm_ascend_hif8.soft_hif8_gemm_decoded_weight(
+        torch.empty(5, 64, dtype=torch.uint8, device="meta"), torch.empty(7, 64, dtype=torch.bfloat16, device="meta"),
+        torch.empty(5, device="meta"), torch.empty(7, device="meta"), None, torch.float16)
+    assert yd.shape == (5, 7) and yd.dtype == torch.float16
+    wd = torch.ops.vllm_ascend_hif8.hif8_decode_bf16(torch.empty(7, 64, dtype=torch.uint8, device="meta"))
+    assert wd.shape == (7, 64) and wd.dtype == torch.bfloat16
     d, ds = torch.ops.vllm_ascend_hif8.hif8_dynamic_quant(x)
     assert d.shape == x.shape and d.dtype == torch.uint8 and ds.shape == (6,) and ds.dtype == torch.float32
     f = torch.ops.vllm_ascend_hif8.soft_hif8_fused_gemm(
@@ -167,7 +173,7 @@ def _layer(input_scale=0.25, k=8):
 def clean_env():
     with patch.dict(os.environ, {}, clear=False):
         for var in ("HIF8_COMPUTE_BACKEND", "HIF8_STATIC_FUSED_GENERATION", "HIF8_STATIC_SCALE_FACTOR",
-                    "HIF8_STATIC_FUSED_SINGLE_ROW"):
+                    "HIF8_STATIC_FUSED_SINGLE_ROW", "HIF8_PREFILL_BF16_WEIGHTS"):
             os.environ.pop(var, None)
         yield
 
@@ -264,6 +270,40 @@ def test_single_row_fusion_is_an_opt_in(clean_env):
         if want_fused:
             fused.assert_called_once_with(x, layer.weight, layer.input_scale, layer.weight_scale, None,
                                           output_dtype=x.dtype)
+
+
+def test_prefill_bf16_weights_route_only_large_m(clean_env):
+    """A layer holding a decoded weight runs M > 4 on it; M <= 4 keeps the codes."""
+    method = W8A8HiFloat8StaticLinearMethod()
+    layer = _layer(k=64)
+    method.process_weights_after_loading(layer)
+    assert layer._hif8_weight_bf16 is None  # opt-in only (and CPU tensors are never decoded)
+    layer._hif8_weight_bf16 = torch.zeros(5, 64, dtype=torch.bfloat16)
+    for rows, want_decoded in ((5, True), (512, True), (4, False), (1, False)):
+        x = torch.zeros((rows, 64), dtype=torch.bfloat16)
+        enc, rs = x.to(torch.uint8), torch.ones(rows)
+        with patch("hif8_rocm.scheme.native.static_quant", return_value=(enc, rs)), \
+             patch("hif8_rocm.scheme.native.soft_linear") as lin, \
+             patch("hif8_rocm.scheme.native.soft_linear_decoded_weight") as dec:
+            method.apply(layer, x)
+        assert dec.called == want_decoded and lin.called != want_decoded, rows
+        if want_decoded:
+            dec.assert_called_once_with(enc, layer._hif8_weight_bf16, rs, layer.weight_scale, None,
+                                        output_dtype=x.dtype)
+
+
+def test_decoded_weight_wrappers_validate_dtypes():
+    with pytest.raises(TypeError, match="uint8"):
+        native.decode_weight(torch.zeros(4, 16, dtype=torch.float32))
+    with pytest.raises(ValueError, match="multiple of 16"):
+        native.decode_weight(torch.zeros(3, 5, dtype=torch.uint8))
+    with pytest.raises(TypeError, match="bfloat16 weight"):
+        native.soft_linear_decoded_weight(torch.zeros(8, 64, dtype=torch.uint8), torch.zeros(4, 64, dtype=torch.uint8),
+                                          torch.ones(8), torch.ones(4), output_dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="incompatible K"):
+        native.soft_linear_decoded_weight(torch.zeros(8, 64, dtype=torch.uint8),
+                                          torch.zeros(4, 128, dtype=torch.bfloat16), torch.ones(8), torch.ones(4),
+                                          output_dtype=torch.bfloat16)
 
 
 def test_scale_factor_env_multiplies_the_checkpoint_scale(clean_env):
