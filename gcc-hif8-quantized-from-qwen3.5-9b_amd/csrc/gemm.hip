@@ -536,6 +536,7 @@ __global__ __launch_bounds__(256) void gemm_simple_kernel(
 // partials (splits x M x N x 4 bytes).
 struct GemmPlan {
   int tile;          // 256 (8 waves) or 128 (4 waves)
+  int bn;            // block columns: tile, or 192 for 256-row tiles (decoded weights only)
   int splits;        // K splits
   bool w_pre;        // W decoded once per call too (large M)
   size_t a_bytes;    // bf16 copy of A
@@ -587,6 +588,15 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k, bool decoded_weight = false)
   // Decoding W once costs ~3 bytes of HBM traffic per weight; the in-kernel
   // decode repeats it once per 256-row tile of M, so from M = 2048 on the
   // one-pass decode wins and the kernel streams both operands by DMA.
+  // Decoded weights: an unsplit 256-tile grid short of one block per CU
+  // takes 256 x 192 blocks when those still fit one wave of blocks (gate_up
+  // at M = 512: 192 -> 256 blocks).  The in-kernel weight decode does not
+  // divide over 192 rows, so the code path keeps 256 x 256.
+  p.bn = p.tile;
+  if (decoded_weight && p.tile == 256 && p.splits == 1 && tile_env == 0) {
+    const int64_t tiles192 = ((m + 255) / 256) * ((n + 191) / 192);
+    if (tiles256 < 256 && tiles192 > tiles256 && tiles192 <= 256) p.bn = 192;
+  }
   p.w_pre = wpre_env >= 0 ? wpre_env > 0 : (p.tile == 256 && p.splits == 1 && m >= 2048);
   p.a_bytes = (size_t(m) * size_t(k) * 2 + 255) / 256 * 256;
   p.w_bytes = p.w_pre ? (size_t(n) * size_t(k) * 2 + 255) / 256 * 256 : 0;
@@ -698,6 +708,8 @@ int launch_gemm_decoded_weight(const LinearArgs &a) {
   if (st) return st;
   float *partial = p.part_bytes ? reinterpret_cast<float *>(ws + p.a_bytes) : nullptr;
   const int splits = p.part_bytes ? p.splits : 1;
+  if (p.tile == 256 && p.bn == 192)
+    return launch_tiled<256, 192, 2, 4, true, true, false>(a, abf, a.weight_bf16, splits, partial);
   if (p.tile == 256) return launch_tiled<256, 256, 2, 4, true, true, false>(a, abf, a.weight_bf16, splits, partial);
   return launch_tiled<128, 128, 2, 2, true, true, false>(a, abf, a.weight_bf16, splits, partial);
 }

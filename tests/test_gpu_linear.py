@@ -208,11 +208,12 @@ def test_decode_bf16_gives_every_code_exactly(native_ops, device):
 
 
 @pytest.mark.parametrize("m,n,k", [(5, 16, 64), (129, 33, 128), (300, 1000, 2048), (512, 4096, 4096),
-                                   (512, 4096, 12288), (2048, 24576, 256), (4096, 2048, 4096)])
+                                   (512, 4096, 12288), (2048, 24576, 256), (4096, 2048, 4096),
+                                   (512, 24500, 256), (300, 24576, 128)])
 def test_decoded_weight_gemm_matches_oracle_and_codes_path(native_ops, device, m, n, k):
     """soft_hif8_gemm_decoded_weight over hif8_decode_bf16(weight): within 1e-2 of the
     float64 oracle and within FP32 summation order of soft_hif8_gemm on the codes
-    (split-K plans at M = 512, 128- and 256-tiles, ragged M and N)."""
+    (split-K plans at M = 512, 128-, 256- and 256 x 192 tiles, ragged M and N)."""
     from hif8_rocm import native as api
 
     a = random_codes((m, k), seed=m + k)
