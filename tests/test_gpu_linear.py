@@ -62,7 +62,7 @@ def test_soft_linear_matches_reference_small(native_ops, device, rows):
     (1, 17, 37), (2, 17, 37), (3, 3, 4), (5, 16, 16), (3, 17, 37), (3, 256, 16),
     (3, 2176, 16), (5, 16, 255), (1, 17, 1024), (2, 17, 1037), (1, 33, 2048),
     (63, 16, 37), (64, 16, 64), (65, 17, 128), (129, 1024, 4097), (130, 300, 4096),
-    (2, 40, 4112), (3, 24, 8192), (4, 9, 4096), (2, 1, 16),
+    (2, 40, 4112), (3, 24, 8192), (4, 9, 4096), (2, 1, 16), (3, 40, 256), (1, 70, 512), (4, 33, 2048),
 ])
 def test_gemm_shapes_and_tails(native_ops, device, rows, channels, k):
     a = random_codes((rows, k), seed=rows * 7 + k)
