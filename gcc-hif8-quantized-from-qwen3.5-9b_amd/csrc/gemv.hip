@@ -661,7 +661,10 @@ int launch_gemv(const LinearArgs &a) {
         a.act, a.act_kind, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out,
         a.out_dtype, int(a.m), int(a.n), int(a.k));
   } else {
-    const int rows = knobs.rows ? knobs.rows : 8;
+    // 8 rows per block; M = 4 over wide weights (N >= 16384: at least 1024
+    // blocks) streams faster with 16 (gate_up 24576 x 4096: 24.8 vs 25.7-26.5
+    // us on MI355X; q/o/k-v and down are slower with 16, M = 1 too).
+    const int rows = knobs.rows ? knobs.rows : (a.m == 4 && a.n >= 16384 ? 16 : 8);
     if (rows >= 16) dispatch_m<16>(a);
     else if (rows >= 8) dispatch_m<8>(a);
     else dispatch_m<4>(a);
