@@ -12,6 +12,7 @@
 //       value heads; beta = sigmoid(b), g = -exp(A_log) softplus(a + dt_bias);
 //       S <- e^g S;  S <- S + k (beta (v - S^T k))^T;  o = S^T q;
 //       out = bf16(rms_norm(o) * w_out * silu(z)).
+//   hif8_bf16_gemv        out = bf16(x w^T) for M <= 4 (the small bf16 projections)
 //   hif8_qk_norm_rope     per-head RMSNorm of q and k, rotary embedding on the
 //       first rotary_dim dims (neox halves), v split off, cache slots.
 #include <math.h>
@@ -93,6 +94,132 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const uint16_t *__restric
   out[idx] = acc / (1.f + expf(-acc));
 }
 
+// Rows of n % 8 == 0, n <= 8 * kNormThreads * kNormChunks, 16-byte aligned:
+// thread t owns 16-byte chunks t + kNormThreads * c, loads all of them at
+// once and keeps the row in registers (the scalar loop above waits on one
+// 2-byte load per iteration and re-reads the row: ~10 us for n = 4096).
+constexpr int kNormChunks = 4;
+
+template <bool kResidual>
+__global__ __launch_bounds__(kNormThreads) void add_rms_norm_vec_kernel(uint16_t *__restrict__ h,
+                                                                        const uint16_t *__restrict__ delta,
+                                                                        const uint16_t *__restrict__ w,
+                                                                        uint16_t *__restrict__ out, int n,
+                                                                        float eps) {
+  __shared__ float red[kNormThreads / kWave];
+  const int chunks = n / 8;
+  uint4 *hr = reinterpret_cast<uint4 *>(h + size_t(blockIdx.x) * n);
+  const uint4 *dr = kResidual ? reinterpret_cast<const uint4 *>(delta + size_t(blockIdx.x) * n) : nullptr;
+  const uint4 *wr = reinterpret_cast<const uint4 *>(w);
+  uint4 *orow = reinterpret_cast<uint4 *>(out + size_t(blockIdx.x) * n);
+  uint4 hv[kNormChunks], dv[kNormChunks], wv[kNormChunks];
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int i = threadIdx.x + kNormThreads * c;
+    if (i < chunks) {
+      hv[c] = hr[i];
+      if constexpr (kResidual) dv[c] = dr[i];
+      wv[c] = wr[i];
+    }
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int i = threadIdx.x + kNormThreads * c;
+    if (i < chunks) {
+      uint32_t hw[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        float lo = __uint_as_float(hw[e] << 16), hi = __uint_as_float(hw[e] & 0xFFFF0000u);
+        if constexpr (kResidual) {
+          const uint32_t dw = e == 0 ? dv[c].x : e == 1 ? dv[c].y : e == 2 ? dv[c].z : dv[c].w;
+          // the residual stream is bf16
+          const uint32_t slo = to_bf(lo + __uint_as_float(dw << 16)), shi = to_bf(hi + __uint_as_float(dw & 0xFFFF0000u));
+          hw[e] = slo | (shi << 16);
+          lo = bf(uint16_t(slo));
+          hi = bf(uint16_t(shi));
+        }
+        ss += lo * lo + hi * hi;
+      }
+      hv[c] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      if constexpr (kResidual) hr[i] = hv[c];
+    }
+  }
+  const float r = rsqrtf(block_sum<kNormThreads>(ss, red) / float(n) + eps);
+#pragma unroll
+  for (int c = 0; c < kNormChunks; ++c) {
+    const int i = threadIdx.x + kNormThreads * c;
+    if (i < chunks) {
+      const uint32_t hw[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
+      const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
+      uint32_t o[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = __uint_as_float(hw[e] << 16) * r * __uint_as_float(ww[e] << 16);
+        const float hi = __uint_as_float(hw[e] & 0xFFFF0000u) * r * __uint_as_float(ww[e] & 0xFFFF0000u);
+        o[e] = uint32_t(to_bf(lo)) | (uint32_t(to_bf(hi)) << 16);
+      }
+      orow[i] = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+  }
+}
+
+// out[m, n] = bf16(sum_k x[m, k] w[n, k]) for m < 4, bf16 operands, FP32
+// accumulation: the small bf16 projections of the decode step (the
+// linear-attention b/a projection, 2 * value heads outputs), which a library
+// GEMM runs in ~14 us.  Block = kSmallRows output rows; thread t sums 16-byte
+// chunks t, t + 256, ... of each; k % 8 == 0, 16-byte aligned rows.
+constexpr int kSmallRows = 4;
+
+template <int kM>
+__global__ __launch_bounds__(kNormThreads) void bf16_gemv_kernel(const uint16_t *__restrict__ x,
+                                                                 const uint16_t *__restrict__ w,
+                                                                 uint16_t *__restrict__ out, int n, int k) {
+  __shared__ float red[kNormThreads / kWave][kSmallRows * kM];
+  const int n0 = blockIdx.x * kSmallRows, chunks = k / 8;
+  float acc[kSmallRows][kM];
+#pragma unroll
+  for (int r = 0; r < kSmallRows; ++r)
+#pragma unroll
+    for (int m = 0; m < kM; ++m) acc[r][m] = 0.f;
+  for (int c = threadIdx.x; c < chunks; c += kNormThreads) {
+    uint4 xv[kM], wv[kSmallRows];
+#pragma unroll
+    for (int m = 0; m < kM; ++m) xv[m] = reinterpret_cast<const uint4 *>(x + size_t(m) * k)[c];
+#pragma unroll
+    for (int r = 0; r < kSmallRows; ++r)
+      wv[r] = reinterpret_cast<const uint4 *>(w + size_t(min(n0 + r, n - 1)) * k)[c];
+#pragma unroll
+    for (int r = 0; r < kSmallRows; ++r) {
+      const uint32_t ww[4] = {wv[r].x, wv[r].y, wv[r].z, wv[r].w};
+#pragma unroll
+      for (int m = 0; m < kM; ++m) {
+        const uint32_t xw[4] = {xv[m].x, xv[m].y, xv[m].z, xv[m].w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          acc[r][m] += __uint_as_float(xw[e] << 16) * __uint_as_float(ww[e] << 16) +
+                       __uint_as_float(xw[e] & 0xFFFF0000u) * __uint_as_float(ww[e] & 0xFFFF0000u);
+      }
+    }
+  }
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+#pragma unroll
+  for (int r = 0; r < kSmallRows; ++r)
+#pragma unroll
+    for (int m = 0; m < kM; ++m) {
+      const float v = wave_sum(acc[r][m]);
+      if (lane == 0) red[wave][r * kM + m] = v;
+    }
+  __syncthreads();
+  if (threadIdx.x < kSmallRows * kM) {
+    const int r = threadIdx.x / kM, m = threadIdx.x % kM;
+    float v = 0.f;
+#pragma unroll
+    for (int i = 0; i < kNormThreads / kWave; ++i) v += red[i][threadIdx.x];
+    if (n0 + r < n) out[size_t(m) * n + n0 + r] = to_bf(v);
+  }
+}
+
 constexpr int kGdnThreads = 128;
 
 // One block per (request, value head); thread j owns column j of the
@@ -142,6 +269,85 @@ __global__ __launch_bounds__(kGdnThreads) void gdn_delta_kernel(
   }
   const float r = rsqrtf(block_sum<kGdnThreads>(j < dv ? o * o : 0.f, red) / float(dv) + eps);
   if (j < dv) {
+    const float z = bf(mixed[size_t(b) * ld + 2 * qk_width + v_heads * dv + hv * dv + j]);
+    out[(size_t(b) * v_heads + hv) * dv + j] = to_bf(o * r * bf(w_out[j]) * (z / (1.f + expf(-z))));
+  }
+}
+
+// The same step with each (request, value head) spread over 1024 threads:
+// thread (part, j) owns rows [part * R, part * R + R) of state column j
+// (R = dk / 8 <= 16), loads them at once and keeps them in registers; the
+// column sums S^T k and S^T q meet in LDS.  One block per head with 128
+// threads walking all dk rows twice took ~33 us per layer (dk = dv = 128).
+// Requires dk % 8 == 0, dk <= 128, dv <= 128.
+constexpr int kGdnParts = 8, kGdnCols = 128, kGdnWideThreads = kGdnParts * kGdnCols;
+constexpr int kGdnRows = 16;  // rows per part, at most
+
+__global__ __launch_bounds__(kGdnWideThreads) void gdn_delta_wide_kernel(
+    const float *__restrict__ conv, int channels, const uint16_t *__restrict__ mixed, int64_t ld,
+    const uint16_t *__restrict__ ba, const float *__restrict__ a_log, const float *__restrict__ dt_bias,
+    float *__restrict__ state, const uint16_t *__restrict__ w_out, uint16_t *__restrict__ out, int k_heads,
+    int v_heads, int dk, int dv, float eps) {
+  __shared__ float qs[kGdnCols], ks[kGdnCols];
+  __shared__ float pa[kGdnParts][kGdnCols], pc[kGdnParts][kGdnCols];
+  __shared__ float red[kGdnWideThreads / kWave];
+  const int b = blockIdx.x / v_heads, hv = blockIdx.x - b * v_heads;
+  const int hk = hv / (v_heads / k_heads);
+  const int qk_width = k_heads * dk;
+  const int j = threadIdx.x % kGdnCols, part = threadIdx.x / kGdnCols;
+  const int rows = dk / kGdnParts, r0 = part * rows;
+  const bool col_ok = j < dv;
+  float *S = state + (size_t(b) * v_heads + hv) * dk * dv;
+  // State rows first (the longest loads), then the conv outputs.
+  float sv[kGdnRows];
+#pragma unroll
+  for (int i = 0; i < kGdnRows; ++i) sv[i] = (i < rows && col_ok) ? S[size_t(r0 + i) * dv + j] : 0.f;
+  const float *cr = conv + size_t(b) * channels;
+  const bool lead = part == 0;
+  const float qi = lead && j < dk ? cr[hk * dk + j] : 0.f;
+  const float ki = lead && j < dk ? cr[qk_width + hk * dk + j] : 0.f;
+  const float vj = col_ok ? cr[2 * qk_width + hv * dv + j] : 0.f;
+  // F.normalize: x / max(||x||, 1e-12); q also scaled by 1 / sqrt(dk).
+  const float qn = fmaxf(sqrtf(block_sum<kGdnWideThreads>(qi * qi, red)), 1e-12f);
+  const float kn = fmaxf(sqrtf(block_sum<kGdnWideThreads>(ki * ki, red)), 1e-12f);
+  const float qv = qi / qn / sqrtf(float(dk)), kv = ki / kn;
+  if (lead) {
+    qs[j] = qv;
+    ks[j] = kv;
+  }
+  const float kq = block_sum<kGdnWideThreads>(kv * qv, red);  // also orders the qs / ks stores
+  const float braw = bf(ba[size_t(b) * 2 * v_heads + hv]);
+  const float araw = bf(ba[size_t(b) * 2 * v_heads + v_heads + hv]) + dt_bias[hv];
+  const float beta = 1.f / (1.f + expf(-braw));
+  const float softplus = araw > 20.f ? araw : log1pf(expf(araw));
+  const float decay = expf(-expf(a_log[hv]) * softplus);
+  float a = 0.f, c = 0.f;
+#pragma unroll
+  for (int i = 0; i < kGdnRows; ++i) {
+    if (i < rows) {
+      a += sv[i] * ks[r0 + i];
+      c += sv[i] * qs[r0 + i];
+    }
+  }
+  pa[part][j] = a;
+  pc[part][j] = c;
+  __syncthreads();
+  a = 0.f;
+  c = 0.f;
+#pragma unroll
+  for (int p = 0; p < kGdnParts; ++p) {
+    a += pa[p][j];
+    c += pc[p][j];
+  }
+  const float delta = beta * (vj - decay * a);
+  const float o = decay * c + delta * kq;
+  if (col_ok) {
+#pragma unroll
+    for (int i = 0; i < kGdnRows; ++i)
+      if (i < rows) S[size_t(r0 + i) * dv + j] = decay * sv[i] + ks[r0 + i] * delta;
+  }
+  const float r = rsqrtf(block_sum<kGdnWideThreads>(lead && col_ok ? o * o : 0.f, red) / float(dv) + eps);
+  if (lead && col_ok) {
     const float z = bf(mixed[size_t(b) * ld + 2 * qk_width + v_heads * dv + hv * dv + j]);
     out[(size_t(b) * v_heads + hv) * dv + j] = to_bf(o * r * bf(w_out[j]) * (z / (1.f + expf(-z))));
   }
@@ -222,7 +428,13 @@ extern "C" int hif8_add_rms_norm(uint16_t *h, const uint16_t *delta, const uint1
   if (rows <= 0 || n <= 0 || rows > 0x7FFFFFFFll || n > 0x7FFFFFFFll)
     return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_add_rms_norm: invalid dimensions");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  if (delta)
+  const bool vec = n % 8 == 0 && n <= 8 * kNormThreads * kNormChunks && aligned(h, 16) && aligned(weight, 16) &&
+                   aligned(out, 16) && (!delta || aligned(delta, 16));
+  if (vec && delta)
+    add_rms_norm_vec_kernel<true><<<unsigned(rows), kNormThreads, 0, s>>>(h, delta, weight, out, int(n), eps);
+  else if (vec)
+    add_rms_norm_vec_kernel<false><<<unsigned(rows), kNormThreads, 0, s>>>(h, nullptr, weight, out, int(n), eps);
+  else if (delta)
     add_rms_norm_kernel<true><<<unsigned(rows), kNormThreads, 0, s>>>(h, delta, weight, out, int(n), eps);
   else
     add_rms_norm_kernel<false><<<unsigned(rows), kNormThreads, 0, s>>>(h, nullptr, weight, out, int(n), eps);
@@ -236,6 +448,25 @@ extern "C" int hif8_silu_mul(const uint16_t *gate_up, uint16_t *out, int64_t row
   const int64_t blocks = std::min<int64_t>((rows * n + 255) / 256, 4096);
   silu_mul_kernel<<<unsigned(blocks), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(gate_up, out, rows, int(n));
   return check_launch("hif8_silu_mul");
+}
+
+extern "C" int hif8_bf16_gemv(const uint16_t *x, const uint16_t *weight, uint16_t *out, int64_t m, int64_t n,
+                              int64_t k, hif8_stream_t stream) {
+  clear_error();
+  if (!x || !weight || !out) return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_bf16_gemv: null pointer argument");
+  if (m < 1 || m > 4 || n <= 0 || k <= 0 || n > 0x7FFFFFFFll || k > 0x7FFFFFFFll)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_bf16_gemv: needs 1 <= M <= 4 and positive N, K");
+  if (k % 8 || !aligned(x, 16) || !aligned(weight, 16))
+    return fail(HIF8_ERR_UNSUPPORTED, "hif8_bf16_gemv: needs K %% 8 == 0 and 16-byte aligned operands");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(unsigned((n + kSmallRows - 1) / kSmallRows));
+  switch (m) {
+    case 1: bf16_gemv_kernel<1><<<grid, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
+    case 2: bf16_gemv_kernel<2><<<grid, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
+    case 3: bf16_gemv_kernel<3><<<grid, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
+    default: bf16_gemv_kernel<4><<<grid, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
+  }
+  return check_launch("hif8_bf16_gemv");
 }
 
 extern "C" int hif8_gdn_decode_step(const uint16_t *mixed_qkvz, int64_t ld, const uint16_t *ba,
@@ -261,8 +492,13 @@ extern "C" int hif8_gdn_decode_step(const uint16_t *mixed_qkvz, int64_t ld, cons
                                                                 int(conv_width));
   int st = check_launch("hif8_gdn_decode_step (conv)");
   if (st) return st;
-  gdn_delta_kernel<<<unsigned(batch * v_heads), kGdnThreads, 0, s>>>(
-      conv_scratch, int(channels), mixed_qkvz, ld, ba, a_log, dt_bias, rec_state, out_norm, out, int(k_heads),
-      int(v_heads), int(k_dim), int(v_dim), eps);
+  if (k_dim % kGdnParts == 0 && k_dim <= kGdnParts * kGdnRows && v_dim <= kGdnCols)
+    gdn_delta_wide_kernel<<<unsigned(batch * v_heads), kGdnWideThreads, 0, s>>>(
+        conv_scratch, int(channels), mixed_qkvz, ld, ba, a_log, dt_bias, rec_state, out_norm, out, int(k_heads),
+        int(v_heads), int(k_dim), int(v_dim), eps);
+  else
+    gdn_delta_kernel<<<unsigned(batch * v_heads), kGdnThreads, 0, s>>>(
+        conv_scratch, int(channels), mixed_qkvz, ld, ba, a_log, dt_bias, rec_state, out_norm, out, int(k_heads),
+        int(v_heads), int(k_dim), int(v_dim), eps);
   return check_launch("hif8_gdn_decode_step (delta rule)");
 }

@@ -537,6 +537,23 @@ at::Tensor Hif8SiluMul(const at::Tensor &gate_up) {
   return out;
 }
 
+at::Tensor Hif8Bf16Gemv(const at::Tensor &x, const at::Tensor &weight) {
+  CheckContiguousDevice(x, "x");
+  CheckContiguousDevice(weight, "weight");
+  TORCH_CHECK(x.scalar_type() == at::kBFloat16 && weight.scalar_type() == at::kBFloat16,
+              "hif8_bf16_gemv takes bfloat16 x and weight");
+  TORCH_CHECK(x.dim() == 2 && weight.dim() == 2 && x.size(1) == weight.size(1),
+              "hif8_bf16_gemv needs x [M, K] and weight [N, K]");
+  const c10::OptionalDeviceGuard guard(x.device());
+  auto out = at::empty({x.size(0), weight.size(0)}, x.options());
+  CheckStatus(hif8_bf16_gemv(reinterpret_cast<const uint16_t *>(x.data_ptr()),
+                             reinterpret_cast<const uint16_t *>(weight.data_ptr()),
+                             reinterpret_cast<uint16_t *>(out.data_ptr()), x.size(0), weight.size(0), x.size(1),
+                             CurrentStream(x.device())),
+              "hif8_bf16_gemv");
+  return out;
+}
+
 at::Tensor Hif8GdnDecodeStep(const at::Tensor &mixed, const at::Tensor &ba, const at::Tensor &conv_weight,
                              at::Tensor &conv_state, const at::Tensor &a_log, const at::Tensor &dt_bias,
                              at::Tensor &rec_state, const at::Tensor &out_norm, int64_t k_heads, int64_t v_heads,
@@ -670,6 +687,7 @@ TORCH_LIBRARY(vllm_ascend_hif8, m) {
   m.def("soft_hif8_fused_gemm(Tensor activation, Tensor weight, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
   m.def("hif8_add_rms_norm(Tensor(a!) h, Tensor? delta, Tensor weight, float eps) -> Tensor");
   m.def("hif8_silu_mul(Tensor gate_up) -> Tensor");
+  m.def("hif8_bf16_gemv(Tensor x, Tensor weight) -> Tensor");
   m.def("hif8_qk_norm_rope(Tensor qkv, Tensor q_norm, Tensor k_norm, Tensor pos, Tensor inv_freq, Tensor block_table, int block_size, int num_heads, int num_kv_heads, int head_size, float eps) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("soft_hif8_gemm_decoded_weight(Tensor activation, Tensor weight_bf16, Tensor token_scale, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
   m.def("hif8_decode_bf16(Tensor codes) -> Tensor");
@@ -689,6 +707,7 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
   m.impl("soft_hif8_fused_gemm", &SoftHif8FusedGemm);
   m.impl("hif8_add_rms_norm", &Hif8AddRmsNorm);
   m.impl("hif8_silu_mul", &Hif8SiluMul);
+  m.impl("hif8_bf16_gemv", &Hif8Bf16Gemv);
   m.impl("hif8_qk_norm_rope", &Hif8QkNormRope);
   m.impl("hif8_gdn_decode_step", &Hif8GdnDecodeStep);
   m.impl("soft_hif8_gemm_decoded_weight", &SoftHif8GemmDecodedWeight);

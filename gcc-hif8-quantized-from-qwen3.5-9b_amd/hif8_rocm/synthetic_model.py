@@ -379,7 +379,7 @@ class HybridModel:
         kernel (conv + recurrence + gated norm in two launches); x [B, H]."""
         c = self.cfg
         qkvz = L["qkvz"](x)
-        ba = torch.nn.functional.linear(x, L["ba"])
+        ba = torch.ops.vllm_ascend_hif8.hif8_bf16_gemv(x, L["ba"])
         o = torch.ops.vllm_ascend_hif8.hif8_gdn_decode_step(
             qkvz, ba, L["conv"], st.conv_states[idx], L["A_log"], L["dt_bias"], st.rec_states[idx], L["out_norm"],
             c.lin_k_heads, c.lin_v_heads, c.lin_k_dim, c.lin_v_dim, c.rms_eps)

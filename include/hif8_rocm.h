@@ -302,6 +302,11 @@ int hif8_paged_decode_attention(const void *query, int q_dtype, const uint8_t *k
  *   out [batch, v_heads * v_dim]; conv_scratch [batch, C] float32 workspace.
  *   k_dim, v_dim <= 128; v_heads a multiple of k_heads.
  */
+/* out [m, n] = bf16(x [m, k] weight [n, k]^T), FP32 accumulation, 1 <= m <= 4,
+ * k % 8 == 0, 16-byte aligned bf16 operands: the decode step's small bf16
+ * projections (glue, no reference counterpart). */
+int hif8_bf16_gemv(const uint16_t *x, const uint16_t *weight, uint16_t *out, int64_t m, int64_t n, int64_t k,
+                   hif8_stream_t stream);
 int hif8_add_rms_norm(uint16_t *h, const uint16_t *delta, const uint16_t *weight, uint16_t *out,
                       int64_t rows, int64_t n, float eps, hif8_stream_t stream);
 int hif8_silu_mul(const uint16_t *gate_up, uint16_t *out, int64_t rows, int64_t n, hif8_stream_t stream);

@@ -80,7 +80,7 @@ def test_single_row_fusion_generates_the_same_tokens(model, device, monkeypatch)
     assert torch.equal(plain, fused)
 
 
-def test_fused_add_rms_norm_and_silu_mul_match_torch(native_ops, device):
+def test_fused_add_rms_norm_silu_mul_and_bf16_gemv_match_torch(native_ops, device):
     from hif8_rocm.synthetic_model import rms_norm
 
     g = torch.Generator(device=device).manual_seed(7)
@@ -95,15 +95,40 @@ def test_fused_add_rms_norm_and_silu_mul_match_torch(native_ops, device):
     torch.testing.assert_close(got.float(), want.float(), rtol=1e-2, atol=1e-2)
     plain = torch.ops.vllm_ascend_hif8.hif8_add_rms_norm(h.clone(), None, w, 1e-6)
     torch.testing.assert_close(plain.float(), rms_norm(h, w, 1e-6).float(), rtol=1e-2, atol=1e-2)
+    # a width the 16-byte path does not take (n % 8 != 0): the scalar kernel
+    h3 = torch.randn(2, 1004, generator=g, device=device).to(torch.bfloat16)
+    d3 = torch.randn(2, 1004, generator=g, device=device).to(torch.bfloat16)
+    w3 = (torch.rand(1004, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    got3_h = h3.clone()
+    got3 = torch.ops.vllm_ascend_hif8.hif8_add_rms_norm(got3_h, d3, w3, 1e-6)
+    assert torch.equal(got3_h, h3 + d3)
+    torch.testing.assert_close(got3.float(), rms_norm(h3 + d3, w3, 1e-6).float(), rtol=1e-2, atol=1e-2)
+    for m, n, k in ((1, 64, 4096), (3, 37, 264), (4, 8, 8)):
+        x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+        w = torch.randn(n, k, generator=g, device=device).to(torch.bfloat16)
+        y = torch.ops.vllm_ascend_hif8.hif8_bf16_gemv(x, w)
+        torch.testing.assert_close(y.float(), (x.float() @ w.float().t()), rtol=1e-2, atol=1e-2)
     gu = torch.randn(5, 600, generator=g, device=device).to(torch.bfloat16)
     act = torch.ops.vllm_ascend_hif8.hif8_silu_mul(gu)
     ref = (torch.nn.functional.silu(gu[:, :300].float()) * gu[:, 300:].float()).to(torch.bfloat16)
     torch.testing.assert_close(act.float(), ref.float(), rtol=1e-2, atol=1e-2)
 
 
-def test_fused_linear_attention_step_matches_torch_step(model, device):
+@pytest.fixture(scope="module")
+def odd_model(native_ops, device):
+    """Linear-attention head sizes the wide delta-rule kernel does not take
+    (k_dim % 8 != 0), so the fused step runs its general kernel."""
+    from hif8_rocm.synthetic_model import HybridConfig, HybridModel
+
+    cfg = dict(TINY, layers=2, lin_k_dim=20, lin_v_dim=24)
+    return HybridModel(HybridConfig(**cfg), device, seed=1)
+
+
+@pytest.mark.parametrize("which", ["model", "odd_model"])
+def test_fused_linear_attention_step_matches_torch_step(which, request, device):
     import copy
 
+    model = request.getfixturevalue(which)
     c = model.cfg
     idx = 0
     L = model.layers[0]
