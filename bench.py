@@ -7,14 +7,19 @@ fused k+v 2048x4096, o 4096x4096, fused gate+up 24576x4096, down 4096x12288)
 runs the static W8A8 linear method (hif8_rocm.scheme): hif8_static_quant of
 the bf16 activation, then soft_hif8_gemm, which runs the HBM-streaming GEMV
 kernel for M <= 4.  The fused single-launch variant (soft_hif8_static_fused_gemm)
-is reported beside it.  One step = that sweep over one layer's weights; five distinct weight copies (966 MB) are
+is reported beside it, and so is the scheme with the MI355X opt-in
+HIF8_STATIC_FUSED_SINGLE_ROW=1 (one-row projections with K <= 4096 in one
+fused launch, equal outputs).  One step = that sweep over one layer's
+weights; five distinct weight copies (966 MB) are
 rotated so the 256 MB Infinity Cache cannot serve them.  Steps are captured
 in HIP graphs and replayed, so host launch overhead is not timed.
 
 ``value`` = algorithmic bytes of the step (weights + activations + scales +
 outputs of every quant and GEMV launch) / wall time per step, in GB/s.
-Secondary figures (prefill GEMM TFLOP/s, static quant GB/s, KV decode
-attention) and a per-kernel table are reported in the same JSON line.
+Secondary figures (prefill GEMM TFLOP/s, also over weights kept decoded to
+bf16 under HIF8_PREFILL_BF16_WEIGHTS=1; static quant GB/s; KV decode
+attention; the synthetic end-to-end decode) and a per-kernel table are
+reported in the same JSON line.
 
 Synthetic data: bf16 activations ~N(0,1) with a static scale absmax/32768;
 weights ~N(0, 0.02) with per-row scales absmax/32768, encoded on the GPU.
