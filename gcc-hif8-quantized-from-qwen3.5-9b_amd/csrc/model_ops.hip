@@ -169,9 +169,9 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_vec_kernel(uint16_t
 // linear-attention b/a projection, 2 * value heads outputs), which a library
 // GEMM runs in ~14 us.  Block = kSmallRows output rows; thread t sums 16-byte
 // chunks t, t + 256, ... of each; k % 8 == 0, 16-byte aligned rows.
-constexpr int kSmallRows = 4;
-
-template <int kM>
+// kSmallRows output rows per block: 4, or 1 for M >= 3 (more blocks for the
+// few outputs: 64 x 4096 at M = 4 took 7.1 us with 4 rows per block).
+template <int kM, int kSmallRows>
 __global__ __launch_bounds__(kNormThreads) void bf16_gemv_kernel(const uint16_t *__restrict__ x,
                                                                  const uint16_t *__restrict__ w,
                                                                  uint16_t *__restrict__ out, int n, int k) {
@@ -459,12 +459,12 @@ extern "C" int hif8_bf16_gemv(const uint16_t *x, const uint16_t *weight, uint16_
   if (k % 8 || !aligned(x, 16) || !aligned(weight, 16))
     return fail(HIF8_ERR_UNSUPPORTED, "hif8_bf16_gemv: needs K %% 8 == 0 and 16-byte aligned operands");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const dim3 grid(unsigned((n + kSmallRows - 1) / kSmallRows));
+  const dim3 grid4{unsigned((n + 3) / 4)}, grid1{unsigned(n)};
   switch (m) {
-    case 1: bf16_gemv_kernel<1><<<grid, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
-    case 2: bf16_gemv_kernel<2><<<grid, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
-    case 3: bf16_gemv_kernel<3><<<grid, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
-    default: bf16_gemv_kernel<4><<<grid, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
+    case 1: bf16_gemv_kernel<1, 4><<<grid4, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
+    case 2: bf16_gemv_kernel<2, 4><<<grid4, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
+    case 3: bf16_gemv_kernel<3, 1><<<grid1, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
+    default: bf16_gemv_kernel<4, 1><<<grid1, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
   }
   return check_launch("hif8_bf16_gemv");
 }
