@@ -21,6 +21,7 @@
 
 #include "hif8_common.h"
 #include "hif8_rocm.h"
+#include "quant_device.h"
 
 namespace hif8 {
 namespace {
@@ -100,13 +101,43 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const uint16_t *__restric
 // 2-byte load per iteration and re-reads the row: ~10 us for n = 4096).
 constexpr int kNormChunks = 4;
 
-template <bool kResidual>
+// Static HiF8 codes of eight bf16 values (four packed pairs) divided by s,
+// as hif8_static_quant encodes them: the product with the reciprocal, or the
+// IEEE quotient for an element near an encode-index boundary or NaN.  Both
+// encode alike everywhere else, so the per-element choice gives the codes of
+// the standalone quant whatever its grouping.
+__device__ __forceinline__ uint2 static_encode8(const uint32_t (&pairs)[4], float s, const uint8_t *lut) {
+  const float r = __builtin_amdgcn_rcpf(s);
+  uint32_t b[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const uint32_t w = pairs[j / 2];
+    const float x = __uint_as_float(j % 2 ? (w & 0xFFFF0000u) : (w << 16));
+    const float q = x * r;
+    if (__builtin_expect(near_index_boundary(q), 0)) {
+      const float v = x / s;
+      b[j] = __builtin_isnan(v) ? uint32_t(kNan) : encode_q(v, lut);
+    } else {
+      b[j] = encode_q(q, lut);
+    }
+  }
+  return make_uint2(b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24), b[4] | (b[5] << 8) | (b[6] << 16) | (b[7] << 24));
+}
+
+// kQuant: also the static HiF8 codes of out with the fixed scale qs[0] (the
+// next projection's input quant) and row_scale[row] = qs[0].
+template <bool kResidual, bool kQuant = false>
 __global__ __launch_bounds__(kNormThreads) void add_rms_norm_vec_kernel(uint16_t *__restrict__ h,
                                                                         const uint16_t *__restrict__ delta,
                                                                         const uint16_t *__restrict__ w,
                                                                         uint16_t *__restrict__ out, int n,
-                                                                        float eps) {
+                                                                        float eps, const float *__restrict__ qs = nullptr,
+                                                                        uint8_t *__restrict__ codes = nullptr,
+                                                                        float *__restrict__ row_scale = nullptr) {
   __shared__ float red[kNormThreads / kWave];
+  __shared__ __attribute__((aligned(16))) uint8_t lut[kQuant ? 8192 : 16];
+  // The table copy is visible after the barriers of the row sum.
+  if constexpr (kQuant) stage_static_encode_table(lut, threadIdx.x, kNormThreads);
   const int chunks = n / 8;
   uint4 *hr = reinterpret_cast<uint4 *>(h + size_t(blockIdx.x) * n);
   const uint4 *dr = kResidual ? reinterpret_cast<const uint4 *>(delta + size_t(blockIdx.x) * n) : nullptr;
@@ -160,8 +191,44 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_vec_kernel(uint16_t
         o[e] = uint32_t(to_bf(lo)) | (uint32_t(to_bf(hi)) << 16);
       }
       orow[i] = make_uint4(o[0], o[1], o[2], o[3]);
+      if constexpr (kQuant)
+        reinterpret_cast<uint2 *>(codes + size_t(blockIdx.x) * n)[i] = static_encode8(o, qs[0], lut);
     }
   }
+  if (kQuant && threadIdx.x == 0) row_scale[blockIdx.x] = qs[0];
+}
+
+// SiLU-mul of rows of n % 8 == 0 straight to static HiF8 codes with the fixed
+// scale qs[0] (the down projection's input quant): codes [rows, n] equal
+// hif8_static_quant(hif8_silu_mul(gate_up)), row_scale[r] = qs[0].
+__global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t *__restrict__ gu,
+                                                             const float *__restrict__ qs,
+                                                             uint8_t *__restrict__ codes,
+                                                             float *__restrict__ row_scale, int64_t rows, int n) {
+  __shared__ __attribute__((aligned(16))) uint8_t lut[8192];
+  stage_static_encode_table(lut, threadIdx.x, 256);
+  __syncthreads();
+  const float s = qs[0];
+  const int groups = n / 8;
+  const int64_t total = rows * groups;
+  for (int64_t i = int64_t(blockIdx.x) * 256 + threadIdx.x; i < total; i += int64_t(gridDim.x) * 256) {
+    const int64_t r = i / groups;
+    const int c = int(i - r * groups);
+    const uint4 g = *reinterpret_cast<const uint4 *>(gu + r * 2 * n + 8 * c);
+    const uint4 u = *reinterpret_cast<const uint4 *>(gu + r * 2 * n + n + 8 * c);
+    const uint32_t gw[4] = {g.x, g.y, g.z, g.w}, uw[4] = {u.x, u.y, u.z, u.w};
+    uint32_t o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float g0 = bf(uint16_t(gw[e])), g1 = bf(uint16_t(gw[e] >> 16));
+      const float u0 = bf(uint16_t(uw[e])), u1 = bf(uint16_t(uw[e] >> 16));
+      // the arithmetic of silu_mul_kernel, element by element
+      o[e] = uint32_t(to_bf(g0 / (1.f + expf(-g0)) * u0)) | (uint32_t(to_bf(g1 / (1.f + expf(-g1)) * u1)) << 16);
+    }
+    reinterpret_cast<uint2 *>(codes + r * n)[c] = static_encode8(o, s, lut);
+  }
+  if (blockIdx.x == 0)
+    for (int64_t r = threadIdx.x; r < rows; r += 256) row_scale[r] = s;
 }
 
 // out[m, n] = bf16(sum_k x[m, k] w[n, k]) for m < 4, bf16 operands, FP32
@@ -439,6 +506,43 @@ extern "C" int hif8_add_rms_norm(uint16_t *h, const uint16_t *delta, const uint1
   else
     add_rms_norm_kernel<false><<<unsigned(rows), kNormThreads, 0, s>>>(h, nullptr, weight, out, int(n), eps);
   return check_launch("hif8_add_rms_norm");
+}
+
+extern "C" int hif8_add_rms_norm_quant(uint16_t *h, const uint16_t *delta, const uint16_t *weight, uint16_t *out,
+                                       const float *input_scale, uint8_t *codes, float *row_scale, int64_t rows,
+                                       int64_t n, float eps, hif8_stream_t stream) {
+  clear_error();
+  if (!h || !weight || !out || !input_scale || !codes || !row_scale)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_add_rms_norm_quant: null pointer argument");
+  if (rows <= 0 || n <= 0 || rows > 0x7FFFFFFFll || n > 0x7FFFFFFFll)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_add_rms_norm_quant: invalid dimensions");
+  if (n % 8 || n > 8 * kNormThreads * kNormChunks || !aligned(h, 16) || !aligned(weight, 16) || !aligned(out, 16) ||
+      (delta && !aligned(delta, 16)) || !aligned(codes, 8))
+    return fail(HIF8_ERR_UNSUPPORTED, "hif8_add_rms_norm_quant: needs n %% 8 == 0, n <= %d and aligned rows",
+                8 * kNormThreads * kNormChunks);
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (delta)
+    add_rms_norm_vec_kernel<true, true><<<unsigned(rows), kNormThreads, 0, s>>>(h, delta, weight, out, int(n), eps,
+                                                                               input_scale, codes, row_scale);
+  else
+    add_rms_norm_vec_kernel<false, true><<<unsigned(rows), kNormThreads, 0, s>>>(h, nullptr, weight, out, int(n), eps,
+                                                                                input_scale, codes, row_scale);
+  return check_launch("hif8_add_rms_norm_quant");
+}
+
+extern "C" int hif8_silu_mul_quant(const uint16_t *gate_up, const float *input_scale, uint8_t *codes,
+                                   float *row_scale, int64_t rows, int64_t n, hif8_stream_t stream) {
+  clear_error();
+  if (!gate_up || !input_scale || !codes || !row_scale)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_silu_mul_quant: null pointer argument");
+  if (rows <= 0 || n <= 0 || n > 0x7FFFFFFFll || rows > 0x7FFFFFFFll)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_silu_mul_quant: invalid dimensions");
+  if (n % 8 || !aligned(gate_up, 16) || !aligned(codes, 8))
+    return fail(HIF8_ERR_UNSUPPORTED, "hif8_silu_mul_quant: needs n %% 8 == 0 and aligned rows");
+  const int64_t blocks = std::min<int64_t>((rows * (n / 8) + 255) / 256, 4096);
+  silu_mul_quant_kernel<<<unsigned(blocks), 256, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+      gate_up, input_scale, codes, row_scale, rows, int(n));
+  return check_launch("hif8_silu_mul_quant");
 }
 
 extern "C" int hif8_silu_mul(const uint16_t *gate_up, uint16_t *out, int64_t rows, int64_t n, hif8_stream_t stream) {

@@ -537,6 +537,65 @@ at::Tensor Hif8SiluMul(const at::Tensor &gate_up) {
   return out;
 }
 
+// The fused static input quant of the two glue ops above: codes and row
+// scales as hif8_static_quant gives them for the bf16 result.
+void CheckInputScale(const at::Tensor &input_scale, const at::Tensor &like) {
+  CheckContiguousDevice(input_scale, "input_scale");
+  TORCH_CHECK(input_scale.scalar_type() == at::kFloat && input_scale.numel() == 1,
+              "input_scale must be one float32 value");
+  TORCH_CHECK(input_scale.device() == like.device(), "input_scale must be on the tensor's device");
+}
+
+std::vector<int64_t> LeadingShape(const at::Tensor &t) {
+  return std::vector<int64_t>(t.sizes().begin(), t.sizes().end() - 1);
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> Hif8AddRmsNormQuant(at::Tensor &h, const c10::optional<at::Tensor> &delta,
+                                                                   const at::Tensor &weight, double eps,
+                                                                   const at::Tensor &input_scale) {
+  CheckContiguousDevice(h, "h");
+  CheckContiguousDevice(weight, "weight");
+  TORCH_CHECK(h.scalar_type() == at::kBFloat16 && weight.scalar_type() == at::kBFloat16,
+              "hif8_add_rms_norm_quant takes bfloat16 tensors");
+  const int64_t n = h.size(-1);
+  TORCH_CHECK(weight.numel() == n, "weight must have the row width");
+  if (delta.has_value()) {
+    CheckContiguousDevice(*delta, "delta");
+    TORCH_CHECK(delta->scalar_type() == at::kBFloat16 && delta->sizes() == h.sizes(), "delta must match h");
+  }
+  CheckInputScale(input_scale, h);
+  const c10::OptionalDeviceGuard guard(h.device());
+  auto out = at::empty_like(h);
+  auto codes = at::empty(h.sizes(), h.options().dtype(at::kByte));
+  auto row_scale = at::empty(LeadingShape(h), h.options().dtype(at::kFloat));
+  CheckStatus(hif8_add_rms_norm_quant(
+                  reinterpret_cast<uint16_t *>(h.data_ptr()),
+                  delta.has_value() ? reinterpret_cast<const uint16_t *>(delta->data_ptr()) : nullptr,
+                  reinterpret_cast<const uint16_t *>(weight.data_ptr()), reinterpret_cast<uint16_t *>(out.data_ptr()),
+                  input_scale.data_ptr<float>(), codes.data_ptr<uint8_t>(), row_scale.data_ptr<float>(),
+                  h.numel() / n, n, float(eps), CurrentStream(h.device())),
+              "hif8_add_rms_norm_quant");
+  return {out, codes, row_scale};
+}
+
+std::tuple<at::Tensor, at::Tensor> Hif8SiluMulQuant(const at::Tensor &gate_up, const at::Tensor &input_scale) {
+  CheckContiguousDevice(gate_up, "gate_up");
+  TORCH_CHECK(gate_up.scalar_type() == at::kBFloat16, "hif8_silu_mul_quant takes bfloat16");
+  TORCH_CHECK(gate_up.size(-1) % 2 == 0, "gate_up width must be even");
+  CheckInputScale(input_scale, gate_up);
+  const int64_t n = gate_up.size(-1) / 2;
+  std::vector<int64_t> shape(gate_up.sizes().begin(), gate_up.sizes().end());
+  shape.back() = n;
+  const c10::OptionalDeviceGuard guard(gate_up.device());
+  auto codes = at::empty(shape, gate_up.options().dtype(at::kByte));
+  auto row_scale = at::empty(LeadingShape(gate_up), gate_up.options().dtype(at::kFloat));
+  CheckStatus(hif8_silu_mul_quant(reinterpret_cast<const uint16_t *>(gate_up.data_ptr()), input_scale.data_ptr<float>(),
+                                  codes.data_ptr<uint8_t>(), row_scale.data_ptr<float>(), gate_up.numel() / (2 * n), n,
+                                  CurrentStream(gate_up.device())),
+              "hif8_silu_mul_quant");
+  return {codes, row_scale};
+}
+
 at::Tensor Hif8Bf16Gemv(const at::Tensor &x, const at::Tensor &weight) {
   CheckContiguousDevice(x, "x");
   CheckContiguousDevice(weight, "weight");
@@ -687,6 +746,9 @@ TORCH_LIBRARY(vllm_ascend_hif8, m) {
   m.def("soft_hif8_fused_gemm(Tensor activation, Tensor weight, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
   m.def("hif8_add_rms_norm(Tensor(a!) h, Tensor? delta, Tensor weight, float eps) -> Tensor");
   m.def("hif8_silu_mul(Tensor gate_up) -> Tensor");
+  m.def("hif8_add_rms_norm_quant(Tensor(a!) h, Tensor? delta, Tensor weight, float eps, Tensor input_scale) -> "
+        "(Tensor, Tensor, Tensor)");
+  m.def("hif8_silu_mul_quant(Tensor gate_up, Tensor input_scale) -> (Tensor, Tensor)");
   m.def("hif8_bf16_gemv(Tensor x, Tensor weight) -> Tensor");
   m.def("hif8_qk_norm_rope(Tensor qkv, Tensor q_norm, Tensor k_norm, Tensor pos, Tensor inv_freq, Tensor block_table, int block_size, int num_heads, int num_kv_heads, int head_size, float eps) -> (Tensor, Tensor, Tensor, Tensor)");
   m.def("soft_hif8_gemm_decoded_weight(Tensor activation, Tensor weight_bf16, Tensor token_scale, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
@@ -707,6 +769,8 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
   m.impl("soft_hif8_fused_gemm", &SoftHif8FusedGemm);
   m.impl("hif8_add_rms_norm", &Hif8AddRmsNorm);
   m.impl("hif8_silu_mul", &Hif8SiluMul);
+  m.impl("hif8_add_rms_norm_quant", &Hif8AddRmsNormQuant);
+  m.impl("hif8_silu_mul_quant", &Hif8SiluMulQuant);
   m.impl("hif8_bf16_gemv", &Hif8Bf16Gemv);
   m.impl("hif8_qk_norm_rope", &Hif8QkNormRope);
   m.impl("hif8_gdn_decode_step", &Hif8GdnDecodeStep);

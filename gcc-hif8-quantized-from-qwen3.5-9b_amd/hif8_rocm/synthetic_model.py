@@ -175,6 +175,12 @@ class StaticLinear:
             self.layer.input_scale.data.copy_((self.amax / HIF8_MAX).clamp_min(1e-30).reshape(1))
         return self.method.apply(self.layer, x)
 
+    def from_codes(self, codes: torch.Tensor, row_scale: torch.Tensor) -> torch.Tensor:
+        """The projection of activations a producer kernel already quantized
+        with this layer's input scale: the GEMV / GEMM half of ``__call__``."""
+        return native.soft_linear(codes, self.layer.weight, row_scale, self.layer.weight_scale, None,
+                                  output_dtype=torch.bfloat16)
+
 
 @dataclass
 class RequestState:
@@ -193,6 +199,10 @@ class RequestState:
 class HybridModel:
     def __init__(self, cfg: HybridConfig, device, seed: int = 0):
         self.cfg = cfg
+        self.calibrating = False
+        # Decode quantizes projection inputs inside the glue kernels; False
+        # runs the scheme's own quant per projection (same codes, more launches).
+        self.fuse_input_quant = True
         self.device = torch.device(device)
         g = torch.Generator(device=self.device).manual_seed(seed)
         c = cfg
@@ -283,12 +293,13 @@ class HybridModel:
         blk = torch.gather(st.block_table.long(), 1, (pos // bs).long())
         return (blk * bs + pos % bs).reshape(-1)
 
-    def _attention_decode(self, L, idx: int, st: RequestState, x: torch.Tensor, pos: torch.Tensor):
+    def _attention_decode(self, L, idx: int, st: RequestState, x: torch.Tensor, pos: torch.Tensor, xq=None):
         """One decode token of full attention: fused q/k norm + rotary + slots,
-        fused KV write, paged HiF8 decode attention; x [B, H], pos [B, 1]."""
+        fused KV write, paged HiF8 decode attention; x [B, H], pos [B, 1];
+        xq: x already quantized for the qkv projection (codes, row scales)."""
         c = self.cfg
         b = x.shape[0]
-        qkv = L["qkv"](x)
+        qkv = L["qkv"](x) if xq is None else L["qkv"].from_codes(*xq)
         q, k, v, slots = torch.ops.vllm_ascend_hif8.hif8_qk_norm_rope(
             qkv, L["q_norm"], L["k_norm"], pos.reshape(b), self.inv_freq, st.block_table, c.block_size, c.heads,
             c.kv_heads, c.head_dim, c.rms_eps)
@@ -374,20 +385,30 @@ class HybridModel:
         o = o.to(h.dtype).reshape(b * t, c.lin_v_width)
         return L["out"](o).reshape(b, t, -1)
 
-    def _linear_attention_decode(self, L, idx: int, st: RequestState, x: torch.Tensor) -> torch.Tensor:
+    def _linear_attention_decode(self, L, idx: int, st: RequestState, x: torch.Tensor, xq=None) -> torch.Tensor:
         """One decode token of the linear-attention mixer with the fused glue
-        kernel (conv + recurrence + gated norm in two launches); x [B, H]."""
+        kernel (conv + recurrence + gated norm in two launches); x [B, H];
+        xq: x already quantized for the qkvz projection."""
         c = self.cfg
-        qkvz = L["qkvz"](x)
+        qkvz = L["qkvz"](x) if xq is None else L["qkvz"].from_codes(*xq)
         ba = torch.ops.vllm_ascend_hif8.hif8_bf16_gemv(x, L["ba"])
         o = torch.ops.vllm_ascend_hif8.hif8_gdn_decode_step(
             qkvz, ba, L["conv"], st.conv_states[idx], L["A_log"], L["dt_bias"], st.rec_states[idx], L["out_norm"],
             c.lin_k_heads, c.lin_v_heads, c.lin_k_dim, c.lin_v_dim, c.rms_eps)
         return L["out"](o)
 
+    def _fuse_input_quant(self) -> bool:
+        """Whether the decode step quantizes projection inputs inside the
+        norm and SiLU-mul kernels (same codes as the scheme's own quant)."""
+        c = self.cfg
+        return (self.fuse_input_quant and not self.calibrating and scheme._static_scale_factor() == 1.0
+                and c.hidden % 8 == 0 and c.hidden <= 8192 and c.intermediate % 8 == 0)
+
     def _forward_decode(self, st: RequestState, ids: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
         """The decode step with fused glue: residual add + RMSNorm in one
-        kernel, SiLU-mul in one, the linear-attention token in two."""
+        kernel, SiLU-mul in one, the linear-attention token in two; the input
+        quant of the qkv / qkvz, gate_up and down projections runs inside the
+        norm and SiLU-mul kernels (``fuse_input_quant``)."""
         c = self.cfg
         ops = torch.ops.vllm_ascend_hif8
         b = ids.shape[0]
@@ -395,16 +416,32 @@ class HybridModel:
                                     validate=False).reshape(b, c.hidden)
         pending = None
         attn_i = lin_i = 0
+        fuse = self._fuse_input_quant()
         for i, L in enumerate(self.layers):
-            x = ops.hif8_add_rms_norm(h, pending, L["input_norm"], c.rms_eps)
-            if c.is_full_attention(i):
-                mix = self._attention_decode(L, attn_i, st, x, pos)
+            full = c.is_full_attention(i)
+            xq = None
+            if fuse:
+                proj = L["qkv"] if full else L["qkvz"]
+                x, codes, rs = ops.hif8_add_rms_norm_quant(h, pending, L["input_norm"], c.rms_eps,
+                                                           proj.layer.input_scale)
+                xq = (codes, rs)
+            else:
+                x = ops.hif8_add_rms_norm(h, pending, L["input_norm"], c.rms_eps)
+            if full:
+                mix = self._attention_decode(L, attn_i, st, x, pos, xq)
                 attn_i += 1
             else:
-                mix = self._linear_attention_decode(L, lin_i, st, x)
+                mix = self._linear_attention_decode(L, lin_i, st, x, xq)
                 lin_i += 1
-            x2 = ops.hif8_add_rms_norm(h, mix, L["post_norm"], c.rms_eps)
-            pending = L["down"](ops.hif8_silu_mul(L["gate_up"](x2)))
+            if fuse:
+                _, codes, rs = ops.hif8_add_rms_norm_quant(h, mix, L["post_norm"], c.rms_eps,
+                                                           L["gate_up"].layer.input_scale)
+                gu = L["gate_up"].from_codes(codes, rs)
+                codes, rs = ops.hif8_silu_mul_quant(gu, L["down"].layer.input_scale)
+                pending = L["down"].from_codes(codes, rs)
+            else:
+                x2 = ops.hif8_add_rms_norm(h, mix, L["post_norm"], c.rms_eps)
+                pending = L["down"](ops.hif8_silu_mul(L["gate_up"](x2)))
         last = ops.hif8_add_rms_norm(h, pending, self.final_norm, c.rms_eps)
         return torch.nn.functional.linear(last, self.lm_head).float()
 

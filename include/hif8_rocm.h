@@ -310,6 +310,18 @@ int hif8_bf16_gemv(const uint16_t *x, const uint16_t *weight, uint16_t *out, int
 int hif8_add_rms_norm(uint16_t *h, const uint16_t *delta, const uint16_t *weight, uint16_t *out,
                       int64_t rows, int64_t n, float eps, hif8_stream_t stream);
 int hif8_silu_mul(const uint16_t *gate_up, uint16_t *out, int64_t rows, int64_t n, hif8_stream_t stream);
+/* The two above with the next projection's static input quant fused in (glue,
+ * no reference counterpart): also codes [rows, n] = the hif8_static_quant
+ * codes of their bf16 result with the fixed scale input_scale[0] (float32
+ * [1]) and row_scale [rows] = input_scale[0], so that the projection runs
+ * straight from codes.  hif8_add_rms_norm_quant still writes out; both need
+ * n % 8 == 0 (the norm also n <= 8192), 16-byte aligned bf16 rows and
+ * 8-byte aligned codes, else HIF8_ERR_UNSUPPORTED. */
+int hif8_add_rms_norm_quant(uint16_t *h, const uint16_t *delta, const uint16_t *weight, uint16_t *out,
+                            const float *input_scale, uint8_t *codes, float *row_scale, int64_t rows, int64_t n,
+                            float eps, hif8_stream_t stream);
+int hif8_silu_mul_quant(const uint16_t *gate_up, const float *input_scale, uint8_t *codes, float *row_scale,
+                        int64_t rows, int64_t n, hif8_stream_t stream);
 int hif8_qk_norm_rope(const uint16_t *qkv, const uint16_t *q_norm, const uint16_t *k_norm, const int64_t *pos,
                       const float *inv_freq, const int32_t *block_table, int64_t max_blocks, int64_t block_size,
                       uint16_t *q_out, uint16_t *k_out, uint16_t *v_out, int64_t *slots, int64_t batch,

@@ -80,6 +80,58 @@ def test_single_row_fusion_generates_the_same_tokens(model, device, monkeypatch)
     assert torch.equal(plain, fused)
 
 
+def test_fused_input_quant_generates_the_same_tokens(model, device):
+    """Decode with the projections' input quant inside the norm and SiLU-mul
+    kernels (the default) and with the scheme's own quant per projection:
+    the codes are equal, so the tokens are too."""
+    from hif8_rocm.synthetic_model import generate
+
+    assert model._fuse_input_quant()
+    g = torch.Generator(device=device).manual_seed(23)
+    prompt = torch.randint(0, model.cfg.vocab, (2, 12), generator=g, device=device)
+    fused, _ = generate(model, prompt, 6, graph=True)
+    model.fuse_input_quant = False
+    try:
+        plain, _ = generate(model, prompt, 6, graph=True)
+    finally:
+        model.fuse_input_quant = True
+    assert torch.equal(plain, fused)
+
+
+@pytest.mark.parametrize("rows,n", [(1, 4096), (4, 4096), (3, 8)])
+def test_glue_with_input_quant_equals_glue_then_static_quant(native_ops, device, rows, n):
+    """hif8_add_rms_norm_quant and hif8_silu_mul_quant: the bf16 result of the
+    plain glue op and, bit for bit, the codes and row scales that
+    hif8_static_quant gives for it (scales from fine to saturating, NaN and
+    Inf inputs)."""
+    from hif8_rocm import native
+
+    ops = torch.ops.vllm_ascend_hif8
+    g = torch.Generator(device=device).manual_seed(rows * 1000 + n)
+    h = (torch.randn(rows, n, generator=g, device=device) * 3).to(torch.bfloat16)
+    d = torch.randn(rows, n, generator=g, device=device).to(torch.bfloat16)
+    w = (torch.rand(n, generator=g, device=device) + 0.5).to(torch.bfloat16)
+    gu = (torch.randn(rows, 2 * n, generator=g, device=device) * 2).to(torch.bfloat16)
+    gu[0, 5] = float("nan")
+    gu[-1, n + 6] = float("inf")
+    for sv in (1e-6, 1e-3, 0.037, 1.0):
+        s = torch.tensor([sv], dtype=torch.float32, device=device)
+        for delta in (d, None):
+            want_h = h.clone()
+            want = ops.hif8_add_rms_norm(want_h, delta, w, 1e-6)
+            got_h = h.clone()
+            got, codes, rs = ops.hif8_add_rms_norm_quant(got_h, delta, w, 1e-6, s)
+            assert torch.equal(got_h, want_h) and torch.equal(got, want)
+            want_codes, want_rs = native.static_quant(want, s)
+            assert torch.equal(codes, want_codes), (sv, delta is None)
+            assert torch.equal(rs.reshape(-1), want_rs.reshape(-1))
+        codes, rs = ops.hif8_silu_mul_quant(gu, s)
+        want_codes, want_rs = native.static_quant(ops.hif8_silu_mul(gu), s)
+        assert torch.equal(codes, want_codes), sv
+        assert torch.equal(rs.reshape(-1), want_rs.reshape(-1))
+    assert codes[0, 5].item() == 0x80  # NaN
+
+
 def test_fused_add_rms_norm_silu_mul_and_bf16_gemv_match_torch(native_ops, device):
     from hif8_rocm.synthetic_model import rms_norm
 
