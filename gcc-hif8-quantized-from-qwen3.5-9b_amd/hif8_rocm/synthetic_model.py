@@ -177,7 +177,12 @@ class StaticLinear:
 
     def from_codes(self, codes: torch.Tensor, row_scale: torch.Tensor) -> torch.Tensor:
         """The projection of activations a producer kernel already quantized
-        with this layer's input scale: the GEMV / GEMM half of ``__call__``."""
+        with this layer's input scale: the GEMV / GEMM half of ``__call__``,
+        routed as the scheme routes it."""
+        decoded = getattr(self.layer, "_hif8_weight_bf16", None)
+        if decoded is not None and codes.numel() // codes.shape[-1] > 4:
+            return native.soft_linear_decoded_weight(codes, decoded, row_scale, self.layer.weight_scale, None,
+                                                     output_dtype=torch.bfloat16)
         return native.soft_linear(codes, self.layer.weight, row_scale, self.layer.weight_scale, None,
                                   output_dtype=torch.bfloat16)
 
