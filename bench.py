@@ -530,16 +530,20 @@ def e2e_decode(torch, device) -> dict:
            "prompt_tokens": E2E_PROMPT, "new_tokens": E2E_NEW, "build_and_calibrate_s": round(time.perf_counter() - t0, 2)}
     g = torch.Generator(device=device).manual_seed(9)
     # b1_single_row_fusion: batch 1 again with HIF8_STATIC_FUSED_SINGLE_ROW=1
-    # (one-row projections with K <= 4096 in one fused launch; same tokens).
+    # and the glue-kernel input quant off, so every one-row projection with
+    # K <= 4096 (qkv / qkvz, gate_up, o / out) runs the fused static-quant
+    # GEMV in one launch (same tokens); down (K = 12288) stays quant + GEMV.
     for b, key, single in ((1, "b1", False), (4, "b4", False), (1, "b1_single_row_fusion", True)):
         prompt = torch.randint(0, cfg.vocab, (b, E2E_PROMPT), generator=g, device=device)
         if single:
             os.environ["HIF8_STATIC_FUSED_SINGLE_ROW"] = "1"
+            model.fuse_input_quant = False
         try:
             generate(model, prompt[:, :64], 4)  # warm-up: allocator, kernels, graph capture path
             _, tm = generate(model, prompt, E2E_NEW)
         finally:
             os.environ.pop("HIF8_STATIC_FUSED_SINGLE_ROW", None)
+            model.fuse_input_quant = True
         step_s = tm["decode"] / tm["decode_steps"]
         total = tm["prefill"] + step_s * (E2E_NEW - 1)
         res[key] = {"prefill_ms": round(tm["prefill"] * 1e3, 2), "ms_per_decode_step": round(step_s * 1e3, 3),

@@ -611,13 +611,10 @@ int launch_tiled(const LinearArgs &a, const void *act, const void *wt, int split
                                             size_t(kWavesM * kWavesN) *
                                                 epilogue_region_bytes<kBM / kWavesM / 16, kBN / kWavesN / 16>());
   constexpr int kT = kWave * kWavesM * kWavesN;
-  static bool configured = false;
-  if (!configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kBPre, kPingPong>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, int(kSmem)) != hipSuccess)
-      return fail(HIF8_ERR_LAUNCH, "soft_hif8 GEMM: cannot reserve %zu bytes of LDS", kSmem);
-    configured = true;
-  }
+  if (const int st = reserve_dynamic_lds(
+          reinterpret_cast<const void *>(&gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kBPre, kPingPong>), kSmem,
+          "soft_hif8 GEMM"))
+    return st;
   const int64_t tiles = ((a.n + kBN - 1) / kBN) * ((a.m + kBM - 1) / kBM);
   const dim3 grid(unsigned((tiles * splits + 7) / 8 * 8));
   gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kBPre, kPingPong><<<grid, kT, kSmem, a.stream>>>(

@@ -554,13 +554,9 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemv_mfma_kernel(
 template <int kM, int kSrc>
 int launch_mfma(const LinearArgs &a) {
   const size_t smem = size_t(kM) * size_t(a.k) * 2 + (kSrc != kActCodes ? 8192 : 0);
-  static size_t configured = 0;  // largest dynamic LDS size set for this instantiation
-  if (smem > configured) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void *>(&gemv_mfma_kernel<kM, kSrc>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, int(smem)) != hipSuccess)
-      return fail(HIF8_ERR_LAUNCH, "soft_hif8 GEMV: cannot reserve %zu bytes of LDS", smem);
-    configured = smem;
-  }
+  if (const int st = reserve_dynamic_lds(reinterpret_cast<const void *>(&gemv_mfma_kernel<kM, kSrc>), smem,
+                                         "soft_hif8 GEMV"))
+    return st;
   gemv_mfma_kernel<kM, kSrc><<<dim3(unsigned((a.n + 15) / 16)), kMfmaThreads, smem, a.stream>>>(
       a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.n), int(a.k));
   return HIF8_OK;

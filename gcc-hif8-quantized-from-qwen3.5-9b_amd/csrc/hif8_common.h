@@ -18,6 +18,11 @@ int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 int check_launch(const char *what);
 // Clears this thread's last error (called on entry of every ABI function).
 void clear_error();
+// Raises the dynamic-LDS limit of `kernel` on the current device to at least
+// `bytes` (hipFuncSetAttribute once per kernel, device and larger size;
+// serialised by a mutex, so concurrent first launches from several host
+// threads are safe).  Returns HIF8_OK or a launch error naming `what`.
+int reserve_dynamic_lds(const void *kernel, size_t bytes, const char *what);
 
 inline bool is_io_dtype(int d) { return d == HIF8_DTYPE_FP16 || d == HIF8_DTYPE_BF16; }
 inline bool aligned(const void *p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }

@@ -439,8 +439,15 @@ __global__ __launch_bounds__(kHeadThreads) void qk_norm_rope_kernel(
   const float x = j < d ? bf(qkv[(size_t(b) * heads + h) * d + j]) : 0.f;
   const int64_t p = pos[b];
   if (h == 0 && j == 0 && slots) {
-    const int64_t blk = block_table[size_t(b) * max_blocks + p / block_size];
-    slots[b] = blk * block_size + p % block_size;
+    // A position outside the table (negative, or past max_blocks pages, e.g.
+    // a replayed graph run past its capacity) gets slot -1, which the cache
+    // write skips as padding; the table is never read out of bounds.
+    int64_t slot = -1;
+    if (p >= 0 && p / block_size < max_blocks) {
+      const int64_t blk = block_table[size_t(b) * max_blocks + p / block_size];
+      if (blk >= 0) slot = blk * block_size + p % block_size;
+    }
+    slots[b] = slot;
   }
   if (h >= hq + hkv) {
     if (j < d) v_out[(size_t(b) * hkv + (h - hq - hkv)) * d + j] = qkv[(size_t(b) * heads + h) * d + j];

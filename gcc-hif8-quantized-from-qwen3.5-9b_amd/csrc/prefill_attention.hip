@@ -1,0 +1,624 @@
+// Multi-token paged attention over HiF8 pages for gfx950: prefill and
+// chunked prefill (several query tokens per request, right-aligned causal
+// mask), decoding the cache pages inside the kernel.
+//
+// Contract (kv_cache.py:314-372 with query_lens; the reference's TND call of
+// npu_fused_infer_attention_score, kv_runtime.py:1470-1563, sparse_mode=3):
+// request b owns query rows query_start_loc[b] .. query_start_loc[b + 1] - 1
+// and seq_lens[b] cached tokens (this step's tokens included); its query row i
+// sits at position seq_lens[b] - q_len + i and, when causal, sees keys
+// 0 .. that position.  K and V rows are decoded to dtype(dec(c) * s_row), the
+// query dtype (kv_cache.py:355-356), and query head hq attends KV head
+// hq / (Hq / Hkv).  A row that sees no key gets zeros.
+//
+// Work split.  A workgroup (4 wavefronts) owns one (request, KV head, query
+// tile of 64 / G tokens, key split): its 64 rows are the (token, query head)
+// pairs of the tile, 16 per wavefront, so the G query heads of a KV head
+// share every decoded K/V tile.  It walks its key range in 64-key tiles:
+//   * all 256 threads load the tile's raw K and V rows (16 bytes per load,
+//     rows found through the block table, any block size), decode them with
+//     an fp32 table in LDS, multiply by the row's scale, round to the query
+//     dtype and store K as [key][D] and V transposed as [D][key] in LDS
+//     (16-byte granules XOR-swizzled so the fragment reads spread over banks);
+//   * each wavefront computes S^T = K Q^T on v_mfma_f32_16x16x32 (A = 16 keys
+//     x 32 dims from LDS, B = its 16 query rows, held in VGPRs for the whole
+//     loop), applies the causal / length mask and an online softmax in FP32
+//     (base 2), and accumulates O^T += V^T P^T on the same MFMA, P rounded to
+//     the query dtype (the reference's probs.to(query.dtype));
+//   * the next tile's raw rows are loaded while the current one computes.
+// The S^T accumulators leave lane (g, n) holding keys 4g + e and 16 + 4g + e
+// of query row n, which are the k-slots 8g + e of the P^T operand of the
+// 32-key step; V^T is stored in that key order, so P needs no data movement.
+//
+// With several key splits per query tile the partial (O, max, sum) go to the
+// caller's workspace and a second kernel merges them.  Shapes outside the
+// MFMA kernel's set (head size not 64/128/256, Dv != D, G not dividing 16)
+// run a one-wavefront-per-(row, head) kernel.
+#include <stddef.h>
+
+#include <algorithm>
+
+#include "hif8_common.h"
+
+namespace hif8 {
+namespace {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kPThreads = 256;  // four wavefronts
+constexpr int kPRows = 64;      // (token, head) rows per workgroup, 16 per wavefront
+constexpr int kKT = 64;         // keys per tile
+constexpr int kTargetBlocks = 512;
+constexpr int kMinSplitTiles = 2;
+
+struct PrefillParams {
+  const void *query;              // [total_q, Hq, D]
+  const uint8_t *key_cache;       // [num_blocks, block_size, Hkv, D + 4]
+  const uint8_t *value_cache;     // [num_blocks, block_size, Hkv, Dv + 4]
+  const void *block_table;        // [batch, bt_stride] int32 or int64
+  const int32_t *query_start_loc; // [batch + 1]
+  const int32_t *seq_lens;        // [batch]
+  void *out;                      // [total_q, Hq, Dv]
+  float *part_o;                  // [items, num_splits, kPRows, Dv]
+  float *part_ml;                 // [items, num_splits, kPRows, 2]
+  int64_t bt_stride;
+  int64_t num_blocks;
+  int block_size, hkv, hq, group, log2_group, d, dv;
+  int tokens_per_tile, q_tiles, num_splits, split_tiles, batch, max_len, causal;
+  int total_q;                    // rows of query / out; rows at or past it are never touched
+  float scale_log2;               // softmax scale * log2(e)
+};
+
+template <bool kBf16>
+__device__ __forceinline__ f32x4_t mfma16(u32x4 a, u32x4 b, f32x4_t c) {
+  if constexpr (kBf16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                   __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a),
+                                                  __builtin_bit_cast(f16x8_t, b), c, 0, 0, 0);
+  }
+}
+
+template <bool kBf16>
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  return uint32_t(float_to_half_bits<kBf16>(lo)) | (uint32_t(float_to_half_bits<kBf16>(hi)) << 16);
+}
+
+__device__ __forceinline__ int clamp_len(int len, int max_len) {
+  return len < 0 ? 0 : (len > max_len ? max_len : len);
+}
+
+// Position of key k (0..63) of a tile in the V^T rows: within each 32-key
+// half, keys 4g + e sit at 8g + e and keys 16 + 4g + e at 8g + 4 + e.
+__device__ __forceinline__ int vt_pos(int k) {
+  const int half = k & 32, kk = k & 31;
+  return half + (kk < 16 ? 8 * (kk >> 2) + (kk & 3) : 8 * ((kk - 16) >> 2) + 4 + (kk & 3));
+}
+
+// Block ids: heavy query tiles (late in the prompt, more keys) first.
+//   blockIdx.x = ((q_tiles - 1 - qt) * batch + b) * hkv + h) * num_splits + split
+template <int kD, bool kBf16, typename BtT>
+__global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(const PrefillParams p) {
+  constexpr int kKPT = kD / 64;        // keys per thread per tile (raw loads)
+  constexpr int kChunks = kD / 16;     // 16-byte code chunks per row
+  constexpr int kQSteps = kD / 32;     // MFMA steps over the head dims
+  constexpr int kDB = kD / 16;         // 16-dim blocks of O^T
+  constexpr int kKGran = kD / 8;       // 16-byte bf16 granules per K row
+  constexpr int kKSwz = (kKGran < 16 ? kKGran : 16) - 1;
+  static_assert(kKPT >= 1 && kKT * kChunks == kPThreads * kKPT, "thread map covers the tile");
+
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+  float *dec = reinterpret_cast<float *>(smem_raw);                    // [256] fp32 decode table
+  float *kbias = dec + 256;                                            // [kKT] 0 or -inf per key
+  uint16_t *ks = reinterpret_cast<uint16_t *>(kbias + kKT);            // [kKT][kD]
+  uint16_t *vt = ks + kKT * kD;                                        // [kD][kKT]
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int split = int(blockIdx.x) % p.num_splits;
+  const int rest = int(blockIdx.x) / p.num_splits;
+  const int h = rest % p.hkv;
+  const int rb = rest / p.hkv;
+  const int b = rb % p.batch;
+  const int qt = p.q_tiles - 1 - rb / p.batch;
+  // A request's rows, clipped to the query tensor (query_start_loc is caller data).
+  const int q_begin = max(p.query_start_loc[b], 0);
+  const int ql = min(p.query_start_loc[b + 1], p.total_q) - q_begin;
+  const int tok0 = qt * p.tokens_per_tile;
+  if (tok0 >= ql) return;  // a query tile past this request's rows (uniform)
+  const int kl = clamp_len(p.seq_lens[b], p.max_len);
+
+  // This lane's query row of the S^T / O^T columns.
+  const int r = wave * 16 + n;
+  const int tok = tok0 + (r >> p.log2_group);
+  const int qhead = h * p.group + (r & (p.group - 1));
+  const bool row_ok = tok < ql;
+  const int tok_last = min(tok0 + p.tokens_per_tile, ql) - 1;
+  // Keys the tile can see, and this split's part of them.
+  const int k_vis = p.causal ? min(kl, kl - ql + tok_last + 1) : kl;
+  const int s_k0 = split * p.split_tiles * kKT;
+  const int s_k1 = min(s_k0 + p.split_tiles * kKT, k_vis);
+  const int ntiles = s_k1 > s_k0 ? (s_k1 - s_k0 + kKT - 1) / kKT : 0;
+  // Keys of this row: [s_k0, lim).
+  const int lim = !row_ok ? s_k0 : (p.causal ? min(s_k1, kl - ql + tok + 1) : s_k1);
+
+  const size_t item = (size_t(b) * p.q_tiles + qt) * p.hkv + h;
+  const size_t part = (item * p.num_splits + split) * kPRows + r;
+  const size_t out_row = (size_t(q_begin + tok) * p.hq + qhead) * kD;
+
+  // Raw rows of a tile: thread (kg, dc) loads chunk dc of keys kg * kKPT + j.
+  const int dc = tid % kChunks, kg = tid / kChunks;
+  const BtT *bt = static_cast<const BtT *>(p.block_table) + size_t(b) * p.bt_stride;
+  u32x4 kraw[kKPT], vraw[kKPT];
+  float kscl[kKPT], vscl[kKPT];
+  auto issue = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < kKPT; ++j) {
+      const int key = k0 + kg * kKPT + j;
+      int64_t blk = -1;
+      if (key < s_k1) blk = int64_t(bt[key / p.block_size]);
+      if (blk >= 0 && blk < p.num_blocks) {
+        const int64_t off = ((blk * p.block_size + key % p.block_size) * p.hkv + h) * int64_t(kD + 4);
+        kraw[j] = *reinterpret_cast<const u32x4_a4 *>(p.key_cache + off + 16 * dc);
+        vraw[j] = *reinterpret_cast<const u32x4_a4 *>(p.value_cache + off + 16 * dc);
+        kscl[j] = *reinterpret_cast<const float *>(p.key_cache + off + kD);
+        vscl[j] = *reinterpret_cast<const float *>(p.value_cache + off + kD);
+      } else {
+        kraw[j] = vraw[j] = u32x4{0, 0, 0, 0};
+        kscl[j] = vscl[j] = 0.f;  // a zero scale marks the key absent
+      }
+    }
+  };
+
+  // The query rows as the B operand: lane (g, n) holds dims 32 i + 8 g .. + 7 of row n.
+  u32x4 qf[kQSteps];
+  {
+    const uint16_t *q = static_cast<const uint16_t *>(p.query) + out_row + 8 * g;
+#pragma unroll
+    for (int i = 0; i < kQSteps; ++i)
+      qf[i] = row_ok ? *reinterpret_cast<const u32x4 *>(q + 32 * i) : u32x4{0, 0, 0, 0};
+  }
+  if (ntiles > 0) issue(s_k0);
+  for (int i = tid; i < 256; i += kPThreads) dec[i] = __uint_as_float(kDeviceTables.decode_f32[i]);
+  __syncthreads();
+
+  f32x4_t oacc[kDB];
+#pragma unroll
+  for (int db = 0; db < kDB; ++db) oacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m = -__builtin_inff(), l = 0.f;
+
+  for (int it = 0; it < ntiles; ++it) {
+    const int k0 = s_k0 + it * kKT;
+    // Decode this tile's raw rows into LDS.
+#pragma unroll
+    for (int j = 0; j < kKPT; ++j) {
+      const int kt = kg * kKPT + j;  // key within the tile
+      const uint32_t kw[4] = {kraw[j][0], kraw[j][1], kraw[j][2], kraw[j][3]};
+      uint32_t kp[8];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        kp[2 * w] = pack2<kBf16>(dec[kw[w] & 0xFFu] * kscl[j], dec[(kw[w] >> 8) & 0xFFu] * kscl[j]);
+        kp[2 * w + 1] = pack2<kBf16>(dec[(kw[w] >> 16) & 0xFFu] * kscl[j], dec[kw[w] >> 24] * kscl[j]);
+      }
+      const int sw = kt & kKSwz;
+      uint16_t *krow = ks + kt * kD;
+      *reinterpret_cast<u32x4 *>(krow + 8 * ((2 * dc) ^ sw)) = u32x4{kp[0], kp[1], kp[2], kp[3]};
+      *reinterpret_cast<u32x4 *>(krow + 8 * ((2 * dc + 1) ^ sw)) = u32x4{kp[4], kp[5], kp[6], kp[7]};
+      if (dc == 0) kbias[kt] = kscl[j] != 0.f ? 0.f : -__builtin_inff();
+    }
+    // V transposed: dim 16 dc + i, kKPT consecutive keys at consecutive positions.
+    {
+      const int pos = vt_pos(kg * kKPT);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int dim = 16 * dc + i;
+        float v[kKPT];
+#pragma unroll
+        for (int j = 0; j < kKPT; ++j) v[j] = dec[(vraw[j][i >> 2] >> (8 * (i & 3))) & 0xFFu] * vscl[j];
+        const int gran = (pos >> 3) ^ (dim & 7);
+        uint16_t *dst = vt + dim * kKT + 8 * gran + (pos & 7);
+        if constexpr (kKPT == 4) {
+          *reinterpret_cast<u32x2 *>(dst) = u32x2{pack2<kBf16>(v[0], v[1]), pack2<kBf16>(v[2], v[3])};
+        } else if constexpr (kKPT == 2) {
+          *reinterpret_cast<uint32_t *>(dst) = pack2<kBf16>(v[0], v[1]);
+        } else {
+          *dst = float_to_half_bits<kBf16>(v[0]);
+        }
+      }
+    }
+    __syncthreads();
+    if (it + 1 < ntiles) issue(k0 + kKT);  // in flight during this tile's math
+
+    // S^T = K Q^T: four 16-key blocks.
+    f32x4_t sacc[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      sacc[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      const int key = 16 * kb + n;
+      const uint16_t *krow = ks + key * kD;
+#pragma unroll
+      for (int i = 0; i < kQSteps; ++i) {
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(krow + 8 * ((4 * i + g) ^ (key & kKSwz)));
+        sacc[kb] = mfma16<kBf16>(a, qf[i], sacc[kb]);
+      }
+    }
+    // Mask and online softmax (base 2): lane (g, n) holds keys 16 kb + 4 g + e of row n.
+    float x[16];
+    float tmax = -__builtin_inff();
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const f32x4_t bias = *reinterpret_cast<const f32x4_t *>(kbias + 16 * kb + 4 * g);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = k0 + 16 * kb + 4 * g + e;
+        const float v = sacc[kb][e] * p.scale_log2 + bias[e];
+        x[4 * kb + e] = key < lim ? v : -__builtin_inff();
+        tmax = fmaxf(tmax, x[4 * kb + e]);
+      }
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+    const float m_new = fmaxf(m, tmax);
+    const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+    float pw[16], psum = 0.f;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      pw[e] = __builtin_amdgcn_exp2f(x[e] - m_use);
+      psum += pw[e];
+    }
+    l = l * alpha + psum;
+    if (!__all(m_new == m || m == -__builtin_inff())) {
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) oacc[db] *= alpha;
+    }
+    m = m_new;
+    // P^T operands of the two 32-key steps.
+    u32x4 pf[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const float *a = pw + 8 * s;      // keys 32 s + 4 g + e
+      const float *c = pw + 8 * s + 4;  // keys 32 s + 16 + 4 g + e
+      pf[s] = u32x4{pack2<kBf16>(a[0], a[1]), pack2<kBf16>(a[2], a[3]), pack2<kBf16>(c[0], c[1]),
+                    pack2<kBf16>(c[2], c[3])};
+    }
+    // O^T += V^T P^T.
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) {
+      const int dim = 16 * db + n;
+      const uint16_t *vrow = vt + dim * kKT;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(vrow + 8 * ((4 * s + g) ^ (dim & 7)));
+        oacc[db] = mfma16<kBf16>(a, pf[s], oacc[db]);
+      }
+    }
+    __syncthreads();  // the tile's LDS is rewritten by the next iteration
+  }
+
+  float lt = l + __shfl_xor(l, 16, kWave);
+  lt += __shfl_xor(lt, 32, kWave);
+  if (!row_ok) return;
+  if (p.num_splits == 1) {
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    uint16_t *o = static_cast<uint16_t *>(p.out) + out_row + 4 * g;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+      *reinterpret_cast<u32x2 *>(o + 16 * db) =
+          u32x2{pack2<kBf16>(oacc[db][0] * inv, oacc[db][1] * inv), pack2<kBf16>(oacc[db][2] * inv, oacc[db][3] * inv)};
+  } else {
+    float *po = p.part_o + part * kD + 4 * g;
+    if (ntiles > 0) {
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) *reinterpret_cast<f32x4_t *>(po + 16 * db) = oacc[db];
+    }
+    if (g == 0) {
+      p.part_ml[2 * part] = ntiles > 0 ? m : -__builtin_inff();
+      p.part_ml[2 * part + 1] = ntiles > 0 ? lt : 0.f;
+    }
+  }
+}
+
+// Merges the key splits of each (query tile, KV head) row:
+//   M = max_s m_s, w_s = 2^(m_s - M), out = sum_s w_s O_s / sum_s w_s l_s.
+// Block = 4 rows x 64 threads, each thread 4 dims; splits with weight 0 (no
+// key) are skipped, so their (unwritten) partial outputs are never read.
+template <bool kBf16>
+__global__ __launch_bounds__(kPThreads) void prefill_combine_kernel(const PrefillParams p) {
+  const int item = blockIdx.x;
+  const int r = int(blockIdx.y) * 4 + int(threadIdx.x >> 6);
+  const int c = threadIdx.x & 63;
+  const int h = item % p.hkv;
+  const int qt = (item / p.hkv) % p.q_tiles;
+  const int b = item / (p.hkv * p.q_tiles);
+  const int q_begin = max(p.query_start_loc[b], 0);
+  const int ql = min(p.query_start_loc[b + 1], p.total_q) - q_begin;
+  const int tok = qt * p.tokens_per_tile + (r >> p.log2_group);
+  if (tok >= ql || 4 * c >= p.dv) return;
+  const int qhead = h * p.group + (r & (p.group - 1));
+  const size_t base = size_t(item) * p.num_splits * kPRows + r;  // part index of split 0
+  float mx = -__builtin_inff();
+  for (int s = 0; s < p.num_splits; ++s) mx = fmaxf(mx, p.part_ml[2 * (base + size_t(s) * kPRows)]);
+  f32x4_t acc{0.f, 0.f, 0.f, 0.f};
+  float total = 0.f;
+  if (mx != -__builtin_inff()) {
+    for (int s = 0; s < p.num_splits; ++s) {
+      const size_t pi = base + size_t(s) * kPRows;
+      const float ms = p.part_ml[2 * pi];
+      if (ms == -__builtin_inff()) continue;
+      const float w = __builtin_amdgcn_exp2f(ms - mx);
+      total += w * p.part_ml[2 * pi + 1];
+      const f32x4_t o = *reinterpret_cast<const f32x4_t *>(p.part_o + pi * p.dv + 4 * c);
+      acc += w * o;
+    }
+  }
+  const float inv = total > 0.f ? 1.f / total : 0.f;
+  uint16_t *o = static_cast<uint16_t *>(p.out) + (size_t(q_begin + tok) * p.hq + qhead) * p.dv + 4 * c;
+  *reinterpret_cast<u32x2 *>(o) = u32x2{pack2<kBf16>(acc[0] * inv, acc[1] * inv), pack2<kBf16>(acc[2] * inv, acc[3] * inv)};
+}
+
+// Any head sizes, group or block size: one wavefront per (query row, query
+// head), keys one at a time with the online softmax; K and V rounded to the
+// query dtype like the MFMA kernel.
+template <bool kBf16, typename BtT>
+__global__ __launch_bounds__(kWave) void paged_prefill_attention_simple(const PrefillParams p, int total_q) {
+  const int row = int(blockIdx.x) / p.hq, head = int(blockIdx.x) % p.hq;
+  if (row >= total_q) return;
+  // The request of this query row: the last b with query_start_loc[b] <= row.
+  int lo = 0, hi = p.batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) / 2;
+    if (p.query_start_loc[mid] <= row) lo = mid;
+    else hi = mid - 1;
+  }
+  const int b = lo;
+  const int q_begin = p.query_start_loc[b];
+  const int ql = p.query_start_loc[b + 1] - q_begin;
+  if (row < q_begin || row - q_begin >= ql) return;  // rows outside every request
+  const int kl = clamp_len(p.seq_lens[b], p.max_len);
+  const int lim = p.causal ? min(kl, kl - ql + (row - q_begin) + 1) : kl;
+  const int h = head / p.group;
+  const int lane = threadIdx.x;
+  const uint16_t *q = static_cast<const uint16_t *>(p.query) + (size_t(row) * p.hq + head) * p.d;
+  const BtT *bt = static_cast<const BtT *>(p.block_table) + size_t(b) * p.bt_stride;
+  const int64_t krow = p.d + 4, vrow = p.dv + 4;
+  constexpr int kMaxPerLane = 8;  // head sizes up to 512
+  float qv[kMaxPerLane], acc[kMaxPerLane];
+#pragma unroll
+  for (int i = 0; i < kMaxPerLane; ++i) {
+    const int dim = lane + kWave * i;
+    qv[i] = dim < p.d ? half_bits_to_float<kBf16>(q[dim]) : 0.f;
+    acc[i] = 0.f;
+  }
+  float m = -__builtin_inff(), l = 0.f;
+  for (int t = 0; t < lim; ++t) {
+    const int64_t blk = int64_t(bt[t / p.block_size]);
+    if (blk < 0 || blk >= p.num_blocks) continue;
+    const int64_t slot = blk * p.block_size + t % p.block_size;
+    const uint8_t *kr = p.key_cache + (slot * p.hkv + h) * krow;
+    const uint8_t *vr = p.value_cache + (slot * p.hkv + h) * vrow;
+    const float ksc = *reinterpret_cast<const float *>(kr + p.d);
+    const float vsc = *reinterpret_cast<const float *>(vr + p.dv);
+    float dot = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i) {
+      const int dim = lane + kWave * i;
+      if (dim < p.d)
+        dot = fmaf(qv[i], half_bits_to_float<kBf16>(float_to_half_bits<kBf16>(
+                              __uint_as_float(kDeviceTables.decode_f32[kr[dim]]) * ksc)), dot);
+    }
+    dot = wave_sum(dot);
+    const float x = dot * p.scale_log2;
+    const float m_new = fmaxf(m, x);
+    const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
+    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+    const float pw = __builtin_amdgcn_exp2f(x - m_use);
+    l = l * alpha + pw;
+    m = m_new;
+#pragma unroll
+    for (int i = 0; i < kMaxPerLane; ++i) {
+      const int dim = lane + kWave * i;
+      acc[i] *= alpha;
+      if (dim < p.dv)
+        acc[i] = fmaf(pw, half_bits_to_float<kBf16>(float_to_half_bits<kBf16>(
+                              __uint_as_float(kDeviceTables.decode_f32[vr[dim]]) * vsc)), acc[i]);
+    }
+  }
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  uint16_t *o = static_cast<uint16_t *>(p.out) + (size_t(row) * p.hq + head) * p.dv;
+#pragma unroll
+  for (int i = 0; i < kMaxPerLane; ++i) {
+    const int dim = lane + kWave * i;
+    if (dim < p.dv) o[dim] = float_to_half_bits<kBf16>(acc[i] * inv);
+  }
+}
+
+// ------------------------------------------------------------- host side
+
+int log2_exact(int64_t v) {
+  int l = 0;
+  while ((int64_t(1) << l) < v) ++l;
+  return (int64_t(1) << l) == v ? l : -1;
+}
+
+bool prefill_mfma_shape(int64_t d, int64_t dv, int64_t group) {
+  return (d == 64 || d == 128 || d == 256) && dv == d && group >= 1 && group <= 16 && log2_exact(group) >= 0;
+}
+
+struct PrefillPlan {
+  int tokens_per_tile, q_tiles, num_splits, split_tiles;
+};
+
+// Query tiles of 64 / G tokens; key splits while the (request, query tile,
+// KV head) items leave fewer than ~512 workgroups, each split at least two
+// 64-key tiles.
+PrefillPlan plan_prefill(int64_t batch, int64_t hkv, int64_t group, int64_t max_query_len, int64_t max_len) {
+  PrefillPlan pl{};
+  pl.tokens_per_tile = int(kPRows / group);
+  pl.q_tiles = int((std::max<int64_t>(max_query_len, 1) + pl.tokens_per_tile - 1) / pl.tokens_per_tile);
+  const int64_t items = batch * pl.q_tiles * hkv;
+  const int64_t kv_tiles = std::max<int64_t>((max_len + kKT - 1) / kKT, 1);
+  int64_t splits = (kTargetBlocks + items - 1) / items;
+  if (splits > kv_tiles) splits = kv_tiles;
+  if (splits < 1) splits = 1;
+  int64_t per = (kv_tiles + splits - 1) / splits;
+  if (per < kMinSplitTiles) per = std::min<int64_t>(kMinSplitTiles, kv_tiles);
+  pl.split_tiles = int(per);
+  pl.num_splits = int((kv_tiles + per - 1) / per);
+  return pl;
+}
+
+size_t prefill_smem(int d) { return size_t(256 + kKT) * 4 + size_t(2) * kKT * d * 2; }
+
+template <int kD, bool kBf16, typename BtT>
+int launch_prefill_mfma(const PrefillParams &p, hipStream_t stream) {
+  const void *fn = reinterpret_cast<const void *>(&paged_prefill_attention_kernel<kD, kBf16, BtT>);
+  const size_t smem = prefill_smem(kD);
+  if (const int st = reserve_dynamic_lds(fn, smem, "hif8_paged_prefill_attention")) return st;
+  const unsigned blocks = unsigned(int64_t(p.q_tiles) * p.batch * p.hkv * p.num_splits);
+  paged_prefill_attention_kernel<kD, kBf16, BtT><<<blocks, kPThreads, smem, stream>>>(p);
+  if (p.num_splits > 1)
+    prefill_combine_kernel<kBf16><<<dim3(unsigned(int64_t(p.batch) * p.q_tiles * p.hkv), kPRows / 4), kPThreads, 0,
+                                    stream>>>(p);
+  return HIF8_OK;
+}
+
+template <bool kBf16, typename BtT>
+int launch_prefill(const PrefillParams &p, bool mfma, int64_t total_q, hipStream_t stream) {
+  if (!mfma) {
+    paged_prefill_attention_simple<kBf16, BtT><<<unsigned(total_q * p.hq), kWave, 0, stream>>>(p, int(total_q));
+    return HIF8_OK;
+  }
+  switch (p.d) {
+    case 64: return launch_prefill_mfma<64, kBf16, BtT>(p, stream);
+    case 128: return launch_prefill_mfma<128, kBf16, BtT>(p, stream);
+    default: return launch_prefill_mfma<256, kBf16, BtT>(p, stream);
+  }
+}
+
+}  // namespace
+}  // namespace hif8
+
+using namespace hif8;
+
+extern "C" size_t hif8_paged_prefill_attention_workspace_size(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                                                              int64_t head_size, int64_t head_size_v,
+                                                              int64_t max_query_len, int64_t max_seq_len) {
+  if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_size <= 0 || head_size_v <= 0 ||
+      max_query_len <= 0 || max_seq_len <= 0 || num_heads % num_kv_heads)
+    return 0;
+  const int64_t group = num_heads / num_kv_heads;
+  if (!prefill_mfma_shape(head_size, head_size_v, group)) return 0;  // the simple kernel needs none
+  const PrefillPlan pl = plan_prefill(batch, num_kv_heads, group, max_query_len, max_seq_len);
+  if (pl.num_splits <= 1) return 0;
+  const size_t parts = size_t(batch) * pl.q_tiles * num_kv_heads * pl.num_splits * kPRows;
+  return parts * size_t(head_size_v + 2) * sizeof(float);
+}
+
+extern "C" int hif8_paged_prefill_attention(const void *query, int q_dtype, const uint8_t *key_cache,
+                                            const uint8_t *value_cache, int64_t num_blocks, int64_t block_size,
+                                            int64_t num_kv_heads, int64_t head_size, int64_t head_size_v,
+                                            const void *block_table, int block_table_dtype,
+                                            int64_t max_blocks_per_seq, const int32_t *query_start_loc,
+                                            const int32_t *seq_lens, int64_t batch, int64_t num_heads,
+                                            int64_t total_query_tokens, int64_t max_query_len, int64_t max_seq_len,
+                                            float scale, int causal, void *out, void *workspace,
+                                            size_t workspace_bytes, hif8_stream_t stream) {
+  clear_error();
+  if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_size <= 0 || head_size_v <= 0 ||
+      num_blocks <= 0 || block_size <= 0 || max_blocks_per_seq <= 0 || max_seq_len < 0 || max_query_len < 0 ||
+      total_query_tokens < 0)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: dimensions must be positive");
+  if (num_heads % num_kv_heads)
+    return fail(HIF8_ERR_INVALID_ARGUMENT,
+                "hif8_paged_prefill_attention: num_heads must be divisible by num_kv_heads");
+  if (head_size % 4 || head_size_v % 4)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: head sizes must be divisible by four");
+  if (head_size > 512 || head_size_v > 512)
+    return fail(HIF8_ERR_UNSUPPORTED, "hif8_paged_prefill_attention: head sizes above 512 are not supported");
+  if (!is_io_dtype(q_dtype))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: query must be float16 or bfloat16");
+  if (block_table_dtype != HIF8_INDEX_INT32 && block_table_dtype != HIF8_INDEX_INT64)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: block_table must be int32 or int64");
+  if (max_seq_len > max_blocks_per_seq * block_size)
+    return fail(HIF8_ERR_INVALID_ARGUMENT,
+                "hif8_paged_prefill_attention: max_seq_len exceeds the block table capacity");
+  if (max_seq_len > 0x7FFFFFFFll || batch > 0x7FFFFFFFll || num_heads > 0xFFFF ||
+      total_query_tokens * num_heads > 0x7FFFFFFFll || max_query_len > 0x7FFFFFFFll)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: dimensions too large");
+  if (batch == 0 || total_query_tokens == 0) return HIF8_OK;
+  if (max_query_len == 0)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: max_query_len must cover the query rows");
+  if (!query || !key_cache || !value_cache || !block_table || !query_start_loc || !seq_lens || !out)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: null pointer argument");
+  if (!aligned(key_cache, 4) || !aligned(value_cache, 4))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: caches must be 4-byte aligned");
+  if (!aligned(query, 2) || !aligned(out, 2))
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: query/out must be 2-byte aligned");
+
+  PrefillParams p{};
+  p.query = query;
+  p.key_cache = key_cache;
+  p.value_cache = value_cache;
+  p.block_table = block_table;
+  p.query_start_loc = query_start_loc;
+  p.seq_lens = seq_lens;
+  p.out = out;
+  p.bt_stride = max_blocks_per_seq;
+  p.num_blocks = num_blocks;
+  p.block_size = int(block_size);
+  p.hkv = int(num_kv_heads);
+  p.hq = int(num_heads);
+  p.group = int(num_heads / num_kv_heads);
+  p.d = int(head_size);
+  p.dv = int(head_size_v);
+  p.batch = int(batch);
+  p.max_len = int(max_seq_len);
+  p.causal = causal ? 1 : 0;
+  p.total_q = int(total_query_tokens);
+  p.scale_log2 = scale * 1.4426950408889634f;
+  const bool mfma = prefill_mfma_shape(head_size, head_size_v, p.group) && aligned(query, 16) && aligned(out, 16);
+  if (mfma) {
+    const PrefillPlan pl = plan_prefill(batch, num_kv_heads, p.group, max_query_len, max_seq_len);
+    p.log2_group = log2_exact(p.group);
+    p.tokens_per_tile = pl.tokens_per_tile;
+    p.q_tiles = pl.q_tiles;
+    p.num_splits = pl.num_splits;
+    p.split_tiles = pl.split_tiles;
+    if (int64_t(p.q_tiles) * batch * num_kv_heads * p.num_splits > 0x7FFFFFFFll)
+      return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: too many query tiles");
+    if (pl.num_splits > 1) {
+      const size_t need = hif8_paged_prefill_attention_workspace_size(batch, num_heads, num_kv_heads, head_size,
+                                                                      head_size_v, max_query_len, max_seq_len);
+      if (!workspace || workspace_bytes < need)
+        return fail(HIF8_ERR_INVALID_ARGUMENT,
+                    "hif8_paged_prefill_attention: workspace of %zu bytes required (got %zu)", need,
+                    workspace_bytes);
+      if (!aligned(workspace, 16))
+        return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: workspace must be 16-byte aligned");
+      p.part_o = static_cast<float *>(workspace);
+      p.part_ml = p.part_o + size_t(batch) * pl.q_tiles * num_kv_heads * pl.num_splits * kPRows * head_size_v;
+    }
+  } else {
+    p.log2_group = 0;
+    p.tokens_per_tile = 1;
+    p.q_tiles = 1;
+    p.num_splits = 1;
+    p.split_tiles = 1;
+  }
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const bool bf16 = q_dtype == HIF8_DTYPE_BF16, i64 = block_table_dtype == HIF8_INDEX_INT64;
+  int st;
+  if (bf16 && i64) st = launch_prefill<true, int64_t>(p, mfma, total_query_tokens, s);
+  else if (bf16) st = launch_prefill<true, int32_t>(p, mfma, total_query_tokens, s);
+  else if (i64) st = launch_prefill<false, int64_t>(p, mfma, total_query_tokens, s);
+  else st = launch_prefill<false, int32_t>(p, mfma, total_query_tokens, s);
+  if (st) return st;
+  return check_launch("hif8_paged_prefill_attention");
+}

@@ -463,6 +463,65 @@ at::Tensor Hif8PagedDecodeAttention(const at::Tensor &query, const at::Tensor &k
   return out;
 }
 
+// Several query tokens per request (kv_runtime.py:1470-1563, TND layout):
+// query [T, Hq, D], query_start_loc [batch + 1] int32, seq_lens [batch] int32
+// -> [T, Hq, Dv]; rows past query_start_loc[batch] are left unwritten.
+at::Tensor Hif8PagedPrefillAttention(const at::Tensor &query, const at::Tensor &key_cache,
+                                     const at::Tensor &value_cache, const at::Tensor &block_table,
+                                     const at::Tensor &query_start_loc, const at::Tensor &seq_lens, double scale,
+                                     int64_t max_query_len, int64_t max_seq_len, bool causal) {
+  CheckContiguousDevice(query, "query");
+  TORCH_CHECK(query.scalar_type() == at::ScalarType::Half || query.scalar_type() == at::ScalarType::BFloat16,
+              "query must have dtype torch.float16 or torch.bfloat16");
+  TORCH_CHECK(query.dim() == 3, "query must have shape [tokens, num_heads, head_size]");
+  const int64_t tokens = query.size(0), heads = query.size(1), d = query.size(2);
+  TORCH_CHECK(heads > 0 && d > 0, "query dimensions must be positive");
+  TORCH_CHECK(key_cache.dim() == 4 && value_cache.dim() == 4,
+              "caches must have shape [num_blocks, block_size, num_kv_heads, width]");
+  const int64_t kv_heads = key_cache.size(2), dv = value_cache.size(3) - 4;
+  CheckCache(key_cache, "key_cache", kv_heads, d + 4);
+  CheckCache(value_cache, "value_cache", kv_heads, dv + 4);
+  TORCH_CHECK(dv > 0, "value_cache rows are too short");
+  TORCH_CHECK(value_cache.size(0) == key_cache.size(0) && value_cache.size(1) == key_cache.size(1),
+              "key_cache and value_cache must have the same blocks");
+  TORCH_CHECK(heads % kv_heads == 0, "num_heads must be divisible by num_kv_heads");
+  CheckContiguousDevice(query_start_loc, "query_start_loc");
+  TORCH_CHECK(query_start_loc.scalar_type() == at::ScalarType::Int && query_start_loc.dim() == 1 &&
+                  query_start_loc.numel() >= 1,
+              "query_start_loc must be an int32 tensor [batch + 1]");
+  const int64_t batch = query_start_loc.numel() - 1;
+  CheckContiguousDevice(block_table, "block_table");
+  const int bt_code = IndexCode(block_table, "block_table");
+  TORCH_CHECK(block_table.dim() == 2 && block_table.size(0) >= batch && block_table.size(1) > 0,
+              "block_table must have shape [batch, max_blocks]");
+  CheckContiguousDevice(seq_lens, "seq_lens");
+  TORCH_CHECK(seq_lens.scalar_type() == at::ScalarType::Int, "seq_lens must have dtype torch.int32");
+  TORCH_CHECK(seq_lens.dim() == 1 && seq_lens.numel() >= batch, "seq_lens must contain one length per request");
+  const int64_t block_size = key_cache.size(1);
+  TORCH_CHECK(max_seq_len >= 0 && max_seq_len <= block_table.size(1) * block_size,
+              "max_seq_len must be within the block table capacity");
+  TORCH_CHECK(max_query_len >= 0, "max_query_len must be non-negative");
+  const auto device = query.device();
+  for (const auto *t : {&key_cache, &value_cache, &block_table, &seq_lens, &query_start_loc})
+    CheckSameDevice(*t, device, "attention operand");
+  const c10::OptionalDeviceGuard guard(device);
+  auto out = at::empty({tokens, heads, dv}, query.options());
+  if (batch == 0 || tokens == 0 || max_query_len == 0) return out;
+  const size_t ws_bytes = hif8_paged_prefill_attention_workspace_size(batch, heads, kv_heads, d, dv, max_query_len,
+                                                                      max_seq_len > 0 ? max_seq_len : 1);
+  at::Tensor workspace;
+  if (ws_bytes) workspace = at::empty({int64_t(ws_bytes)}, query.options().dtype(at::ScalarType::Byte));
+  CheckStatus(hif8_paged_prefill_attention(
+                  query.data_ptr(), DtypeCode(query.scalar_type()), key_cache.data_ptr<uint8_t>(),
+                  value_cache.data_ptr<uint8_t>(), key_cache.size(0), block_size, kv_heads, d, dv,
+                  block_table.data_ptr(), bt_code, block_table.size(1), query_start_loc.data_ptr<int32_t>(),
+                  seq_lens.data_ptr<int32_t>(), batch, heads, tokens, max_query_len, max_seq_len, float(scale),
+                  causal ? 1 : 0, out.data_ptr(), ws_bytes ? workspace.data_ptr() : nullptr, ws_bytes,
+                  CurrentStream(device)),
+              "hif8_paged_prefill_attention");
+  return out;
+}
+
 // Token-embedding gather-decode (scheme.py:121-131): ids of any shape -> [*ids.shape, dim] bf16.
 at::Tensor Hif8EmbeddingLookup(const at::Tensor &ids, const at::Tensor &weight, const at::Tensor &weight_scale,
                                const c10::optional<at::Tensor> &invalid_ids) {
@@ -504,6 +563,7 @@ at::Tensor Hif8AddRmsNorm(at::Tensor &h, const c10::optional<at::Tensor> &delta,
   CheckContiguousDevice(weight, "weight");
   TORCH_CHECK(h.scalar_type() == at::kBFloat16 && weight.scalar_type() == at::kBFloat16,
               "hif8_add_rms_norm takes bfloat16 tensors");
+  TORCH_CHECK(h.dim() >= 1 && h.size(-1) > 0, "hif8_add_rms_norm needs rows of positive width");
   const int64_t n = h.size(-1);
   TORCH_CHECK(weight.numel() == n, "weight must have the row width");
   if (delta.has_value()) {
@@ -524,7 +584,8 @@ at::Tensor Hif8AddRmsNorm(at::Tensor &h, const c10::optional<at::Tensor> &delta,
 at::Tensor Hif8SiluMul(const at::Tensor &gate_up) {
   CheckContiguousDevice(gate_up, "gate_up");
   TORCH_CHECK(gate_up.scalar_type() == at::kBFloat16, "hif8_silu_mul takes bfloat16");
-  TORCH_CHECK(gate_up.size(-1) % 2 == 0, "gate_up width must be even");
+  TORCH_CHECK(gate_up.dim() >= 1 && gate_up.size(-1) > 0 && gate_up.size(-1) % 2 == 0,
+              "gate_up width must be even and positive");
   const int64_t n = gate_up.size(-1) / 2;
   std::vector<int64_t> shape(gate_up.sizes().begin(), gate_up.sizes().end());
   shape.back() = n;
@@ -557,6 +618,7 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> Hif8AddRmsNormQuant(at::Tensor &h
   CheckContiguousDevice(weight, "weight");
   TORCH_CHECK(h.scalar_type() == at::kBFloat16 && weight.scalar_type() == at::kBFloat16,
               "hif8_add_rms_norm_quant takes bfloat16 tensors");
+  TORCH_CHECK(h.dim() >= 1 && h.size(-1) > 0, "hif8_add_rms_norm_quant needs rows of positive width");
   const int64_t n = h.size(-1);
   TORCH_CHECK(weight.numel() == n, "weight must have the row width");
   if (delta.has_value()) {
@@ -581,7 +643,8 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor> Hif8AddRmsNormQuant(at::Tensor &h
 std::tuple<at::Tensor, at::Tensor> Hif8SiluMulQuant(const at::Tensor &gate_up, const at::Tensor &input_scale) {
   CheckContiguousDevice(gate_up, "gate_up");
   TORCH_CHECK(gate_up.scalar_type() == at::kBFloat16, "hif8_silu_mul_quant takes bfloat16");
-  TORCH_CHECK(gate_up.size(-1) % 2 == 0, "gate_up width must be even");
+  TORCH_CHECK(gate_up.dim() >= 1 && gate_up.size(-1) > 0 && gate_up.size(-1) % 2 == 0,
+              "gate_up width must be even and positive");
   CheckInputScale(input_scale, gate_up);
   const int64_t n = gate_up.size(-1) / 2;
   std::vector<int64_t> shape(gate_up.sizes().begin(), gate_up.sizes().end());
@@ -687,13 +750,15 @@ std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> Hif8QkNormRope(
 std::tuple<at::Tensor, at::Tensor> Hif8StaticQuantMeta(const at::Tensor &x, const at::Tensor &fixed_scale) {
   (void)fixed_scale;
   auto data = at::empty_like(x, x.options().dtype(at::kByte));
-  const int64_t rows = x.dim() ? x.numel() / x.size(-1) : 1;
+  int64_t rows = 1;  // product of the leading dimensions (no division: the last may be 0)
+  for (int64_t i = 0; i + 1 < x.dim(); ++i) rows *= x.size(i);
   return {data, at::empty({rows}, x.options().dtype(at::kFloat))};
 }
 
 std::tuple<at::Tensor, at::Tensor> Hif8DynamicQuantMeta(const at::Tensor &x) {
   auto data = at::empty_like(x, x.options().dtype(at::kByte));
-  const int64_t rows = x.dim() ? x.numel() / x.size(-1) : 1;
+  int64_t rows = 1;  // product of the leading dimensions (no division: the last may be 0)
+  for (int64_t i = 0; i + 1 < x.dim(); ++i) rows *= x.size(i);
   return {data, at::empty({rows}, x.options().dtype(at::kFloat))};
 }
 
@@ -724,6 +789,12 @@ at::Tensor Hif8PagedDecodeAttentionMeta(const at::Tensor &query, const at::Tenso
   return at::empty({query.size(0), query.size(1), value_cache.size(3) - 4}, query.options());
 }
 
+at::Tensor Hif8PagedPrefillAttentionMeta(const at::Tensor &query, const at::Tensor &, const at::Tensor &value_cache,
+                                         const at::Tensor &, const at::Tensor &, const at::Tensor &, double, int64_t,
+                                         int64_t, bool) {
+  return at::empty({query.size(0), query.size(1), value_cache.size(3) - 4}, query.options());
+}
+
 at::Tensor Hif8EmbeddingLookupMeta(const at::Tensor &ids, const at::Tensor &weight, const at::Tensor &,
                                    const c10::optional<at::Tensor> &) {
   std::vector<int64_t> shape(ids.sizes().begin(), ids.sizes().end());
@@ -741,6 +812,7 @@ TORCH_LIBRARY(vllm_ascend_hif8, m) {
   m.def("soft_hif8_static_fused_gemm(Tensor activation, Tensor weight, Tensor fixed_scale, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
   m.def("hif8_kv_cache_write(Tensor key, Tensor value, Tensor(a!) key_cache, Tensor(b!) value_cache, Tensor slot_mapping, Tensor key_scale, Tensor value_scale, Tensor(c!)? invalid_slots=None) -> ()");
   m.def("hif8_paged_decode_attention(Tensor query, Tensor key_cache, Tensor value_cache, Tensor block_table, Tensor seq_lens, float scale, int max_seq_len) -> Tensor");
+  m.def("hif8_paged_prefill_attention(Tensor query, Tensor key_cache, Tensor value_cache, Tensor block_table, Tensor query_start_loc, Tensor seq_lens, float scale, int max_query_len, int max_seq_len, bool causal=True) -> Tensor");
   m.def("hif8_embedding_lookup(Tensor input_ids, Tensor weight, Tensor weight_scale, Tensor(a!)? invalid_ids=None) -> Tensor");
   m.def("hif8_dynamic_quant(Tensor x) -> (Tensor, Tensor)");
   m.def("soft_hif8_fused_gemm(Tensor activation, Tensor weight, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
@@ -764,6 +836,7 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
   m.impl("soft_hif8_static_fused_gemm", &SoftHif8StaticFusedGemm);
   m.impl("hif8_kv_cache_write", &Hif8KVCacheWrite);
   m.impl("hif8_paged_decode_attention", &Hif8PagedDecodeAttention);
+  m.impl("hif8_paged_prefill_attention", &Hif8PagedPrefillAttention);
   m.impl("hif8_embedding_lookup", &Hif8EmbeddingLookup);
   m.impl("hif8_dynamic_quant", &Hif8DynamicQuant);
   m.impl("soft_hif8_fused_gemm", &SoftHif8FusedGemm);
@@ -786,6 +859,7 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
   m.impl("soft_hif8_static_fused_gemm", &LinearMeta);
   m.impl("hif8_kv_cache_write", &Hif8KVCacheWriteMeta);
   m.impl("hif8_paged_decode_attention", &Hif8PagedDecodeAttentionMeta);
+  m.impl("hif8_paged_prefill_attention", &Hif8PagedPrefillAttentionMeta);
   m.impl("hif8_embedding_lookup", &Hif8EmbeddingLookupMeta);
   m.impl("hif8_dynamic_quant", &Hif8DynamicQuantMeta);
   m.impl("soft_hif8_fused_gemm", &FusedLinearMeta);

@@ -27,7 +27,7 @@ ARCH = os.environ.get("HIF8_OFFLOAD_ARCH", "gfx950")
 ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 
 HIP_SOURCES = ["capi.hip", "static_quant.hip", "gemv.hip", "gemm.hip", "linear_api.hip", "kv_cache.hip",
-               "embedding.hip", "model_ops.hip"]
+               "embedding.hip", "model_ops.hip", "prefill_attention.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

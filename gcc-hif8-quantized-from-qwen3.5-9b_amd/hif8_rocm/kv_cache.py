@@ -241,11 +241,122 @@ def paged_decode_attention(
         query.contiguous(), key_cache, value_cache, table, lens_dev, float(scale), int(max_seq_len))
 
 
+def paged_attention(
+    query: torch.Tensor,
+    key_cache: torch.Tensor,
+    value_cache: torch.Tensor,
+    block_table: torch.Tensor,
+    seq_lens: Sequence[int] | torch.Tensor,
+    *,
+    scale: float,
+    query_lens: Sequence[int] | None = None,
+    query_start_loc: torch.Tensor | None = None,
+    causal: bool = True,
+    max_query_len: int | None = None,
+    max_seq_len: int | None = None,
+    validate: bool = True,
+) -> torch.Tensor:
+    """Attention over HiF8 pages for any number of query tokens per request.
+
+    ``query`` is ``[T, Hq, D]`` in the TND layout; request b owns the next
+    ``query_lens[b]`` rows, which are the last positions of its
+    ``seq_lens[b]`` cached tokens (this step's cache write included), and with
+    ``causal`` row i sees keys ``0 .. seq_lens[b] - query_lens[b] + i`` - the
+    contract of ``paged_attention_reference`` with ``query_lens``
+    (kv_cache.py:314-372) and of the reference's TND attention call
+    (kv_runtime.py:1470-1563).  Returns ``[T, Hq, Dv]``.
+
+    The request split comes from ``query_lens`` (host integers, as the
+    reference's oracle takes them; rows must add up to T) or from
+    ``query_start_loc`` (an int32 device tensor ``[B + 1]``, the cumulative
+    form of the reference's ``actual_seq_lengths_q`` with a leading 0; pass
+    ``max_query_len`` to avoid a host synchronisation).  One query row per
+    request runs the decode kernel; otherwise the multi-token kernel.
+    """
+    _check_caches(key_cache, value_cache)
+    if query.ndim != 3:
+        raise ValueError("query must have shape [tokens, num_heads, head_size]")
+    if query.shape[1] % key_cache.shape[2]:
+        raise ValueError("num_heads must be divisible by num_kv_heads")
+    if (query_lens is None) == (query_start_loc is None):
+        raise ValueError("pass exactly one of query_lens and query_start_loc")
+    tokens = query.shape[0]
+    if query_lens is not None:
+        q_lengths = [int(v) for v in query_lens]
+        if any(v < 0 for v in q_lengths) or sum(q_lengths) != tokens:
+            raise ValueError("query_lens must describe every query row")
+        batch = len(q_lengths)
+        if not isinstance(seq_lens, torch.Tensor):
+            lengths = [int(v) for v in seq_lens]
+            if len(lengths) != batch:
+                raise ValueError("one sequence length is required per request")
+            for q_len, kv_len in zip(q_lengths, lengths):
+                if q_len and kv_len < q_len:
+                    raise ValueError(
+                        "HIF8 post-update KV length cannot be shorter than its query "
+                        f"length, got q={q_len}, kv={kv_len}")
+        if batch == tokens and all(v == 1 for v in q_lengths):
+            # The decode case: each row is its request's last position.
+            return paged_decode_attention(query, key_cache, value_cache, block_table, seq_lens, scale=scale,
+                                          max_seq_len=max_seq_len, validate=validate)
+        starts = [0]
+        for v in q_lengths:
+            starts.append(starts[-1] + v)
+        loc = torch.tensor(starts, dtype=torch.int32).to(query.device)
+        if max_query_len is None:
+            max_query_len = max(q_lengths, default=0)
+    else:
+        if query_start_loc.ndim != 1 or query_start_loc.numel() < 1:
+            raise ValueError("query_start_loc must have shape [batch + 1]")
+        batch = query_start_loc.numel() - 1
+        loc = query_start_loc.to(device=query.device, dtype=torch.int32).contiguous()
+        if max_query_len is None:
+            max_query_len = int((loc[1:] - loc[:-1]).max().item()) if batch else 0
+    if block_table.ndim != 2 or block_table.shape[0] < batch:
+        raise ValueError("block_table must have shape [batch, max_blocks]")
+    block_size = key_cache.shape[1]
+    if isinstance(seq_lens, torch.Tensor):
+        lens_dev = seq_lens.to(device=query.device, dtype=torch.int32).contiguous()
+        if lens_dev.numel() < batch:
+            raise ValueError("one sequence length is required per request")
+        if max_seq_len is None:
+            max_seq_len = int(lens_dev[:batch].max().item()) if batch else 0
+    else:
+        lengths = [int(v) for v in seq_lens]
+        if len(lengths) != batch:
+            raise ValueError("one sequence length is required per request")
+        if any(v < 0 for v in lengths):
+            raise ValueError("sequence lengths must be non-negative")
+        lens_dev = torch.tensor(lengths, dtype=torch.int32).to(query.device)
+        if max_seq_len is None:
+            max_seq_len = max(lengths, default=0)
+    if max_seq_len > block_table.shape[1] * block_size:
+        raise ValueError("block_table has too few entries for a sequence length")
+    table = block_table[:batch]
+    if table.dtype not in (torch.int32, torch.int64):
+        table = table.to(torch.int64)
+    table = table.to(query.device).contiguous()
+    if validate and batch and max_seq_len > 0:
+        if bool((lens_dev[:batch] > max_seq_len).any()):
+            raise ValueError("max_seq_len is smaller than a sequence length")
+        needed = (max_seq_len + block_size - 1) // block_size
+        used = (torch.arange(needed, device=query.device)[None, :] * block_size
+                < lens_dev[:batch, None].to(torch.int64))
+        ids = table[:, :needed].to(torch.int64)
+        if bool(((ids < 0) | (ids >= key_cache.shape[0]))[used].any()):
+            raise IndexError("block_table references a block outside the cache")
+    extension = native.load_extension()
+    return native._operator("hif8_paged_prefill_attention", extension)(
+        query.contiguous(), key_cache, value_cache, table, loc, lens_dev, float(scale), int(max_query_len),
+        int(max_seq_len), bool(causal))
+
+
 __all__ = [
     "HIF8_CACHE_DTYPE",
     "HIF8_SCALE_BYTES",
     "Hif8KVCacheLayout",
     "pack_kv_rows",
+    "paged_attention",
     "paged_decode_attention",
     "unpack_kv_rows",
     "write_kv_cache",

@@ -40,34 +40,40 @@ class NativeExtensionUnavailable(RuntimeError):
 
 
 def load_extension() -> ModuleType:
-    """Load and validate the native extension, caching success or failure (native.py:32-50)."""
+    """Import ``hif8_rocm._C`` once and hand it back (reference loader: native.py:32-50).
+
+    The outcome is memoised either way: after a failed import every later
+    call raises :class:`NativeExtensionUnavailable` again, chained to the
+    original error, without retrying the import.
+    """
     global _extension, _load_error
     if _extension is not None:
         return _extension
     if _load_error is not None:
-        raise NativeExtensionUnavailable(_error_message()) from _load_error
+        raise NativeExtensionUnavailable(_unavailable_text()) from _load_error
     try:
-        candidate = importlib.import_module(_EXTENSION_MODULE)
-        missing = [s for s in _REQUIRED_SYMBOLS if not callable(getattr(candidate, s, None))]
-        if missing:
-            raise ImportError(f"native extension is missing required symbols: {', '.join(missing)}")
-        _extension = candidate
-        return candidate
-    except BaseException as error:  # noqa: BLE001 - cached and re-raised as NativeExtensionUnavailable
-        _load_error = error
-        raise NativeExtensionUnavailable(_error_message()) from error
+        module = importlib.import_module(_EXTENSION_MODULE)
+        absent = [name for name in _REQUIRED_SYMBOLS if not callable(getattr(module, name, None))]
+        if absent:
+            raise ImportError("hif8_rocm._C lacks the operator entry points " + ", ".join(absent))
+    except BaseException as exc:  # noqa: BLE001 - memoised, surfaced as NativeExtensionUnavailable
+        _load_error = exc
+        raise NativeExtensionUnavailable(_unavailable_text()) from exc
+    _extension = module
+    return module
 
 
-def _error_message() -> str:
-    detail = f": {_load_error}" if _load_error is not None else ""
+def _unavailable_text() -> str:
+    cause = "" if _load_error is None else f" ({_load_error})"
     return (
-        "HiFloat8 HIP operators are unavailable"
-        f"{detail}. Build them with __graft_entry__.build() (or python -m hif8_rocm._build); "
-        "the production path intentionally has no decoded-weight or floating-point fallback."
+        f"the HiF8 HIP extension could not be loaded{cause}; compile it with __graft_entry__.build() "
+        "or python -m hif8_rocm._build. These operators run only on the HIP kernels (there is "
+        "no decoded-weight or floating-point fallback)."
     )
 
 
 def is_available() -> bool:
+    """True when the extension imports and exports every required operator."""
     try:
         load_extension()
     except NativeExtensionUnavailable:
@@ -76,7 +82,7 @@ def is_available() -> bool:
 
 
 def reset_extension_cache() -> None:
-    """Reset loader state for isolated tests."""
+    """Forget the memoised import result, so that the next call imports again."""
     global _extension, _load_error
     _extension = None
     _load_error = None

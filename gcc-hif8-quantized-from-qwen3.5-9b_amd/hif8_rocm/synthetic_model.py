@@ -340,22 +340,15 @@ class HybridModel:
                                                 validate=False)
             o = o.reshape(b, 1, c.heads * c.head_dim)
         else:
-            # Prefill: the prompt's rows decoded from the HiF8 cache (as the
-            # reference's attention reads them), causal attention in fp32.
-            kd = self._decoded_rows(kc, self._slots(st, pos), c.kv_heads).reshape(b, t, c.kv_heads, c.head_dim)
-            vd = self._decoded_rows(vc, self._slots(st, pos), c.kv_heads).reshape(b, t, c.kv_heads, c.head_dim)
-            rep = c.heads // c.kv_heads
-            qf = q.float().transpose(1, 2).contiguous()
-            kf = kd.float().repeat_interleave(rep, dim=2).transpose(1, 2).contiguous()
-            vf = vd.float().repeat_interleave(rep, dim=2).transpose(1, 2).contiguous()
-            o = torch.nn.functional.scaled_dot_product_attention(qf, kf, vf, is_causal=True, scale=scale)
-            o = o.transpose(1, 2).reshape(b, t, c.heads * c.head_dim).to(h.dtype)
+            # Prefill or a continued (chunked) prefill: the t new rows of each
+            # request are its last t positions of st.seq_lens cached tokens,
+            # attended with the right-aligned causal mask over the HiF8 pages
+            # (pages decoded inside the kernel, as for decode).
+            o = kv_cache.paged_attention(q.reshape(b * t, c.heads, c.head_dim).contiguous(), kc, vc,
+                                         st.block_table, st.seq_lens, scale=scale, query_lens=[t] * b,
+                                         max_query_len=t, max_seq_len=st.max_len, validate=False)
+            o = o.reshape(b, t, c.heads * c.head_dim)
         return L["o"](o.reshape(b * t, -1)).reshape(b, t, -1)
-
-    def _decoded_rows(self, cache: torch.Tensor, slots: torch.Tensor, heads: int) -> torch.Tensor:
-        rows = cache.reshape(-1, heads, cache.shape[-1])[slots.long()]
-        data, scale = kv_cache.unpack_kv_rows(rows, self.cfg.head_dim)
-        return native.scaled_decode(data.reshape(-1, self.cfg.head_dim).contiguous(), scale.reshape(-1).contiguous())
 
     def _linear_attention(self, L, idx: int, st: RequestState, h: torch.Tensor, decode: bool):
         c = self.cfg
@@ -463,7 +456,9 @@ class HybridModel:
         """ids, pos [B, T] (T = 1 when decode); returns the last position's logits [B, vocab] (fp32).
 
         The caller sets ``st.seq_lens`` to the lengths including these tokens
-        before a decode step (the decode attention reads them)."""
+        before the call: the attention layers read them, and the T rows of a
+        prefill are the last T positions of those lengths (so a prefill may
+        continue a request whose earlier tokens are already cached)."""
         c = self.cfg
         if decode:
             return self._forward_decode(st, ids, pos)
@@ -488,6 +483,7 @@ class HybridModel:
         st = self.new_state(batch, tokens)
         ids = torch.randint(0, self.cfg.vocab, (batch, tokens), generator=g, device=self.device)
         pos = torch.arange(tokens, device=self.device).expand(batch, tokens).contiguous()
+        st.seq_lens.fill_(tokens)
         self.set_calibrating(True)
         try:
             self.forward(st, ids, pos, decode=False)

@@ -279,6 +279,48 @@ int hif8_paged_decode_attention(const void *query, int q_dtype, const uint8_t *k
                                 void *workspace, size_t workspace_bytes, hif8_stream_t stream);
 
 /*
+ * Bytes of workspace hif8_paged_prefill_attention needs for these sizes (0 if none);
+ * the key-split plan depends only on these arguments (ACLNN GetWorkspaceSize phase,
+ * csrc/extension/hif8_native.cpp:202-239).
+ */
+size_t hif8_paged_prefill_attention_workspace_size(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
+                                                   int64_t head_size, int64_t head_size_v,
+                                                   int64_t max_query_len, int64_t max_seq_len);
+
+/*
+ * Paged HiF8 attention for several query tokens per request: prefill and chunked
+ * prefill.  Replaces the TND branch of _forward_hif8_attention
+ * (src/vllm_ascend_hif8/kv_runtime.py:1470-1563, the sequence plan of
+ * _attention_sequence_plan :588-641, npu_fused_infer_attention_score with
+ * sparse_mode=3 when causal) whose contract is paged_attention_reference with
+ * query_lens (kv_cache.py:314-372).  Pages are decoded inside the kernel.
+ *   query [total_query_tokens, num_heads, D] fp16/bf16 (TND layout)
+ *   query_start_loc [batch + 1] int32 on the device: request b owns query rows
+ *     query_start_loc[b] .. query_start_loc[b + 1] - 1 (the reference's cumulative
+ *     actual_seq_lengths_q is query_start_loc[1:]); rows from query_start_loc[batch]
+ *     to total_query_tokens - 1 are not written
+ *   seq_lens [batch] int32 on the device: cached tokens of each request after this
+ *     step's cache write, clamped to [0, max_seq_len]
+ *   max_query_len >= every request's query length (sizes the grid)
+ *   causal: query row i of request b sits at position seq_lens[b] - q_len_b + i and
+ *     sees keys 0 .. that position (right-aligned mask, kv_cache.py:365-369); 0: every
+ *     row sees all seq_lens[b] keys
+ *   out [total_query_tokens, num_heads, Dv] in the query dtype, K/V rows decoded to the
+ *     query dtype as dtype(dec(code) * row scale) (kv_cache.py:355-356); a row that sees
+ *     no key gets zeros; tokens whose block id lies outside [0, num_blocks) are left out
+ *   workspace  at least hif8_paged_prefill_attention_workspace_size(...) bytes, 16-byte
+ *              aligned (may be NULL when that size is 0)
+ */
+int hif8_paged_prefill_attention(const void *query, int q_dtype, const uint8_t *key_cache,
+                                 const uint8_t *value_cache, int64_t num_blocks, int64_t block_size,
+                                 int64_t num_kv_heads, int64_t head_size, int64_t head_size_v,
+                                 const void *block_table, int block_table_dtype, int64_t max_blocks_per_seq,
+                                 const int32_t *query_start_loc, const int32_t *seq_lens, int64_t batch,
+                                 int64_t num_heads, int64_t total_query_tokens, int64_t max_query_len,
+                                 int64_t max_seq_len, float scale, int causal, void *out, void *workspace,
+                                 size_t workspace_bytes, hif8_stream_t stream);
+
+/*
  * Decode-step glue of the synthetic hybrid model (the end-to-end workload).
  * These have no counterpart among the reference's operators: they fuse the
  * bf16 / fp32 model parts that the reference leaves to vLLM (norms, the MLP
@@ -293,7 +335,9 @@ int hif8_paged_decode_attention(const void *query, int q_dtype, const uint8_t *k
  *   (q_norm / k_norm [D]) then rotated on the first rotary_dim dims (halves i, i + r/2,
  *   angle pos[b] * inv_freq[i], float32 inv_freq [r/2], int64 pos [batch]); if slots is
  *   not NULL, slots[b] = block_table[b, pos / block_size] * block_size + pos % block_size
- *   (int32 block_table [batch, max_blocks]).  D <= 256.
+ *   (int32 block_table [batch, max_blocks]), or -1 (a padding slot the cache write
+ *   skips) when pos < 0, pos / block_size >= max_blocks or the table entry is negative.
+ *   D <= 256.
  * hif8_gdn_decode_step: one token of the gated delta rule for batch requests.
  *   mixed_qkvz [batch, ld]: q | k (k_heads x k_dim each) | v | z (v_heads x v_dim each)
  *   ba [batch, 2 v_heads]: b | a;  conv_weight [C, conv_width], C = 2 k_heads k_dim + v_heads v_dim;

@@ -21,7 +21,10 @@ function) is listed per function:
 * scaled decode                      - exhaustive 256 bytes x scale set, bf16 RNE
                                       checked against torch's own conversion
 * KV pack/unpack/scatter/gather      - reference known answers (byte layout)
-* paged attention                    - textbook softmax attention in float64
+* paged attention                    - textbook softmax attention in float64; a
+                                      pure-Python per-row loop twin; closed forms that
+                                      fix the right-aligned causal mask (uniform keys:
+                                      output = mean of the visible values)
 * embedding gather-decode            - the reference formula executed by torch on the
                                       CPU (bf16 table, bf16 scale, bf16 product) and
                                       closed-form products
@@ -506,51 +509,88 @@ def decode_kv_rows(data: np.ndarray, scale: np.ndarray) -> np.ndarray:
 
 def paged_attention_reference(query: np.ndarray, key_cache: np.ndarray, value_cache: np.ndarray,
                               block_table: np.ndarray, seq_lens, block_size: int, scale: float,
-                              rounding: str = "bf16") -> np.ndarray:
-    """Decode (one query token per request) paged attention (kv_cache.py:314-372).
+                              rounding: str = "bf16", query_lens=None, causal: bool = True) -> np.ndarray:
+    """Paged attention over HiF8 pages (kv_cache.py:314-372).
 
-    ``query`` is [B, Hq, D] float32 holding bf16 values.  K/V rows are gathered,
-    decoded as bf16_RNE(dec(b) * s_row) and query head h attends KV head
-    h // (Hq / Hkv), the head ``repeat_interleave`` gives it (kv_cache.py:355-363).
-    ``rounding="bf16"`` reproduces the reference's bf16 intermediate roundings
-    (logits, probabilities and output are bf16 tensors in kv_cache.py:364-371);
-    ``rounding="f64"`` keeps every intermediate in float64.  A request with no
-    tokens yields zeros (an empty weighted sum).
+    ``query`` holds bf16 values as float32.  Without ``query_lens`` it is
+    [B, Hq, D], one query token per request (decode).  With ``query_lens`` it
+    is [T, Hq, D] in the TND layout: request b owns the next query_lens[b]
+    rows, and those rows are the LAST query_lens[b] positions of its
+    seq_lens[b] cached tokens (kv_cache.py:321-346), so with ``causal`` query
+    row i of request b sees keys 0 .. seq_lens[b] - query_lens[b] + i (the
+    right-aligned mask of kv_cache.py:365-369; sparse_mode=3 in
+    kv_runtime.py:1526-1540).  Without ``causal`` every row sees every key.
+
+    K/V rows are gathered, decoded as bf16_RNE(dec(b) * s_row) and query head
+    h attends KV head h // (Hq / Hkv), the head ``repeat_interleave`` gives it
+    (kv_cache.py:355-363).  ``rounding="bf16"`` reproduces the reference's
+    bf16 intermediate roundings (logits, probabilities and output are bf16
+    tensors in kv_cache.py:364-371); ``rounding="f64"`` keeps every
+    intermediate in float64.  A query row that sees no key (an empty request,
+    or a row whose position is negative because query_lens[b] > seq_lens[b],
+    which the reference's attention plan rejects, kv_runtime.py:626-633)
+    yields zeros.
     """
     q = np.asarray(query, dtype=np.float64)
-    bsz, hq, d = q.shape
+    rows_total, hq, d = q.shape
+    lengths = [int(v) for v in seq_lens]
+    bsz = len(lengths)
+    if query_lens is None:
+        q_lengths = [1] * bsz
+    else:
+        q_lengths = [int(v) for v in query_lens]
+    if len(q_lengths) != bsz or sum(q_lengths) != rows_total or any(v < 0 for v in q_lengths):
+        raise ValueError("query_lens must describe every query row")
     kw = key_cache.shape[-1] - SCALE_BYTES
     vw = value_cache.shape[-1] - SCALE_BYTES
-    krows = gather_kv_rows(key_cache, block_table, seq_lens, block_size)
-    vrows = gather_kv_rows(value_cache, block_table, seq_lens, block_size)
-    out = np.zeros((bsz, hq, vw), dtype=np.float64)
+    krows = gather_kv_rows(key_cache, block_table, lengths, block_size)
+    vrows = gather_kv_rows(value_cache, block_table, lengths, block_size)
+    out = np.zeros((rows_total, hq, vw), dtype=np.float64)
     hkv = key_cache.shape[2]
     if hq % hkv:
         raise ValueError("num_heads must be divisible by num_kv_heads")
     group = hq // hkv
+    q0 = 0
     for b in range(bsz):
+        ql, kl = q_lengths[b], lengths[b]
+        rows = slice(q0, q0 + ql)
+        q0 += ql
+        if ql == 0 or kl == 0:
+            continue
         kd, ks = unpack_kv_rows(krows[b], kw)
         vd, vs = unpack_kv_rows(vrows[b], vw)
-        if kd.shape[0] == 0:
-            continue
         keys = round_bf16(decode_kv_rows(kd, ks)).astype(np.float64)      # [L, Hkv, D]
         vals = round_bf16(decode_kv_rows(vd, vs)).astype(np.float64)
-        qg = q[b].reshape(hkv, group, d)                                  # head h = j * group + g
-        logits = np.einsum("jgd,kjd->jgk", qg, keys).reshape(hq, -1)      # [Hq, L]
+        qg = q[rows].reshape(ql, hkv, group, d)                           # head h = j * group + g
+        logits = np.einsum("qjgd,kjd->qjgk", qg, keys, optimize=True)     # [ql, Hkv, G, L]
+        visible = np.ones((ql, kl), dtype=bool)
+        if causal:
+            positions = np.arange(ql) + kl - ql                           # right-aligned query positions
+            visible = np.arange(kl)[None, :] <= positions[:, None]
+        mask = visible[:, None, None, :]
+        seen = visible.any(axis=1)                                        # rows with at least one key
         if rounding == "bf16":
             logits = round_bf16(logits).astype(np.float64)
             logits = round_bf16(logits * np.float32(scale)).astype(np.float64)
+            logits = np.where(mask, logits, -np.inf)
             mx = logits.max(axis=-1, keepdims=True)
-            e = np.exp((logits - mx).astype(np.float32)).astype(np.float64)
-            probs = round_bf16(e / e.sum(axis=-1, keepdims=True)).astype(np.float64)
-            res = np.einsum("jgk,kjd->jgd", probs.reshape(hkv, group, -1), vals)
-            out[b] = round_bf16(res.reshape(hq, vw))
+            mx = np.where(np.isfinite(mx), mx, 0.0)
+            with np.errstate(invalid="ignore"):
+                e = np.exp((logits - mx).astype(np.float32)).astype(np.float64)
+                probs = round_bf16(e / e.sum(axis=-1, keepdims=True)).astype(np.float64)
+            probs = np.where(mask, probs, 0.0)
+            res = np.einsum("qjgk,kjd->qjgd", probs, vals, optimize=True).reshape(ql, hq, vw)
+            res = round_bf16(res)
         else:
-            logits = logits * scale
+            logits = np.where(mask, logits * scale, -np.inf)
             mx = logits.max(axis=-1, keepdims=True)
-            e = np.exp(logits - mx)
-            probs = e / e.sum(axis=-1, keepdims=True)
-            out[b] = np.einsum("jgk,kjd->jgd", probs.reshape(hkv, group, -1), vals).reshape(hq, vw)
+            mx = np.where(np.isfinite(mx), mx, 0.0)
+            e = np.where(mask, np.exp(logits - mx), 0.0)
+            with np.errstate(invalid="ignore"):
+                probs = e / e.sum(axis=-1, keepdims=True)
+            probs = np.where(mask, probs, 0.0)
+            res = np.einsum("qjgk,kjd->qjgd", probs, vals, optimize=True).reshape(ql, hq, vw)
+        out[rows] = np.where(seen[:, None, None], res, 0.0)
     return out
 
 

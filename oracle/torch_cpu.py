@@ -1,0 +1,58 @@
+"""Torch-CPU restatement of the reference's CPU GEMV path, for the timed CPU
+baseline.
+
+TEST INFRASTRUCTURE ONLY.  Only ``tests/`` and the ``cpu_baseline`` leg of
+``bench.py`` may import this module: it is the baseline that is timed on the
+GPU box's host cores, never part of the product.
+
+It restates, with torch CPU tensor ops so that it runs on every host thread
+that ``torch.set_num_threads`` grants:
+
+* the static activation quant of the reference's CPU oracle
+  (``calibration.saturating_encode_tensor`` / ``static_quantize_tensor``,
+  calibration.py:139-201, with the vectorised encode of
+  ``torch_codec.encode_tensor``, torch_codec.py:32-49): divide by the scale in
+  FP32, clamp finite values to +-2^15, index the 4096-entry magnitude table by
+  (exponent, top four mantissa bits), sign except for zero, Inf / NaN by the
+  full mantissa;
+* the soft-decode GEMV of the reference's op test
+  (tests/test_npu_ops.py:334-336): decode-table activations times their row
+  scale, decode-table weights times their channel scale, one FP32 matmul.
+
+Pinned by ``tests/test_oracle_torch_cpu.py``: codes equal the numpy oracle's
+``static_quant_rows`` bit for bit on every bf16 pattern and on random FP32
+values, and the GEMV is within FP32 rounding of ``linear_u8_u8`` (float64).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from oracle import hif8_oracle as o
+
+_MAG = torch.from_numpy(o.LUT4096.astype("int32"))
+_DECODE = torch.from_numpy(o.DECODE_F32.copy())
+
+
+def static_quant(x: torch.Tensor, scale: float) -> torch.Tensor:
+    """Saturating static encode of ``x / scale`` (float32 division) -> uint8 codes."""
+    q = x.to(torch.float32) / torch.tensor(scale, dtype=torch.float32)
+    finite = torch.isfinite(q)
+    q = torch.where(finite, q.clamp(-o.MAX_FINITE, o.MAX_FINITE), q)
+    bits = q.view(torch.int32)
+    exponent = (bits >> 23) & 0xFF
+    mantissa = bits & 0x7FFFFF
+    sign = (bits >> 24) & 0x80
+    mag = _MAG[exponent * 16 + (mantissa >> 19)]
+    code = torch.where(mag == 0, mag, mag | sign)
+    special = exponent == 0xFF
+    code = torch.where(special, torch.where(mantissa != 0, torch.full_like(code, o.NAN_CODE), sign | o.PINF), code)
+    return code.to(torch.uint8)
+
+
+def soft_gemv(a_codes: torch.Tensor, a_scale: torch.Tensor, w_codes: torch.Tensor,
+              w_scale: torch.Tensor) -> torch.Tensor:
+    """(dec(a) * a_scale[:, None]) @ (dec(w) * w_scale[:, None])^T in FP32."""
+    a = _DECODE[a_codes.to(torch.int32)] * a_scale.reshape(-1, 1)
+    w = _DECODE[w_codes.to(torch.int32)] * w_scale.reshape(-1, 1)
+    return a @ w.T

@@ -41,3 +41,20 @@ def hif8_weight(n: int, k: int, seed: int) -> tuple[np.ndarray, np.ndarray]:
 def random_codes(shape, seed: int, high: int = 111) -> np.ndarray:
     """Finite codes 0..110 (no Inf/NaN), as the reference tests draw them."""
     return np.random.default_rng(seed).integers(0, high, shape, dtype=np.uint8)
+
+
+C1_SEED = 20261201
+
+
+def c1_operands():
+    """BASELINE configs[0] (the CPU-reference GEMV): x bf16 [1, 4096] ~ N(0, 1)
+    with input_scale = absmax / 32768; W fp32 [12288, 4096] ~ N(0, 0.02) with
+    per-row scale = row absmax / 32768, encoded by the oracle.  One seeded CPU
+    generator drives both.  Returns (x bf16, input_scale f32 [1], W fp32,
+    W codes u8, W scales f32)."""
+    g = torch.Generator().manual_seed(C1_SEED)
+    x = torch.randn(1, 4096, generator=g, dtype=torch.float32).to(torch.bfloat16)
+    w = (torch.randn(12288, 4096, generator=g, dtype=torch.float32) * 0.02).numpy()
+    ws = (np.abs(w).max(axis=1) / HIF8_MAX).astype(np.float32)
+    wq, _ = o.static_quant_rows(w, ws)
+    return x, input_scale_of(x), w, wq, ws

@@ -131,3 +131,39 @@ def test_gemm_workspace_query_follows_the_split_plan(lib):
     assert b"workspace" in lib.hif8_last_error()
     assert ws(_p(), _p(), _p(), _p(), None, -1, _p(), 1, 512, 4096, 4096, _p(16), 1 << 30, None) == 1
     assert b"aligned" in lib.hif8_last_error()
+
+
+def test_prefill_attention_contract_and_workspace_plan(lib):
+    """Multi-token paged attention: the key-split workspace follows the plan
+    (64 / G tokens per query tile, splits while the tiles leave < 512
+    workgroups, two or more 64-key tiles per split), and invalid arguments are
+    rejected before any launch."""
+    size = lib.hif8_paged_prefill_attention_workspace_size
+    size.argtypes = [ctypes.c_int64] * 7
+    size.restype = ctypes.c_size_t
+    # B=1, q 17, ctx 4096, G 4: 2 query tiles x 4 heads, 64 key tiles in 32 splits of 2.
+    assert size(1, 16, 4, 256, 256, 17, 4096) == 1 * 2 * 4 * 32 * 64 * (256 + 2) * 4
+    # Enough query tiles to fill the GPU: no split, no workspace.
+    assert size(4, 16, 4, 256, 256, 512, 4096) == 0
+    # Shapes for the one-wavefront kernel need none.
+    assert size(1, 12, 4, 64, 64, 17, 4096) == 0 and size(1, 16, 4, 24, 24, 17, 4096) == 0
+    assert size(0, 16, 4, 256, 256, 17, 4096) == 0 and size(1, 15, 4, 256, 256, 17, 4096) == 0
+    f = lib.hif8_paged_prefill_attention
+    f.argtypes = ([ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 5 +
+                  [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p] +
+                  [ctypes.c_int64] * 5 + [ctypes.c_float, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p,
+                                          ctypes.c_size_t, ctypes.c_void_p])
+    a = _p(256)
+
+    def call(heads=16, kv_heads=4, d=256, ws=None, ws_bytes=0, query=a, bt_dtype=0, max_seq=4096, q_dtype=1):
+        return f(query, q_dtype, a, a, 64, 128, kv_heads, d, d, a, bt_dtype, 32, a, a, 1, heads, 17, 17, max_seq,
+                 0.0625, 1, a, ws, ws_bytes, None)
+
+    assert call(heads=15) == 1 and b"divisible by num_kv_heads" in lib.hif8_last_error()
+    assert call(d=26) == 1 and b"divisible by four" in lib.hif8_last_error()
+    assert call(bt_dtype=5) == 1 and b"int32 or int64" in lib.hif8_last_error()
+    assert call(q_dtype=7) == 1 and b"float16 or bfloat16" in lib.hif8_last_error()
+    assert call(max_seq=32 * 128 + 1) == 1 and b"block table capacity" in lib.hif8_last_error()
+    assert call(query=None) == 1 and b"null pointer" in lib.hif8_last_error()
+    assert call() == 1 and b"workspace of" in lib.hif8_last_error()
+    assert call(ws=_p(264), ws_bytes=1 << 30) == 1 and b"16-byte aligned" in lib.hif8_last_error()

@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from _data import LAYER_SHAPES, bf16_activation, hif8_weight, input_scale_of, random_codes
+from _data import LAYER_SHAPES, bf16_activation, c1_operands, hif8_weight, input_scale_of, random_codes
 from oracle import hif8_oracle as o
 
 pytestmark = pytest.mark.gpu
@@ -104,8 +104,30 @@ def test_decode_gemv_config_shapes(native_ops, device, m, n, k):
     assert torch.equal(fused, y)
 
 
+def test_cpu_reference_gemv_config(native_ops, device):
+    """M = 1, N = 12288, K = 4096 from seeded fp32 weights
+    (reference oracle form: tests/test_npu_ops.py:334-344).  The activation
+    codes from hif8_static_quant are bit-exact against the oracle; every one
+    of the 12288 outputs of soft_linear is within 1e-2 of linear_u8_u8."""
+    from hif8_rocm import native as api
+
+    x, s, _, wq, ws = c1_operands()
+    xq, xs = o.static_quant_rows(x.float().numpy(), s.numpy())
+    data, rs = api.static_quant(x.to(device), s.to(device))
+    torch.cuda.synchronize()
+    assert np.array_equal(data.cpu().numpy(), xq)
+    assert np.array_equal(rs.cpu().numpy(), xs)
+    y = api.soft_linear(data, _t(wq, device), rs, _t(ws, device), None, output_dtype=torch.bfloat16)
+    assert tuple(y.shape) == (1, 12288) and y.dtype == torch.bfloat16
+    _check(y, o.linear_u8_u8(xq, xs, wq, ws))
+    fused = api.soft_static_fused_linear(x.to(device), _t(wq, device), s.to(device), _t(ws, device), None,
+                                         output_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, y)
+
+
 @pytest.mark.parametrize("m", [512, 4096])
-@pytest.mark.parametrize("n,k", [(2048, 4096), (4096, 12288), (24576, 4096)])
+@pytest.mark.parametrize("n,k", [(4096, 4096), (2048, 4096), (4096, 12288), (24576, 4096)])
 @pytest.mark.parametrize("heavy", [False, True])
 def test_prefill_gemm_config_shapes(native_ops, device, m, n, k, heavy):
     """BASELINE config 3 (sampled rows checked against the oracle at full size)."""

@@ -1,0 +1,171 @@
+"""Multi-token paged HiF8 attention (prefill / chunked prefill) on the GPU
+against the oracle's paged_attention_reference with query_lens
+(kv_cache.py:314-372; right-aligned causal mask kv_cache.py:365-369), within
+rtol = atol = 1e-2 of the float64 oracle (and of the bf16-rounding oracle up
+to that oracle's own distance from the float64 one).
+
+Cases: BASELINE configs[3]'s cache shape (Hq 16, Hkv 4, D 256, 128-token
+pages, shuffled page table) at q_len in {1, 17, 512} over ctx {512, 4096};
+ragged batches with empty requests; causal off; rows whose positions precede
+the first key; key splits with the combine; other head sizes, GQA groups and
+block sizes; fp16 queries; int64 tables; mixed row scales; the any-shape
+kernel.  A bound relative to each output row's magnitude catches indexing
+errors that the absolute tolerance would hide."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from _kv import build_cache, randn
+from oracle import hif8_oracle as o
+
+pytestmark = pytest.mark.gpu
+
+
+def _run_op(device, q, kc, vc, table, lens, qlens, scale, causal, max_query_len=None):
+    """The torch op directly, with query_start_loc built from qlens (no routing)."""
+    loc = torch.tensor(np.concatenate([[0], np.cumsum(qlens)]), dtype=torch.int32, device=device)
+    out = torch.ops.vllm_ascend_hif8.hif8_paged_prefill_attention(
+        q.to(device), kc, vc, table.to(device), loc, torch.tensor(lens, dtype=torch.int32, device=device),
+        scale, max(qlens) if max_query_len is None else max_query_len, max(lens), causal)
+    torch.cuda.synchronize()
+    return out
+
+
+def _check(device, lens, qlens, hq, hkv, d, bs, *, causal=True, dtype=torch.bfloat16, bt_dtype=torch.int32,
+           seed=0, dv=None, mixed=False, bound=2e-2, q_mul=1.0, via_api=False):
+    from hif8_rocm import kv_cache
+
+    kc, vc, table = build_cache(device, lens, hkv, d, bs, seed, dv=dv, bt_dtype=bt_dtype, mixed=mixed)
+    q = randn((sum(qlens), hq, d), seed + 1, q_mul, dtype)
+    scale = 1.0 / math.sqrt(d)
+    print(f"case lens={lens[:4]} qlens={qlens[:4]} hq={hq} hkv={hkv} d={d} bs={bs} causal={causal}", flush=True)
+    if via_api:
+        out = kv_cache.paged_attention(q.to(device), kc, vc, table.to(device), lens, scale=scale, query_lens=qlens,
+                                       causal=causal)
+        torch.cuda.synchronize()
+    else:
+        out = _run_op(device, q, kc, vc, table, lens, qlens, scale, causal)
+    got = out.float().cpu().numpy()
+    kcn, vcn, tn = kc.cpu().numpy(), vc.cpu().numpy(), table.numpy()
+    qn = q.float().numpy()
+    ref = o.paged_attention_reference(qn, kcn, vcn, tn, lens, bs, scale, rounding="f64", query_lens=qlens,
+                                      causal=causal)
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-2)
+    if q_mul <= 1.0:
+        # The bf16 variant rounds every logit to bf16 as the reference's CPU
+        # einsum does; rows that see only a few keys turn that rounding into
+        # weight changes of several percent, so each element may also differ
+        # by the gap between the two oracles themselves.
+        ref16 = o.paged_attention_reference(qn, kcn, vcn, tn, lens, bs, scale, rounding="bf16", query_lens=qlens,
+                                            causal=causal)
+        slack = np.abs(ref16 - ref)
+        bad = np.abs(got - ref16) > 1e-2 + 1e-2 * np.abs(ref16) + slack
+        assert not bad.any(), (int(bad.sum()), float(np.abs(got - ref16)[bad].max()))
+    err = np.abs(got - ref).max(axis=-1)
+    mag = np.abs(ref).max(axis=-1)
+    worst = float((err / np.maximum(mag, 1e-3)).max())
+    print(f"  max err {float(err.max()):.3e}, max err/|out| {worst:.3e}", flush=True)
+    assert worst < bound, worst
+    return got, ref
+
+
+@pytest.mark.parametrize("ctx", [512, 4096])
+@pytest.mark.parametrize("q_len", [1, 17, 512])
+def test_prefill_config_shapes(native_ops, device, ctx, q_len):
+    """q_len new tokens at the end of a ctx-token request (chunked prefill when
+    q_len < ctx), next to a second request with its own shorter chunk."""
+    second = max(1, q_len // 2)
+    _check(device, [ctx, ctx // 2 + 3], [q_len, second], 16, 4, 256, 128, seed=ctx + q_len)
+
+
+def test_prefill_from_empty_cache_whole_prompt(native_ops, device):
+    # The usual prefill: every prompt token is a query row (q_len == seq_len).
+    _check(device, [512, 300, 64], [512, 300, 64], 16, 4, 256, 128, seed=11)
+
+
+def test_prefill_through_the_api_and_decode_routing(native_ops, device):
+    _check(device, [700, 90], [33, 90], 16, 4, 256, 128, seed=12, via_api=True)
+    # One row per request routes to the decode kernel and matches the oracle too.
+    _check(device, [700, 90, 5], [1, 1, 1], 16, 4, 256, 128, seed=13, via_api=True)
+
+
+def test_prefill_ragged_batch_with_empty_requests(native_ops, device):
+    _check(device, [10, 0, 129, 300, 64, 1], [3, 0, 129, 65, 0, 1], 16, 4, 256, 128, seed=14)
+
+
+def test_prefill_without_causal_mask(native_ops, device):
+    _check(device, [300, 77], [40, 77], 16, 4, 256, 128, causal=False, seed=15)
+
+
+def test_prefill_long_context_key_splits(native_ops, device):
+    # Few query tiles over a long context: the key range is split over
+    # workgroups and merged by the combine kernel.
+    _check(device, [16384, 5000], [9, 64], 16, 4, 256, 128, seed=16)
+
+
+def test_prefill_rows_before_the_first_key_are_zero(native_ops, device):
+    # More query rows than cached tokens (the reference's plan rejects this;
+    # the kernel gives the rows at negative positions zeros, like the oracle).
+    got, _ = _check(device, [5, 40], [9, 40], 16, 4, 256, 128, seed=17)
+    assert not got[:4].any()
+
+
+def test_prefill_mixed_row_scales(native_ops, device):
+    _check(device, [400, 129], [100, 20], 16, 4, 256, 128, seed=18, mixed=True)
+
+
+def test_prefill_peaked_softmax(native_ops, device):
+    _check(device, [1000, 300], [200, 31], 16, 4, 256, 128, seed=19, q_mul=8.0, bound=1e-2)
+
+
+def test_prefill_fp16_query(native_ops, device):
+    _check(device, [600, 130], [70, 130], 16, 4, 256, 128, dtype=torch.float16, seed=20)
+
+
+@pytest.mark.parametrize("hq,hkv,d,bs,lens,qlens,bt_dtype", [
+    (8, 2, 128, 16, [45, 300, 47], [45, 20, 1], torch.int64),   # block size 16: tiles span pages
+    (16, 1, 64, 32, [100, 64], [37, 64], torch.int32),           # group 16: 4 tokens per tile
+    (8, 8, 128, 64, [70, 200], [70, 3], torch.int64),            # group 1: 64 tokens per tile
+    (16, 4, 256, 48, [200, 97], [66, 97], torch.int32),          # block size 48 (not a power of two)
+    (4, 2, 64, 128, [1000], [130], torch.int32),                 # group 2
+    (16, 2, 128, 128, [513], [300], torch.int32),                # group 8
+])
+def test_prefill_other_shapes(native_ops, device, hq, hkv, d, bs, lens, qlens, bt_dtype):
+    _check(device, lens, qlens, hq, hkv, d, bs, bt_dtype=bt_dtype, seed=hq + d + bs)
+
+
+@pytest.mark.parametrize("hq,hkv,d,dv,bs,lens,qlens", [
+    (4, 2, 24, 24, 4, [9, 3, 0], [4, 3, 0]),     # head size outside the MFMA set
+    (4, 2, 64, 32, 8, [40, 17], [12, 2]),        # head_size_v != head_size
+    (20, 1, 64, 64, 16, [33], [33]),             # group 20 > 16
+    (12, 4, 64, 64, 16, [50, 20], [7, 20]),      # group 3, not a power of two
+])
+def test_prefill_any_shape_kernel(native_ops, device, hq, hkv, d, dv, bs, lens, qlens):
+    _check(device, lens, qlens, hq, hkv, d, bs, dv=dv, seed=d + dv + hq)
+
+
+def test_prefill_is_deterministic(native_ops, device):
+    kc, vc, table = build_cache(device, [4096], 4, 256, 128, 21)
+    q = randn((30, 16, 256), 22)
+    a = _run_op(device, q, kc, vc, table, [4096], [30], 0.0625, True)
+    b = _run_op(device, q, kc, vc, table, [4096], [30], 0.0625, True)
+    assert torch.equal(a, b)
+
+
+def test_prefill_api_validation(native_ops, device):
+    from hif8_rocm import kv_cache
+
+    kc, vc, table = build_cache(device, [100], 4, 256, 128, 23)
+    q = randn((10, 16, 256), 24).to(device)
+    with pytest.raises(ValueError, match="describe every query row"):
+        kv_cache.paged_attention(q, kc, vc, table.to(device), [100], scale=0.0625, query_lens=[9])
+    with pytest.raises(ValueError, match="cannot be shorter"):
+        kv_cache.paged_attention(q, kc, vc, table.to(device), [5], scale=0.0625, query_lens=[10])
+    bad = table.clone()
+    bad[0, 0] = kc.shape[0] + 3
+    with pytest.raises(IndexError, match="outside the cache"):
+        kv_cache.paged_attention(q, kc, vc, bad.to(device), [100], scale=0.0625, query_lens=[10])

@@ -51,9 +51,32 @@ def test_decode_steps_agree_with_prefill(model, device):
     full = torch.cat([prompt] + toks[:steps], dim=1)
     st2 = model.new_state(b, full.shape[1])
     pos2 = torch.arange(full.shape[1], device=device).expand(b, -1).contiguous()
+    st2.seq_lens.fill_(full.shape[1])
     ref = model.forward(st2, full, pos2, decode=False)
     cos = torch.nn.functional.cosine_similarity(logits, ref, dim=-1)
     assert float(cos.min()) > 0.995, cos
+
+
+def test_chunked_prefill_continues_the_cached_request(model, device):
+    """A prompt prefilled in two chunks (the second chunk's rows attend the
+    first chunk's cached pages through the right-aligned causal mask, and the
+    linear-attention layers carry their conv / recurrent state) gives the
+    logits of one prefill of the whole prompt."""
+    b, t1, t2 = 2, 20, 13
+    g = torch.Generator(device=device).manual_seed(4)
+    prompt = torch.randint(0, model.cfg.vocab, (b, t1 + t2), generator=g, device=device)
+    whole = model.new_state(b, t1 + t2)
+    whole.seq_lens.fill_(t1 + t2)
+    ref = model.forward(whole, prompt, torch.arange(t1 + t2, device=device).expand(b, -1).contiguous(), decode=False)
+    st = model.new_state(b, t1 + t2)
+    st.seq_lens.fill_(t1)
+    model.forward(st, prompt[:, :t1], torch.arange(t1, device=device).expand(b, -1).contiguous(), decode=False)
+    st.seq_lens.fill_(t1 + t2)
+    got = model.forward(st, prompt[:, t1:], torch.arange(t1, t1 + t2, device=device).expand(b, -1).contiguous(),
+                        decode=False)
+    cos = torch.nn.functional.cosine_similarity(got, ref, dim=-1)
+    assert float(cos.min()) > 0.995, cos
+    assert torch.equal(got.argmax(-1), ref.argmax(-1))
 
 
 def test_graph_replay_matches_eager_decode(model, device):
@@ -69,15 +92,21 @@ def test_graph_replay_matches_eager_decode(model, device):
 
 def test_single_row_fusion_generates_the_same_tokens(model, device, monkeypatch):
     """HIF8_STATIC_FUSED_SINGLE_ROW=1 swaps quant -> GEMV for the fused kernel
-    on one-row projections; the logits, hence the tokens, are unchanged."""
+    on one-row projections; the logits, hence the tokens, are unchanged.  The
+    glue-kernel input quant is switched off, so that every one-row projection
+    with K <= 4096 (qkv / qkvz, gate_up, o / out) goes through the scheme and
+    the fused kernel, not only the o / out projections."""
     from hif8_rocm.synthetic_model import generate
 
     g = torch.Generator(device=device).manual_seed(21)
     prompt = torch.randint(0, model.cfg.vocab, (1, 12), generator=g, device=device)
+    glue, _ = generate(model, prompt, 6, graph=True)
+    monkeypatch.setattr(model, "fuse_input_quant", False)
     plain, _ = generate(model, prompt, 6, graph=True)
     monkeypatch.setenv("HIF8_STATIC_FUSED_SINGLE_ROW", "1")
     fused, _ = generate(model, prompt, 6, graph=True)
     assert torch.equal(plain, fused)
+    assert torch.equal(glue, plain)
 
 
 def test_fused_input_quant_generates_the_same_tokens(model, device):

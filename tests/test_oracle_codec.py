@@ -233,6 +233,22 @@ def test_static_quant_matches_scalar_codec_on_all_bf16_inputs():
         assert np.array_equal(data.reshape(-1), np.array(want, np.uint8)), s
 
 
+def test_cpu_reference_config_weight_bytes_match_the_scalar_codec():
+    """the fp32 weights' codes (row scale absmax / 32768)
+    from the vectorised oracle equal the scalar codec on sampled rows, and
+    each row's absmax lands exactly on the HiF8 maximum."""
+    from _data import c1_operands
+
+    x, s, w, wq, ws = c1_operands()
+    assert w.shape == (12288, 4096) and wq.dtype == np.uint8 and ws.shape == (12288,)
+    assert float(s[0]) == float(x.float().abs().max()) / 32768.0
+    for r in np.random.default_rng(0).choice(12288, 6, replace=False):
+        q = w[r] / ws[r]
+        want = [o.encode_scalar(min(max(float(v), -o.MAX_FINITE), o.MAX_FINITE)) for v in q]
+        assert np.array_equal(wq[r], np.array(want, np.uint8)), r
+        assert o.SAT_CODE in (wq[r] & 0x7F)
+
+
 # --- linear (reference.py:10-43; test_reference.py:8-12) ---
 
 def test_exact_small_matrix():

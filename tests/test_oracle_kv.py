@@ -139,3 +139,129 @@ def test_attention_matches_per_token_loop_and_empty_requests():
             w = [math.exp(x - m) for x in logits]
             want = [sum(wi * r[i] for wi, r in zip(w, rows)) / sum(w) for i in range(d)]
             assert np.allclose(out[b, h], want, rtol=1e-12, atol=1e-12)
+
+
+# ---------------------------------------------------------------- multi-token (prefill / chunked prefill)
+
+def _attention_loop(query, kc, vc, table, lens, bs, scale, query_lens, causal):
+    """Per query row and head, keys walked through the block table one token
+    at a time and the softmax written out by hand (no array code shared with
+    the oracle): query row i of request b sits at position lens[b] -
+    query_lens[b] + i (kv_cache.py:365-369)."""
+    hq, d = query.shape[1], query.shape[2]
+    hkv = kc.shape[2]
+    group = hq // hkv
+    flat_k, flat_v = kc.reshape(-1, hkv, d + 4), vc.reshape(-1, hkv, d + 4)
+    out, r = [], 0
+    for b, (ql, kl) in enumerate(zip(query_lens, lens)):
+        for i in range(ql):
+            last = kl - ql + i if causal else kl - 1
+            heads = []
+            for h in range(hq):
+                j = h // group
+                logits, rows = [], []
+                for t in range(min(last + 1, kl)):
+                    slot = table[b, t // bs] * bs + t % bs
+                    kd, ksc = o.unpack_kv_rows(flat_k[slot:slot + 1], d)
+                    vd, vsc = o.unpack_kv_rows(flat_v[slot:slot + 1], d)
+                    k = [_bf16(o.decode_scalar(int(c)) * ksc[0, j]) for c in kd[0, j]]
+                    rows.append([_bf16(o.decode_scalar(int(c)) * vsc[0, j]) for c in vd[0, j]])
+                    logits.append(scale * sum(float(a) * b_ for a, b_ in zip(query[r, h], k)))
+                if not logits:
+                    heads.append([0.0] * d)
+                    continue
+                m = max(logits)
+                w = [math.exp(x - m) for x in logits]
+                heads.append([sum(wi * row[x] for wi, row in zip(w, rows)) / sum(w) for x in range(d)])
+            out.append(heads)
+            r += 1
+    return np.asarray(out, np.float64).reshape(r, hq, d)
+
+
+def _random_paged_cache(rng, nb, bs, hkv, d):
+    kc = np.zeros((nb, bs, hkv, d + 4), np.uint8)
+    vc = np.zeros_like(kc)
+    kvals = rng.standard_normal((nb * bs, hkv, d)).astype(np.float32)
+    vvals = rng.standard_normal((nb * bs, hkv, d)).astype(np.float32)
+    ks = (np.abs(kvals).max(axis=(0, 2)) / 32768.0).astype(np.float32)
+    vs = (np.abs(vvals).max(axis=(0, 2)) / 32768.0).astype(np.float32)
+    o.scatter_kv_rows(kc, _cache_from_values(kvals, ks), np.arange(nb * bs), bs)
+    o.scatter_kv_rows(vc, _cache_from_values(vvals, vs), np.arange(nb * bs), bs)
+    return kc, vc
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_multi_token_attention_matches_per_row_loop(causal):
+    rng = np.random.default_rng(17)
+    hkv, group, d, bs, nb = 2, 2, 8, 4, 8
+    kc, vc = _random_paged_cache(rng, nb, bs, hkv, d)
+    table = np.array([[6, 1, 3, -1], [0, 7, 2, 5], [4, -1, -1, -1], [-1, -1, -1, -1]])
+    lens, qlens = [9, 14, 3, 0], [4, 14, 1, 0]
+    q = rng.standard_normal((sum(qlens), hkv * group, d)).astype(np.float32)
+    out = o.paged_attention_reference(q, kc, vc, table, lens, bs, 0.35, rounding="f64", query_lens=qlens,
+                                      causal=causal)
+    want = _attention_loop(q, kc, vc, table, lens, bs, 0.35, qlens, causal)
+    assert out.shape == (sum(qlens), hkv * group, d)
+    assert np.allclose(out, want, rtol=1e-12, atol=1e-12)
+    bf = o.paged_attention_reference(q, kc, vc, table, lens, bs, 0.35, rounding="bf16", query_lens=qlens,
+                                     causal=causal)
+    assert np.allclose(bf, out, rtol=0, atol=3e-2)
+
+
+def test_right_aligned_causal_mask_closed_form():
+    # Zero keys make every visible logit equal, so each output is the mean of
+    # the values the row may see.  Value row t is the constant t + 1 (exact in
+    # HiF8), so row i of a request with L cached tokens and q query rows sees
+    # positions 0 .. L - q + i and outputs (L - q + i + 2) / 2.  A mask
+    # aligned to the top-left (row i sees 0 .. i) would give (i + 2) / 2.
+    bs, d, hkv = 4, 4, 1
+    lens, qlens = [11, 6], [5, 6]
+    nb = 5
+    kc = _cache_from_values(np.zeros((nb * bs, hkv, d), np.float32), np.ones(1, np.float32)).reshape(nb, bs, hkv, d + 4)
+    vc = np.zeros_like(kc)
+    table = np.array([[2, 0, 4], [1, 3, -1]])
+    # Write value t + 1 at token t of each request.
+    for b, n in enumerate(lens):
+        for t in range(n):
+            slot = table[b, t // bs] * bs + t % bs
+            row = _cache_from_values(np.full((1, hkv, d), t + 1, np.float32), np.ones(1, np.float32))
+            vc.reshape(-1, hkv, d + 4)[slot] = row[0]
+    q = np.ones((sum(qlens), 2, d), np.float32)
+    out = o.paged_attention_reference(q, kc, vc, table, lens, bs, 1.0, rounding="f64", query_lens=qlens)
+    r = 0
+    for n, ql in zip(lens, qlens):
+        for i in range(ql):
+            right = (n - ql + i + 2) / 2.0
+            assert np.allclose(out[r], right, rtol=0, atol=1e-12), (n, ql, i)
+            if n != ql:
+                assert not np.allclose(out[r], (i + 2) / 2.0)
+            r += 1
+    # Without the mask every row sees the whole request: mean of 1 .. L.
+    full = o.paged_attention_reference(q, kc, vc, table, lens, bs, 1.0, rounding="f64", query_lens=qlens,
+                                       causal=False)
+    assert np.allclose(full[:5], (lens[0] + 1) / 2.0) and np.allclose(full[5:], (lens[1] + 1) / 2.0)
+
+
+def test_one_query_row_per_request_is_the_decode_case():
+    rng = np.random.default_rng(23)
+    hkv, group, d, bs, nb = 2, 4, 8, 4, 6
+    kc, vc = _random_paged_cache(rng, nb, bs, hkv, d)
+    table = np.array([[5, 2, 0], [1, 3, 4]])
+    lens = [7, 12]
+    q = rng.standard_normal((2, hkv * group, d)).astype(np.float32)
+    for rounding in ("f64", "bf16"):
+        dec = o.paged_attention_reference(q, kc, vc, table, lens, bs, 0.5, rounding=rounding)
+        pre = o.paged_attention_reference(q, kc, vc, table, lens, bs, 0.5, rounding=rounding, query_lens=[1, 1])
+        assert np.array_equal(dec, pre)
+
+
+def test_rows_before_the_first_key_are_zero_and_lengths_are_checked():
+    rng = np.random.default_rng(29)
+    kc, vc = _random_paged_cache(rng, 2, 4, 1, 4)
+    q = rng.standard_normal((5, 1, 4)).astype(np.float32)
+    # Five query rows over three cached tokens: rows 0 and 1 sit at negative
+    # positions and see nothing.
+    out = o.paged_attention_reference(q, kc, vc, np.array([[1]]), [3], 4, 1.0, rounding="f64", query_lens=[5])
+    assert not out[:2].any() and np.abs(out[2:]).sum() > 0
+    with pytest.raises(ValueError):
+        o.paged_attention_reference(q, kc, vc, np.array([[1]]), [3], 4, 1.0, query_lens=[4])

@@ -1,0 +1,40 @@
+"""Pins the torch-CPU baseline port (oracle/torch_cpu.py) against the numpy
+oracle: static-quant codes bit for bit on every bf16 pattern (several scales,
+NaN / Inf / saturation included) and random FP32 values, and the soft-decode
+GEMV within FP32 rounding of the float64 linear_u8_u8."""
+
+import numpy as np
+import torch
+
+from oracle import hif8_oracle as o
+from oracle import torch_cpu
+
+
+def test_static_quant_codes_equal_the_numpy_oracle_on_every_bf16_pattern():
+    bits = torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    x = bits.to(torch.float32)
+    for scale in (1.0, 3.0, 1e-3, 0.0625, 7.5e4):
+        got = torch_cpu.static_quant(x, scale).numpy()
+        want, _ = o.static_quant_rows(x.numpy().reshape(1, -1), np.array([scale], np.float32))
+        assert np.array_equal(got, want.reshape(-1)), scale
+
+
+def test_static_quant_codes_on_random_fp32():
+    rng = np.random.default_rng(7)
+    raw = rng.integers(0, 2 ** 32, 200_000, dtype=np.uint64).astype(np.uint32).view(np.float32)
+    x = torch.from_numpy(raw.copy())
+    got = torch_cpu.static_quant(x, 0.37).numpy()
+    want, _ = o.static_quant_rows(raw.reshape(1, -1), np.array([0.37], np.float32))
+    assert np.array_equal(got, want.reshape(-1))
+
+
+def test_soft_gemv_matches_linear_u8_u8():
+    rng = np.random.default_rng(11)
+    a = rng.integers(0, 111, (2, 512), dtype=np.uint8)
+    w = rng.integers(0, 111, (96, 512), dtype=np.uint8)
+    sa = (rng.random(2, dtype=np.float32) + 0.5) * 1e-2
+    sw = (rng.random(96, dtype=np.float32) + 0.5) * 1e-3
+    got = torch_cpu.soft_gemv(torch.from_numpy(a), torch.from_numpy(sa), torch.from_numpy(w),
+                              torch.from_numpy(sw)).numpy()
+    want = o.linear_u8_u8(a, sa, w, sw)
+    assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
