@@ -40,6 +40,7 @@
 #include <stddef.h>
 #include <stdlib.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "quant_device.h"
@@ -849,39 +850,41 @@ extern "C" size_t hif8_paged_decode_attention_workspace_size(int64_t batch, int6
   return size_t(batch) * size_t(plan.num_splits) * size_t(num_heads) * size_t(head_size_v + 2) * sizeof(float);
 }
 
-extern "C" int hif8_paged_decode_attention(const void *query, int q_dtype, const uint8_t *key_cache,
-                                           const uint8_t *value_cache, int64_t num_blocks, int64_t block_size,
-                                           int64_t num_kv_heads, int64_t head_size, int64_t head_size_v,
-                                           const void *block_table, int block_table_dtype,
-                                           int64_t max_blocks_per_seq, const int32_t *seq_lens, int64_t batch,
-                                           int64_t num_heads, int64_t max_seq_len, float scale, void *out,
-                                           void *workspace, size_t workspace_bytes, hif8_stream_t stream) {
-  clear_error();
+namespace hif8 {
+namespace {
+
+// The decode attention of both entry points below; `name` prefixes errors.
+int decode_attention(const char *name, const void *query, int q_dtype, const uint8_t *key_cache,
+                     const uint8_t *value_cache, int64_t num_blocks, int64_t block_size, int64_t num_kv_heads,
+                     int64_t head_size, int64_t head_size_v, const void *block_table, int block_table_dtype,
+                     int64_t max_blocks_per_seq, const int32_t *seq_lens, int64_t batch, int64_t num_heads,
+                     int64_t max_seq_len, float scale, void *out, void *workspace, size_t workspace_bytes,
+                     hif8_stream_t stream) {
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_size <= 0 || head_size_v <= 0 ||
       num_blocks <= 0 || block_size <= 0 || max_blocks_per_seq <= 0 || max_seq_len < 0)
-    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_decode_attention: dimensions must be positive");
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: dimensions must be positive", name);
   if (num_heads % num_kv_heads)
-    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_decode_attention: num_heads must be divisible by num_kv_heads");
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: num_heads must be divisible by num_kv_heads", name);
   if (head_size % 4 || head_size_v % 4)
-    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_decode_attention: head sizes must be divisible by four");
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: head sizes must be divisible by four", name);
   if (head_size > 512 || head_size_v > 512)
-    return fail(HIF8_ERR_UNSUPPORTED, "hif8_paged_decode_attention: head sizes above 512 are not supported");
+    return fail(HIF8_ERR_UNSUPPORTED, "%s: head sizes above 512 are not supported", name);
   if (!is_io_dtype(q_dtype))
-    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_decode_attention: query must be float16 or bfloat16");
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: query must be float16 or bfloat16", name);
   if (block_table_dtype != HIF8_INDEX_INT32 && block_table_dtype != HIF8_INDEX_INT64)
-    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_decode_attention: block_table must be int32 or int64");
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: block_table must be int32 or int64", name);
   if (max_seq_len > max_blocks_per_seq * block_size)
     return fail(HIF8_ERR_INVALID_ARGUMENT,
-                "hif8_paged_decode_attention: max_seq_len exceeds the block table capacity");
+                "%s: max_seq_len exceeds the block table capacity", name);
   if (max_seq_len > 0x7FFFFFFFll || batch > 0x7FFFFFFFll || num_heads > 0xFFFF)
-    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_decode_attention: dimensions too large");
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: dimensions too large", name);
   if (batch == 0) return HIF8_OK;
   if (!query || !key_cache || !value_cache || !block_table || !seq_lens || !out)
-    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_decode_attention: null pointer argument");
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: null pointer argument", name);
   if (!aligned(key_cache, 4) || !aligned(value_cache, 4))
-    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_decode_attention: caches must be 4-byte aligned");
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: caches must be 4-byte aligned", name);
   if (!aligned(query, 2) || !aligned(out, 2))
-    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_decode_attention: query/out must be 2-byte aligned");
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: query/out must be 2-byte aligned", name);
 
   AttnParams p{};
   p.query = query;
@@ -912,10 +915,10 @@ extern "C" int hif8_paged_decode_attention(const void *query, int q_dtype, const
                                                                      head_size_v, max_seq_len);
       if (!workspace || workspace_bytes < need)
         return fail(HIF8_ERR_INVALID_ARGUMENT,
-                    "hif8_paged_decode_attention: workspace of %zu bytes required (got %zu)", need,
+                    "%s: workspace of %zu bytes required (got %zu)", name, need,
                     workspace_bytes);
       if (!aligned(workspace, 16))
-        return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_decode_attention: workspace must be 16-byte aligned");
+        return fail(HIF8_ERR_INVALID_ARGUMENT, "%s: workspace must be 16-byte aligned", name);
       p.part_o = static_cast<float *>(workspace);
       p.part_ml = p.part_o + size_t(batch) * plan.num_splits * num_heads * head_size_v;
     }
@@ -929,5 +932,89 @@ extern "C" int hif8_paged_decode_attention(const void *query, int q_dtype, const
   else if (bf16) launch_attention<true, int32_t>(p, mfma, batch, s);
   else if (i64) launch_attention<false, int64_t>(p, mfma, batch, s);
   else launch_attention<false, int32_t>(p, mfma, batch, s);
-  return check_launch("hif8_paged_decode_attention");
+  return check_launch(name);
+}
+
+}  // namespace
+}  // namespace hif8
+
+extern "C" int hif8_paged_decode_attention(const void *query, int q_dtype, const uint8_t *key_cache,
+                                           const uint8_t *value_cache, int64_t num_blocks, int64_t block_size,
+                                           int64_t num_kv_heads, int64_t head_size, int64_t head_size_v,
+                                           const void *block_table, int block_table_dtype,
+                                           int64_t max_blocks_per_seq, const int32_t *seq_lens, int64_t batch,
+                                           int64_t num_heads, int64_t max_seq_len, float scale, void *out,
+                                           void *workspace, size_t workspace_bytes, hif8_stream_t stream) {
+  clear_error();
+  return decode_attention("hif8_paged_decode_attention", query, q_dtype, key_cache, value_cache, num_blocks,
+                          block_size, num_kv_heads, head_size, head_size_v, block_table, block_table_dtype,
+                          max_blocks_per_seq, seq_lens, batch, num_heads, max_seq_len, scale, out, workspace,
+                          workspace_bytes, stream);
+}
+
+// ------------------------------------------------- allocation-free variant
+
+namespace hif8 {
+namespace {
+
+// The split partials of hif8_paged_decode_attention_noalloc: one array per
+// GPU, held until the process ends.  Host code never uses `scratch` itself
+// (on the host it names a stand-in, not device memory): it resolves each
+// device's address once with hipGetSymbolAddress and passes that.
+constexpr size_t kScratchBytes = size_t(HIF8_DECODE_ATTENTION_SCRATCH_BYTES);
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+constexpr int kMaxScratchDevices = 64;
+
+// This device's address of `scratch`, resolved on the first call per device
+// (with that device current) and kept.
+int scratch_address(const char *name, void **out) {
+  int device = -1;
+  if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= kMaxScratchDevices)
+    return fail(HIF8_ERR_LAUNCH, "%s: no usable current HIP device", name);
+  static std::mutex lock;
+  static void *address[kMaxScratchDevices] = {};
+  std::lock_guard<std::mutex> guard(lock);
+  if (!address[device]) {
+    void *ptr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || !ptr)
+      return fail(HIF8_ERR_LAUNCH, "%s: cannot resolve the scratch array on device %d: %s", name, device,
+                  hipGetErrorString(err));
+    address[device] = ptr;
+  }
+  *out = address[device];
+  return HIF8_OK;
+}
+
+}  // namespace
+}  // namespace hif8
+
+extern "C" int hif8_paged_decode_attention_noalloc(const void *query, int q_dtype, const uint8_t *key_cache,
+                                                   const uint8_t *value_cache, int64_t num_blocks,
+                                                   int64_t block_size, int64_t num_kv_heads, int64_t head_size,
+                                                   int64_t head_size_v, const void *block_table,
+                                                   int block_table_dtype, int64_t max_blocks_per_seq,
+                                                   const int32_t *seq_lens, int64_t batch, int64_t num_heads,
+                                                   int64_t max_seq_len, float scale, void *out,
+                                                   hif8_stream_t stream) {
+  static const char *kName = "hif8_paged_decode_attention_noalloc";
+  clear_error();
+  // The same split plan (hence the same results) as hif8_paged_decode_attention;
+  // the partials go to this device's scratch array, which bounds the sizes.
+  const size_t need = batch > 0 && max_seq_len > 0
+                          ? hif8_paged_decode_attention_workspace_size(batch, num_heads, num_kv_heads, head_size,
+                                                                       head_size_v, max_seq_len)
+                          : 0;
+  if (need > kScratchBytes)
+    return fail(HIF8_ERR_UNSUPPORTED,
+                "%s: these sizes need %zu bytes of split partials, more than the %zu-byte scratch array; "
+                "call hif8_paged_decode_attention with a workspace instead",
+                kName, need, kScratchBytes);
+  void *ws = nullptr;
+  if (need > 0) {
+    if (const int st = scratch_address(kName, &ws)) return st;
+  }
+  return decode_attention(kName, query, q_dtype, key_cache, value_cache, num_blocks, block_size, num_kv_heads,
+                          head_size, head_size_v, block_table, block_table_dtype, max_blocks_per_seq, seq_lens,
+                          batch, num_heads, max_seq_len, scale, out, ws, need > 0 ? kScratchBytes : 0, stream);
 }

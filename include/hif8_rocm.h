@@ -279,6 +279,28 @@ int hif8_paged_decode_attention(const void *query, int q_dtype, const uint8_t *k
                                 void *workspace, size_t workspace_bytes, hif8_stream_t stream);
 
 /*
+ * hif8_paged_decode_attention without a workspace argument, allocating nothing.
+ * No counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels, split plan and results as
+ * hif8_paged_decode_attention; the split partials live in a file-scope device
+ * array of HIF8_DECODE_ATTENTION_SCRATCH_BYTES per GPU, held until the process
+ * ends.  Sizes whose workspace (hif8_paged_decode_attention_workspace_size) exceeds
+ * that array are rejected with HIF8_ERR_UNSUPPORTED before any launch (e.g. batch 4
+ * at 16384 tokens needs 8.5 MB and fits; batch 64 at 16384 does not).  Every call
+ * on one GPU shares that GPU's array: calls that overlap on one GPU (other streams,
+ * other host threads) race and must be serialised by the caller.
+ */
+#define HIF8_DECODE_ATTENTION_SCRATCH_BYTES (16u << 20)
+int hif8_paged_decode_attention_noalloc(const void *query, int q_dtype, const uint8_t *key_cache,
+                                        const uint8_t *value_cache, int64_t num_blocks, int64_t block_size,
+                                        int64_t num_kv_heads, int64_t head_size, int64_t head_size_v,
+                                        const void *block_table, int block_table_dtype,
+                                        int64_t max_blocks_per_seq, const int32_t *seq_lens, int64_t batch,
+                                        int64_t num_heads, int64_t max_seq_len, float scale, void *out,
+                                        hif8_stream_t stream);
+
+/*
  * Bytes of workspace hif8_paged_prefill_attention needs for these sizes (0 if none);
  * the key-split plan depends only on these arguments (ACLNN GetWorkspaceSize phase,
  * csrc/extension/hif8_native.cpp:202-239).
