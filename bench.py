@@ -439,7 +439,7 @@ def measured_ceilings(torch, device) -> dict:
             "hipblaslt_bf16_gemm": gemm}
 
 
-def cpu_baseline(budget_s: float = 12.0) -> dict:
+def cpu_baseline(budget_s: float = 5.0) -> dict:
     """The numpy oracle's decode-GEMV sweep on the host (single-threaded numpy gather + BLAS)."""
     import numpy as np
 
@@ -468,6 +468,138 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
     return {"value": round(step_bytes * done / elapsed / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"{done} full decode sweep step(s) (M in {{1,4}} x 5 projections, quant + LUT-decode + fp32 "
                       f"matmul) of the numpy oracle, {elapsed:.1f} s, OMP/BLAS threads 1"}
+
+
+C1_SEED = 20261201
+C1_N, C1_K = 12288, 4096
+
+
+def c1_operands():
+    """BASELINE configs[0] on the CPU: x bf16 [1, 4096] ~ N(0, 1) with input_scale =
+    absmax / 32768; W fp32 [12288, 4096] ~ N(0, 0.02) with per-row scale = row
+    absmax / 32768, encoded by the torch-CPU port of the reference codec (bit-equal
+    to the oracle).  One seeded generator drives both, as in tests/_data.py."""
+    import torch
+
+    from oracle import torch_cpu
+
+    g = torch.Generator().manual_seed(C1_SEED)
+    x = torch.randn(1, C1_K, generator=g, dtype=torch.float32).to(torch.bfloat16)
+    s = torch.tensor([float(x.float().abs().max()) / HIF8_MAX], dtype=torch.float32)
+    w = torch.randn(C1_N, C1_K, generator=g, dtype=torch.float32) * 0.02
+    ws = (w.abs().amax(dim=1) / HIF8_MAX).to(torch.float32)
+    wq = torch_cpu.static_quant(w, ws.reshape(-1, 1))
+    return x, s, wq, ws
+
+
+def cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or "unknown"
+
+
+def c1_cpu_baseline(threads: int, runs: int = 5, warmup: int = 2) -> dict:
+    """BASELINE configs[0] timed on the host: the torch-CPU
+    restatement of the reference's CPU path - static encode of x (x / scale,
+    saturate, LUT encode), then decode-LUT weights x channel scale and one fp32
+    matmul with the decoded activation (tests/test_npu_ops.py:334-336).  Median
+    of `runs` runs after `warmup`, at `threads` torch threads and at one."""
+    import torch
+
+    from oracle import torch_cpu
+
+    x, s, wq, ws = c1_operands()
+    nbytes = gemv_bytes(1, C1_N, C1_K) + quant_bytes(1, C1_K)
+    out = {}
+    for n in (threads, 1):
+        torch.set_num_threads(n)
+        times = []
+        for i in range(warmup + runs):
+            t0 = time.perf_counter()
+            xq = torch_cpu.static_quant(x.float(), float(s[0]))
+            torch_cpu.soft_gemv(xq, s, wq, ws)
+            if i >= warmup:
+                times.append(time.perf_counter() - t0)
+        times.sort()
+        med = times[len(times) // 2]
+        out[n] = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "us_per_gemv": round(med * 1e6, 1),
+                  "cores": n}
+    torch.set_num_threads(threads)
+    return out
+
+
+def c1_gpu(torch, native, device) -> dict:
+    """BASELINE configs[0] on the GPU: static_quant + soft_linear (M = 1, N 12288,
+    K 4096 -> the GEMV kernel) on the seeded weights, 6 weight copies (302 MB)
+    rotated past the Infinity Cache; graphs of 20 launches."""
+    x, s, wq, ws = c1_operands()
+    copies = [(wq.to(device), ws.to(device)) for _ in range(6)]
+    xd, sd = x.to(device), s.to(device)
+    q, rs = native.static_quant(xd, sd)
+    per = 20
+
+    def both():
+        for i in range(per):
+            qq, rr = native.static_quant(xd, sd)
+            w, sc = copies[i % len(copies)]
+            native.soft_linear(qq, w, rr, sc, None, output_dtype=torch.bfloat16)
+
+    def gemv():
+        for i in range(per):
+            w, sc = copies[i % len(copies)]
+            native.soft_linear(q, w, rs, sc, None, output_dtype=torch.bfloat16)
+    ms_both = time_graphs(torch, [capture(torch, both)], 3) / per
+    ms_gemv = time_graphs(torch, [capture(torch, gemv)], 3) / per
+    gb = gemv_bytes(1, C1_N, C1_K)
+    qb = quant_bytes(1, C1_K)
+    res = {"workload": "BASELINE configs[0]: M=1 GEMV, N 12288, K 4096, seeded fp32 N(0,0.02) weights encoded "
+                       "with per-row absmax/32768 scales, x ~ N(0,1) bf16 with a static absmax/32768 scale",
+           "gemv_us": round(ms_gemv * 1e3, 3), "gemv_bytes": gb,
+           "gemv_GBps": round(gb / (ms_gemv * 1e-3) / 1e9, 1),
+           "gemv_frac_hbm": round(gb / (ms_gemv * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "quant_plus_gemv_us": round(ms_both * 1e3, 3),
+           "quant_plus_gemv_GBps": round((gb + qb) / (ms_both * 1e-3) / 1e9, 1)}
+    del copies
+    return res
+
+
+def prefill_attention_flops(ctx: int, q_len: int) -> int:
+    """QK^T and PV multiply-adds of one request's causal rows (row i sees ctx - q_len + i + 1 keys)."""
+    visible = sum(ctx - q_len + i + 1 for i in range(q_len))
+    return 4 * KV_HQ * KV_D * visible
+
+
+def prefill_attention_bench(kvs: "KVSetup") -> dict:
+    """Multi-token paged attention (hif8_paged_prefill_attention) over the same
+    HiF8 page pool: a whole 512-token prompt, 512- and 17-token chunks at the
+    end of a 4096-token context, batch 1 and 4; graphs of 4 calls over
+    disjoint random pages.  Work = causal QK^T + PV flops."""
+    torch = kvs.torch
+    res = {}
+    g = torch.Generator(device=kvs.device).manual_seed(6)
+    for batch, ctx, q_len in ((1, 512, 512), (1, 4096, 512), (4, 4096, 512), (1, 4096, 17), (4, 4096, 17)):
+        tables = kvs.tables(batch, ctx, max_tables=4)
+        q = torch.randn(batch * q_len, KV_HQ, KV_D, generator=g, device=kvs.device).to(torch.bfloat16)
+        lens = torch.full((batch,), ctx, dtype=torch.int32, device=kvs.device)
+        loc = torch.arange(0, batch * q_len + 1, q_len, dtype=torch.int32, device=kvs.device)
+        op = torch.ops.vllm_ascend_hif8.hif8_paged_prefill_attention
+
+        def fn(tables=tables, q=q, lens=lens, loc=loc):
+            for t in tables:
+                op(q, kvs.kc, kvs.vc, t, loc, lens, KV_D ** -0.5, q_len, ctx, True)
+        ms = time_graphs(torch, [capture(torch, fn)], 5) / len(tables)
+        fl = batch * prefill_attention_flops(ctx, q_len)
+        tf = fl / (ms * 1e-3) / 1e12
+        res[f"b{batch}_ctx{ctx}_q{q_len}"] = {"us": round(ms * 1e3, 2), "flops": fl, "TFLOPs": round(tf, 1),
+                                              "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 4)}
+        log(f"prefill attention b={batch} ctx={ctx} q={q_len}: {ms * 1e3:.1f} us, {tf:.1f} TFLOP/s")
+    return res
 
 
 def profile_pass(st: Setup, reps: int = 3) -> None:
@@ -573,14 +705,27 @@ def main() -> None:
         sys.exit(2)
 
     cpu = kv_cpu = None
+    # The host's thread share: OMP_NUM_THREADS where the pool sets it (16 per GPU
+    # on the GPU boxes), else every CPU; never more than the CPUs present.
+    nproc = os.cpu_count() or 1
+    threads = min(int(os.environ.get("OMP_NUM_THREADS") or nproc), nproc)
     if not args.no_cpu_baseline and not args.profile_pass:
         for var in ("OMP_NUM_THREADS", "OPENBLAS_NUM_THREADS", "MKL_NUM_THREADS"):
             os.environ[var] = "1"
-        log("cpu baseline (numpy oracle) ...")
-        cpu = cpu_baseline()
-        log(f"cpu baseline {cpu['value']} GB/s")
+        log("cpu baseline (numpy oracle decode sweep, 1 thread) ...")
+        sweep_cpu = cpu_baseline()
+        log(f"cpu baseline sweep {sweep_cpu['value']} GB/s")
         kv_cpu = kv_cpu_baseline()
         log(f"kv cpu baseline {kv_cpu['value']} us/token")
+        log(f"cpu baseline C1 (torch-CPU port, {threads} and 1 threads) ...")
+        c1 = c1_cpu_baseline(threads)
+        model = cpu_model()
+        cpu = {"value": c1[threads]["value"], "unit": "GB/s", "cores": threads, "kind": "port",
+               "sample": f"BASELINE configs[0] (M=1 GEMV 12288x4096 + static quant of x): torch-CPU port of the "
+                         f"reference CPU path (codec encode, decode-LUT weights x scale, fp32 matmul), median of 5 "
+                         f"after 2 warm-up runs, {c1[threads]['us_per_gemv']} us per GEMV at {threads} threads",
+               "nproc": nproc, "cpu_model": model, "single_thread": c1[1], "decode_sweep_numpy_1thread": sweep_cpu}
+        log(f"cpu baseline C1: {c1[threads]['value']} GB/s at {threads} threads, {c1[1]['value']} GB/s at 1")
 
     import torch
 
@@ -649,6 +794,9 @@ def main() -> None:
                               "us_per_launch": gdom["us"]}
     all_gemv_gbs = sum(v["bytes"] for v in gemv) / (sum(v["us"] for v in gemv) * 1e-6) / 1e9
 
+    log("configs[0] GEMV ...")
+    c1 = c1_gpu(torch, native, device)
+    log(f"c1 gemv: {c1['gemv_us']} us, {c1['gemv_GBps']} GB/s")
     log("ceilings (plain copy, hipBLASLt bf16 GEMM) ...")
     ceilings = measured_ceilings(torch, device)
     log("scaled decode and embedding ...")
@@ -658,6 +806,8 @@ def main() -> None:
     kvs = KVSetup(torch, device)
     kv_attn = kv_attention_bench(kvs, args.steps)
     kv_write = kv_write_bench(kvs)
+    log("multi-token (prefill) attention ...")
+    prefill_attn = prefill_attention_bench(kvs)
     kv_dom = kv_attn[f"b{KV_BATCH[-1]}_ctx{KV_CTX[-1]}"]
     e2e = None
     if not args.no_e2e:
@@ -710,6 +860,13 @@ def main() -> None:
             "cpu_baseline": kv_cpu,
             "kv_cache_write": kv_write,
         },
+        "prefill_attention": {
+            "workload": "multi-token paged attention over the same HiF8 pages (Hq 16, Hkv 4, D 256, page 128): "
+                        "q_len new rows at the end of ctx cached tokens, right-aligned causal mask; flops = causal "
+                        "QK^T + PV",
+            "configs": prefill_attn,
+        },
+        "c1_gemv": c1,
         "decode_sweep_fused_GBps": round(fused_gbs, 1),
         "decode_sweep_single_row_fusion": {"GBps": round(single_gbs, 1), "us_per_step": round(single_ms * 1e3, 1),
                                            "routing": "scheme apply with HIF8_STATIC_FUSED_SINGLE_ROW=1: M=1 "

@@ -68,7 +68,7 @@ struct PrefillParams {
   float *part_ml;                 // [items, num_splits, kPRows, 2]
   int64_t bt_stride;
   int64_t num_blocks;
-  int block_size, hkv, hq, group, log2_group, d, dv;
+  int block_size, log2_block_size, hkv, hq, group, log2_group, d, dv;  // log2_block_size -1: not a power of two
   int tokens_per_tile, q_tiles, num_splits, split_tiles, batch, max_len, causal;
   int total_q;                    // rows of query / out; rows at or past it are never touched
   float scale_log2;               // softmax scale * log2(e)
@@ -152,27 +152,43 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
   const size_t part = (item * p.num_splits + split) * kPRows + r;
   const size_t out_row = (size_t(q_begin + tok) * p.hq + qhead) * kD;
 
-  // Raw rows of a tile: thread (kg, dc) loads chunk dc of keys kg * kKPT + j.
-  const int dc = tid % kChunks, kg = tid / kChunks;
+  // Raw rows of a tile: thread (kq, dc) loads 16-byte chunk dc of the kKPT
+  // consecutive keys kq * kKPT + j (all in one cache block: block_size %
+  // kKPT == 0).  Consecutive threads take consecutive key groups, so the
+  // transposed V stores of one instruction fill whole V^T rows.
+  constexpr int kGroups = kKT / kKPT;
+  const int kq = tid % kGroups, dc = tid / kGroups;
   const BtT *bt = static_cast<const BtT *>(p.block_table) + size_t(b) * p.bt_stride;
+  const int64_t rec = int64_t(p.hkv) * (kD + 4);
+  // Block id of this thread's keys in the tile starting at k0 (-1: none).
+  auto block_of = [&](int k0) -> int64_t {
+    const int key = k0 + kq * kKPT;
+    const int safe = min(key, max(p.max_len - 1, 0));  // within the table: max_len <= its capacity
+    const int idx = p.log2_block_size >= 0 ? safe >> p.log2_block_size : safe / p.block_size;
+    const int64_t blk = int64_t(bt[idx]);
+    return key < s_k1 ? blk : int64_t(-1);
+  };
+  const int64_t blk_first = block_of(s_k0);  // its load needs no request length
+  // Loads only: the validity of each key travels in `ok` and is applied when
+  // the tile is decoded, so nothing here waits for the loads.
   u32x4 kraw[kKPT], vraw[kKPT];
   float kscl[kKPT], vscl[kKPT];
-  auto issue = [&](int k0) {
+  uint32_t ok = 0;
+  auto issue = [&](int k0, int64_t blk) {
+    const int key0 = k0 + kq * kKPT;
+    const bool blk_ok = blk >= 0 && blk < p.num_blocks;
+    const int in_blk = p.log2_block_size >= 0 ? key0 & (p.block_size - 1) : key0 % p.block_size;
+    const int64_t row0 = blk_ok ? (blk * p.block_size + in_blk) * rec + int64_t(h) * (kD + 4) : 0;
+    ok = 0;
 #pragma unroll
     for (int j = 0; j < kKPT; ++j) {
-      const int key = k0 + kg * kKPT + j;
-      int64_t blk = -1;
-      if (key < s_k1) blk = int64_t(bt[key / p.block_size]);
-      if (blk >= 0 && blk < p.num_blocks) {
-        const int64_t off = ((blk * p.block_size + key % p.block_size) * p.hkv + h) * int64_t(kD + 4);
-        kraw[j] = *reinterpret_cast<const u32x4_a4 *>(p.key_cache + off + 16 * dc);
-        vraw[j] = *reinterpret_cast<const u32x4_a4 *>(p.value_cache + off + 16 * dc);
-        kscl[j] = *reinterpret_cast<const float *>(p.key_cache + off + kD);
-        vscl[j] = *reinterpret_cast<const float *>(p.value_cache + off + kD);
-      } else {
-        kraw[j] = vraw[j] = u32x4{0, 0, 0, 0};
-        kscl[j] = vscl[j] = 0.f;  // a zero scale marks the key absent
-      }
+      const bool kok = blk_ok && key0 + j < s_k1;
+      const int64_t off = kok ? row0 + j * rec : 0;  // absent keys read the cache's first row, then drop it
+      kraw[j] = *reinterpret_cast<const u32x4_a4 *>(p.key_cache + off + 16 * dc);
+      vraw[j] = *reinterpret_cast<const u32x4_a4 *>(p.value_cache + off + 16 * dc);
+      kscl[j] = *reinterpret_cast<const float *>(p.key_cache + off + kD);
+      vscl[j] = *reinterpret_cast<const float *>(p.value_cache + off + kD);
+      ok |= uint32_t(kok) << j;
     }
   };
 
@@ -184,9 +200,13 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
     for (int i = 0; i < kQSteps; ++i)
       qf[i] = row_ok ? *reinterpret_cast<const u32x4 *>(q + 32 * i) : u32x4{0, 0, 0, 0};
   }
-  if (ntiles > 0) issue(s_k0);
-  for (int i = tid; i < 256; i += kPThreads) dec[i] = __uint_as_float(kDeviceTables.decode_f32[i]);
-  __syncthreads();
+  int64_t blk_next = -1;  // block id for the tile after the one in flight
+  if (ntiles > 0) {
+    issue(s_k0, blk_first);
+    if (ntiles > 1) blk_next = block_of(s_k0 + kKT);
+  }
+  for (int i = tid; i < 256; i += kPThreads) dec[i] = __uint_as_float(decode_bits(uint32_t(i)));
+  lds_barrier();
 
   f32x4_t oacc[kDB];
 #pragma unroll
@@ -195,32 +215,51 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
 
   for (int it = 0; it < ntiles; ++it) {
     const int k0 = s_k0 + it * kKT;
-    // Decode this tile's raw rows into LDS.
+    // Decode this tile's raw rows into LDS; absent keys become zeros and a
+    // -inf logit bias.
 #pragma unroll
     for (int j = 0; j < kKPT; ++j) {
-      const int kt = kg * kKPT + j;  // key within the tile
-      const uint32_t kw[4] = {kraw[j][0], kraw[j][1], kraw[j][2], kraw[j][3]};
+      const int kt = kq * kKPT + j;  // key within the tile
+      const bool kok = (ok >> j) & 1u;
+      const float ksc = kok ? kscl[j] : 0.f;
+      uint32_t kw[4];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) kw[w] = kok ? kraw[j][w] : 0u;
       uint32_t kp[8];
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
-        kp[2 * w] = pack2<kBf16>(dec[kw[w] & 0xFFu] * kscl[j], dec[(kw[w] >> 8) & 0xFFu] * kscl[j]);
-        kp[2 * w + 1] = pack2<kBf16>(dec[(kw[w] >> 16) & 0xFFu] * kscl[j], dec[kw[w] >> 24] * kscl[j]);
+        kp[2 * w] = pack2<kBf16>(dec[kw[w] & 0xFFu] * ksc, dec[(kw[w] >> 8) & 0xFFu] * ksc);
+        kp[2 * w + 1] = pack2<kBf16>(dec[(kw[w] >> 16) & 0xFFu] * ksc, dec[kw[w] >> 24] * ksc);
       }
-      const int sw = kt & kKSwz;
+      const int sw = (kt ^ (kt >> 4)) & kKSwz;
       uint16_t *krow = ks + kt * kD;
       *reinterpret_cast<u32x4 *>(krow + 8 * ((2 * dc) ^ sw)) = u32x4{kp[0], kp[1], kp[2], kp[3]};
       *reinterpret_cast<u32x4 *>(krow + 8 * ((2 * dc + 1) ^ sw)) = u32x4{kp[4], kp[5], kp[6], kp[7]};
-      if (dc == 0) kbias[kt] = kscl[j] != 0.f ? 0.f : -__builtin_inff();
+      if (dc == 0) kbias[kt] = kok ? 0.f : -__builtin_inff();
     }
-    // V transposed: dim 16 dc + i, kKPT consecutive keys at consecutive positions.
+    // V transposed: dim 16 dc + i', kKPT consecutive keys at consecutive
+    // positions.  Odd chunks walk their dims in the order i ^ 1, so the four
+    // rows one store instruction writes alternate between the two bank halves.
     {
-      const int pos = vt_pos(kg * kKPT);
+      const int pos = vt_pos(kq * kKPT);
+      float vsc[kKPT];
+      uint32_t vw[kKPT][4];
+#pragma unroll
+      for (int j = 0; j < kKPT; ++j) {
+        const bool vok = (ok >> j) & 1u;
+        vsc[j] = vok ? vscl[j] : 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) vw[j][w] = vok ? vraw[j][w] : 0u;
+      }
+      const int flip = dc & 1;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int dim = 16 * dc + i;
+        const int ii = i ^ flip;          // same 4-byte word as i
+        const int dim = 16 * dc + ii;
+        const int sh = 8 * (ii & 3);
         float v[kKPT];
 #pragma unroll
-        for (int j = 0; j < kKPT; ++j) v[j] = dec[(vraw[j][i >> 2] >> (8 * (i & 3))) & 0xFFu] * vscl[j];
+        for (int j = 0; j < kKPT; ++j) v[j] = dec[(vw[j][i >> 2] >> sh) & 0xFFu] * vsc[j];
         const int gran = (pos >> 3) ^ (dim & 7);
         uint16_t *dst = vt + dim * kKT + 8 * gran + (pos & 7);
         if constexpr (kKPT == 4) {
@@ -232,8 +271,11 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
         }
       }
     }
-    __syncthreads();
-    if (it + 1 < ntiles) issue(k0 + kKT);  // in flight during this tile's math
+    lds_barrier();
+    if (it + 1 < ntiles) {  // in flight during this tile's math
+      issue(k0 + kKT, blk_next);
+      if (it + 2 < ntiles) blk_next = block_of(k0 + 2 * kKT);
+    }
 
     // S^T = K Q^T: four 16-key blocks.
     f32x4_t sacc[4];
@@ -241,10 +283,11 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
     for (int kb = 0; kb < 4; ++kb) {
       sacc[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       const int key = 16 * kb + n;
+      const int sw = (key ^ (key >> 4)) & kKSwz;
       const uint16_t *krow = ks + key * kD;
 #pragma unroll
       for (int i = 0; i < kQSteps; ++i) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(krow + 8 * ((4 * i + g) ^ (key & kKSwz)));
+        const u32x4 a = *reinterpret_cast<const u32x4 *>(krow + 8 * ((4 * i + g) ^ sw));
         sacc[kb] = mfma16<kBf16>(a, qf[i], sacc[kb]);
       }
     }
@@ -299,7 +342,7 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
         oacc[db] = mfma16<kBf16>(a, pf[s], oacc[db]);
       }
     }
-    __syncthreads();  // the tile's LDS is rewritten by the next iteration
+    lds_barrier();  // the tile's LDS is rewritten by the next iteration
   }
 
   float lt = l + __shfl_xor(l, 16, kWave);
@@ -325,42 +368,60 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
   }
 }
 
-// Merges the key splits of each (query tile, KV head) row:
+// Merges the key splits of one (query tile, KV head) row:
 //   M = max_s m_s, w_s = 2^(m_s - M), out = sum_s w_s O_s / sum_s w_s l_s.
-// Block = 4 rows x 64 threads, each thread 4 dims; splits with weight 0 (no
-// key) are skipped, so their (unwritten) partial outputs are never read.
+// One workgroup per row: wavefront 0 reads every split's (m, l) at once (one
+// split per lane) and leaves the weights in LDS; then the four wavefronts take
+// every fourth split, each lane four output dims, and their sums meet in LDS.
+// Splits with weight 0 (no key) are skipped, so their (unwritten) partial
+// outputs are never read.
+constexpr int kMaxCombineSplits = 64;
+
 template <bool kBf16>
 __global__ __launch_bounds__(kPThreads) void prefill_combine_kernel(const PrefillParams p) {
+  __shared__ float wsh[kMaxCombineSplits];
+  __shared__ f32x4_t red[4][64];
+  __shared__ float total_sh;
   const int item = blockIdx.x;
-  const int r = int(blockIdx.y) * 4 + int(threadIdx.x >> 6);
-  const int c = threadIdx.x & 63;
+  const int r = blockIdx.y;
   const int h = item % p.hkv;
   const int qt = (item / p.hkv) % p.q_tiles;
   const int b = item / (p.hkv * p.q_tiles);
   const int q_begin = max(p.query_start_loc[b], 0);
   const int ql = min(p.query_start_loc[b + 1], p.total_q) - q_begin;
   const int tok = qt * p.tokens_per_tile + (r >> p.log2_group);
-  if (tok >= ql || 4 * c >= p.dv) return;
-  const int qhead = h * p.group + (r & (p.group - 1));
+  if (tok >= ql) return;  // uniform: a row past the request
+  const int tid = threadIdx.x, lane = tid & 63, grp = tid >> 6;
   const size_t base = size_t(item) * p.num_splits * kPRows + r;  // part index of split 0
-  float mx = -__builtin_inff();
-  for (int s = 0; s < p.num_splits; ++s) mx = fmaxf(mx, p.part_ml[2 * (base + size_t(s) * kPRows)]);
+  if (grp == 0) {
+    const bool have = lane < p.num_splits;
+    const size_t pi = base + size_t(have ? lane : 0) * kPRows;
+    const float ms = have ? p.part_ml[2 * pi] : -__builtin_inff();
+    const float ls = have ? p.part_ml[2 * pi + 1] : 0.f;
+    const float mx = wave_max(ms);
+    const float w = ms == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
+    if (have) wsh[lane] = w;
+    const float total = wave_sum(w * ls);
+    if (lane == 0) total_sh = total;
+  }
+  __syncthreads();
   f32x4_t acc{0.f, 0.f, 0.f, 0.f};
-  float total = 0.f;
-  if (mx != -__builtin_inff()) {
-    for (int s = 0; s < p.num_splits; ++s) {
-      const size_t pi = base + size_t(s) * kPRows;
-      const float ms = p.part_ml[2 * pi];
-      if (ms == -__builtin_inff()) continue;
-      const float w = __builtin_amdgcn_exp2f(ms - mx);
-      total += w * p.part_ml[2 * pi + 1];
-      const f32x4_t o = *reinterpret_cast<const f32x4_t *>(p.part_o + pi * p.dv + 4 * c);
-      acc += w * o;
+  if (4 * lane < p.dv) {
+#pragma unroll 4
+    for (int s = grp; s < p.num_splits; s += 4) {
+      const float w = wsh[s];
+      if (w != 0.f) acc += w * *reinterpret_cast<const f32x4_t *>(p.part_o + (base + size_t(s) * kPRows) * p.dv + 4 * lane);
     }
   }
-  const float inv = total > 0.f ? 1.f / total : 0.f;
-  uint16_t *o = static_cast<uint16_t *>(p.out) + (size_t(q_begin + tok) * p.hq + qhead) * p.dv + 4 * c;
-  *reinterpret_cast<u32x2 *>(o) = u32x2{pack2<kBf16>(acc[0] * inv, acc[1] * inv), pack2<kBf16>(acc[2] * inv, acc[3] * inv)};
+  red[grp][lane] = acc;
+  __syncthreads();
+  if (grp == 0 && 4 * lane < p.dv) {
+    const f32x4_t y = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+    const float inv = total_sh > 0.f ? 1.f / total_sh : 0.f;
+    const int qhead = h * p.group + (r & (p.group - 1));
+    uint16_t *o = static_cast<uint16_t *>(p.out) + (size_t(q_begin + tok) * p.hq + qhead) * p.dv + 4 * lane;
+    *reinterpret_cast<u32x2 *>(o) = u32x2{pack2<kBf16>(y[0] * inv, y[1] * inv), pack2<kBf16>(y[2] * inv, y[3] * inv)};
+  }
 }
 
 // Any head sizes, group or block size: one wavefront per (query row, query
@@ -447,8 +508,9 @@ int log2_exact(int64_t v) {
   return (int64_t(1) << l) == v ? l : -1;
 }
 
-bool prefill_mfma_shape(int64_t d, int64_t dv, int64_t group) {
-  return (d == 64 || d == 128 || d == 256) && dv == d && group >= 1 && group <= 16 && log2_exact(group) >= 0;
+bool prefill_mfma_shape(int64_t d, int64_t dv, int64_t group, int64_t block_size) {
+  return (d == 64 || d == 128 || d == 256) && dv == d && group >= 1 && group <= 16 && log2_exact(group) >= 0 &&
+         block_size % 4 == 0;
 }
 
 struct PrefillPlan {
@@ -469,6 +531,7 @@ PrefillPlan plan_prefill(int64_t batch, int64_t hkv, int64_t group, int64_t max_
   if (splits < 1) splits = 1;
   int64_t per = (kv_tiles + splits - 1) / splits;
   if (per < kMinSplitTiles) per = std::min<int64_t>(kMinSplitTiles, kv_tiles);
+  if ((kv_tiles + per - 1) / per > kMaxCombineSplits) per = (kv_tiles + kMaxCombineSplits - 1) / kMaxCombineSplits;
   pl.split_tiles = int(per);
   pl.num_splits = int((kv_tiles + per - 1) / per);
   return pl;
@@ -484,7 +547,7 @@ int launch_prefill_mfma(const PrefillParams &p, hipStream_t stream) {
   const unsigned blocks = unsigned(int64_t(p.q_tiles) * p.batch * p.hkv * p.num_splits);
   paged_prefill_attention_kernel<kD, kBf16, BtT><<<blocks, kPThreads, smem, stream>>>(p);
   if (p.num_splits > 1)
-    prefill_combine_kernel<kBf16><<<dim3(unsigned(int64_t(p.batch) * p.q_tiles * p.hkv), kPRows / 4), kPThreads, 0,
+    prefill_combine_kernel<kBf16><<<dim3(unsigned(int64_t(p.batch) * p.q_tiles * p.hkv), kPRows), kPThreads, 0,
                                     stream>>>(p);
   return HIF8_OK;
 }
@@ -514,7 +577,7 @@ extern "C" size_t hif8_paged_prefill_attention_workspace_size(int64_t batch, int
       max_query_len <= 0 || max_seq_len <= 0 || num_heads % num_kv_heads)
     return 0;
   const int64_t group = num_heads / num_kv_heads;
-  if (!prefill_mfma_shape(head_size, head_size_v, group)) return 0;  // the simple kernel needs none
+  if (!prefill_mfma_shape(head_size, head_size_v, group, 4)) return 0;  // the simple kernel needs none
   const PrefillPlan pl = plan_prefill(batch, num_kv_heads, group, max_query_len, max_seq_len);
   if (pl.num_splits <= 1) return 0;
   const size_t parts = size_t(batch) * pl.q_tiles * num_kv_heads * pl.num_splits * kPRows;
@@ -573,6 +636,7 @@ extern "C" int hif8_paged_prefill_attention(const void *query, int q_dtype, cons
   p.bt_stride = max_blocks_per_seq;
   p.num_blocks = num_blocks;
   p.block_size = int(block_size);
+  p.log2_block_size = log2_exact(block_size);
   p.hkv = int(num_kv_heads);
   p.hq = int(num_heads);
   p.group = int(num_heads / num_kv_heads);
@@ -583,7 +647,8 @@ extern "C" int hif8_paged_prefill_attention(const void *query, int q_dtype, cons
   p.causal = causal ? 1 : 0;
   p.total_q = int(total_query_tokens);
   p.scale_log2 = scale * 1.4426950408889634f;
-  const bool mfma = prefill_mfma_shape(head_size, head_size_v, p.group) && aligned(query, 16) && aligned(out, 16);
+  const bool mfma = prefill_mfma_shape(head_size, head_size_v, p.group, block_size) && aligned(query, 16) &&
+                    aligned(out, 16);
   if (mfma) {
     const PrefillPlan pl = plan_prefill(batch, num_kv_heads, p.group, max_query_len, max_seq_len);
     p.log2_group = log2_exact(p.group);

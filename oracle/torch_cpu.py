@@ -34,9 +34,13 @@ _MAG = torch.from_numpy(o.LUT4096.astype("int32"))
 _DECODE = torch.from_numpy(o.DECODE_F32.copy())
 
 
-def static_quant(x: torch.Tensor, scale: float) -> torch.Tensor:
-    """Saturating static encode of ``x / scale`` (float32 division) -> uint8 codes."""
-    q = x.to(torch.float32) / torch.tensor(scale, dtype=torch.float32)
+def static_quant(x: torch.Tensor, scale) -> torch.Tensor:
+    """Saturating static encode of ``x / scale`` (float32 division) -> uint8 codes.
+
+    ``scale`` is one float or a float32 tensor broadcast against ``x`` (e.g.
+    ``[rows, 1]`` for per-row weight scales)."""
+    s = scale.to(torch.float32) if isinstance(scale, torch.Tensor) else torch.tensor(scale, dtype=torch.float32)
+    q = x.to(torch.float32) / s
     finite = torch.isfinite(q)
     q = torch.where(finite, q.clamp(-o.MAX_FINITE, o.MAX_FINITE), q)
     bits = q.view(torch.int32)

@@ -38,3 +38,12 @@ def test_soft_gemv_matches_linear_u8_u8():
                               torch.from_numpy(sw)).numpy()
     want = o.linear_u8_u8(a, sa, w, sw)
     assert np.allclose(got, want, rtol=1e-5, atol=1e-6)
+
+
+def test_static_quant_with_per_row_scales():
+    rng = np.random.default_rng(13)
+    w = (rng.standard_normal((64, 300)) * 0.02).astype(np.float32)
+    ws = (np.abs(w).max(axis=1) / 32768.0).astype(np.float32)
+    got = torch_cpu.static_quant(torch.from_numpy(w), torch.from_numpy(ws).reshape(-1, 1)).numpy()
+    want, _ = o.static_quant_rows(w, ws)
+    assert np.array_equal(got, want)
