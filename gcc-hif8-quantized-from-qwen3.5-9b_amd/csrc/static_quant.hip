@@ -21,24 +21,55 @@ constexpr int kThreads = 256;
 // (M=1, K=4096: 10.2 vs 3.4 us) because of its data-dependent branches.
 
 // One thread = 16 consecutive elements of one row (requires k % 16 == 0 and
-// 16-byte aligned x / data).  Grid-stride over the flattened chunks.
+// 16-byte aligned x / data); grid-stride over the chunks with the next chunk
+// loaded while the current one is encoded.  The 8 KiB table is staged once
+// per workgroup (up to 16 per CU: more waves in flight measured faster than
+// fewer workgroups walking more chunks): its loads go first, then the first
+// chunk's, so the table's LDS stores wait only for the table (loads return in
+// order) and the barrier, which waits for LDS traffic only, leaves the chunk
+// in flight.  One encode in the loop body keeps the kernel small: a launch
+// this short pays for every instruction it fetches cold.
 template <bool kBf16>
 __global__ __launch_bounds__(kThreads) void static_quant_vec16(
     const uint16_t *__restrict__ x, const float *__restrict__ fixed, uint8_t *__restrict__ out,
     float *__restrict__ row_scale, uint32_t n_chunks, uint32_t k_chunks, uint32_t scale_count) {
   __shared__ __attribute__((aligned(16))) uint8_t lut[8192];
-  stage_static_encode_table(lut, threadIdx.x, kThreads);
-  __syncthreads();
-  const uint32_t stride = gridDim.x * kThreads;
-  for (uint32_t c = blockIdx.x * kThreads + threadIdx.x; c < n_chunks; c += stride) {
-    const uint32_t row = c / k_chunks;
-    const float s = fixed[row % scale_count];
-    if (c == row * k_chunks) row_scale[row] = s;
+  static_assert(8192 == 2 * 16 * kThreads, "two 16-byte table words per thread");
+  const uint4 *tsrc = reinterpret_cast<const uint4 *>(kDeviceTables.static_encode);
+  const uint4 t0 = tsrc[threadIdx.x], t1 = tsrc[threadIdx.x + kThreads];
+  const uint64_t stride = uint64_t(gridDim.x) * kThreads;
+  uint64_t c = uint64_t(blockIdx.x) * kThreads + threadIdx.x;  // 64-bit: no wrap near 2^32 chunks
+  // A chunk's data and its row's scale are loaded together, one chunk ahead.
+  uint4 a0{}, a1{};
+  float sc = 0.f;
+  // Unconditional loads (a chunk past the end reloads the last one, unused),
+  // so the compiler can count them and wait for exactly the ones it needs.
+  auto fetch = [&](uint64_t ch) {
+    const uint64_t safe = ch < n_chunks ? ch : n_chunks - 1;
+    const uint4 *src = reinterpret_cast<const uint4 *>(x + safe * 16);
+    a0 = src[0];
+    a1 = src[1];
+    sc = fixed[scale_count == 1 ? 0u : (uint32_t(safe) / k_chunks) % scale_count];
+  };
+  fetch(c);
+  reinterpret_cast<uint4 *>(lut)[threadIdx.x] = t0;
+  reinterpret_cast<uint4 *>(lut)[threadIdx.x + kThreads] = t1;
+  lds_barrier();
+  for (; c < n_chunks; c += stride) {
+    const uint32_t v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+    const float s = sc;
+    fetch(c + stride);
+    const uint32_t row = uint32_t(c) / k_chunks;
+    if (uint32_t(c) == row * k_chunks) row_scale[row] = s;
     float xf[16];
-    load16<kBf16>(x + size_t(c) * 16, xf);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      xf[2 * i] = lo_to_float<kBf16>(v[i]);
+      xf[2 * i + 1] = hi_to_float<kBf16>(v[i]);
+    }
     uint32_t w[4];
     static_encode16(xf, s, lut, w);
-    *reinterpret_cast<uint4 *>(out + size_t(c) * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    *reinterpret_cast<uint4 *>(out + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
   }
 }
 
@@ -199,7 +230,7 @@ extern "C" int hif8_static_quant(const void *x, int x_dtype, int64_t rows, int64
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const uint16_t *xs = static_cast<const uint16_t *>(x);
   if (k % 16 == 0 && aligned(x, 16) && aligned(data, 16) && n_chunks <= 0xFFFFFFFFull) {
-    const dim3 grid(grid_for(n_chunks, 8)), block(kThreads);
+    const dim3 grid(grid_for(n_chunks, 16)), block(kThreads);
     const uint32_t nc = uint32_t(n_chunks), kc = uint32_t(k / 16), sc = uint32_t(scale_count);
     if (bf16) static_quant_vec16<true><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
     else static_quant_vec16<false><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
