@@ -626,6 +626,30 @@ def profile_pass(st: Setup, reps: int = 3) -> None:
                 w, ws = st.weights[i % N_COPIES][name]
                 native.soft_linear(q, w, rs, ws, None, output_dtype=torch.bfloat16)
     torch.cuda.synchronize()
+    log("profile pass: linear done")
+    # KV path: decode attention (b4 ctx16384, b1 ctx512), the fused cache write
+    # of 4096 tokens, multi-token attention (b1, 512 rows over 4096 tokens);
+    # each `reps` times over distinct random pages.
+    kvs = KVSetup(torch, st.device)
+    for batch, ctx in ((4, 16384), (1, 512)):
+        lens = torch.full((batch,), ctx, dtype=torch.int32, device=st.device)
+        for t in kvs.tables(batch, ctx, max_tables=reps):
+            torch.ops.vllm_ascend_hif8.hif8_paged_decode_attention(kvs.q[batch], kvs.kc, kvs.vc, t, lens,
+                                                                   KV_D ** -0.5, ctx)
+    torch.cuda.synchronize()
+    g = torch.Generator(device=st.device).manual_seed(3)
+    k = torch.randn(4096, KV_HKV, KV_D, generator=g, device=st.device).to(torch.bfloat16)
+    v = torch.randn(4096, KV_HKV, KV_D, generator=g, device=st.device).to(torch.bfloat16)
+    perm = torch.randperm(kvs.num_blocks * KV_BS, generator=kvs.perm_gen)[:4096].to(st.device)
+    for _ in range(reps):
+        torch.ops.vllm_ascend_hif8.hif8_kv_cache_write(k, v, kvs.kc, kvs.vc, perm, kvs.ks, kvs.vs, None)
+    q = torch.randn(512, KV_HQ, KV_D, generator=g, device=st.device).to(torch.bfloat16)
+    loc = torch.tensor([0, 512], dtype=torch.int32, device=st.device)
+    lens = torch.tensor([4096], dtype=torch.int32, device=st.device)
+    for t in kvs.tables(1, 4096, max_tables=reps):
+        torch.ops.vllm_ascend_hif8.hif8_paged_prefill_attention(q, kvs.kc, kvs.vc, t, loc, lens, KV_D ** -0.5,
+                                                                512, 4096, True)
+    torch.cuda.synchronize()
     log("profile pass done")
 
 
