@@ -222,7 +222,8 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
     for (int r = 0; r < kR; ++r) {
       // Rows past n re-read row n-1; their sums are never stored.
       const int row = min(n0 + r, n - 1);
-      wq[r] = reinterpret_cast<const u32x4 *>(weight + size_t(row) * k)[c];
+      // Weights are read once per call: non-temporal (streaming) loads.
+      wq[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(weight + size_t(row) * k) + c);
     }
   };
   // The decode table is computed, one entry per thread, rather than copied
