@@ -288,6 +288,25 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
   auto out = at::empty({activation.size(0), weight.size(0)}, activation.options().dtype(output_dtype));
   const void *bias_ptr = bias.has_value() ? bias->data_ptr() : nullptr;
   const int bias_dtype = bias.has_value() ? DtypeCode(bias->scalar_type()) : HIF8_DTYPE_NONE;
+  const int64_t m = activation.size(0), n = weight.size(0), k = activation.size(1);
+  if (m >= 2 || k > 4096) {
+    // Every block of the single-launch kernel encodes the whole activation,
+    // which costs more than a separate quant launch once there are several
+    // rows or a long K (measured on MI355X); the two launches give the same
+    // codes and the same GEMV, hence equal outputs.
+    auto codes = at::empty({m, k}, activation.options().dtype(at::ScalarType::Byte));
+    auto row_scale = at::empty({m}, activation.options().dtype(at::ScalarType::Float));
+    const auto stream = CurrentStream(device);
+    CheckStatus(hif8_static_quant(activation.data_ptr(), DtypeCode(activation.scalar_type()), m, k,
+                                  fixed_scale.data_ptr<float>(), 1, codes.data_ptr<uint8_t>(),
+                                  row_scale.data_ptr<float>(), stream),
+                "soft_hif8_static_fused_gemm");
+    CheckStatus(soft_hif8_gemm(codes.data_ptr<uint8_t>(), weight.data_ptr<uint8_t>(), row_scale.data_ptr<float>(),
+                               channel_scale.data_ptr<float>(), bias_ptr, bias_dtype, out.data_ptr(),
+                               DtypeCode(output_dtype), m, n, k, stream),
+                "soft_hif8_static_fused_gemm");
+    return out;
+  }
   CheckStatus(soft_hif8_static_fused_gemm(activation.data_ptr(), DtypeCode(activation.scalar_type()),
                                           weight.data_ptr<uint8_t>(), fixed_scale.data_ptr<float>(),
                                           channel_scale.data_ptr<float>(), bias_ptr, bias_dtype, out.data_ptr(),
