@@ -8,24 +8,21 @@
 //
 // A block computes a BM x BN tile in K steps of 64.  Each step's tiles sit in
 // LDS as bf16 (double buffered, 16-byte granules XOR-swizzled by row so that
-// the MFMA fragment reads are bank-conflict free):
-//   * W: each thread loads 16-byte code chunks into VGPRs one step ahead,
-//     decodes them with the 256-entry bf16 table in LDS and stores the bf16
-//     granules;
-//   * A, with a workspace: the activation codes are first decoded once to a
-//     bf16 matrix (decode_rows_kernel), and every step copies its A tile
-//     straight into LDS with global_load_lds_dwordx4 (no registers, no
-//     table lookups).  Without a workspace A is decoded like W.  Decoding A
-//     once instead of once per column tile halves the in-kernel table
-//     lookups, whose LDS latency bounds the decode phase of a step;
-//   * W, with a workspace and M >= 2048: decoded once per call the same way
-//     (the in-kernel decode would repeat it for every 256-row tile of M) and
-//     copied by DMA like A, so the K loop is MFMA, fragment reads and copies.
-//     A caller that keeps the weight decoded (soft_hif8_gemm_decoded_weight)
-//     gets that kernel at every M without the per-call weight decode.
-// 256 x 256 blocks run eight wavefronts in a 2 x 4 arrangement (128 x 64
-// each, two waves per SIMD) whose two wave rows alternate between MFMA and
-// decode half a step apart; 128 x 128 blocks run four in a 2 x 2 arrangement.
+// the MFMA fragment reads are bank-conflict free).  Two kernels:
+//   * gemm_kernel, W decoded in the kernel: each thread loads 16-byte W code
+//     chunks into VGPRs one step ahead, decodes them with the 256-entry bf16
+//     table in LDS and stores the bf16 granules.  With a workspace the
+//     activation codes are first decoded once to a bf16 matrix
+//     (decode_rows_kernel) and every step copies its A tile straight into
+//     LDS with global_load_lds_dwordx4; without one A is decoded like W.
+//     256 x 256 blocks run eight wavefronts in a 2 x 4 arrangement (128 x 64
+//     each, two waves per SIMD) whose two wave rows alternate between MFMA
+//     and decode half a step apart; 128 x 128 blocks run four in 2 x 2.
+//   * gemm_dma_kernel, both operands bf16 in HBM: the weight decoded once per
+//     call (M >= 2048, where the in-kernel decode would repeat per 256-row
+//     tile of M) or kept decoded by the caller (soft_hif8_gemm_decoded_weight).
+//     Every step copies both tiles into LDS by DMA and the K loop is MFMAs
+//     and fragment reads in a hand-pinned order (4 x 2 waves of 64 x 128).
 // The epilogue scales and rounds each wave's outputs into LDS and stores
 // them as 16-byte row chunks (full 128-byte row segments per 8 lanes).
 //
@@ -36,6 +33,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "linear.h"
 
@@ -43,6 +41,7 @@ namespace hif8 {
 namespace {
 
 constexpr int kBK = 64;  // bytes (= bf16 elements) of K per stage
+constexpr int kMaxDmaK = 1 << 23;  // gemm_dma_kernel: a tile's rows in 32-bit byte offsets
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -237,7 +236,7 @@ __device__ __forceinline__ void store_tile_lds(const f32x4_t (&acc)[kTM][kTN], u
 // a lookup address is then the code shifted left by one, a single SDWA op.
 //   kAPre      A is a bf16 matrix (decoded beforehand) copied into LDS by DMA
 //   kPingPong  the two wave rows alternate MFMA and decode half a step apart
-template <int kBM, int kBN, int kWavesM, int kWavesN, bool kAPre, bool kBPre, bool kPingPong>
+template <int kBM, int kBN, int kWavesM, int kWavesN, bool kAPre, bool kPingPong>
 __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
     const void *__restrict__ A, const float *__restrict__ ts, const void *__restrict__ W,
     const float *__restrict__ cs, const void *__restrict__ bias, int bias_dtype,
@@ -246,22 +245,19 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
   constexpr int kT = kWave * kWavesM * kWavesN;         // threads per block
   constexpr int kWaves = kWavesM * kWavesN;
   static_assert(!kPingPong || kWavesM == 2, "ping-pong pairs the two wave rows");
-  static_assert(!kBPre || (kAPre && !kPingPong), "W by DMA needs A by DMA and no decode phase");
   // Threads sharing one decode: all of them, or (ping-pong) one wave row,
   // which decodes its half of the A rows and its half of the W rows.
   constexpr int kDecT = kPingPong ? kT / 2 : kT;
   constexpr int kDecA = kPingPong ? kBM / 2 : kBM, kDecB = kPingPong ? kBN / 2 : kBN;
   constexpr int kChunksA = kAPre ? 0 : kDecA * (kBK / 16) / kDecT;  // 16-byte code chunks per thread
-  constexpr int kChunksB = kBPre ? 0 : kDecB * (kBK / 16) / kDecT;
+  constexpr int kChunksB = kDecB * (kBK / 16) / kDecT;
   constexpr int kRowsPass = kDecT / 4;                   // tile rows covered per chunk pass
   constexpr int kWM = kBM / kWavesM, kWN = kBN / kWavesN;  // wave sub-tile
   constexpr int kTM = kWM / 16, kTN = kWN / 16;          // 16x16 MFMA tiles per wave
   constexpr uint32_t kStageA = kBM * kBK * 2, kStageB = kBN * kBK * 2;
   // Tiles by DMA: 1 KiB (8 rows) per instruction, spread over the waves.
   constexpr int kDmaPerWave = kBM * kBK * 2 / 1024 / kWaves;
-  constexpr int kDmaPerWaveB = kBN * kBK * 2 / 1024 / kWaves;
   static_assert(!kAPre || kDmaPerWave * kWaves * 1024 == int(kStageA), "A tile DMA split");
-  static_assert(!kBPre || kDmaPerWaveB * kWaves * 1024 == int(kStageB), "W tile DMA split");
 
   __shared__ __attribute__((aligned(16))) uint16_t lut[256];
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
@@ -313,28 +309,12 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
       pdma[j] = static_cast<const uint8_t *>(A) + (size_t(min(m0 + r, M - 1)) * K + k_first + g * 8) * 2;
     }
   }
-  const uint8_t *pdmb[kBPre ? kDmaPerWaveB : 1];
-  if constexpr (kBPre) {
-#pragma unroll
-    for (int j = 0; j < kDmaPerWaveB; ++j) {
-      const int q = wave * kDmaPerWaveB + j;
-      const int r = 8 * q + (lane >> 3);
-      const int g = (lane & 7) ^ (r & 7);
-      pdmb[j] = static_cast<const uint8_t *>(W) + (size_t(min(n0 + r, N - 1)) * K + k_first + g * 8) * 2;
-    }
-  }
   auto dma_a = [&](int kt, int stage) {
     if constexpr (kAPre) {
       const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_address(sa + stage * kStageA)) +
                            uint32_t(wave * kDmaPerWave) * 1024u;
 #pragma unroll
       for (int j = 0; j < kDmaPerWave; ++j) dma16(pdma[j] + size_t(kt) * kBK * 2, dst + 1024u * j);
-    }
-    if constexpr (kBPre) {
-      const uint32_t dst = __builtin_amdgcn_readfirstlane(lds_address(sb + stage * kStageB)) +
-                           uint32_t(wave * kDmaPerWaveB) * 1024u;
-#pragma unroll
-      for (int j = 0; j < kDmaPerWaveB; ++j) dma16(pdmb[j] + size_t(kt) * kBK * 2, dst + 1024u * j);
     }
   };
 
@@ -473,6 +453,176 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
                            ts, cs, bias, bias_dtype, out, out_dtype, M, N);
 }
 
+// Both operands already bf16 (A decoded once per call, W decoded once per
+// call or kept decoded by the caller): every K step copies the A and W tiles
+// into LDS by DMA and the K loop is MFMAs and fragment reads only, scheduled
+// by hand.  A K step of 64 is two 32-wide slices; each wave holds the
+// fragments of two slices in registers and reads the next slice's fragments
+// while the MFMAs of the current one run (one ds_read_b128 between every few
+// MFMAs: left to itself the compiler reads each fragment right before its
+// first MFMA and waits for it there).  One barrier per step, between the two
+// slices: after it the step's stage may be overwritten (the copy of step
+// kt + 2 is issued right there) and the next step's tile has landed, so the
+// second slice's MFMAs run while the next step's first fragments are read.
+// Wave sub-tiles are 64 rows x (kBN / kWavesN) columns: each A fragment feeds
+// kTN MFMAs in a row.
+template <int kBM, int kBN, int kWavesM, int kWavesN>
+__global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_dma_kernel(
+    const uint16_t *__restrict__ A, const float *__restrict__ ts, const uint16_t *__restrict__ W,
+    const float *__restrict__ cs, const void *__restrict__ bias, int bias_dtype,
+    void *__restrict__ out, int out_dtype, int M, int N, int K, float *__restrict__ partial,
+    int splits, int ksteps) {
+  constexpr int kWaves = kWavesM * kWavesN;
+  constexpr int kWM = kBM / kWavesM, kWN = kBN / kWavesN;
+  constexpr int kTM = kWM / 16, kTN = kWN / 16;
+  constexpr uint32_t kStageA = kBM * kBK * 2, kStageB = kBN * kBK * 2, kStage = kStageA + kStageB;
+  constexpr int kDmaA = int(kStageA) / 1024 / kWaves, kDmaB = int(kStageB) / 1024 / kWaves;
+  static_assert(kDmaA * kWaves * 1024 == int(kStageA) && kDmaB * kWaves * 1024 == int(kStageB),
+                "tile copies split evenly over the waves");
+  constexpr int kReads = kTM + kTN, kMfmas = kTM * kTN;
+  // MFMAs between two reads: the reads fill the first three quarters of a
+  // slice, so the last one has a quarter of the slice to land.
+  constexpr int kPerRead = kMfmas * 3 / 4 / kReads > 0 ? kMfmas * 3 / 4 / kReads : 1;
+
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  int m0, n0, split;
+  if (!tile_of<kBM, kBN>(M, N, splits, m0, n0, split)) return;
+  const size_t k_first = size_t(split) * ksteps * kBK;
+
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int frow = lane & 15, fgrp = lane >> 4;
+
+  // Copy sources: instruction j of this wave fills 1 KiB q = wave * kDma + j
+  // of the tile (rows 8q .. 8q + 7, 128 bytes each); lane i lands at row
+  // 8q + i / 8, slot i % 8, which holds granule (i % 8) ^ (row & 7).  Byte
+  // offsets from the tile's first row in this split (rows past the last one
+  // read the last row); the host keeps kBM x K x 2 below 2^32.
+  uint32_t oa[kDmaA], ob[kDmaB];
+#pragma unroll
+  for (int j = 0; j < kDmaA; ++j) {
+    const int r = 8 * (wave * kDmaA + j) + (lane >> 3);
+    oa[j] = uint32_t(min(m0 + r, M - 1) - m0) * uint32_t(K) * 2u + uint32_t((lane & 7) ^ (r & 7)) * 16u;
+  }
+#pragma unroll
+  for (int j = 0; j < kDmaB; ++j) {
+    const int r = 8 * (wave * kDmaB + j) + (lane >> 3);
+    ob[j] = uint32_t(min(n0 + r, N - 1) - n0) * uint32_t(K) * 2u + uint32_t((lane & 7) ^ (r & 7)) * 16u;
+  }
+  const uint16_t *a_split = A + size_t(m0) * K + k_first, *w_split = W + size_t(n0) * K + k_first;
+  const uint32_t lds0 = lds_address(smem);
+  auto copy = [&](int kt, int stage) {
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + uint32_t(stage) * kStage);
+    const uint16_t *sa = a_split + size_t(kt) * kBK, *sw = w_split + size_t(kt) * kBK;
+#pragma unroll
+    for (int j = 0; j < kDmaA; ++j) dma16_offset(sa, oa[j], dst + uint32_t(wave * kDmaA + j) * 1024u);
+#pragma unroll
+    for (int j = 0; j < kDmaB; ++j) dma16_offset(sw, ob[j], dst + kStageA + uint32_t(wave * kDmaB + j) * 1024u);
+  };
+
+  // Fragment of 16x16x32 tile (i, j), slice kk: lane holds row frow, K
+  // elements 8 fgrp .. 8 fgrp + 7 of the slice, i.e. granule 4 kk + fgrp.
+  // Rows of one fragment start at a multiple of 16, so the swizzle term is
+  // frow & 7 for every fragment of the lane.
+  const uint32_t g0 = uint32_t((fgrp ^ (frow & 7)) * 16), g1 = g0 ^ 64u;
+  const uint32_t ra = uint32_t(wm * kWM + frow) * 128u, rb = kStageA + uint32_t(wn * kWN + frow) * 128u;
+  bf16x8_t fa0[kTM], fb0[kTN], fa1[kTM], fb1[kTN];
+  auto read = [&](bf16x8_t (&fa)[kTM], bf16x8_t (&fb)[kTN], const uint8_t *stage, uint32_t g) {
+#pragma unroll
+    for (int i = 0; i < kTM; ++i)
+      fa[i] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4 *>(stage + ra + i * 2048 + g));
+#pragma unroll
+    for (int j = 0; j < kTN; ++j)
+      fb[j] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4 *>(stage + rb + j * 2048 + g));
+  };
+  f32x4_t acc[kTM][kTN];
+#pragma unroll
+  for (int i = 0; i < kTM; ++i)
+#pragma unroll
+    for (int j = 0; j < kTN; ++j) acc[i][j] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // One 32-wide slice, its order pinned by scheduling barriers: the MFMAs of
+  // (fa, fb); after every kPerRead of them one read of the next slice's
+  // fragments (into na, nb, from stage `next`, granule offset g); and, with
+  // kCopy, one of this wave's copies of step copy_kt into stage copy_stage
+  // after every kCopyEvery MFMAs (spread over the slice; issuing them
+  // together at its start measured the same).
+  constexpr int kCopies = kDmaA + kDmaB;
+  constexpr int kCopyEvery = kMfmas / kCopies > 0 ? kMfmas / kCopies : 1;
+  auto slice = [&](auto do_read, auto do_copy, const bf16x8_t (&fa)[kTM], const bf16x8_t (&fb)[kTN],
+                   bf16x8_t (&na)[kTM], bf16x8_t (&nb)[kTN], const uint8_t *next, uint32_t g, int copy_kt,
+                   int copy_stage) {
+    constexpr bool kRead = decltype(do_read)::value, kCopy = decltype(do_copy)::value;
+    const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + uint32_t(copy_stage) * kStage);
+    const uint16_t *sa = a_split + size_t(copy_kt) * kBK, *sw = w_split + size_t(copy_kt) * kBK;
+#pragma unroll
+    for (int p = 0; p < kMfmas; ++p) {
+      acc[p / kTN][p % kTN] =
+          __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[p / kTN], fb[p % kTN], acc[p / kTN][p % kTN], 0, 0, 0);
+      if constexpr (kRead) {
+        if (p % kPerRead == kPerRead - 1 && p / kPerRead < kReads) {
+          const int r = p / kPerRead;
+          if (r < kTM)
+            na[r] = __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4 *>(next + ra + r * 2048 + g));
+          else
+            nb[r - kTM] =
+                __builtin_bit_cast(bf16x8_t, *reinterpret_cast<const u32x4 *>(next + rb + (r - kTM) * 2048 + g));
+        }
+      }
+      if constexpr (kCopy) {
+        if (p % kCopyEvery == 0 && p / kCopyEvery < kCopies) {
+          const int d = p / kCopyEvery;
+          if (d < kDmaA)
+            dma16_offset(sa, oa[d], dst + uint32_t(wave * kDmaA + d) * 1024u);
+          else
+            dma16_offset(sw, ob[d - kDmaA], dst + kStageA + uint32_t(wave * kDmaB + d - kDmaA) * 1024u);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  const std::true_type yes;
+  const std::false_type no;
+
+  // The loop body is free of branches (a branch there splits the
+  // accumulators' live ranges into copies): the last step runs after it, and
+  // the copy that the second-to-last step would issue for step KT repeats
+  // step KT - 1 into the stage nobody reads any more.
+  const int KT = ksteps;
+  copy(0, 0);
+  if (KT > 1) {
+    copy(1, 1);
+    wait_vmcnt<kDmaA + kDmaB>();
+  } else {
+    wait_vmcnt<0>();
+  }
+  lds_barrier();
+  read(fa0, fb0, smem, g0);
+  for (int kt = 0; kt + 1 < KT; ++kt) {
+    // Slice 0 of step kt (registers 0) while slice 1 is read (registers 1).
+    slice(yes, no, fa0, fb0, fa1, fb1, smem + (kt & 1) * kStage, g1, 0, 0);
+    // This wave's copy of step kt + 1 has landed and its reads of stage
+    // kt & 1 are done; after the barrier the same holds for every wave.
+    wait_vmcnt<0>();
+    lds_barrier();
+    // Slice 1 of step kt while slice 0 of step kt + 1 is read and step
+    // kt + 2 is copied into the stage step kt used.
+    slice(yes, yes, fa1, fb1, fa0, fb0, smem + ((kt + 1) & 1) * kStage, g0, min(kt + 2, KT - 1), kt & 1);
+  }
+  slice(yes, no, fa0, fb0, fa1, fb1, smem + ((KT - 1) & 1) * kStage, g1, 0, 0);
+  slice(no, no, fa1, fb1, fa0, fb0, smem, g0, 0, 0);
+  wait_vmcnt<0>();  // the repeated copy of the last step
+
+  if (partial) {
+    store_tile<kTM, kTN>(acc, m0 + wm * kWM, n0 + wn * kWN, frow, fgrp, ts, cs, bias, bias_dtype, out, out_dtype,
+                         M, N, partial, split);
+    return;
+  }
+  lds_barrier();  // every wave is done reading the stages
+  store_tile_lds<kTM, kTN>(acc, smem + wave * epilogue_region_bytes<kTM, kTN>(), m0 + wm * kWM, n0 + wn * kWN, lane,
+                           ts, cs, bias, bias_dtype, out, out_dtype, M, N);
+}
+
 // Split-K epilogue: out = (sum over s of partial[s]) * ts[m] * cs[n] (+ b[n]),
 // four consecutive columns per thread (N % 4 == 0), splits added in order.
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(
@@ -558,6 +708,16 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k, bool decoded_weight = false)
   static const int tile_env = env_int("HIF8_GEMM_TILE", 0);
   static const int split_env = env_int("HIF8_GEMM_SPLIT", 0);
   static const int wpre_env = env_int("HIF8_GEMM_WPRE", -1);
+  // Decoding W once costs ~3 bytes of HBM traffic per weight; the in-kernel
+  // decode repeats it once per 256-row tile of M, so from M = 2048 on the
+  // codes path decodes W once per call into the workspace and runs the plan
+  // of the decoded-weight path (both operands by DMA).
+  if (!decoded_weight && (wpre_env >= 0 ? wpre_env > 0 : m >= 2048) && k < kMaxDmaK && k % kBK == 0) {
+    GemmPlan p = plan_gemm(m, n, k, true);
+    p.w_pre = true;
+    p.w_bytes = (size_t(n) * size_t(k) * 2 + 255) / 256 * 256;
+    return p;
+  }
   GemmPlan p;
   const int64_t tiles256 = ((m + 255) / 256) * ((n + 255) / 256);
   const int64_t ksteps = k / kBK;
@@ -585,9 +745,6 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k, bool decoded_weight = false)
         p.splits *= 2;
     }
   }
-  // Decoding W once costs ~3 bytes of HBM traffic per weight; the in-kernel
-  // decode repeats it once per 256-row tile of M, so from M = 2048 on the
-  // one-pass decode wins and the kernel streams both operands by DMA.
   // Decoded weights: an unsplit 256-tile grid short of one block per CU
   // takes 256 x 192 blocks when those still fit one wave of blocks (gate_up
   // at M = 512: 192 -> 256 blocks).  The in-kernel weight decode does not
@@ -597,14 +754,14 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k, bool decoded_weight = false)
     const int64_t tiles192 = ((m + 255) / 256) * ((n + 191) / 192);
     if (tiles256 < 256 && tiles192 > tiles256 && tiles192 <= 256) p.bn = 192;
   }
-  p.w_pre = wpre_env >= 0 ? wpre_env > 0 : (p.tile == 256 && p.splits == 1 && m >= 2048);
+  p.w_pre = false;
   p.a_bytes = (size_t(m) * size_t(k) * 2 + 255) / 256 * 256;
   p.w_bytes = p.w_pre ? (size_t(n) * size_t(k) * 2 + 255) / 256 * 256 : 0;
   p.part_bytes = p.splits > 1 ? size_t(p.splits) * size_t(m) * size_t(n) * sizeof(float) : 0;
   return p;
 }
 
-template <int kBM, int kBN, int kWavesM, int kWavesN, bool kAPre, bool kBPre, bool kPingPong>
+template <int kBM, int kBN, int kWavesM, int kWavesN, bool kAPre, bool kPingPong>
 int launch_tiled(const LinearArgs &a, const void *act, const void *wt, int splits, float *partial) {
   // K-step stages, or the epilogue regions if larger; + 512 B of static LDS (the table).
   constexpr size_t kSmem = std::max<size_t>(2 * size_t(kBM + kBN) * kBK * 2,
@@ -612,12 +769,12 @@ int launch_tiled(const LinearArgs &a, const void *act, const void *wt, int split
                                                 epilogue_region_bytes<kBM / kWavesM / 16, kBN / kWavesN / 16>());
   constexpr int kT = kWave * kWavesM * kWavesN;
   if (const int st = reserve_dynamic_lds(
-          reinterpret_cast<const void *>(&gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kBPre, kPingPong>), kSmem,
+          reinterpret_cast<const void *>(&gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kPingPong>), kSmem,
           "soft_hif8 GEMM"))
     return st;
   const int64_t tiles = ((a.n + kBN - 1) / kBN) * ((a.m + kBM - 1) / kBM);
   const dim3 grid(unsigned((tiles * splits + 7) / 8 * 8));
-  gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kBPre, kPingPong><<<grid, kT, kSmem, a.stream>>>(
+  gemm_kernel<kBM, kBN, kWavesM, kWavesN, kAPre, kPingPong><<<grid, kT, kSmem, a.stream>>>(
       act, a.act_scale, wt, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.m),
       int(a.n), int(a.k), partial, splits, int(a.k / kBK / splits));
   int st = check_launch("soft_hif8 GEMM");
@@ -629,13 +786,46 @@ int launch_tiled(const LinearArgs &a, const void *act, const void *wt, int split
   return check_launch("soft_hif8 GEMM (split-K reduce)");
 }
 
+// Launch of gemm_dma_kernel (+ the split-K reduce when partial is set).
+template <int kBM, int kBN, int kWavesM, int kWavesN>
+int launch_dma(const LinearArgs &a, const uint16_t *act, const uint16_t *wt, int splits, float *partial) {
+  constexpr size_t kSmem = std::max<size_t>(2 * size_t(kBM + kBN) * kBK * 2,
+                                            size_t(kWavesM * kWavesN) *
+                                                epilogue_region_bytes<kBM / kWavesM / 16, kBN / kWavesN / 16>());
+  constexpr int kT = kWave * kWavesM * kWavesN;
+  if (const int st = reserve_dynamic_lds(reinterpret_cast<const void *>(&gemm_dma_kernel<kBM, kBN, kWavesM, kWavesN>),
+                                         kSmem, "soft_hif8 GEMM"))
+    return st;
+  const int64_t tiles = ((a.n + kBN - 1) / kBN) * ((a.m + kBM - 1) / kBM);
+  const dim3 grid(unsigned((tiles * splits + 7) / 8 * 8));
+  gemm_dma_kernel<kBM, kBN, kWavesM, kWavesN><<<grid, kT, kSmem, a.stream>>>(
+      act, a.act_scale, wt, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.m), int(a.n),
+      int(a.k), partial, splits, int(a.k / kBK / splits));
+  int st = check_launch("soft_hif8 GEMM");
+  if (st || !partial) return st;
+  const size_t quads = size_t(a.m) * size_t(a.n / 4);
+  const unsigned blocks = unsigned(std::min<size_t>((quads + 255) / 256, 4096));
+  splitk_reduce_kernel<<<blocks, 256, 0, a.stream>>>(partial, splits, a.act_scale, a.channel_scale, a.bias,
+                                                   a.bias_dtype, a.out, a.out_dtype, int(a.m), int(a.n));
+  return check_launch("soft_hif8 GEMM (split-K reduce)");
+}
+
+// Both operands bf16 in HBM: the DMA-fed kernel with the plan's block shape.
+int launch_bf16_operands(const LinearArgs &a, const GemmPlan &p, const uint16_t *act, const uint16_t *wt, int splits,
+                         float *partial) {
+  if (a.k >= kMaxDmaK) return fail(HIF8_ERR_UNSUPPORTED, "soft_hif8 GEMM: K >= %d", kMaxDmaK);
+  if (p.tile == 256 && p.bn == 192) return launch_dma<256, 192, 4, 2>(a, act, wt, splits, partial);
+  if (p.tile == 256) return launch_dma<256, 256, 4, 2>(a, act, wt, splits, partial);
+  return launch_dma<128, 128, 2, 2>(a, act, wt, splits, partial);
+}
+
 template <bool kAPre>
 int launch_plan(const LinearArgs &a, const GemmPlan &p, const void *act, int splits, float *partial) {
   static const int pingpong = env_int("HIF8_GEMM_PINGPONG", 1);
   if (p.tile == 256)
-    return pingpong ? launch_tiled<256, 256, 2, 4, kAPre, false, true>(a, act, a.weight, splits, partial)
-                    : launch_tiled<256, 256, 2, 4, kAPre, false, false>(a, act, a.weight, splits, partial);
-  return launch_tiled<128, 128, 2, 2, kAPre, false, false>(a, act, a.weight, splits, partial);
+    return pingpong ? launch_tiled<256, 256, 2, 4, kAPre, true>(a, act, a.weight, splits, partial)
+                    : launch_tiled<256, 256, 2, 4, kAPre, false>(a, act, a.weight, splits, partial);
+  return launch_tiled<128, 128, 2, 2, kAPre, false>(a, act, a.weight, splits, partial);
 }
 
 }  // namespace
@@ -679,10 +869,8 @@ int launch_gemm(const LinearArgs &a) {
   }
   float *partial = p.part_bytes ? reinterpret_cast<float *>(ws + p.a_bytes + p.w_bytes) : nullptr;
   if (p.w_pre) {
-    const void *wbf = ws + p.a_bytes;
-    const int splits = p.part_bytes ? p.splits : 1;
-    if (p.tile == 256) return launch_tiled<256, 256, 2, 4, true, true, false>(a, abf, wbf, splits, partial);
-    return launch_tiled<128, 128, 2, 2, true, true, false>(a, abf, wbf, splits, partial);
+    const uint16_t *wbf = reinterpret_cast<const uint16_t *>(ws + p.a_bytes);
+    return launch_bf16_operands(a, p, abf, wbf, p.part_bytes ? p.splits : 1, partial);
   }
   return launch_plan<true>(a, p, abf, p.part_bytes ? p.splits : 1, partial);
 }
@@ -704,11 +892,7 @@ int launch_gemm_decoded_weight(const LinearArgs &a) {
   const int st = check_launch("soft_hif8 GEMM (activation decode)");
   if (st) return st;
   float *partial = p.part_bytes ? reinterpret_cast<float *>(ws + p.a_bytes) : nullptr;
-  const int splits = p.part_bytes ? p.splits : 1;
-  if (p.tile == 256 && p.bn == 192)
-    return launch_tiled<256, 192, 2, 4, true, true, false>(a, abf, a.weight_bf16, splits, partial);
-  if (p.tile == 256) return launch_tiled<256, 256, 2, 4, true, true, false>(a, abf, a.weight_bf16, splits, partial);
-  return launch_tiled<128, 128, 2, 2, true, true, false>(a, abf, a.weight_bf16, splits, partial);
+  return launch_bf16_operands(a, p, abf, a.weight_bf16, p.part_bytes ? p.splits : 1, partial);
 }
 
 int launch_decode_bf16(const uint8_t *codes, uint16_t *out, size_t elements, hipStream_t stream) {

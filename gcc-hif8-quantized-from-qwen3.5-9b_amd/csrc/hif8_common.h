@@ -107,6 +107,22 @@ __device__ __forceinline__ void dma16(const void *src, uint32_t lds_base) {
       : "memory");
 }
 
+// dma16 with a wave-uniform 64-bit base (SGPRs) and a 32-bit per-lane byte
+// offset: lane i's 16 bytes come from base + voffset.
+__device__ __forceinline__ void dma16_offset(const void *base, uint32_t voffset, uint32_t lds_base) {
+  const uint32_t lds = __builtin_amdgcn_readfirstlane(lds_base);
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %3\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(voffset), "s"(base), "s"(lds)
+      : "memory");
+}
+
 // s_waitcnt with vmcnt(n) only (lgkmcnt / expcnt left at their maxima).
 template <int kN>
 __device__ __forceinline__ void wait_vmcnt() {

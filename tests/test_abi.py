@@ -112,6 +112,9 @@ def test_gemm_workspace_query_follows_the_split_plan(lib):
     # also the bf16 copy of W (N*K*2), plus split partials.
     # Enough 256 x 256 tiles to fill the GPU: no split.  GEMV-sized M: no workspace.
     assert size(4096, 24576, 4096) == 4096 * 4096 * 2 + 24576 * 4096 * 2
+    # From M = 2048 the plan is the decoded-weight one: k+v at M = 4096 runs
+    # 512 unsplit 128 x 128 tiles instead of 128 256-tiles split in two.
+    assert size(4096, 2048, 4096) == 4096 * 4096 * 2 + 2048 * 4096 * 2
     assert size(1024, 24576, 4096) == 1024 * 4096 * 2
     assert size(4, 4096, 4096) == 0
     # Prefill M=512 over a 4096 x 4096 projection: 128 tiles of 128 x 128, K split in 4.
