@@ -55,21 +55,34 @@ __device__ __forceinline__ void static_encode16(const float (&xf)[16], float s, 
                                                 uint32_t (&w)[4]) {
   const float r = __builtin_amdgcn_rcpf(s);
   float q[16];
-  bool redo = false;
+  // One decision for the 16 products: the smallest distance to an index
+  // boundary (a min tree) and whether any product of the wavefront is NaN
+  // (pairwise unordered compares into a lane mask; a NaN anywhere sends the
+  // whole wavefront down the exact path, which encodes every value alike).
+  uint32_t nearest = 0xFFFFFFFFu;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     q[j] = xf[j] * r;
-    redo |= near_index_boundary(q[j]);
+    // Bits 18..0 of u + margin, moved to the top (one add-shift).
+    nearest = min(nearest, (__float_as_uint(q[j]) + kNearMargin) << 13);
   }
+  uint64_t nan_lanes = 0;
+#pragma unroll
+  for (int j = 0; j < 16; j += 2) nan_lanes |= __builtin_amdgcn_fcmpf(q[j], q[j + 1], 8);  // FCMP_UNO
+  const bool redo = nearest <= (2u * kNearMargin) << 13 || nan_lanes != 0;
   if (__builtin_expect(!redo, 1)) {
     // No value is NaN or near an index boundary: the product encodes exactly
-    // like the correctly rounded quotient.
+    // like the correctly rounded quotient.  Bytes 0 and 2 (1 and 3) of a
+    // word are looked up into the two halves of one register, then merged.
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      uint32_t b[4];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) b[j] = encode_q(q[4 * i + j], lut);
-      w[i] = b[0] | (b[1] << 8) | (b[2] << 16) | (b[3] << 24);
+      typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+      u16x2_t even, odd;
+      even.x = lut[__float_as_uint(q[4 * i]) >> 19];
+      even.y = lut[__float_as_uint(q[4 * i + 2]) >> 19];
+      odd.x = lut[__float_as_uint(q[4 * i + 1]) >> 19];
+      odd.y = lut[__float_as_uint(q[4 * i + 3]) >> 19];
+      w[i] = __builtin_bit_cast(uint32_t, even) | (__builtin_bit_cast(uint32_t, odd) << 8);
     }
   } else {
 #pragma unroll

@@ -8,6 +8,8 @@
 // as few VALU cycles per element as possible: static_encode16 multiplies by a
 // per-row reciprocal and falls back to an IEEE division only next to an
 // encode-index boundary (the argument is spelled out in quant_device.h).
+#include <stdlib.h>
+
 #include <algorithm>
 
 #include "quant_device.h"
@@ -29,19 +31,23 @@ constexpr int kThreads = 256;
 // order) and the barrier, which waits for LDS traffic only, leaves the chunk
 // in flight.  One encode in the loop body keeps the kernel small: a launch
 // this short pays for every instruction it fetches cold.
-template <bool kBf16>
+// kRowScales: more than one fixed scale (row r uses fixed[r % scale_count]);
+// with one, no chunk needs its row index and the loop has no division.  The
+// per-row output scales are written before the loop, one row per thread.
+template <bool kBf16, bool kRowScales>
 __global__ __launch_bounds__(kThreads) void static_quant_vec16(
     const uint16_t *__restrict__ x, const float *__restrict__ fixed, uint8_t *__restrict__ out,
-    float *__restrict__ row_scale, uint32_t n_chunks, uint32_t k_chunks, uint32_t scale_count) {
+    float *__restrict__ row_scale, uint32_t n_chunks, uint32_t k_chunks, uint32_t scale_count, uint32_t rows) {
   __shared__ __attribute__((aligned(16))) uint8_t lut[8192];
   static_assert(8192 == 2 * 16 * kThreads, "two 16-byte table words per thread");
   const uint4 *tsrc = reinterpret_cast<const uint4 *>(kDeviceTables.static_encode);
   const uint4 t0 = tsrc[threadIdx.x], t1 = tsrc[threadIdx.x + kThreads];
   const uint64_t stride = uint64_t(gridDim.x) * kThreads;
   uint64_t c = uint64_t(blockIdx.x) * kThreads + threadIdx.x;  // 64-bit: no wrap near 2^32 chunks
-  // A chunk's data and its row's scale are loaded together, one chunk ahead.
+  // A chunk's data (and with kRowScales its row's scale) are loaded
+  // together, one chunk ahead.
   uint4 a0{}, a1{};
-  float sc = 0.f;
+  float sc = kRowScales ? 0.f : fixed[0];
   // Unconditional loads (a chunk past the end reloads the last one, unused),
   // so the compiler can count them and wait for exactly the ones it needs.
   auto fetch = [&](uint64_t ch) {
@@ -49,9 +55,10 @@ __global__ __launch_bounds__(kThreads) void static_quant_vec16(
     const uint4 *src = reinterpret_cast<const uint4 *>(x + safe * 16);
     a0 = src[0];
     a1 = src[1];
-    sc = fixed[scale_count == 1 ? 0u : (uint32_t(safe) / k_chunks) % scale_count];
+    if constexpr (kRowScales) sc = fixed[(uint32_t(safe) / k_chunks) % scale_count];
   };
   fetch(c);
+  for (uint64_t r = c; r < rows; r += stride) row_scale[r] = fixed[kRowScales ? uint32_t(r) % scale_count : 0u];
   reinterpret_cast<uint4 *>(lut)[threadIdx.x] = t0;
   reinterpret_cast<uint4 *>(lut)[threadIdx.x + kThreads] = t1;
   lds_barrier();
@@ -59,8 +66,6 @@ __global__ __launch_bounds__(kThreads) void static_quant_vec16(
     const uint32_t v[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
     const float s = sc;
     fetch(c + stride);
-    const uint32_t row = uint32_t(c) / k_chunks;
-    if (uint32_t(c) == row * k_chunks) row_scale[row] = s;
     float xf[16];
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
@@ -231,9 +236,14 @@ extern "C" int hif8_static_quant(const void *x, int x_dtype, int64_t rows, int64
   const uint16_t *xs = static_cast<const uint16_t *>(x);
   if (k % 16 == 0 && aligned(x, 16) && aligned(data, 16) && n_chunks <= 0xFFFFFFFFull) {
     const dim3 grid(grid_for(n_chunks, 16)), block(kThreads);
-    const uint32_t nc = uint32_t(n_chunks), kc = uint32_t(k / 16), sc = uint32_t(scale_count);
-    if (bf16) static_quant_vec16<true><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
-    else static_quant_vec16<false><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc);
+    const uint32_t nc = uint32_t(n_chunks), kc = uint32_t(k / 16), sc = uint32_t(scale_count), r = uint32_t(rows);
+    if (sc == 1) {
+      if (bf16) static_quant_vec16<true, false><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc, r);
+      else static_quant_vec16<false, false><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc, r);
+    } else {
+      if (bf16) static_quant_vec16<true, true><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc, r);
+      else static_quant_vec16<false, true><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, nc, kc, sc, r);
+    }
   } else {
     const dim3 grid(grid_for(n, 8)), block(kThreads);
     if (bf16) static_quant_scalar<true><<<grid, block, 0, s>>>(xs, fixed_scale, data, row_scale, n, uint64_t(k), uint32_t(scale_count));
