@@ -464,32 +464,50 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_kernel(
 // slices: after it the step's stage may be overwritten (the copy of step
 // kt + 2 is issued right there) and the next step's tile has landed, so the
 // second slice's MFMAs run while the next step's first fragments are read.
-// Wave sub-tiles are 64 rows x (kBN / kWavesN) columns: each A fragment feeds
-// kTN MFMAs in a row.
-template <int kBM, int kBN, int kWavesM, int kWavesN>
+// Wave sub-tiles are kBM / kWavesM rows x kBN / kWavesN columns: each A
+// fragment feeds kTN MFMAs in a row.
+//
+// kWDec: W is the uint8 code matrix, decoded in the kernel.  Each thread
+// loads 16-byte code chunks of the W tile a step ahead into VGPRs; during the
+// first slice of step kt it looks the codes of tile kt + 1 up in the 256-entry
+// bf16 table (LDS address 0) and stores them into that tile's stage (free
+// since the barrier of step kt - 1), lookups and the packing of their results
+// a few MFMAs apart, then loads the codes of tile kt + 2.  The A tile still
+// comes by DMA.
+template <int kBM, int kBN, int kWavesM, int kWavesN, bool kWDec>
 __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_dma_kernel(
-    const uint16_t *__restrict__ A, const float *__restrict__ ts, const uint16_t *__restrict__ W,
+    const uint16_t *__restrict__ A, const float *__restrict__ ts, const void *__restrict__ Wv,
     const float *__restrict__ cs, const void *__restrict__ bias, int bias_dtype,
     void *__restrict__ out, int out_dtype, int M, int N, int K, float *__restrict__ partial,
     int splits, int ksteps) {
   constexpr int kWaves = kWavesM * kWavesN;
+  constexpr int kT = kWave * kWaves;
   constexpr int kWM = kBM / kWavesM, kWN = kBN / kWavesN;
   constexpr int kTM = kWM / 16, kTN = kWN / 16;
   constexpr uint32_t kStageA = kBM * kBK * 2, kStageB = kBN * kBK * 2, kStage = kStageA + kStageB;
-  constexpr int kDmaA = int(kStageA) / 1024 / kWaves, kDmaB = int(kStageB) / 1024 / kWaves;
-  static_assert(kDmaA * kWaves * 1024 == int(kStageA) && kDmaB * kWaves * 1024 == int(kStageB),
+  constexpr int kDmaA = int(kStageA) / 1024 / kWaves, kDmaB = kWDec ? 0 : int(kStageB) / 1024 / kWaves;
+  static_assert(kDmaA * kWaves * 1024 == int(kStageA) && (kWDec || kDmaB * kWaves * 1024 == int(kStageB)),
                 "tile copies split evenly over the waves");
+  constexpr int kDec = kWDec ? kBN * kBK / 8 / kT : 0;  // 8-code W chunks per thread and step
+  static_assert(!kWDec || kDec * 8 * kT == kBN * kBK, "W decode split evenly over the threads");
+  const uint16_t *W = static_cast<const uint16_t *>(Wv);
+  const uint8_t *Wc = static_cast<const uint8_t *>(Wv);
   constexpr int kReads = kTM + kTN, kMfmas = kTM * kTN;
   // MFMAs between two reads: the reads fill the first three quarters of a
   // slice, so the last one has a quarter of the slice to land.
   constexpr int kPerRead = kMfmas * 3 / 4 / kReads > 0 ? kMfmas * 3 / 4 / kReads : 1;
 
+  // The decode table first (the only static LDS object: address 0), then the stages.
+  __shared__ __attribute__((aligned(16))) uint16_t lut[kWDec ? 256 : 8];
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   int m0, n0, split;
   if (!tile_of<kBM, kBN>(M, N, splits, m0, n0, split)) return;
   const size_t k_first = size_t(split) * ksteps * kBK;
 
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  if constexpr (kWDec) {
+    if (tid < 256) lut[tid] = uint16_t(decode_bits(uint32_t(tid)) >> 16);
+  }
   const int wm = wave / kWavesN, wn = wave % kWavesN;
   const int frow = lane & 15, fgrp = lane >> 4;
 
@@ -498,7 +516,7 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_dma_kernel(
   // 8q + i / 8, slot i % 8, which holds granule (i % 8) ^ (row & 7).  Byte
   // offsets from the tile's first row in this split (rows past the last one
   // read the last row); the host keeps kBM x K x 2 below 2^32.
-  uint32_t oa[kDmaA], ob[kDmaB];
+  uint32_t oa[kDmaA], ob[kDmaB > 0 ? kDmaB : 1];
 #pragma unroll
   for (int j = 0; j < kDmaA; ++j) {
     const int r = 8 * (wave * kDmaA + j) + (lane >> 3);
@@ -511,6 +529,38 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_dma_kernel(
   }
   const uint16_t *a_split = A + size_t(m0) * K + k_first, *w_split = W + size_t(n0) * K + k_first;
   const uint32_t lds0 = lds_address(smem);
+
+  // W codes (kWDec): chunk c of this thread is q = tid + c * kT of the tile,
+  // row q / 8, codes 8 (q % 8) .. 8 (q % 8) + 7 of the step's 64, which
+  // decode to granule q % 8 of the row.
+  uint32_t wco[kDec > 0 ? kDec : 1], wdst[kDec > 0 ? kDec : 1];
+  uint2 wq[kDec > 0 ? kDec : 1];
+  if constexpr (kWDec) {
+#pragma unroll
+    for (int c = 0; c < kDec; ++c) {
+      const int q = tid + c * kT, r = q >> 3, gq = q & 7;
+      wco[c] = uint32_t(min(n0 + r, N - 1) - n0) * uint32_t(K) + uint32_t(gq) * 8u;
+      wdst[c] = kStageA + uint32_t(r) * 128u + uint32_t((gq ^ (r & 7)) * 16);
+    }
+  }
+  const uint8_t *wc_split = Wc + size_t(n0) * K + k_first;
+  auto load_codes = [&](int kt) {
+#pragma unroll
+    for (int c = 0; c < kDec; ++c) wq[c] = *reinterpret_cast<const uint2 *>(wc_split + size_t(kt) * kBK + wco[c]);
+  };
+  // Chunk c: looks up its 8 codes (8 table entries), then packs them into
+  // its bf16 granule in the stage at `stage`.
+  uint32_t lk[8];
+  auto lookup = [&](int c) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) lk[j] = lut[(((j >> 2) ? wq[c].y : wq[c].x) >> (8 * (j & 3))) & 0xFFu];
+  };
+  auto pack_store = [&](int c, uint8_t *stage) {
+    u32x4 v;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[i] = lk[2 * i] | (lk[2 * i + 1] << 16);
+    *reinterpret_cast<u32x4 *>(stage + wdst[c]) = v;
+  };
   auto copy = [&](int kt, int stage) {
     const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + uint32_t(stage) * kStage);
     const uint16_t *sa = a_split + size_t(kt) * kBK, *sw = w_split + size_t(kt) * kBK;
@@ -549,12 +599,19 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_dma_kernel(
   // together at its start measured the same).
   constexpr int kCopies = kDmaA + kDmaB;
   constexpr int kCopyEvery = kMfmas / kCopies > 0 ? kMfmas / kCopies : 1;
-  auto slice = [&](auto do_read, auto do_copy, const bf16x8_t (&fa)[kTM], const bf16x8_t (&fb)[kTN],
-                   bf16x8_t (&na)[kTM], bf16x8_t (&nb)[kTN], const uint8_t *next, uint32_t g, int copy_kt,
-                   int copy_stage) {
+  // Decode positions (kWDec, first slice of a step): the lookups of chunk c
+  // after MFMA c * kDecStep, its packing and store kDecGap MFMAs later; the
+  // next codes' loads after the last store.
+  constexpr int kDecStep = kDec > 0 ? (kMfmas * 3 / 4) / kDec : 1;
+  constexpr int kDecGap = kDecStep / 2 > 0 ? kDecStep / 2 : 1;
+  auto slice = [&](auto do_read, auto do_copy, auto do_decode, const bf16x8_t (&fa)[kTM],
+                   const bf16x8_t (&fb)[kTN], bf16x8_t (&na)[kTM], bf16x8_t (&nb)[kTN], const uint8_t *next,
+                   uint32_t g, int copy_kt, int copy_stage, uint8_t *dec_stage, int codes_kt) {
     constexpr bool kRead = decltype(do_read)::value, kCopy = decltype(do_copy)::value;
+    constexpr bool kDecode = decltype(do_decode)::value;
     const uint32_t dst = __builtin_amdgcn_readfirstlane(lds0 + uint32_t(copy_stage) * kStage);
     const uint16_t *sa = a_split + size_t(copy_kt) * kBK, *sw = w_split + size_t(copy_kt) * kBK;
+    if constexpr (kDecode) wait_vmcnt<kDmaA>();  // this step's codes (the A copy issued after them may fly on)
 #pragma unroll
     for (int p = 0; p < kMfmas; ++p) {
       acc[p / kTN][p % kTN] =
@@ -578,6 +635,12 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_dma_kernel(
             dma16_offset(sw, ob[d - kDmaA], dst + kStageA + uint32_t(wave * kDmaB + d - kDmaA) * 1024u);
         }
       }
+      if constexpr (kDecode) {
+        if (p % kDecStep == 0 && p / kDecStep < kDec) lookup(p / kDecStep);
+        if (p >= kDecGap && (p - kDecGap) % kDecStep == 0 && (p - kDecGap) / kDecStep < kDec)
+          pack_store((p - kDecGap) / kDecStep, dec_stage);
+        if (p == (kDec - 1) * kDecStep + kDecGap + 1) load_codes(codes_kt);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
@@ -589,29 +652,50 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_dma_kernel(
   // the copy that the second-to-last step would issue for step KT repeats
   // step KT - 1 into the stage nobody reads any more.
   const int KT = ksteps;
-  copy(0, 0);
-  if (KT > 1) {
-    copy(1, 1);
-    wait_vmcnt<kDmaA + kDmaB>();
+  if constexpr (kWDec) {
+    // Tile 0: codes and A copy; its codes decoded here (one code buffer, so
+    // tile 1's codes are loaded after), then tile 1's codes and A copy.
+    load_codes(0);
+    copy(0, 0);
+    wait_vmcnt<kDmaA>();
+    lds_barrier();  // the table
+#pragma unroll
+    for (int c = 0; c < kDec; ++c) {
+      lookup(c);
+      pack_store(c, smem);
+    }
+    load_codes(min(1, KT - 1));
+    copy(min(1, KT - 1), 1);
+    wait_vmcnt<kDmaA + kDec>();  // tile 0's A copy
   } else {
-    wait_vmcnt<0>();
+    copy(0, 0);
+    if (KT > 1) {
+      copy(1, 1);
+      wait_vmcnt<kDmaA + kDmaB>();
+    } else {
+      wait_vmcnt<0>();
+    }
   }
   lds_barrier();
   read(fa0, fb0, smem, g0);
   for (int kt = 0; kt + 1 < KT; ++kt) {
-    // Slice 0 of step kt (registers 0) while slice 1 is read (registers 1).
-    slice(yes, no, fa0, fb0, fa1, fb1, smem + (kt & 1) * kStage, g1, 0, 0);
-    // This wave's copy of step kt + 1 has landed and its reads of stage
-    // kt & 1 are done; after the barrier the same holds for every wave.
-    wait_vmcnt<0>();
+    // Slice 0 of step kt (registers 0) while slice 1 is read (registers 1)
+    // and (kWDec) the codes of tile kt + 1 are decoded into its stage.
+    slice(yes, no, std::integral_constant<bool, kWDec>{}, fa0, fb0, fa1, fb1, smem + (kt & 1) * kStage, g1, 0, 0,
+          smem + ((kt + 1) & 1) * kStage, min(kt + 2, KT - 1));
+    // This wave's copy of step kt + 1 has landed (and its stores of the
+    // decoded W) and its reads of stage kt & 1 are done; after the barrier
+    // the same holds for every wave.  The codes of tile kt + 2 may fly on.
+    wait_vmcnt<kDec>();
     lds_barrier();
     // Slice 1 of step kt while slice 0 of step kt + 1 is read and step
     // kt + 2 is copied into the stage step kt used.
-    slice(yes, yes, fa1, fb1, fa0, fb0, smem + ((kt + 1) & 1) * kStage, g0, min(kt + 2, KT - 1), kt & 1);
+    slice(yes, yes, no, fa1, fb1, fa0, fb0, smem + ((kt + 1) & 1) * kStage, g0, min(kt + 2, KT - 1), kt & 1, smem,
+          0);
   }
-  slice(yes, no, fa0, fb0, fa1, fb1, smem + ((KT - 1) & 1) * kStage, g1, 0, 0);
-  slice(no, no, fa1, fb1, fa0, fb0, smem, g0, 0, 0);
-  wait_vmcnt<0>();  // the repeated copy of the last step
+  slice(yes, no, no, fa0, fb0, fa1, fb1, smem + ((KT - 1) & 1) * kStage, g1, 0, 0, smem, 0);
+  slice(no, no, no, fa1, fb1, fa0, fb0, smem, g0, 0, 0, smem, 0);
+  wait_vmcnt<0>();  // the repeated copy (and codes) of the last step
 
   if (partial) {
     store_tile<kTM, kTN>(acc, m0 + wm * kWM, n0 + wn * kWN, frow, fgrp, ts, cs, bias, bias_dtype, out, out_dtype,
@@ -786,19 +870,21 @@ int launch_tiled(const LinearArgs &a, const void *act, const void *wt, int split
   return check_launch("soft_hif8 GEMM (split-K reduce)");
 }
 
-// Launch of gemm_dma_kernel (+ the split-K reduce when partial is set).
-template <int kBM, int kBN, int kWavesM, int kWavesN>
-int launch_dma(const LinearArgs &a, const uint16_t *act, const uint16_t *wt, int splits, float *partial) {
+// Launch of gemm_dma_kernel (+ the split-K reduce when partial is set); wt
+// is the bf16 weight, or (kWDec) the codes.
+template <int kBM, int kBN, int kWavesM, int kWavesN, bool kWDec = false>
+int launch_dma(const LinearArgs &a, const uint16_t *act, const void *wt, int splits, float *partial) {
   constexpr size_t kSmem = std::max<size_t>(2 * size_t(kBM + kBN) * kBK * 2,
                                             size_t(kWavesM * kWavesN) *
                                                 epilogue_region_bytes<kBM / kWavesM / 16, kBN / kWavesN / 16>());
   constexpr int kT = kWave * kWavesM * kWavesN;
-  if (const int st = reserve_dynamic_lds(reinterpret_cast<const void *>(&gemm_dma_kernel<kBM, kBN, kWavesM, kWavesN>),
-                                         kSmem, "soft_hif8 GEMM"))
+  if (const int st = reserve_dynamic_lds(
+          reinterpret_cast<const void *>(&gemm_dma_kernel<kBM, kBN, kWavesM, kWavesN, kWDec>), kSmem,
+          "soft_hif8 GEMM"))
     return st;
   const int64_t tiles = ((a.n + kBN - 1) / kBN) * ((a.m + kBM - 1) / kBM);
   const dim3 grid(unsigned((tiles * splits + 7) / 8 * 8));
-  gemm_dma_kernel<kBM, kBN, kWavesM, kWavesN><<<grid, kT, kSmem, a.stream>>>(
+  gemm_dma_kernel<kBM, kBN, kWavesM, kWavesN, kWDec><<<grid, kT, kSmem, a.stream>>>(
       act, a.act_scale, wt, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.m), int(a.n),
       int(a.k), partial, splits, int(a.k / kBK / splits));
   int st = check_launch("soft_hif8 GEMM");
@@ -822,6 +908,13 @@ int launch_bf16_operands(const LinearArgs &a, const GemmPlan &p, const uint16_t 
 template <bool kAPre>
 int launch_plan(const LinearArgs &a, const GemmPlan &p, const void *act, int splits, float *partial) {
   static const int pingpong = env_int("HIF8_GEMM_PINGPONG", 1);
+  // An unsplit 256-tile grid short of one block per CU that 256 x 192 blocks
+  // fill in one wave (gate_up at M = 512: 192 -> 256 blocks) runs the DMA
+  // kernel with the weight decoded in it (142 -> 111 us there; at 256 x 256
+  // it measured no faster than the ping-pong kernel).
+  const int64_t tiles_m = (a.m + 255) / 256, t256 = tiles_m * ((a.n + 255) / 256), t192 = tiles_m * ((a.n + 191) / 192);
+  if (kAPre && p.tile == 256 && splits == 1 && a.k < kMaxDmaK && t256 < 256 && t192 > t256 && t192 <= 256)
+    return launch_dma<256, 192, 4, 2, true>(a, static_cast<const uint16_t *>(act), a.weight, splits, partial);
   if (p.tile == 256)
     return pingpong ? launch_tiled<256, 256, 2, 4, kAPre, true>(a, act, a.weight, splits, partial)
                     : launch_tiled<256, 256, 2, 4, kAPre, false>(a, act, a.weight, splits, partial);
