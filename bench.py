@@ -312,7 +312,7 @@ def per_kernel_table(st: Setup, launches: int = 20) -> dict:
                 gbs = fb / (ms * 1e-3) / 1e9
                 table[f"{name}_m{m}_fused"] = {"kernel": "fused_quant_gemv", "us": round(ms * 1e3, 3), "bytes": fb,
                                                "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
-    for m, k in ((4096, 4096), (512, 4096), (1, 4096), (4, 12288)):
+    for m, k in ((4096, 4096), (4096, 12288), (512, 4096), (1, 4096), (4, 12288)):
         x, s = st.x[(m, k)]
 
         def fq(x=x, s=s):

@@ -604,6 +604,8 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_dma_kernel(
   // next codes' loads after the last store.
   constexpr int kDecStep = kDec > 0 ? (kMfmas * 3 / 4) / kDec : 1;
   constexpr int kDecGap = kDecStep / 2 > 0 ? kDecStep / 2 : 1;
+  static_assert(!kWDec || (kDecGap <= kDecStep && (kDec - 1) * kDecStep + kDecGap + 1 < kMfmas),
+                "each chunk packed before the next lookups; the next codes loaded within the slice");
   auto slice = [&](auto do_read, auto do_copy, auto do_decode, const bf16x8_t (&fa)[kTM],
                    const bf16x8_t (&fb)[kTN], bf16x8_t (&na)[kTM], bf16x8_t (&nb)[kTN], const uint8_t *next,
                    uint32_t g, int copy_kt, int copy_stage, uint8_t *dec_stage, int codes_kt) {
@@ -636,9 +638,11 @@ __global__ __launch_bounds__(kWave * kWavesM * kWavesN, 1) void gemm_dma_kernel(
         }
       }
       if constexpr (kDecode) {
-        if (p % kDecStep == 0 && p / kDecStep < kDec) lookup(p / kDecStep);
+        // A chunk's packing comes before the next chunk's lookups (one
+        // register set holds the looked-up entries).
         if (p >= kDecGap && (p - kDecGap) % kDecStep == 0 && (p - kDecGap) / kDecStep < kDec)
           pack_store((p - kDecGap) / kDecStep, dec_stage);
+        if (p % kDecStep == 0 && p / kDecStep < kDec) lookup(p / kDecStep);
         if (p == (kDec - 1) * kDecStep + kDecGap + 1) load_codes(codes_kt);
       }
       __builtin_amdgcn_sched_barrier(0);
