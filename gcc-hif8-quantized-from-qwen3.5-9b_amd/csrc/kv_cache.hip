@@ -13,17 +13,20 @@
 // encoder as hif8_static_quant, so the bytes equal quant -> pack -> scatter.
 //
 // Decode attention (kv_runtime.py:1470-1563 semantics, oracle kv_cache.py:314-372):
-// one query token per request, GQA group G = Hq / Hkv.  A workgroup is one
-// wavefront and owns one (request, token range = "split", KV head); the block
-// ids of the KV heads of one split are adjacent modulo 8, so they run on one
-// XCD and share its L2.  The wavefront walks its range in 32-token tiles:
-//   * K rows go from HBM straight into VGPRs in the MFMA A-operand layout
-//     (token = lane % 16, 64 contiguous bytes per lane) and S^T = K Q^T runs
-//     on v_mfma_f32_16x16x32 (B = the G query heads of the KV head, padded to
-//     16 columns);
-//   * V rows are copied raw into LDS by DMA (global_load_lds_dwordx4) and read
-//     transposed (8 tokens x 4 dims per lane), and O^T += V^T P' runs on the
-//     same MFMA with the softmax weights P' rounded to bf16;
+// one query token per request, GQA group G = Hq / Hkv.  A workgroup owns one
+// (request, token range = "split", KV head) and has D / 64 wavefronts, one
+// per 64-dim slice of K and V (so a tile's decode work is spread over the
+// SIMDs); the block ids of the KV heads of one split are adjacent modulo 8, so
+// they run on one XCD and share its L2.  The workgroup walks its range in
+// 32-token tiles:
+//   * K slices go from HBM straight into VGPRs in the MFMA A-operand layout
+//     (token = lane % 16, 16 contiguous bytes per lane) and each wavefront's
+//     share of S^T = K Q^T runs on v_mfma_f32_16x16x32 (B = the G query heads
+//     of the KV head, padded to 16 columns); the shares are summed through
+//     LDS in wavefront order, so every wavefront runs the same softmax;
+//   * V slices are copied raw into LDS by DMA (global_load_lds_dwordx4) and
+//     read transposed (8 tokens x 4 dims per lane), and O^T += V^T P' runs on
+//     the same MFMA with the softmax weights P' rounded to bf16;
 //   * both operands are decoded through per-wave LDS tables that hold
 //     dtype(dec(c) * s) for the tile's row scale s - which is how the
 //     reference decodes K and V before its attention
@@ -145,7 +148,6 @@ __global__ __launch_bounds__(kThreads) void kv_write_scalar(
 // -------------------------------------------------------------- attention
 
 constexpr int kTile = 32;        // tokens per tile: two 16-row MFMA blocks
-constexpr int kWaves = 4;        // KV heads per workgroup, one wavefront each
 constexpr int kMaxSplits = 4096; // combine kernel's LDS weight array
 
 struct AttnParams {
@@ -216,42 +218,42 @@ __device__ __forceinline__ f32x4_t mfma16(u32x4 a, u32x4 b, f32x4_t c) {
 
 
 // MFMA mapping (v_mfma_f32_16x16x32: A row = lane % 16, B column = lane % 16,
-// k-slots 8 * (lane / 16) + j; D[i][j] in lane (i / 4) * 16 + j, element i % 4):
-//   S^T = K Q^T : A row = token of a 16-token block; lane group g holds dims
-//                 [g * D/4, (g+1) * D/4), eight per MFMA; B column = query head.
+// k-slots 8 * (lane / 16) + j; D[i][j] in lane (i / 4) * 16 + j, element i % 4).
+// A workgroup has D / 64 wavefronts; wavefront w owns dims [64 w, 64 w + 64)
+// of K and V, so each one decodes a quarter of the codes of a D = 256 tile:
+//   S^T = K Q^T : A row = token of a 16-token block; lane group g holds the
+//                 16 dims 64 w + 16 g + [0, 16) (two MFMAs of 8 k-slots), one
+//                 16-byte load per lane; B column = query head.  The partial
+//                 scores of the wavefronts are summed through LDS in wavefront
+//                 order, so every wavefront holds the same S and runs the same
+//                 online softmax.
 //   O^T = V^T P': k-slot j of group g is token 4g + j (j < 4) or 16 + 4g + j - 4,
 //                 which is where the S^T accumulators of the two 16-token blocks
 //                 leave those tokens, so P' needs no data movement; A row r of
-//                 MFMA (db, q) is dim 64 db + 4 r + q, so lane (g, n) ends up with
-//                 dims 64 db + 16 g + [0, 16) of query head n contiguous.
-// V tiles reach LDS by DMA, 16-byte granule c of token t stored at granule
-// c ^ swz(t), swz(t) = 4 * ((t >> 2) % (D / 64)): the transposed reads of the
-// four lane groups (tokens 4g + j) then fall in four different bank quarters.
+//                 MFMA q is dim 64 w + 4 r + q, so lane (g, n) ends up with
+//                 dims 64 w + 16 g + [0, 16) of query head n contiguous.
+// Each wavefront copies the 64-byte V slice of its dims into LDS by DMA; the
+// 16-byte granule c of token t lands in slot 64 (t >> 4) + 16 (t & 3) +
+// 4 ((t >> 2) & 3) + c, so the transposed reads (token 4g + j for the four lane
+// groups) touch 64 different banks.
 //
-// A workgroup is one wavefront and owns one (request, context split, KV
-// head).  Workgroups of the Hkv heads of one split get block ids that are
-// equal modulo 8, so they run on the same XCD and the cache lines their rows
-// share are read from HBM once.
+// Workgroups of the Hkv heads of one split get block ids that are equal
+// modulo 8, so they run on the same XCD and the cache lines their rows share
+// are read from HBM once.
 template <int kD, bool kQBf16, bool kPaged, typename BtT>
-__global__ __launch_bounds__(kWave, 2) void paged_decode_attention_kernel(const AttnParams p) {
+__global__ __launch_bounds__(kWave * (kD / 64), 4) void paged_decode_attention_kernel(const AttnParams p) {
   constexpr int kRow = kD + 4;            // bytes per cache row
-  constexpr int kLaneK = kD / 4;          // K bytes per lane per 16-token block
-  constexpr int kKChunks = kD / 64;       // 16-byte K loads per lane per block
-  constexpr int kQkSteps = kD / 32;       // MFMAs per 16-token block
-  constexpr int kGranules = kD / 16;      // 16-byte granules per V row
-  constexpr int kVDma = kTile * kGranules / 64;  // DMA instructions per V tile
-  constexpr int kVBytes = kTile * kD;     // one V tile in LDS
-  constexpr int kDBlocks = kD / 64;
-  static_assert(kTile * kGranules % 64 == 0, "whole DMA instructions per tile");
+  constexpr int kWd = kD / 64;            // wavefronts per workgroup, 64 dims each
+  constexpr int kSlice = kTile * 64;      // one wavefront's V bytes of a tile
+  static_assert(kTile == 32, "the V slot map and the P' layout assume 32-token tiles");
+  static_assert(kD % 64 == 0 && kWd >= 1 && kWd <= 4, "64-dim slices");
 
-  // One LDS block, so the decode tables sit at fixed addresses: a lookup is
-  // one SDWA shift of the code plus a ds_read_u16 with the table's offset.
   struct Smem {
-    uint16_t k_tab[256];     // query dtype(dec(c) * k_tab_scale)
-    uint16_t v_tab[256];     // bf16(dec(c) * v_tab_scale)
-    float dec[256];          // fp32 dec(c), the source of both
-    float scl[64];           // K | V factors of the tile's tokens (0 = masked)
-    uint8_t vtile[2][kVBytes];  // double-buffered V tile
+    uint16_t k_tab[kWd][256];      // query dtype(dec(c) * k_tab_scale), per wavefront
+    uint16_t v_tab[kWd][256];      // bf16(dec(c) * v_tab_scale), per wavefront
+    float scl[kWd][64];            // K | V factors of the tile's tokens (0 = masked)
+    f32x4_t sx[2][kWd][2][kWave];  // partial scores [tile parity][wavefront][16-token block][lane]
+    uint8_t vtile[2][kWd][kSlice]; // double-buffered V slices
   };
   __shared__ __attribute__((aligned(16))) Smem smem;
 
@@ -261,7 +263,8 @@ __global__ __launch_bounds__(kWave, 2) void paged_decode_attention_kernel(const 
   if (bs_idx >= p.batch * p.num_splits) return;  // padding block (uniform)
   const int b = bs_idx / p.num_splits;
   const int split = bs_idx - b * p.num_splits;
-  const int lane = threadIdx.x;
+  const int wv = __builtin_amdgcn_readfirstlane(int(threadIdx.x) >> 6);
+  const int lane = int(threadIdx.x) & 63;
   const int n = lane & 15, g = lane >> 4;
   const bool head_ok = n < p.group;
   const int qhead = h * p.group + (head_ok ? n : 0);
@@ -308,37 +311,43 @@ __global__ __launch_bounds__(kWave, 2) void paged_decode_attention_kernel(const 
     return ok ? (slot0 + (t & ((1 << lg) - 1))) * rec + head_off : head_off;
   };
 
-  u32x4 kr[2][kKChunks];  // K operand bytes of the tile being computed / loaded
-  float sn;               // K (lanes 0-31) or V (lanes 32-63) scale of token lane % 32
-  bool tile_ok_next;      // the next tile's block is valid (paged path)
-  uint8_t *const vbuf = &smem.vtile[0][0];
-  const uint32_t vbuf_lds = __builtin_amdgcn_readfirstlane(lds_address(vbuf));
+  const int dim0 = 64 * wv;  // first dim of this wavefront
+  u32x4 kn[2];               // K bytes (dims dim0 + 16 g + [0, 16)) of the tile in flight
+  float sn;                  // K (lanes 0-31) or V (lanes 32-63) scale of token lane % 32
+  bool tile_ok_next;         // the block of the tile in flight is valid (paged path)
+  const uint32_t vbuf_lds = __builtin_amdgcn_readfirstlane(lds_address(&smem.vtile[0][wv][0]));
+  // DMA lane -> token of the V slot map: lane i of copy j fills slot 64 j + i.
+  const int dma_tok = 4 * ((lane >> 2) & 3) + (lane >> 4);
   // Loads of tile t0 whose tokens end at t_last: V by DMA into buffer `buf`,
-  // scales into sn, K into VGPRs.  Tokens past t_last address t_last (generic
+  // scales into sn, K into kn.  Tokens past t_last address t_last (generic
   // path) or stay inside the tile's block (paged path); they are masked later.
-  auto issue_v = [&](int t0, int t_last, int buf) {
-    const uint32_t dst = vbuf_lds + uint32_t(buf * kVBytes);
+  auto issue = [&](int t0, int t_last, int buf) {
+    const uint32_t dst = vbuf_lds + uint32_t(buf * kWd * kSlice);
     if constexpr (kPaged) {
       bool ok;
       const int64_t base = tile_row(t0, ok);
       tile_ok_next = ok;
 #pragma unroll
-      for (int j = 0; j < kVDma; ++j) {
-        const int s = lane + 64 * j, tok = s / kGranules, gl = s % kGranules;
-        const int col = gl ^ ((4 * (tok >> 2)) & (kGranules - 1));
-        dma16(p.value_cache + base + tok * rec + 16 * col, dst + 1024u * j);
-      }
+      for (int j = 0; j < 2; ++j)
+        dma16(p.value_cache + base + (16 * j + dma_tok) * rec + dim0 + 16 * (lane & 3), dst + 1024u * j);
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+        kn[s] = *reinterpret_cast<const u32x4_a4 *>(p.key_cache + base + (16 * s + n) * rec + dim0 + 16 * g);
       sn = *reinterpret_cast<const float *>((lane < 32 ? p.key_cache : p.value_cache) + base +
                                             (lane & 31) * rec + kD);
     } else {
       tile_ok_next = true;
 #pragma unroll
-      for (int j = 0; j < kVDma; ++j) {
-        const int s = lane + 64 * j, tok = s / kGranules, gl = s % kGranules;
-        const int col = gl ^ ((4 * (tok >> 2)) & (kGranules - 1));
+      for (int j = 0; j < 2; ++j) {
         bool ok;
-        const int64_t off = token_row(min(t0 + tok, t_last), ok);
-        dma16(p.value_cache + off + 16 * col, dst + 1024u * j);
+        const int64_t off = token_row(min(t0 + 16 * j + dma_tok, t_last), ok);
+        dma16(p.value_cache + off + dim0 + 16 * (lane & 3), dst + 1024u * j);
+      }
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        bool ok;
+        const int64_t off = token_row(min(t0 + 16 * s + n, t_last), ok);
+        kn[s] = *reinterpret_cast<const u32x4_a4 *>(p.key_cache + off + dim0 + 16 * g);
       }
       bool ok;
       const int64_t off = token_row(min(t0 + (lane & 31), t_last), ok);
@@ -346,43 +355,21 @@ __global__ __launch_bounds__(kWave, 2) void paged_decode_attention_kernel(const 
       sn = ok ? v : 0.f;  // a zero scale masks the token
     }
   };
-  auto issue_k = [&](int t0, int t_last) {
-    if constexpr (kPaged) {
-      bool ok;
-      const int64_t base = tile_row(t0, ok);
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const uint8_t *src = p.key_cache + base + (16 * s + n) * rec + kLaneK * g;
-#pragma unroll
-        for (int c = 0; c < kKChunks; ++c) kr[s][c] = *reinterpret_cast<const u32x4_a4 *>(src + 16 * c);
-      }
-    } else {
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        bool ok;
-        const int64_t off = token_row(min(t0 + 16 * s + n, t_last), ok);
-        const uint8_t *src = p.key_cache + off + kLaneK * g;
-#pragma unroll
-        for (int c = 0; c < kKChunks; ++c) kr[s][c] = *reinterpret_cast<const u32x4_a4 *>(src + 16 * c);
-      }
-    }
-  };
 
   // Prologue, independent of the request length: the first tile, the
   // query, the fp32 decode table.
   const int len_raw = p.seq_lens[b];
-  issue_v(t_begin, t_cap - 1, 0);
-  issue_k(t_begin, t_cap - 1);
-  u32x4 qf[kQkSteps];
+  issue(t_begin, t_cap - 1, 0);
+  u32x4 qf[2];
   {
-    // Q^T operand: lane (g, n) holds dims [g*D/4, (g+1)*D/4) of query head n.
-    const uint16_t *q = static_cast<const uint16_t *>(p.query) + out_row + kLaneK * g;
-#pragma unroll
-    for (int i = 0; i < kQkSteps; ++i)
-      qf[i] = head_ok ? reinterpret_cast<const u32x4 *>(q)[i] : u32x4{0, 0, 0, 0};
+    // Q^T operand: lane (g, n) holds dims dim0 + 16 g + [0, 16) of query head n.
+    const u32x4 *q = reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(p.query) + out_row + dim0 + 16 * g);
+    qf[0] = head_ok ? q[0] : u32x4{0, 0, 0, 0};
+    qf[1] = head_ok ? q[1] : u32x4{0, 0, 0, 0};
   }
+  float decf[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) smem.dec[lane + 64 * i] = __uint_as_float(kDeviceTables.decode_f32[lane + 64 * i]);
+  for (int i = 0; i < 4; ++i) decf[i] = __uint_as_float(kDeviceTables.decode_f32[lane + 64 * i]);
   // The scales the tables currently hold (NaN: not built yet).
   float k_tab_scale = __builtin_nanf(""), v_tab_scale = __builtin_nanf("");
 
@@ -390,8 +377,8 @@ __global__ __launch_bounds__(kWave, 2) void paged_decode_attention_kernel(const 
   if (t_begin >= len) {  // an empty split
     wait_vmcnt<0>();     // no copy may still target LDS when the wave ends
     if (split == 0) {    // an empty request: zero output
-      uint16_t *o = static_cast<uint16_t *>(p.out) + (size_t(b) * p.hq + h * p.group) * kD;
-      for (int i = lane; i < p.group * kD; i += kWave) o[i] = 0;
+      uint16_t *o = static_cast<uint16_t *>(p.out) + (size_t(b) * p.hq + h * p.group) * kD + dim0;
+      for (int i = lane; i < p.group * 64; i += kWave) o[(i >> 6) * kD + (i & 63)] = 0;
     }
     return;
   }
@@ -399,34 +386,89 @@ __global__ __launch_bounds__(kWave, 2) void paged_decode_attention_kernel(const 
   const int n_splits_b = (len + p.split_tokens - 1) / p.split_tokens;
   const int ntiles = (t_end - t_begin + kTile - 1) / kTile;
 
-  f32x4_t oacc[kDBlocks][4];
+  f32x4_t oacc[4];
 #pragma unroll
-  for (int db = 0; db < kDBlocks; ++db)
-#pragma unroll
-    for (int q = 0; q < 4; ++q) oacc[db][q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  for (int q = 0; q < 4; ++q) oacc[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m = -__builtin_inff(), l = 0.f;
-  float *sc = smem.scl;
+  float *sc = smem.scl[wv];
+  const uint16_t *kl = smem.k_tab[wv];
+  const uint16_t *vl = smem.v_tab[wv];
 
-  // One tile.
-  auto tile = [&](const uint8_t *vt, int t0, bool more) {
-    const uint16_t *kl = smem.k_tab;
-    const uint16_t *vl = smem.v_tab;
-    // S^T = K Q^T for the two 16-token blocks.
+  for (int it = 0; it < ntiles; ++it) {
+    const int t0 = t_begin + it * kTile;
+    const int nvalid = min(kTile, t_end - t0);
+    wait_vmcnt<0>();
+    const float s_cur = sn;
+    const bool blk_ok = tile_ok_next;
+    const u32x4 kc[2] = {kn[0], kn[1]};
+    uint8_t *vt = &smem.vtile[it & 1][wv][0];
+    // The next tile is in flight during this one.
+    if (it + 1 < ntiles) issue(t0 + kTile, t_end - 1, (it + 1) & 1);
+
+    // A block id outside the cache masks the whole tile.
+    const bool valid = blk_ok && (lane & 31) < nvalid && s_cur != 0.f;
+    // When the valid K rows (lanes 0-31) or V rows (lanes 32-63) of the tile
+    // share one scale (always, for a cache written with static per-head
+    // scales), that table holds dtype(dec(c) * scale) - the values the
+    // reference decodes K/V to (kv_cache.py:355-356) - and the rows get unit
+    // factors; otherwise it holds the exact dec(c) and the row scales multiply
+    // the logits (K) and softmax weights (V) in FP32.
+    const uint64_t vball = __ballot(valid);
+    const int k_first = __builtin_ffsll(vball & 0xFFFFFFFFull) - 1;
+    const int v_first = __builtin_ffsll(vball & 0xFFFFFFFF00000000ull) - 1;
+    const float k_one = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s_cur), max(k_first, 0)));
+    const float v_one = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s_cur), max(v_first, 32)));
+    const uint64_t same = __ballot(!valid || s_cur == (lane < 32 ? k_one : v_one));
+    const bool k_uniform = (same & 0xFFFFFFFFull) == 0xFFFFFFFFull;
+    const bool v_uniform = (same >> 32) == 0xFFFFFFFFull;
+    const float k_want = k_uniform ? k_one : 1.f, v_want = v_uniform ? v_one : 1.f;
+    if (!(k_want == k_tab_scale)) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) smem.k_tab[wv][lane + 64 * i] = float_to_half_bits<kQBf16>(decf[i] * k_want);
+      k_tab_scale = k_want;
+    }
+    if (!(v_want == v_tab_scale)) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) smem.v_tab[wv][lane + 64 * i] = float_to_bf16_bits(decf[i] * v_want);
+      v_tab_scale = v_want;
+    }
+    sc[lane] = valid ? ((lane < 32 ? k_uniform : v_uniform) ? 1.f : s_cur) : 0.f;
+    if (!__all(valid)) {
+      // Masked tokens: zero their V codes so that 0 * Inf / NaN cannot reach O.
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int tok = 16 * j + dma_tok;
+        if (!(tok < nvalid && sc[tok] != 0.f))
+          *reinterpret_cast<u32x4 *>(vt + 1024 * j + 16 * lane) = u32x4{0, 0, 0, 0};
+      }
+    }
+
+    // This wavefront's share of S^T = K Q^T for the two 16-token blocks.
     f32x4_t sacc[2];
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
-      sacc[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int i = 0; i < kQkSteps; ++i) {
-        const u32x4 w = kr[s][i >> 1];
-        const u32x4 a = (i & 1) ? decode8(kl, w[2], w[3]) : decode8(kl, w[0], w[1]);
-        sacc[s] = mfma16<kQBf16>(a, qf[i], sacc[s]);
-      }
+      sacc[s] = mfma16<kQBf16>(decode8(kl, kc[s][0], kc[s][1]), qf[0], f32x4_t{0.f, 0.f, 0.f, 0.f});
+      sacc[s] = mfma16<kQBf16>(decode8(kl, kc[s][2], kc[s][3]), qf[1], sacc[s]);
     }
-    if (more) {  // the next tile is in flight during softmax and P V
-      const int tn = t0 + kTile;
-      issue_k(tn, t_end - 1);
-      issue_v(tn, t_end - 1, 1 - ((vt - vbuf) / kVBytes));
+    if constexpr (kWd > 1) {
+      // Sum the partial scores in wavefront order (the same in every wavefront).
+      // Columns of padding heads are zero in every partial and stay unsummed.
+      const int par = it & 1;
+      if (head_ok) {
+        smem.sx[par][wv][0][lane] = sacc[0];
+        smem.sx[par][wv][1][lane] = sacc[1];
+      }
+      lds_barrier();
+      if (head_ok) {
+        f32x4_t s0 = smem.sx[par][0][0][lane], s1 = smem.sx[par][0][1][lane];
+#pragma unroll
+        for (int w2 = 1; w2 < kWd; ++w2) {
+          s0 += smem.sx[par][w2][0][lane];
+          s1 += smem.sx[par][w2][1][lane];
+        }
+        sacc[0] = s0;
+        sacc[1] = s1;
+      }
     }
 
     // Online softmax over this tile (base 2).  Lane (g, n) holds tokens
@@ -459,110 +501,46 @@ __global__ __launch_bounds__(kWave, 2) void paged_decode_attention_kernel(const 
     // from a finite value (before that the accumulators are zero).
     if (!__all(m_new == m || m == -__builtin_inff())) {
 #pragma unroll
-      for (int db = 0; db < kDBlocks; ++db)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) oacc[db][q] *= alpha;
+      for (int q = 0; q < 4; ++q) oacc[q] *= alpha;
     }
     m = m_new;
     const u32x4 pb{pack_half2<true>(pw[0] * vs0[0], pw[1] * vs0[1]), pack_half2<true>(pw[2] * vs0[2], pw[3] * vs0[3]),
                    pack_half2<true>(pw[4] * vs1[0], pw[5] * vs1[1]), pack_half2<true>(pw[6] * vs1[2], pw[7] * vs1[3])};
 
-    // O^T += V^T P'.
+    // O^T += V^T P' over this wavefront's 64 dims: word j holds dims
+    // dim0 + 4n + [0, 4) of token 4g + j (j < 4) or 16 + 4g + j - 4.
+    uint32_t w[8];
 #pragma unroll
-    for (int db = 0; db < kDBlocks; ++db) {
-      uint32_t w[8];
+    for (int j = 0; j < 8; ++j)
+      w[j] = *reinterpret_cast<const uint32_t *>(vt + 1024 * (j >> 2) + 256 * (j & 3) + 64 * g + 4 * n);
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int tl = j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4);
-        const int gran = (4 * db + (n >> 2)) ^ ((4 * (tl >> 2)) & (kGranules - 1));
-        w[j] = *reinterpret_cast<const uint32_t *>(vt + tl * kD + 16 * gran + 4 * (n & 3));
-      }
-#pragma unroll
-      for (int q = 0; q < 4; ++q) oacc[db][q] = mfma16<true>(decode_column(vl, w, q), pb, oacc[db][q]);
-    }
-  };
-
-  // Tile k is issued during tile k - 1 (or in the prologue) and waited for
-  // at the top of iteration k.
-  for (int it = 0; it < ntiles; ++it) {
-    const int t0 = t_begin + it * kTile;
-    const int nvalid = min(kTile, t_end - t0);
-    const bool more = it + 1 < ntiles;
-    wait_vmcnt<0>();
-    const float s_cur = sn;
-    const uint8_t *vt = vbuf + (it & 1) * kVBytes;
-    // A block id outside the cache masks the whole tile.
-    const bool valid = tile_ok_next && (lane & 31) < nvalid && s_cur != 0.f;
-    // When the valid K rows (lanes 0-31) or V rows (lanes 32-63) of the tile
-    // share one scale (always, for a cache written with static per-head
-    // scales), that table holds dtype(dec(c) * scale) - the values the
-    // reference decodes K/V to (kv_cache.py:355-356) - and the rows get unit
-    // factors; otherwise it holds the exact dec(c) and the row scales multiply
-    // the logits (K) and softmax weights (V) in FP32.
-    const uint64_t vball = __ballot(valid);
-    const int k_first = __builtin_ffsll(vball & 0xFFFFFFFFull) - 1;
-    const int v_first = __builtin_ffsll(vball & 0xFFFFFFFF00000000ull) - 1;
-    const float k_one = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s_cur), max(k_first, 0)));
-    const float v_one = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, s_cur), max(v_first, 32)));
-    const uint64_t same = __ballot(!valid || s_cur == (lane < 32 ? k_one : v_one));
-    const bool k_uniform = (same & 0xFFFFFFFFull) == 0xFFFFFFFFull;
-    const bool v_uniform = (same >> 32) == 0xFFFFFFFFull;
-    const float k_want = k_uniform ? k_one : 1.f, v_want = v_uniform ? v_one : 1.f;
-    if (!(k_want == k_tab_scale)) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        smem.k_tab[lane + 64 * i] = float_to_half_bits<kQBf16>(smem.dec[lane + 64 * i] * k_want);
-      k_tab_scale = k_want;
-    }
-    if (!(v_want == v_tab_scale)) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) smem.v_tab[lane + 64 * i] = float_to_bf16_bits(smem.dec[lane + 64 * i] * v_want);
-      v_tab_scale = v_want;
-    }
-    sc[lane] = valid ? ((lane < 32 ? k_uniform : v_uniform) ? 1.f : s_cur) : 0.f;
-    if (!__all(valid)) {
-      // Masked tokens: zero their V codes so that 0 * Inf / NaN cannot reach O.
-#pragma unroll
-      for (int j = 0; j < kVDma; ++j) {
-        const int s = lane + 64 * j, tok = s / kGranules;
-        if (!(tok < nvalid && sc[tok] != 0.f))
-          *reinterpret_cast<u32x4 *>(const_cast<uint8_t *>(vt) + 16 * s) = u32x4{0, 0, 0, 0};
-      }
-    }
-    tile(vt, t0, more);
+    for (int q = 0; q < 4; ++q) oacc[q] = mfma16<true>(decode_column(vl, w, q), pb, oacc[q]);
   }
   float lt = l + __shfl_xor(l, 16, kWave);
   lt += __shfl_xor(lt, 32, kWave);
   if (!head_ok) return;
   if (n_splits_b == 1) {
     const float inv = lt > 0.f ? 1.f / lt : 0.f;
-    uint16_t *o = static_cast<uint16_t *>(p.out) + out_row + 16 * g;
+    uint16_t *o = static_cast<uint16_t *>(p.out) + out_row + dim0 + 16 * g;
+    uint32_t packed[8];
 #pragma unroll
-    for (int db = 0; db < kDBlocks; ++db) {
-      uint32_t packed[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        // Contiguous dim 2i (and 2i + 1) of this lane's 16 is element
-        // (2i) / 4 of accumulator (2i) % 4.
-        const int d0 = 2 * i, d1 = 2 * i + 1;
-        packed[i] = pack_half2<kQBf16>(oacc[db][d0 & 3][d0 >> 2] * inv, oacc[db][d1 & 3][d1 >> 2] * inv);
-      }
-      reinterpret_cast<u32x4 *>(o + 64 * db)[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
-      reinterpret_cast<u32x4 *>(o + 64 * db)[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
+    for (int i = 0; i < 8; ++i) {
+      // Contiguous dim 2i (and 2i + 1) of this lane's 16 is element
+      // (2i) / 4 of accumulator (2i) % 4.
+      const int d0 = 2 * i, d1 = 2 * i + 1;
+      packed[i] = pack_half2<kQBf16>(oacc[d0 & 3][d0 >> 2] * inv, oacc[d1 & 3][d1 >> 2] * inv);
     }
+    reinterpret_cast<u32x4 *>(o)[0] = u32x4{packed[0], packed[1], packed[2], packed[3]};
+    reinterpret_cast<u32x4 *>(o)[1] = u32x4{packed[4], packed[5], packed[6], packed[7]};
   } else {
     const size_t part = (size_t(b) * p.num_splits + split) * p.hq + qhead;
-    float *po = p.part_o + part * kD + 16 * g;
+    float *po = p.part_o + part * kD + dim0 + 16 * g;
 #pragma unroll
-    for (int db = 0; db < kDBlocks; ++db) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        // dims 4i .. 4i+3 of this lane's 16: element i of accumulators 0..3
-        reinterpret_cast<f32x4_t *>(po + 64 * db)[i] =
-            f32x4_t{oacc[db][0][i], oacc[db][1][i], oacc[db][2][i], oacc[db][3][i]};
-      }
+    for (int i = 0; i < 4; ++i) {
+      // dims 4i .. 4i+3 of this lane's 16: element i of accumulators 0..3
+      reinterpret_cast<f32x4_t *>(po)[i] = f32x4_t{oacc[0][i], oacc[1][i], oacc[2][i], oacc[3][i]};
     }
-    if (g == 0) {
+    if (g == 0 && wv == 0) {
       p.part_ml[2 * part] = m;
       p.part_ml[2 * part + 1] = lt;
     }
@@ -753,7 +731,7 @@ template <int kD, bool kQBf16, typename BtT>
 void launch_mfma(const AttnParams &p, int64_t batch, hipStream_t stream) {
   // Block id = ((request split group of 8) * Hkv + head) * 8 + position in the group.
   const int64_t groups = (batch * p.num_splits + 7) / 8;
-  const dim3 grid(unsigned(groups * 8 * p.hkv)), block(kWave);
+  const dim3 grid(unsigned(groups * 8 * p.hkv)), block(kWave * (kD / 64));
   if (p.block_size % kTile == 0) paged_decode_attention_kernel<kD, kQBf16, true, BtT><<<grid, block, 0, stream>>>(p);
   else paged_decode_attention_kernel<kD, kQBf16, false, BtT><<<grid, block, 0, stream>>>(p);
   if (p.num_splits > 1)

@@ -177,6 +177,23 @@ def test_attention_ragged_lengths_and_empty_requests(native_ops, device):
     _check_attention(device, [0, 1, 31, 32, 33, 127, 129, 1000], 16, 4, 256, 128, seed=3)
 
 
+def test_attention_ragged_few_splits_and_repeated(native_ops, device):
+    # One-tile splits (at most 16 per request): empty, one-split and
+    # many-split requests side by side, and repeated calls give equal bytes.
+    from hif8_rocm import kv_cache
+
+    lens = [0, 100, 512, 33, 64, 1]
+    for seed in (11, 12):
+        _check_attention(device, lens, 16, 4, 256, 128, seed=seed)
+    kc, vc, table = _build_cache(device, lens, 4, 256, 128, 13)
+    q = _randn((len(lens), 16, 256), 14).to(device)
+    first = kv_cache.paged_decode_attention(q, kc, vc, table.to(device), lens, scale=0.0625)
+    for _ in range(3):
+        again = kv_cache.paged_decode_attention(q, kc, vc, table.to(device), lens, scale=0.0625)
+        torch.cuda.synchronize()
+        assert torch.equal(again, first)
+
+
 def test_attention_multi_tile_splits_with_tails(native_ops, device):
     _check_attention(device, [16379, 16384, 9000, 1], 16, 4, 256, 128, seed=4)
 
