@@ -812,7 +812,7 @@ def main() -> None:
         gemm_layer[f"m{m}"] = {"TFLOPs": round(tf, 1), "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 4),
                                "us_per_layer": round(us, 1)}
     gdom = table["gate_up_m4096"]
-    gemm_layer["roofline"] = {"kernel": "activation decode + gemm_kernel<256,256> (gate_up 4096x24576x4096)",
+    gemm_layer["roofline"] = {"kernel": "activation + weight decode + gemm_dma_kernel<256,256> (gate_up 4096x24576x4096)",
                               "bound": "mfma", "achieved": gdom["TFLOPs"], "peak": BF16_PEAK_TFLOPS,
                               "unit": "TFLOP/s", "frac": gdom["frac_bf16"], "flops_per_launch": gdom["flops"],
                               "us_per_launch": gdom["us"]}
