@@ -105,8 +105,10 @@ __global__ __launch_bounds__(kThreads) void kv_write_vec16(
     uint32_t w[4];
     static_encode16(xf, s, lut, w);
     uint8_t *row = (is_v ? value_cache : key_cache) + (uint64_t(slot) * hkv + h) * (width + 4);
-    *reinterpret_cast<u32x4_a4 *>(row + 16 * col) = u32x4{w[0], w[1], w[2], w[3]};
-    if (col == 0) *reinterpret_cast<float *>(row + width) = s;
+    // Non-temporal stores: the pages are read by a later step's attention,
+    // not by this one (4096 tokens: 9.5 -> 9.0 us on MI355X).
+    __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]}, reinterpret_cast<u32x4_a4 *>(row + 16 * col));
+    if (col == 0) __builtin_nontemporal_store(s, reinterpret_cast<float *>(row + width));
   }
 }
 

@@ -18,6 +18,7 @@ namespace hif8 {
 namespace {
 
 constexpr int kThreads = 256;
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 // The vector kernel always stages the 8 KiB table: measured on MI355X, the
 // table-free arithmetic encoder is ~3x slower even for a single block
 // (M=1, K=4096: 10.2 vs 3.4 us) because of its data-dependent branches.
@@ -74,7 +75,9 @@ __global__ __launch_bounds__(kThreads) void static_quant_vec16(
     }
     uint32_t w[4];
     static_encode16(xf, s, lut, w);
-    *reinterpret_cast<uint4 *>(out + c * 16) = make_uint4(w[0], w[1], w[2], w[3]);
+    // Non-temporal store (M=4096, K=4096: 13.35 -> 12.33 us on MI355X; the
+    // same hint on the loads measured slower).
+    __builtin_nontemporal_store(u32x4{w[0], w[1], w[2], w[3]}, reinterpret_cast<u32x4 *>(out + c * 16));
   }
 }
 

@@ -88,12 +88,12 @@ def test_workspace_size_follows_the_split_plan(lib):
     f = lib.hif8_paged_decode_attention_workspace_size
     f.restype = ctypes.c_size_t
     f.argtypes = [ctypes.c_int64] * 6
-    # One request of 16384 tokens = 512 tiles x 4 KV heads: 2 tiles per split keeps
-    # 1024 wavefronts -> 256 splits x 16 heads x (256 + 2) floats.
-    assert f(1, 16, 4, 256, 256, 16384) == 256 * 16 * 258 * 4
-    # Batch 4: at most 4 tiles per split -> 128 splits per request.
-    assert f(4, 16, 4, 256, 256, 16384) == 4 * 128 * 16 * 258 * 4
-    # Batch 1, 4096 tokens: 512 wavefronts with one tile each -> 128 splits.
+    # One request of 16384 tokens = 512 tiles x 4 KV heads: 4 tiles per split keeps
+    # 512 workgroups -> 128 splits x 16 heads x (256 + 2) floats.
+    assert f(1, 16, 4, 256, 256, 16384) == 128 * 16 * 258 * 4
+    # Batch 4: at most 8 tiles per split -> 64 splits per request.
+    assert f(4, 16, 4, 256, 256, 16384) == 4 * 64 * 16 * 258 * 4
+    # Batch 1, 4096 tokens: 512 workgroups with one tile each -> 128 splits.
     assert f(1, 16, 4, 256, 256, 4096) == 128 * 16 * 258 * 4
     assert f(1, 16, 4, 256, 256, 32) == 0          # a single split needs no workspace
     assert f(1, 16, 4, 24, 24, 4096) == 0          # any-shape kernel
