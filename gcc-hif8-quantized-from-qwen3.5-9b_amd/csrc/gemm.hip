@@ -64,15 +64,28 @@ __device__ __forceinline__ void decode16(const uint16_t *lut, const u32x4 q, u32
   hi = u32x4{p[4], p[5], p[6], p[7]};
 }
 
-// Activation codes [rows, K] -> bf16 [rows, K], 16 codes per thread and pass.
+// Codes [rows, K] -> bf16 [rows, K], 16 codes per thread and pass.  The
+// table is computed (one entry per thread), so the first chunk's load goes
+// out before it and stays in flight across the LDS-only barrier; each pass
+// loads the next chunk before decoding the current one (a chunk past the end
+// re-reads the last one, unused).
 __global__ __launch_bounds__(256) void decode_rows_kernel(const uint8_t *__restrict__ a,
                                                           uint16_t *__restrict__ out, size_t chunks) {
   __shared__ __attribute__((aligned(16))) uint16_t lut[256];
-  lut[threadIdx.x] = kDeviceTables.decode_bf16[threadIdx.x];
-  __syncthreads();
-  for (size_t c = size_t(blockIdx.x) * 256 + threadIdx.x; c < chunks; c += size_t(gridDim.x) * 256) {
+  if (chunks == 0) return;
+  const size_t stride = size_t(gridDim.x) * 256;
+  size_t c = size_t(blockIdx.x) * 256 + threadIdx.x;
+  auto fetch = [&](size_t ch) {
+    return *reinterpret_cast<const u32x4 *>(a + (ch < chunks ? ch : chunks - 1) * 16);
+  };
+  u32x4 q = fetch(c);
+  lut[threadIdx.x] = uint16_t(decode_bits(threadIdx.x) >> 16);
+  lds_barrier();
+  for (; c < chunks; c += stride) {
+    const u32x4 cur = q;
+    q = fetch(c + stride);
     u32x4 lo, hi;
-    decode16(lut, *reinterpret_cast<const u32x4 *>(a + c * 16), lo, hi);
+    decode16(lut, cur, lo, hi);
     u32x4 *o = reinterpret_cast<u32x4 *>(out + c * 16);
     o[0] = lo;
     o[1] = hi;
