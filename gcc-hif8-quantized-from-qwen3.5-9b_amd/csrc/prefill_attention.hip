@@ -35,6 +35,7 @@
 // MFMA kernel's set (head size not 64/128/256, Dv != D, G not dividing 16)
 // run a one-wavefront-per-(row, head) kernel.
 #include <stddef.h>
+#include <stdlib.h>
 
 #include <algorithm>
 
@@ -55,6 +56,14 @@ constexpr int kPRows = 64;      // (token, head) rows per workgroup, 16 per wave
 constexpr int kKT = 64;         // keys per tile
 constexpr int kTargetBlocks = 512;
 constexpr int kMinSplitTiles = 2;
+constexpr int kIThreads = 512;  // tile-image kernel: eight wavefronts
+constexpr int kIWaves = kIThreads / 64;
+constexpr int kIRows = 128;     // its (token, head) rows per workgroup
+constexpr int kITargetBlocks = 256;
+
+// Bytes of one decoded 64-key tile image: K rows [64][D], V^T rows [D][64]
+// (16-bit values, swizzled as in LDS), 64 fp32 logit biases, padded to 1 KiB.
+constexpr uint32_t img_bytes(int d) { return (uint32_t(4 * kKT * d + 4 * kKT) + 1023u) / 1024u * 1024u; }
 
 struct PrefillParams {
   const void *query;              // [total_q, Hq, D]
@@ -72,6 +81,8 @@ struct PrefillParams {
   int tokens_per_tile, q_tiles, num_splits, split_tiles, batch, max_len, causal;
   int total_q;                    // rows of query / out; rows at or past it are never touched
   float scale_log2;               // softmax scale * log2(e)
+  uint8_t *img;                   // decoded tile images [batch][hkv][img_tiles] (tile-image path)
+  int img_tiles;                  // 64-key tiles per (request, KV head) in img
 };
 
 template <bool kBf16>
@@ -99,6 +110,155 @@ __device__ __forceinline__ int clamp_len(int len, int max_len) {
 __device__ __forceinline__ int vt_pos(int k) {
   const int half = k & 32, kk = k & 31;
   return half + (kk < 16 ? 8 * (kk >> 2) + (kk & 3) : 8 * ((kk - 16) >> 2) + 4 + (kk & 3));
+}
+
+// Decodes one 64-key tile from the raw rows a thread holds (thread (kq, dc):
+// 16-byte chunk dc of keys kq * kD / 64 + j; bit j of `ok` says the key is
+// present) into K rows [64][kD] and V^T rows [kD][64] in P^T key order, both
+// granule-swizzled, and a per-key logit bias; absent keys become zeros and a
+// -inf bias.  The destinations are LDS or a tile image in global memory with
+// the same layout.
+template <int kD, bool kBf16>
+__device__ __forceinline__ void decode_tile(const float *dec, const u32x4 (&kraw)[kD / 64],
+                                            const u32x4 (&vraw)[kD / 64], const float (&kscl)[kD / 64],
+                                            const float (&vscl)[kD / 64], uint32_t ok, int kq, int dc,
+                                            uint16_t *ks, uint16_t *vt, float *kbias) {
+  constexpr int kKPT = kD / 64;
+  constexpr int kKGran = kD / 8;
+  constexpr int kKSwz = (kKGran < 16 ? kKGran : 16) - 1;
+#pragma unroll
+  for (int j = 0; j < kKPT; ++j) {
+    const int kt = kq * kKPT + j;  // key within the tile
+    const bool kok = (ok >> j) & 1u;
+    const float ksc = kok ? kscl[j] : 0.f;
+    uint32_t kw[4];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) kw[w] = kok ? kraw[j][w] : 0u;
+    uint32_t kp[8];
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      kp[2 * w] = pack2<kBf16>(dec[kw[w] & 0xFFu] * ksc, dec[(kw[w] >> 8) & 0xFFu] * ksc);
+      kp[2 * w + 1] = pack2<kBf16>(dec[(kw[w] >> 16) & 0xFFu] * ksc, dec[kw[w] >> 24] * ksc);
+    }
+    const int sw = (kt ^ (kt >> 4)) & kKSwz;
+    uint16_t *krow = ks + kt * kD;
+    *reinterpret_cast<u32x4 *>(krow + 8 * ((2 * dc) ^ sw)) = u32x4{kp[0], kp[1], kp[2], kp[3]};
+    *reinterpret_cast<u32x4 *>(krow + 8 * ((2 * dc + 1) ^ sw)) = u32x4{kp[4], kp[5], kp[6], kp[7]};
+    if (dc == 0) kbias[kt] = kok ? 0.f : -__builtin_inff();
+  }
+  // V transposed: dim 16 dc + i', kKPT consecutive keys at consecutive
+  // positions.  Odd chunks walk their dims in the order i ^ 1, so the four
+  // rows one store instruction writes alternate between the two bank halves.
+  {
+    const int pos = vt_pos(kq * kKPT);
+    float vsc[kKPT];
+    uint32_t vw[kKPT][4];
+#pragma unroll
+    for (int j = 0; j < kKPT; ++j) {
+      const bool vok = (ok >> j) & 1u;
+      vsc[j] = vok ? vscl[j] : 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) vw[j][w] = vok ? vraw[j][w] : 0u;
+    }
+    const int flip = dc & 1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int ii = i ^ flip;          // same 4-byte word as i
+      const int dim = 16 * dc + ii;
+      const int sh = 8 * (ii & 3);
+      float v[kKPT];
+#pragma unroll
+      for (int j = 0; j < kKPT; ++j) v[j] = dec[(vw[j][i >> 2] >> sh) & 0xFFu] * vsc[j];
+      const int gran = (pos >> 3) ^ (dim & 7);
+      uint16_t *dst = vt + dim * kKT + 8 * gran + (pos & 7);
+      if constexpr (kKPT == 4) {
+        *reinterpret_cast<u32x2 *>(dst) = u32x2{pack2<kBf16>(v[0], v[1]), pack2<kBf16>(v[2], v[3])};
+      } else if constexpr (kKPT == 2) {
+        *reinterpret_cast<uint32_t *>(dst) = pack2<kBf16>(v[0], v[1]);
+      } else {
+        *dst = float_to_half_bits<kBf16>(v[0]);
+      }
+    }
+  }}
+
+// One 64-key tile of a wavefront's 16 query rows, K ([key][D]) and V^T
+// ([D][key] in P^T key order) in LDS with the granule swizzles above:
+// S^T = K Q^T, the causal / length mask (keys at or past `lim`) and the
+// per-key bias, the online softmax update of (m, l) in base 2, and
+// O^T += V^T P^T with P rounded to the query dtype.
+template <int kD, bool kBf16>
+__device__ __forceinline__ void tile_math(const uint16_t *ks, const uint16_t *vt, const float *kbias,
+                                          const u32x4 (&qf)[kD / 32], int k0, int lim, float scale_log2, int n,
+                                          int g, float &m, float &l, f32x4_t (&oacc)[kD / 16]) {
+  constexpr int kQSteps = kD / 32;
+  constexpr int kDB = kD / 16;
+  constexpr int kKGran = kD / 8;
+  constexpr int kKSwz = (kKGran < 16 ? kKGran : 16) - 1;
+  // S^T = K Q^T: four 16-key blocks.
+  f32x4_t sacc[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    sacc[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    const int key = 16 * kb + n;
+    const int sw = (key ^ (key >> 4)) & kKSwz;
+    const uint16_t *krow = ks + key * kD;
+#pragma unroll
+    for (int i = 0; i < kQSteps; ++i) {
+      const u32x4 a = *reinterpret_cast<const u32x4 *>(krow + 8 * ((4 * i + g) ^ sw));
+      sacc[kb] = mfma16<kBf16>(a, qf[i], sacc[kb]);
+    }
+  }
+  // Mask and online softmax (base 2): lane (g, n) holds keys 16 kb + 4 g + e of row n.
+  float x[16];
+  float tmax = -__builtin_inff();
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    const f32x4_t bias = *reinterpret_cast<const f32x4_t *>(kbias + 16 * kb + 4 * g);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int key = k0 + 16 * kb + 4 * g + e;
+      const float v = sacc[kb][e] * scale_log2 + bias[e];
+      x[4 * kb + e] = key < lim ? v : -__builtin_inff();
+      tmax = fmaxf(tmax, x[4 * kb + e]);
+    }
+  }
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
+  const float m_new = fmaxf(m, tmax);
+  const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
+  const float alpha = __builtin_amdgcn_exp2f(m - m_use);
+  float pw[16], psum = 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    pw[e] = __builtin_amdgcn_exp2f(x[e] - m_use);
+    psum += pw[e];
+  }
+  l = l * alpha + psum;
+  if (!__all(m_new == m || m == -__builtin_inff())) {
+#pragma unroll
+    for (int db = 0; db < kDB; ++db) oacc[db] *= alpha;
+  }
+  m = m_new;
+  // P^T operands of the two 32-key steps.
+  u32x4 pf[2];
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    const float *a = pw + 8 * s;      // keys 32 s + 4 g + e
+    const float *c = pw + 8 * s + 4;  // keys 32 s + 16 + 4 g + e
+    pf[s] = u32x4{pack2<kBf16>(a[0], a[1]), pack2<kBf16>(a[2], a[3]), pack2<kBf16>(c[0], c[1]),
+                  pack2<kBf16>(c[2], c[3])};
+  }
+  // O^T += V^T P^T.
+#pragma unroll
+  for (int db = 0; db < kDB; ++db) {
+    const int dim = 16 * db + n;
+    const uint16_t *vrow = vt + dim * kKT;
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      const u32x4 a = *reinterpret_cast<const u32x4 *>(vrow + 8 * ((4 * s + g) ^ (dim & 7)));
+      oacc[db] = mfma16<kBf16>(a, pf[s], oacc[db]);
+    }
+  }
 }
 
 // Block ids: heavy query tiles (late in the prompt, more keys) first.
@@ -215,134 +375,161 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
 
   for (int it = 0; it < ntiles; ++it) {
     const int k0 = s_k0 + it * kKT;
-    // Decode this tile's raw rows into LDS; absent keys become zeros and a
-    // -inf logit bias.
-#pragma unroll
-    for (int j = 0; j < kKPT; ++j) {
-      const int kt = kq * kKPT + j;  // key within the tile
-      const bool kok = (ok >> j) & 1u;
-      const float ksc = kok ? kscl[j] : 0.f;
-      uint32_t kw[4];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) kw[w] = kok ? kraw[j][w] : 0u;
-      uint32_t kp[8];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        kp[2 * w] = pack2<kBf16>(dec[kw[w] & 0xFFu] * ksc, dec[(kw[w] >> 8) & 0xFFu] * ksc);
-        kp[2 * w + 1] = pack2<kBf16>(dec[(kw[w] >> 16) & 0xFFu] * ksc, dec[kw[w] >> 24] * ksc);
-      }
-      const int sw = (kt ^ (kt >> 4)) & kKSwz;
-      uint16_t *krow = ks + kt * kD;
-      *reinterpret_cast<u32x4 *>(krow + 8 * ((2 * dc) ^ sw)) = u32x4{kp[0], kp[1], kp[2], kp[3]};
-      *reinterpret_cast<u32x4 *>(krow + 8 * ((2 * dc + 1) ^ sw)) = u32x4{kp[4], kp[5], kp[6], kp[7]};
-      if (dc == 0) kbias[kt] = kok ? 0.f : -__builtin_inff();
-    }
-    // V transposed: dim 16 dc + i', kKPT consecutive keys at consecutive
-    // positions.  Odd chunks walk their dims in the order i ^ 1, so the four
-    // rows one store instruction writes alternate between the two bank halves.
-    {
-      const int pos = vt_pos(kq * kKPT);
-      float vsc[kKPT];
-      uint32_t vw[kKPT][4];
-#pragma unroll
-      for (int j = 0; j < kKPT; ++j) {
-        const bool vok = (ok >> j) & 1u;
-        vsc[j] = vok ? vscl[j] : 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) vw[j][w] = vok ? vraw[j][w] : 0u;
-      }
-      const int flip = dc & 1;
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int ii = i ^ flip;          // same 4-byte word as i
-        const int dim = 16 * dc + ii;
-        const int sh = 8 * (ii & 3);
-        float v[kKPT];
-#pragma unroll
-        for (int j = 0; j < kKPT; ++j) v[j] = dec[(vw[j][i >> 2] >> sh) & 0xFFu] * vsc[j];
-        const int gran = (pos >> 3) ^ (dim & 7);
-        uint16_t *dst = vt + dim * kKT + 8 * gran + (pos & 7);
-        if constexpr (kKPT == 4) {
-          *reinterpret_cast<u32x2 *>(dst) = u32x2{pack2<kBf16>(v[0], v[1]), pack2<kBf16>(v[2], v[3])};
-        } else if constexpr (kKPT == 2) {
-          *reinterpret_cast<uint32_t *>(dst) = pack2<kBf16>(v[0], v[1]);
-        } else {
-          *dst = float_to_half_bits<kBf16>(v[0]);
-        }
-      }
-    }
+    decode_tile<kD, kBf16>(dec, kraw, vraw, kscl, vscl, ok, kq, dc, ks, vt, kbias);
     lds_barrier();
     if (it + 1 < ntiles) {  // in flight during this tile's math
       issue(k0 + kKT, blk_next);
       if (it + 2 < ntiles) blk_next = block_of(k0 + 2 * kKT);
     }
 
-    // S^T = K Q^T: four 16-key blocks.
-    f32x4_t sacc[4];
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      sacc[kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-      const int key = 16 * kb + n;
-      const int sw = (key ^ (key >> 4)) & kKSwz;
-      const uint16_t *krow = ks + key * kD;
-#pragma unroll
-      for (int i = 0; i < kQSteps; ++i) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(krow + 8 * ((4 * i + g) ^ sw));
-        sacc[kb] = mfma16<kBf16>(a, qf[i], sacc[kb]);
-      }
-    }
-    // Mask and online softmax (base 2): lane (g, n) holds keys 16 kb + 4 g + e of row n.
-    float x[16];
-    float tmax = -__builtin_inff();
-#pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const f32x4_t bias = *reinterpret_cast<const f32x4_t *>(kbias + 16 * kb + 4 * g);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = k0 + 16 * kb + 4 * g + e;
-        const float v = sacc[kb][e] * p.scale_log2 + bias[e];
-        x[4 * kb + e] = key < lim ? v : -__builtin_inff();
-        tmax = fmaxf(tmax, x[4 * kb + e]);
-      }
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-    const float m_new = fmaxf(m, tmax);
-    const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m - m_use);
-    float pw[16], psum = 0.f;
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      pw[e] = __builtin_amdgcn_exp2f(x[e] - m_use);
-      psum += pw[e];
-    }
-    l = l * alpha + psum;
-    if (!__all(m_new == m || m == -__builtin_inff())) {
-#pragma unroll
-      for (int db = 0; db < kDB; ++db) oacc[db] *= alpha;
-    }
-    m = m_new;
-    // P^T operands of the two 32-key steps.
-    u32x4 pf[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      const float *a = pw + 8 * s;      // keys 32 s + 4 g + e
-      const float *c = pw + 8 * s + 4;  // keys 32 s + 16 + 4 g + e
-      pf[s] = u32x4{pack2<kBf16>(a[0], a[1]), pack2<kBf16>(a[2], a[3]), pack2<kBf16>(c[0], c[1]),
-                    pack2<kBf16>(c[2], c[3])};
-    }
-    // O^T += V^T P^T.
-#pragma unroll
-    for (int db = 0; db < kDB; ++db) {
-      const int dim = 16 * db + n;
-      const uint16_t *vrow = vt + dim * kKT;
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        const u32x4 a = *reinterpret_cast<const u32x4 *>(vrow + 8 * ((4 * s + g) ^ (dim & 7)));
-        oacc[db] = mfma16<kBf16>(a, pf[s], oacc[db]);
-      }
-    }
+    tile_math<kD, kBf16>(ks, vt, kbias, qf, k0, lim, p.scale_log2, n, g, m, l, oacc);
     lds_barrier();  // the tile's LDS is rewritten by the next iteration
+  }
+
+  float lt = l + __shfl_xor(l, 16, kWave);
+  lt += __shfl_xor(lt, 32, kWave);
+  if (!row_ok) return;
+  if (p.num_splits == 1) {
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    uint16_t *o = static_cast<uint16_t *>(p.out) + out_row + 4 * g;
+#pragma unroll
+    for (int db = 0; db < kDB; ++db)
+      *reinterpret_cast<u32x2 *>(o + 16 * db) =
+          u32x2{pack2<kBf16>(oacc[db][0] * inv, oacc[db][1] * inv), pack2<kBf16>(oacc[db][2] * inv, oacc[db][3] * inv)};
+  } else {
+    float *po = p.part_o + part * kD + 4 * g;
+    if (ntiles > 0) {
+#pragma unroll
+      for (int db = 0; db < kDB; ++db) *reinterpret_cast<f32x4_t *>(po + 16 * db) = oacc[db];
+    }
+    if (g == 0) {
+      p.part_ml[2 * part] = ntiles > 0 ? m : -__builtin_inff();
+      p.part_ml[2 * part + 1] = ntiles > 0 ? lt : 0.f;
+    }
+  }
+}
+
+// Tile images for the prefill path (long query ranges, where every query tile
+// of a (request, KV head) would decode the same pages again): workgroup
+// (b, h, tile) decodes keys 64 tile .. + 63 of request b, KV head h once into
+// global memory in exactly the layout the attention step copies into LDS.
+// Tiles at or past the request's length are not written (never read).
+template <int kD, bool kBf16, typename BtT>
+__global__ __launch_bounds__(kPThreads) void prefill_decode_tiles_kernel(const PrefillParams p) {
+  constexpr int kKPT = kD / 64;
+  constexpr int kGroups = kKT / kKPT;
+  constexpr uint32_t kImg = img_bytes(kD);
+  static_assert(kKT * (kD / 16) == kPThreads * kKPT, "thread map covers the tile");
+  __shared__ float dec[256];
+  const int tid = threadIdx.x;
+  const int tile = int(blockIdx.x) % p.img_tiles;
+  const int bh = int(blockIdx.x) / p.img_tiles;
+  const int h = bh % p.hkv, b = bh / p.hkv;
+  const int kl = clamp_len(p.seq_lens[b], p.max_len);
+  const int k0 = tile * kKT;
+  if (k0 >= kl) return;  // uniform
+  const int kq = tid % kGroups, dc = tid / kGroups;
+  const BtT *bt = static_cast<const BtT *>(p.block_table) + size_t(b) * p.bt_stride;
+  const int key0 = k0 + kq * kKPT;  // kKPT keys in one cache block: block_size % kKPT == 0
+  const int safe = min(key0, p.max_len - 1);
+  const int idx = p.log2_block_size >= 0 ? safe >> p.log2_block_size : safe / p.block_size;
+  const int64_t blk = int64_t(bt[idx]);
+  const bool blk_ok = blk >= 0 && blk < p.num_blocks;
+  const int in_blk = p.log2_block_size >= 0 ? key0 & (p.block_size - 1) : key0 % p.block_size;
+  const int64_t rec = int64_t(p.hkv) * (kD + 4);
+  const int64_t row0 = blk_ok ? (blk * p.block_size + in_blk) * rec + int64_t(h) * (kD + 4) : 0;
+  u32x4 kraw[kKPT], vraw[kKPT];
+  float kscl[kKPT], vscl[kKPT];
+  uint32_t ok = 0;
+#pragma unroll
+  for (int j = 0; j < kKPT; ++j) {
+    const bool kok = blk_ok && key0 + j < kl;
+    const int64_t off = kok ? row0 + j * rec : 0;  // absent keys read the cache's first row, then drop it
+    kraw[j] = *reinterpret_cast<const u32x4_a4 *>(p.key_cache + off + 16 * dc);
+    vraw[j] = *reinterpret_cast<const u32x4_a4 *>(p.value_cache + off + 16 * dc);
+    kscl[j] = *reinterpret_cast<const float *>(p.key_cache + off + kD);
+    vscl[j] = *reinterpret_cast<const float *>(p.value_cache + off + kD);
+    ok |= uint32_t(kok) << j;
+  }
+  dec[tid] = __uint_as_float(decode_bits(uint32_t(tid)));
+  lds_barrier();
+  uint8_t *im = p.img + ((size_t(b) * p.hkv + h) * p.img_tiles + tile) * kImg;
+  uint16_t *ks = reinterpret_cast<uint16_t *>(im);
+  decode_tile<kD, kBf16>(dec, kraw, vraw, kscl, vscl, ok, kq, dc, ks, ks + kKT * kD,
+                         reinterpret_cast<float *>(im + 4 * kKT * kD));
+}
+
+// Prefill over tile images: a workgroup of eight wavefronts owns (request,
+// KV head, query tile of 128 / G tokens, key split), 128 rows, 16 per
+// wavefront; per 64-key tile it copies the image into one of two LDS stages
+// by DMA (global_load_lds_dwordx4, 1 KiB per instruction) while the previous
+// tile's math runs, with one barrier per tile: after it, the tile has landed
+// for every wavefront and every wavefront is done with the stage the next
+// copy overwrites.
+template <int kD, bool kBf16>
+__global__ __launch_bounds__(kIThreads) void paged_prefill_attention_img_kernel(const PrefillParams p) {
+  constexpr int kDB = kD / 16;
+  constexpr int kQSteps = kD / 32;
+  constexpr uint32_t kImg = img_bytes(kD);
+  constexpr int kCopies = int(kImg / 1024);
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int n = lane & 15, g = lane >> 4;
+  const int split = int(blockIdx.x) % p.num_splits;
+  const int rest = int(blockIdx.x) / p.num_splits;
+  const int h = rest % p.hkv;
+  const int rb = rest / p.hkv;
+  const int b = rb % p.batch;
+  const int qt = p.q_tiles - 1 - rb / p.batch;
+  const int q_begin = max(p.query_start_loc[b], 0);
+  const int ql = min(p.query_start_loc[b + 1], p.total_q) - q_begin;
+  const int tok0 = qt * p.tokens_per_tile;
+  if (tok0 >= ql) return;  // uniform
+  const int kl = clamp_len(p.seq_lens[b], p.max_len);
+  const int r = wave * 16 + n;
+  const int tok = tok0 + (r >> p.log2_group);
+  const int qhead = h * p.group + (r & (p.group - 1));
+  const bool row_ok = tok < ql;
+  const int tok_last = min(tok0 + p.tokens_per_tile, ql) - 1;
+  const int k_vis = p.causal ? min(kl, kl - ql + tok_last + 1) : kl;
+  const int s_k0 = split * p.split_tiles * kKT;
+  const int s_k1 = min(s_k0 + p.split_tiles * kKT, k_vis);
+  const int ntiles = s_k1 > s_k0 ? (s_k1 - s_k0 + kKT - 1) / kKT : 0;
+  const int lim = !row_ok ? s_k0 : (p.causal ? min(s_k1, kl - ql + tok + 1) : s_k1);
+  const size_t item = (size_t(b) * p.q_tiles + qt) * p.hkv + h;
+  const size_t part = (item * p.num_splits + split) * kIRows + r;
+  const size_t out_row = (size_t(q_begin + tok) * p.hq + qhead) * kD;
+
+  // Tile t of this (request, KV head) lands in stage s: copy instruction j
+  // (wavefront j % 8) moves bytes 1024 j .. + 1023, lane i 16 of them.
+  const uint8_t *img = p.img + (size_t(b) * p.hkv + h) * p.img_tiles * kImg + 16 * lane;
+  const uint32_t lds0 = lds_address(smem_raw);
+  const int t0 = s_k0 / kKT;
+  auto copy = [&](int t, int stage) {
+    const uint8_t *src = img + size_t(t) * kImg;
+    for (int j = wave; j < kCopies; j += kIWaves) dma16(src + 1024 * j, lds0 + uint32_t(stage) * kImg + 1024u * j);
+  };
+  u32x4 qf[kQSteps];
+  {
+    const uint16_t *q = static_cast<const uint16_t *>(p.query) + out_row + 8 * g;
+#pragma unroll
+    for (int i = 0; i < kQSteps; ++i)
+      qf[i] = row_ok ? *reinterpret_cast<const u32x4 *>(q + 32 * i) : u32x4{0, 0, 0, 0};
+  }
+  if (ntiles > 0) copy(t0, 0);
+  f32x4_t oacc[kDB];
+#pragma unroll
+  for (int db = 0; db < kDB; ++db) oacc[db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  float m = -__builtin_inff(), l = 0.f;
+  for (int it = 0; it < ntiles; ++it) {
+    wait_vmcnt<0>();  // this wavefront's copies of tile it (the only ones in flight)
+    lds_barrier();
+    if (it + 1 < ntiles) copy(t0 + it + 1, (it + 1) & 1);
+    const uint8_t *st = smem_raw + (it & 1) * kImg;
+    const uint16_t *ks = reinterpret_cast<const uint16_t *>(st);
+    tile_math<kD, kBf16>(ks, ks + kKT * kD, reinterpret_cast<const float *>(st + 4 * kKT * kD), qf,
+                         s_k0 + it * kKT, lim, p.scale_log2, n, g, m, l, oacc);
   }
 
   float lt = l + __shfl_xor(l, 16, kWave);
@@ -377,7 +564,7 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
 // outputs are never read.
 constexpr int kMaxCombineSplits = 64;
 
-template <bool kBf16>
+template <bool kBf16, int kRows>
 __global__ __launch_bounds__(kPThreads) void prefill_combine_kernel(const PrefillParams p) {
   __shared__ float wsh[kMaxCombineSplits];
   __shared__ f32x4_t red[4][64];
@@ -392,10 +579,10 @@ __global__ __launch_bounds__(kPThreads) void prefill_combine_kernel(const Prefil
   const int tok = qt * p.tokens_per_tile + (r >> p.log2_group);
   if (tok >= ql) return;  // uniform: a row past the request
   const int tid = threadIdx.x, lane = tid & 63, grp = tid >> 6;
-  const size_t base = size_t(item) * p.num_splits * kPRows + r;  // part index of split 0
+  const size_t base = size_t(item) * p.num_splits * kRows + r;  // part index of split 0
   if (grp == 0) {
     const bool have = lane < p.num_splits;
-    const size_t pi = base + size_t(have ? lane : 0) * kPRows;
+    const size_t pi = base + size_t(have ? lane : 0) * kRows;
     const float ms = have ? p.part_ml[2 * pi] : -__builtin_inff();
     const float ls = have ? p.part_ml[2 * pi + 1] : 0.f;
     const float mx = wave_max(ms);
@@ -410,7 +597,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_combine_kernel(const Prefil
 #pragma unroll 4
     for (int s = grp; s < p.num_splits; s += 4) {
       const float w = wsh[s];
-      if (w != 0.f) acc += w * *reinterpret_cast<const f32x4_t *>(p.part_o + (base + size_t(s) * kPRows) * p.dv + 4 * lane);
+      if (w != 0.f) acc += w * *reinterpret_cast<const f32x4_t *>(p.part_o + (base + size_t(s) * kRows) * p.dv + 4 * lane);
     }
   }
   red[grp][lane] = acc;
@@ -515,18 +702,37 @@ bool prefill_mfma_shape(int64_t d, int64_t dv, int64_t group, int64_t block_size
 
 struct PrefillPlan {
   int tokens_per_tile, q_tiles, num_splits, split_tiles;
+  bool img;       // tile-image path: pages decoded once, then attention over the images
+  int img_tiles;  // 64-key tiles per (request, KV head) in the images
+  int rows;       // (token, head) rows per workgroup
 };
 
-// Query tiles of 64 / G tokens; key splits while the (request, query tile,
-// KV head) items leave fewer than ~512 workgroups, each split at least two
-// 64-key tiles.
+// The in-kernel decode path when at most two query tiles of 64 rows cover
+// the longest query (every page is decoded at most twice; measured on
+// MI355X, 17 rows x 4 heads over 4096 keys: B=1 29.6 vs 29.1 us, B=4 47.1 vs
+// 55.6 us with images); beyond that each query tile would decode the same
+// pages again, and the pages are decoded once into tile images first (64
+// rows per workgroup -> 128; 512 rows over 4096 keys: B=4 461 -> 214 us).
+// Query tiles of rows / G tokens; key splits while the (request, query tile,
+// KV head) items leave fewer than ~512 (in-kernel) or ~256 (images, one
+// eight-wave workgroup per CU) workgroups, each split at least two 64-key
+// tiles.
 PrefillPlan plan_prefill(int64_t batch, int64_t hkv, int64_t group, int64_t max_query_len, int64_t max_len) {
   PrefillPlan pl{};
-  pl.tokens_per_tile = int(kPRows / group);
+  const int64_t kv_tiles = std::max<int64_t>((max_len + kKT - 1) / kKT, 1);
+  static const int img_env = [] {
+    const char *v = getenv("HIF8_PREFILL_IMAGES");  // tuning: 0 never, 1 for every multi-tile query
+    return v && *v ? atoi(v) : -1;
+  }();
+  pl.img = img_env == 0 ? false
+                       : std::max<int64_t>(max_query_len, 1) * group > (img_env == 1 ? 1 : 2) * kPRows;
+  pl.rows = pl.img ? kIRows : kPRows;
+  pl.img_tiles = pl.img ? int(kv_tiles) : 0;
+  pl.tokens_per_tile = int(pl.rows / group);
   pl.q_tiles = int((std::max<int64_t>(max_query_len, 1) + pl.tokens_per_tile - 1) / pl.tokens_per_tile);
   const int64_t items = batch * pl.q_tiles * hkv;
-  const int64_t kv_tiles = std::max<int64_t>((max_len + kKT - 1) / kKT, 1);
-  int64_t splits = (kTargetBlocks + items - 1) / items;
+  const int64_t target = pl.img ? kITargetBlocks : kTargetBlocks;
+  int64_t splits = (target + items - 1) / items;
   if (splits > kv_tiles) splits = kv_tiles;
   if (splits < 1) splits = 1;
   int64_t per = (kv_tiles + splits - 1) / splits;
@@ -547,8 +753,23 @@ int launch_prefill_mfma(const PrefillParams &p, hipStream_t stream) {
   const unsigned blocks = unsigned(int64_t(p.q_tiles) * p.batch * p.hkv * p.num_splits);
   paged_prefill_attention_kernel<kD, kBf16, BtT><<<blocks, kPThreads, smem, stream>>>(p);
   if (p.num_splits > 1)
-    prefill_combine_kernel<kBf16><<<dim3(unsigned(int64_t(p.batch) * p.q_tiles * p.hkv), kPRows), kPThreads, 0,
-                                    stream>>>(p);
+    prefill_combine_kernel<kBf16, kPRows><<<dim3(unsigned(int64_t(p.batch) * p.q_tiles * p.hkv), kPRows), kPThreads,
+                                            0, stream>>>(p);
+  return HIF8_OK;
+}
+
+template <int kD, bool kBf16, typename BtT>
+int launch_prefill_img(const PrefillParams &p, hipStream_t stream) {
+  prefill_decode_tiles_kernel<kD, kBf16, BtT>
+      <<<unsigned(int64_t(p.batch) * p.hkv * p.img_tiles), kPThreads, 0, stream>>>(p);
+  const void *fn = reinterpret_cast<const void *>(&paged_prefill_attention_img_kernel<kD, kBf16>);
+  const size_t smem = 2 * size_t(img_bytes(kD));
+  if (const int st = reserve_dynamic_lds(fn, smem, "hif8_paged_prefill_attention")) return st;
+  const unsigned blocks = unsigned(int64_t(p.q_tiles) * p.batch * p.hkv * p.num_splits);
+  paged_prefill_attention_img_kernel<kD, kBf16><<<blocks, kIThreads, smem, stream>>>(p);
+  if (p.num_splits > 1)
+    prefill_combine_kernel<kBf16, kIRows><<<dim3(unsigned(int64_t(p.batch) * p.q_tiles * p.hkv), kIRows), kPThreads,
+                                            0, stream>>>(p);
   return HIF8_OK;
 }
 
@@ -557,6 +778,13 @@ int launch_prefill(const PrefillParams &p, bool mfma, int64_t total_q, hipStream
   if (!mfma) {
     paged_prefill_attention_simple<kBf16, BtT><<<unsigned(total_q * p.hq), kWave, 0, stream>>>(p, int(total_q));
     return HIF8_OK;
+  }
+  if (p.img) {
+    switch (p.d) {
+      case 64: return launch_prefill_img<64, kBf16, BtT>(p, stream);
+      case 128: return launch_prefill_img<128, kBf16, BtT>(p, stream);
+      default: return launch_prefill_img<256, kBf16, BtT>(p, stream);
+    }
   }
   switch (p.d) {
     case 64: return launch_prefill_mfma<64, kBf16, BtT>(p, stream);
@@ -579,9 +807,10 @@ extern "C" size_t hif8_paged_prefill_attention_workspace_size(int64_t batch, int
   const int64_t group = num_heads / num_kv_heads;
   if (!prefill_mfma_shape(head_size, head_size_v, group, 4)) return 0;  // the simple kernel needs none
   const PrefillPlan pl = plan_prefill(batch, num_kv_heads, group, max_query_len, max_seq_len);
-  if (pl.num_splits <= 1) return 0;
-  const size_t parts = size_t(batch) * pl.q_tiles * num_kv_heads * pl.num_splits * kPRows;
-  return parts * size_t(head_size_v + 2) * sizeof(float);
+  const size_t images = pl.img ? size_t(batch) * num_kv_heads * pl.img_tiles * img_bytes(int(head_size)) : 0;
+  if (pl.num_splits <= 1) return images;
+  const size_t parts = size_t(batch) * pl.q_tiles * num_kv_heads * pl.num_splits * pl.rows;
+  return images + parts * size_t(head_size_v + 2) * sizeof(float);
 }
 
 extern "C" int hif8_paged_prefill_attention(const void *query, int q_dtype, const uint8_t *key_cache,
@@ -656,19 +885,27 @@ extern "C" int hif8_paged_prefill_attention(const void *query, int q_dtype, cons
     p.q_tiles = pl.q_tiles;
     p.num_splits = pl.num_splits;
     p.split_tiles = pl.split_tiles;
-    if (int64_t(p.q_tiles) * batch * num_kv_heads * p.num_splits > 0x7FFFFFFFll)
+    p.img = nullptr;
+    p.img_tiles = pl.img_tiles;
+    if (int64_t(p.q_tiles) * batch * num_kv_heads * p.num_splits > 0x7FFFFFFFll ||
+        batch * num_kv_heads * int64_t(pl.img_tiles) > 0x7FFFFFFFll)
       return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: too many query tiles");
-    if (pl.num_splits > 1) {
-      const size_t need = hif8_paged_prefill_attention_workspace_size(batch, num_heads, num_kv_heads, head_size,
-                                                                      head_size_v, max_query_len, max_seq_len);
+    const size_t need = hif8_paged_prefill_attention_workspace_size(batch, num_heads, num_kv_heads, head_size,
+                                                                    head_size_v, max_query_len, max_seq_len);
+    if (need > 0) {
       if (!workspace || workspace_bytes < need)
         return fail(HIF8_ERR_INVALID_ARGUMENT,
                     "hif8_paged_prefill_attention: workspace of %zu bytes required (got %zu)", need,
                     workspace_bytes);
       if (!aligned(workspace, 16))
         return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: workspace must be 16-byte aligned");
-      p.part_o = static_cast<float *>(workspace);
-      p.part_ml = p.part_o + size_t(batch) * pl.q_tiles * num_kv_heads * pl.num_splits * kPRows * head_size_v;
+      uint8_t *ws = static_cast<uint8_t *>(workspace);
+      const size_t images = pl.img ? size_t(batch) * num_kv_heads * pl.img_tiles * img_bytes(int(head_size)) : 0;
+      if (pl.img) p.img = ws;
+      if (pl.num_splits > 1) {
+        p.part_o = reinterpret_cast<float *>(ws + images);
+        p.part_ml = p.part_o + size_t(batch) * pl.q_tiles * num_kv_heads * pl.num_splits * pl.rows * head_size_v;
+      }
     }
   } else {
     p.log2_group = 0;
