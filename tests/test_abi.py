@@ -137,17 +137,22 @@ def test_gemm_workspace_query_follows_the_split_plan(lib):
 
 
 def test_prefill_attention_contract_and_workspace_plan(lib):
-    """Multi-token paged attention: the key-split workspace follows the plan
-    (64 / G tokens per query tile, splits while the tiles leave < 512
-    workgroups, two or more 64-key tiles per split), and invalid arguments are
-    rejected before any launch."""
+    """Multi-token paged attention: the workspace follows the plan (up to two
+    query tiles of 64 / G tokens: in-kernel page decode, key splits while the
+    tiles leave < 512 workgroups; more: tile images of every 64-key tile,
+    66560 bytes each at D=256, and 128 / G tokens per query tile with splits
+    below 256 workgroups; two or more 64-key tiles per split), and invalid
+    arguments are rejected before any launch."""
     size = lib.hif8_paged_prefill_attention_workspace_size
     size.argtypes = [ctypes.c_int64] * 7
     size.restype = ctypes.c_size_t
     # B=1, q 17, ctx 4096, G 4: 2 query tiles x 4 heads, 64 key tiles in 32 splits of 2.
     assert size(1, 16, 4, 256, 256, 17, 4096) == 1 * 2 * 4 * 32 * 64 * (256 + 2) * 4
-    # Enough query tiles to fill the GPU: no split, no workspace.
-    assert size(4, 16, 4, 256, 256, 512, 4096) == 0
+    # B=4, q 512: tile images (4 x 4 heads x 64 tiles); 16 query tiles x 4 heads x 4 fill
+    # the 256 workgroups, no split.
+    assert size(4, 16, 4, 256, 256, 512, 4096) == 4 * 4 * 64 * 66560
+    # B=1, q 512: images + 4 splits of 16 tiles for 16 query tiles x 4 heads of 128 rows.
+    assert size(1, 16, 4, 256, 256, 512, 4096) == 4 * 64 * 66560 + 16 * 4 * 4 * 128 * (256 + 2) * 4
     # Shapes for the one-wavefront kernel need none.
     assert size(1, 12, 4, 64, 64, 17, 4096) == 0 and size(1, 16, 4, 24, 24, 17, 4096) == 0
     assert size(0, 16, 4, 256, 256, 17, 4096) == 0 and size(1, 15, 4, 256, 256, 17, 4096) == 0
