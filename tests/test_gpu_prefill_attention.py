@@ -9,8 +9,10 @@ pages, shuffled page table) at q_len in {1, 17, 512} over ctx {512, 4096};
 ragged batches with empty requests; causal off; rows whose positions precede
 the first key; key splits with the combine; other head sizes, GQA groups and
 block sizes; fp16 queries; int64 tables; mixed row scales; the any-shape
-kernel.  A bound relative to each output row's magnitude catches indexing
-errors that the absolute tolerance would hide."""
+kernel.  Queries of more than two 64-row tiles (rows = tokens x query
+heads per KV head) run the tile-image path, shorter ones the in-kernel page
+decode; both appear above.  A bound relative to each output row's magnitude
+catches indexing errors that the absolute tolerance would hide."""
 
 import math
 
@@ -149,11 +151,13 @@ def test_prefill_any_shape_kernel(native_ops, device, hq, hkv, d, dv, bs, lens, 
 
 
 def test_prefill_is_deterministic(native_ops, device):
+    # 30 rows: the in-kernel page decode; 100 rows: tile images, with key splits.
     kc, vc, table = build_cache(device, [4096], 4, 256, 128, 21)
-    q = randn((30, 16, 256), 22)
-    a = _run_op(device, q, kc, vc, table, [4096], [30], 0.0625, True)
-    b = _run_op(device, q, kc, vc, table, [4096], [30], 0.0625, True)
-    assert torch.equal(a, b)
+    for rows in (30, 100):
+        q = randn((rows, 16, 256), 22)
+        a = _run_op(device, q, kc, vc, table, [4096], [rows], 0.0625, True)
+        b = _run_op(device, q, kc, vc, table, [4096], [rows], 0.0625, True)
+        assert torch.equal(a, b), rows
 
 
 def test_prefill_api_validation(native_ops, device):
