@@ -505,7 +505,7 @@ def cpu_model() -> str:
 
 
 def c1_cpu_baseline(threads: int, runs: int = 5, warmup: int = 2) -> dict:
-    """BASELINE configs[0] timed on the host: the torch-CPU
+    """BASELINE configs[0] timed on the host's CPU threads: the torch-CPU
     restatement of the reference's CPU path - static encode of x (x / scale,
     saturate, LUT encode), then decode-LUT weights x channel scale and one fp32
     matmul with the decoded activation (tests/test_npu_ops.py:334-336).  Median
