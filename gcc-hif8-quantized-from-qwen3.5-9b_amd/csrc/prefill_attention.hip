@@ -583,60 +583,58 @@ __global__ __launch_bounds__(kWaves * 64) void paged_prefill_attention_img_kerne
   }
 }
 
-// Merges the key splits of one (query tile, KV head) row:
-//   M = max_s m_s, w_s = 2^(m_s - M), out = sum_s w_s O_s / sum_s w_s l_s.
-// One workgroup per row: wavefront 0 reads every split's (m, l) at once (one
-// split per lane) and leaves the weights in LDS; then the four wavefronts take
-// every fourth split, each lane four output dims, and their sums meet in LDS.
-// Splits with weight 0 (no key) are skipped, so their (unwritten) partial
-// outputs are never read.
+// Merges the key splits of each (query tile, KV head) row:
+//   M = max_s m_s, w_s = 2^(m_s - M), out = sum_s w_s O_s / sum_s w_s l_s,
+// splits added in order.  One wavefront per row, four rows per workgroup:
+// lane s reads split s's (m, l); then each lane adds its four output dims of
+// every split, eight splits' loads issued before their adds.  Splits with
+// weight 0 (no key) are skipped, so their unwritten partial outputs are
+// never read.  (One workgroup per row with the splits spread over four
+// wavefronts measured 11.7 us for 8192 rows of 4 splits.)
 constexpr int kMaxCombineSplits = 64;
 
 template <bool kBf16, int kRows>
 __global__ __launch_bounds__(kPThreads) void prefill_combine_kernel(const PrefillParams p) {
-  __shared__ float wsh[kMaxCombineSplits];
-  __shared__ f32x4_t red[4][64];
-  __shared__ float total_sh;
   const int item = blockIdx.x;
-  const int r = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int r = int(blockIdx.y) * (kPThreads / kWave) + (threadIdx.x >> 6);
   const int h = item % p.hkv;
   const int qt = (item / p.hkv) % p.q_tiles;
   const int b = item / (p.hkv * p.q_tiles);
   const int q_begin = max(p.query_start_loc[b], 0);
   const int ql = min(p.query_start_loc[b + 1], p.total_q) - q_begin;
   const int tok = qt * p.tokens_per_tile + (r >> p.log2_group);
-  if (tok >= ql) return;  // uniform: a row past the request
-  const int tid = threadIdx.x, lane = tid & 63, grp = tid >> 6;
+  if (r >= kRows || tok >= ql) return;  // wavefront-uniform: a row past the request
   const size_t base = size_t(item) * p.num_splits * kRows + r;  // part index of split 0
-  if (grp == 0) {
-    const bool have = lane < p.num_splits;
-    const size_t pi = base + size_t(have ? lane : 0) * kRows;
-    const float ms = have ? p.part_ml[2 * pi] : -__builtin_inff();
-    const float ls = have ? p.part_ml[2 * pi + 1] : 0.f;
-    const float mx = wave_max(ms);
-    const float w = ms == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
-    if (have) wsh[lane] = w;
-    const float total = wave_sum(w * ls);
-    if (lane == 0) total_sh = total;
-  }
-  __syncthreads();
+  const bool have = lane < p.num_splits;
+  const size_t pi = base + size_t(have ? lane : 0) * kRows;
+  const float ms = have ? p.part_ml[2 * pi] : -__builtin_inff();
+  const float ls = have ? p.part_ml[2 * pi + 1] : 0.f;
+  const float mx = wave_max(ms);
+  const float w = ms == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
+  const float total = wave_sum(w * ls);
+  const bool dims_ok = 4 * lane < p.dv;
   f32x4_t acc{0.f, 0.f, 0.f, 0.f};
-  if (4 * lane < p.dv) {
-#pragma unroll 4
-    for (int s = grp; s < p.num_splits; s += 4) {
-      const float w = wsh[s];
-      if (w != 0.f) acc += w * *reinterpret_cast<const f32x4_t *>(p.part_o + (base + size_t(s) * kRows) * p.dv + 4 * lane);
+  for (int s0 = 0; s0 < p.num_splits; s0 += 8) {
+    float ws[8];
+    f32x4_t v[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int s = s0 + j;
+      ws[j] = __shfl(w, s < p.num_splits ? s : 0, kWave);  // every lane active here
+      if (s >= p.num_splits) ws[j] = 0.f;
+      v[j] = dims_ok && ws[j] != 0.f
+                 ? *reinterpret_cast<const f32x4_t *>(p.part_o + (base + size_t(s) * kRows) * p.dv + 4 * lane)
+                 : f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc += ws[j] * v[j];
   }
-  red[grp][lane] = acc;
-  __syncthreads();
-  if (grp == 0 && 4 * lane < p.dv) {
-    const f32x4_t y = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
-    const float inv = total_sh > 0.f ? 1.f / total_sh : 0.f;
-    const int qhead = h * p.group + (r & (p.group - 1));
-    uint16_t *o = static_cast<uint16_t *>(p.out) + (size_t(q_begin + tok) * p.hq + qhead) * p.dv + 4 * lane;
-    *reinterpret_cast<u32x2 *>(o) = u32x2{pack2<kBf16>(y[0] * inv, y[1] * inv), pack2<kBf16>(y[2] * inv, y[3] * inv)};
-  }
+  if (!dims_ok) return;
+  const float inv = total > 0.f ? 1.f / total : 0.f;
+  const int qhead = h * p.group + (r & (p.group - 1));
+  uint16_t *o = static_cast<uint16_t *>(p.out) + (size_t(q_begin + tok) * p.hq + qhead) * p.dv + 4 * lane;
+  *reinterpret_cast<u32x2 *>(o) = u32x2{pack2<kBf16>(acc[0] * inv, acc[1] * inv), pack2<kBf16>(acc[2] * inv, acc[3] * inv)};
 }
 
 // Any head sizes, group or block size: one wavefront per (query row, query
@@ -781,8 +779,8 @@ int launch_prefill_mfma(const PrefillParams &p, hipStream_t stream) {
   const unsigned blocks = unsigned(int64_t(p.q_tiles) * p.batch * p.hkv * p.num_splits);
   paged_prefill_attention_kernel<kD, kBf16, BtT><<<blocks, kPThreads, smem, stream>>>(p);
   if (p.num_splits > 1)
-    prefill_combine_kernel<kBf16, kPRows><<<dim3(unsigned(int64_t(p.batch) * p.q_tiles * p.hkv), kPRows), kPThreads,
-                                            0, stream>>>(p);
+    prefill_combine_kernel<kBf16, kPRows>
+        <<<dim3(unsigned(int64_t(p.batch) * p.q_tiles * p.hkv), kPRows / (kPThreads / kWave)), kPThreads, 0, stream>>>(p);
   return HIF8_OK;
 }
 
@@ -800,8 +798,8 @@ int launch_prefill_img(const PrefillParams &p, hipStream_t stream) {
     return st;
   kern<<<blocks, kIThreads, smem, stream>>>(p);
   if (p.num_splits > 1)
-    prefill_combine_kernel<kBf16, kIRows><<<dim3(unsigned(int64_t(p.batch) * p.q_tiles * p.hkv), kIRows), kPThreads,
-                                            0, stream>>>(p);
+    prefill_combine_kernel<kBf16, kIRows>
+        <<<dim3(unsigned(int64_t(p.batch) * p.q_tiles * p.hkv), kIRows / (kPThreads / kWave)), kPThreads, 0, stream>>>(p);
   return HIF8_OK;
 }
 
