@@ -180,11 +180,16 @@ __device__ __forceinline__ void store_out(void *out, int dtype, size_t i, float 
 constexpr int gemv_min_waves(int m, int rows) { return rows > 8 ? 2 : m == 1 ? 6 : m == 2 ? 4 : 2; }
 
 // kOneChunk: k <= 16 * kThreads, so each thread owns at most one 16-byte
-// column chunk per row (code activations only).
+// column chunk per row (code activations or a fixed activation scale).
+//
+// act and weight carry no __restrict__: as restrict read-only operands their
+// loads count as invariant, and the compiler sinks the one-chunk preload below
+// the LDS barrier to its first use, serialising the set-up and the weight
+// fetch that the preload exists to overlap.
 template <int kM, int kR, int kSrc, bool kOneChunk>
 __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
-    const void *__restrict__ act, const float *__restrict__ act_scale,
-    const uint8_t *__restrict__ weight, const float *__restrict__ cs,
+    const void *act, const float *__restrict__ act_scale,
+    const uint8_t *weight, const float *__restrict__ cs,
     const void *__restrict__ bias, int bias_dtype, void *__restrict__ out, int out_dtype,
     int n, int k) {
   constexpr int kV = kR * kM;
@@ -226,25 +231,37 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
       wq[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(weight + size_t(row) * k) + c);
     }
   };
-  // The decode table is computed, one entry per thread, rather than copied
-  // from global memory, so in the one-chunk kernel the chunk's loads go out
-  // before it and stay in flight across the LDS barrier: the kernel pays one
-  // memory round trip before its first products, not two.  (A copied table
-  // would have to wait for those loads: global loads return in order.  That
-  // is why the fused kinds, which copy the 8 KiB encode table, load after
-  // the barrier: loading first measured slower for them at M = 1.)  In a
-  // loop the preloaded registers stay live across the loop and the kernel
-  // spills, hence the separate one-chunk kernel.
-  static_assert(!kOneChunk || !kFused, "the one-chunk kernel takes code activations");
-  const uint16_t entry = uint16_t(decode_bits(uint32_t(tid)) >> 16);
-  if (kOneChunk && tid < chunks) load(tid);
-  dec_lut[tid] = entry;
+  // In the one-chunk kernel the chunk's loads go out before the LDS set-up
+  // and stay in flight across the barrier: the kernel pays one memory round
+  // trip before its first products, not two.  The 256-entry decode table is
+  // computed, one entry per thread; the fused kinds' 8 KiB encode table is
+  // copied from global memory, so its loads are issued first and its LDS
+  // stores wait for them alone (global loads return in order).  The chunk
+  // load is unconditional (a thread past the last chunk re-reads it and
+  // skips its products): a load under a branch makes the wait counts after
+  // the branch conservative, and the table stores would wait for the weights
+  // too.  In a loop the preloaded registers stay live across the loop and
+  // the kernel spills, hence the separate one-chunk kernel; preloading two or
+  // three chunks per thread (k up to 12288) measured no faster for code
+  // activations and slower fused.
+  static_assert(!kOneChunk || !kDynamic, "the one-chunk kernel takes a fixed activation scale");
+  u32x4 enc_part[2];
   if constexpr (kFused) {
     const u32x4 *src = reinterpret_cast<const u32x4 *>(kDeviceTables.static_encode);
-    u32x4 *dst = reinterpret_cast<u32x4 *>(enc_lut);
-    dst[tid] = src[tid];
-    dst[tid + kThreads] = src[tid + kThreads];
+    enc_part[0] = src[tid];
+    enc_part[1] = src[tid + kThreads];
   }
+  const uint16_t entry = uint16_t(decode_bits(uint32_t(tid)) >> 16);
+  if constexpr (kOneChunk) load(min(tid, chunks - 1));
+  dec_lut[tid] = entry;
+  if constexpr (kFused) {
+    u32x4 *dst = reinterpret_cast<u32x4 *>(enc_lut);
+    dst[tid] = enc_part[0];
+    dst[tid + kThreads] = enc_part[1];
+  }
+  // Without this fence the scheduler moves work across the preload and the
+  // one-chunk kernels spill.
+  if constexpr (kOneChunk) __builtin_amdgcn_sched_barrier(0);
   lds_barrier();
 
   // Activation scale of each row: the fixed one, or (dynamic) the row's
@@ -592,12 +609,20 @@ void dispatch_src(const LinearArgs &a, dim3 grid) {
             a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
       break;
     case kActF16:
-      gemv_kernel<kM, kR, kActF16, false><<<grid, kThreads, 0, a.stream>>>(
-          a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
+      if (k <= 16 * kThreads)
+        gemv_kernel<kM, kR, kActF16, true><<<grid, kThreads, 0, a.stream>>>(
+            a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
+      else
+        gemv_kernel<kM, kR, kActF16, false><<<grid, kThreads, 0, a.stream>>>(
+            a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
       break;
     case kActBf16:
-      gemv_kernel<kM, kR, kActBf16, false><<<grid, kThreads, 0, a.stream>>>(
-          a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
+      if (k <= 16 * kThreads)
+        gemv_kernel<kM, kR, kActBf16, true><<<grid, kThreads, 0, a.stream>>>(
+            a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
+      else
+        gemv_kernel<kM, kR, kActBf16, false><<<grid, kThreads, 0, a.stream>>>(
+            a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
       break;
     case kActF16Dyn:
       gemv_kernel<kM, kR, kActF16Dyn, false><<<grid, kThreads, 0, a.stream>>>(

@@ -289,13 +289,15 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
   const void *bias_ptr = bias.has_value() ? bias->data_ptr() : nullptr;
   const int bias_dtype = bias.has_value() ? DtypeCode(bias->scalar_type()) : HIF8_DTYPE_NONE;
   const int64_t m = activation.size(0), n = weight.size(0), k = activation.size(1);
-  if (m >= 2 || k > 4096 || n >= 12288) {
-    // Every block of the single-launch kernel encodes the whole activation,
-    // which costs more than a separate quant launch once there are several
-    // rows, a long K or many blocks (measured on MI355X at M = 1, K = 4096
-    // in graphs: N = 4096 6.2 vs 7.2 us, 8192 9.0 vs 9.4, 12288 11.5-12.0 vs
-    // 11.7-11.9, 24576 20.3-21.5 vs 19.0-20.0); the two launches give the
-    // same codes and the same GEMV, hence equal outputs.
+  if (m >= 2) {
+    // Every block of the single-launch kernel encodes its whole activation
+    // chunk, which costs more than a separate quant launch once there are
+    // several rows (measured on MI355X in graphs at M = 4: q 4096x4096 14.3
+    // vs 9.9 us, gate_up 24576x4096 38.1 vs 26.6).  One row is faster fused
+    // at every layer shape (q 6.5 vs 9.0 us, k/v 2048x4096 5.0 vs 7.6, o 6.7
+    // vs 8.3, gate_up 19.7 vs 20.5, down 4096x12288 14.0 vs 14.4-16.0).  The
+    // two launches give the same codes and the same GEMV, hence equal
+    // outputs.
     auto codes = at::empty({m, k}, activation.options().dtype(at::ScalarType::Byte));
     auto row_scale = at::empty({m}, activation.options().dtype(at::ScalarType::Float));
     const auto stream = CurrentStream(device);

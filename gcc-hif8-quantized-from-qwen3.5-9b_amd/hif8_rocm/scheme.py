@@ -11,13 +11,13 @@ static-quant GEMV only when ``HIF8_STATIC_FUSED_GENERATION=1``, M <= 4 and
 K < 1024, because on its hardware the fused kernel pays a global barrier.
 The MI355X fused kernel has none (every block encodes its own activation
 chunk) and its outputs equal quant -> GEMM bit for bit.  Measured on
-MI355X, one token row with K <= 4096 is faster fused (q 6.9 vs 9.0 us,
-fused k/v 5.3 vs 7.9, o 7.2 vs 8.5, gate_up 21.9 vs 23.4: the separate
-quant launch costs about 4 us of launch and cold-cache latency), while
-K = 12288 (down 15.3 vs 14.4) and two or more rows at the large shapes are
-faster separate (each block re-encodes M*K values).
-``HIF8_STATIC_FUSED_SINGLE_ROW=1`` opts into fusing one token row with
-K <= 4096 as well; it changes which kernels run, not the outputs.
+MI355X in HIP graphs, one token row is faster fused at every layer shape
+(q 6.5 vs 9.0 us, fused k/v 5.0 vs 7.6, o 6.7 vs 8.3, gate_up 19.7 vs
+20.5, down 14.0 vs 14.4-16.0: the separate quant launch costs 3-4 us of
+launch and cold-cache latency), while four rows are faster separate (each
+block re-encodes M*K values: q 14.3 vs 9.9 us).
+``HIF8_STATIC_FUSED_SINGLE_ROW=1`` opts into fusing one token row; it
+changes which kernels run, not the outputs.
 
 ``HIF8_PREFILL_BF16_WEIGHTS=1`` (read in ``process_weights_after_loading``)
 keeps each weight decoded to bf16 beside its codes (2 bytes per element;
@@ -41,9 +41,8 @@ _COMPUTE_BACKEND_ENV = "HIF8_COMPUTE_BACKEND"
 _SOFT_HIF8_BACKEND = "soft_hif8"
 _STATIC_FUSED_GENERATION_ENV = "HIF8_STATIC_FUSED_GENERATION"
 _STATIC_SCALE_FACTOR_ENV = "HIF8_STATIC_SCALE_FACTOR"
-# MI355X opt-in: fuse one token row up to this K (measured; see the module text).
+# MI355X opt-in: fuse one token row (measured; see the module text).
 _STATIC_FUSED_SINGLE_ROW_ENV = "HIF8_STATIC_FUSED_SINGLE_ROW"
-_FUSED_SINGLE_ROW_MAX_K = 4096
 # MI355X opt-in: keep each static weight decoded to bf16 for prefill GEMMs.
 _PREFILL_BF16_WEIGHTS_ENV = "HIF8_PREFILL_BF16_WEIGHTS"
 
@@ -127,17 +126,13 @@ class W8A8HiFloat8StaticLinearMethod:
 
         Fused when the reference would fuse (``HIF8_STATIC_FUSED_GENERATION=1``,
         M <= 4, K < 1024) and, with ``HIF8_STATIC_FUSED_SINGLE_ROW=1``, for
-        one token row with K <= 4096; the two routes give equal outputs."""
+        one token row; the two routes give equal outputs."""
         del tp_rank
         token_rows = x.numel() // x.shape[-1]
         k = x.shape[-1]
         use_fused = (
             token_rows <= 4 and os.environ.get(_STATIC_FUSED_GENERATION_ENV) == "1" and k < 1024
-        ) or (
-            token_rows == 1
-            and k <= _FUSED_SINGLE_ROW_MAX_K
-            and os.environ.get(_STATIC_FUSED_SINGLE_ROW_ENV) == "1"
-        )
+        ) or (token_rows == 1 and os.environ.get(_STATIC_FUSED_SINGLE_ROW_ENV) == "1")
         scale_factor = _static_scale_factor()
         fixed_scale = layer.input_scale
         if scale_factor != 1.0:

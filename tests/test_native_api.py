@@ -247,12 +247,12 @@ def test_fused_generation_is_opt_in_and_limited_to_small_shapes(clean_env):
 
 
 def test_single_row_fusion_is_an_opt_in(clean_env):
-    """HIF8_STATIC_FUSED_SINGLE_ROW=1 fuses one token row with K <= 4096 and
+    """HIF8_STATIC_FUSED_SINGLE_ROW=1 fuses one token row, whatever K, and
     nothing else; unset, routing is the reference's."""
     method = W8A8HiFloat8StaticLinearMethod()
     out = torch.randn(1, 5)
     cases = [(None, (1, 4096), False), ("1", (1, 4096), True), ("1", (1, 8), True), ("1", (2, 4096), False),
-             ("1", (1, 4112), False), ("0", (1, 64), False)]
+             ("1", (1, 12288), True), (None, (1, 12288), False), ("0", (1, 64), False)]
     for flag, shape, want_fused in cases:
         if flag is None:
             os.environ.pop("HIF8_STATIC_FUSED_SINGLE_ROW", None)
