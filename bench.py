@@ -278,7 +278,10 @@ def decode_step_fn(st: Setup, copy: int, fused: bool = False):
 
 
 def per_kernel_table(st: Setup, launches: int = 20) -> dict:
-    """Per-launch time of each GEMV / GEMM / quant, from graphs of back-to-back launches."""
+    """Per-launch time of each GEMV / GEMM / quant, from graphs of back-to-back launches.
+
+    Each fused static-quant GEMV row also carries ``quant_then_gemv_us``: the
+    same projection as static quant + GEMV, two launches per call in one graph."""
     torch, native = st.torch, st.native
     table = {}
     for m in DECODE_M + PREFILL_M:
@@ -308,10 +311,19 @@ def per_kernel_table(st: Setup, launches: int = 20) -> dict:
                         w, ws = st.weights[i % N_COPIES][name]
                         native.soft_static_fused_linear(x, w, s, ws, None, output_dtype=torch.bfloat16)
                 ms = time_graphs(torch, [capture(torch, ff)], 3) / per
+
+                # The same work as two launches (static quant, then the GEMV) in one graph.
+                def f2(x=x, s=s, name=name):
+                    for i in range(per):
+                        w, ws = st.weights[i % N_COPIES][name]
+                        qq, rr = native.static_quant(x, s)
+                        native.soft_linear(qq, w, rr, ws, None, output_dtype=torch.bfloat16)
+                ms2 = time_graphs(torch, [capture(torch, f2)], 3) / per
                 fb = gemv_bytes(m, n, k) + m * k  # bf16 x instead of u8 codes
                 gbs = fb / (ms * 1e-3) / 1e9
                 table[f"{name}_m{m}_fused"] = {"kernel": "fused_quant_gemv", "us": round(ms * 1e3, 3), "bytes": fb,
-                                               "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+                                               "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
+                                               "quant_then_gemv_us": round(ms2 * 1e3, 3)}
     for m, k in ((4096, 4096), (4096, 12288), (512, 4096), (1, 4096), (4, 12288)):
         x, s = st.x[(m, k)]
 
