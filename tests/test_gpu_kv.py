@@ -19,14 +19,13 @@ import numpy as np
 import pytest
 import torch
 
+from _kv import KEY_SCALES_L3, VALUE_SCALES_L3
 from _kv import build_cache as _build_cache
 from _kv import randn as _randn
 from oracle import hif8_oracle as o
 
 pytestmark = pytest.mark.gpu
 
-KEY_SCALES_L3 = [0.9432383179664612, 0.7343872785568237, 0.9391698241233826, 1.1160656213760376]
-VALUE_SCALES_L3 = [0.3244977593421936, 0.416015625, 0.5311850309371948, 0.3086029291152954]
 HIF8_MAX = 32768.0
 
 
@@ -136,10 +135,11 @@ def test_write_rejects_or_skips_slots_past_the_cache(native_ops, device):
 # -------------------------------------------------------------- attention
 
 def _check_attention(device, lens, hq, hkv, d, bs, *, dtype=torch.bfloat16, bt_dtype=torch.int32, seed=0,
-                     q_mul=1.0, dv=None, mixed=False, bound=2e-2):
+                     q_mul=1.0, dv=None, mixed=False, bound=2e-2, scales=None, kv_mul=(1.0, 1.0)):
     from hif8_rocm import kv_cache
 
-    kc, vc, table = _build_cache(device, lens, hkv, d, bs, seed, dv=dv, bt_dtype=bt_dtype, mixed=mixed)
+    kc, vc, table = _build_cache(device, lens, hkv, d, bs, seed, dv=dv, bt_dtype=bt_dtype, mixed=mixed,
+                                 scales=scales, kv_mul=kv_mul)
     q = _randn((len(lens), hq, d), seed + 1, q_mul, dtype)
     scale = 1.0 / math.sqrt(d)
     out = kv_cache.paged_decode_attention(q.to(device), kc, vc, table.to(device), lens, scale=scale)
@@ -171,6 +171,18 @@ def _check_attention(device, lens, hq, hkv, d, bs, *, dtype=torch.bfloat16, bt_d
 @pytest.mark.parametrize("ctx", [512, 4096, 16384])
 def test_attention_decode_configs(native_ops, device, batch, ctx):
     _check_attention(device, [ctx] * batch, 16, 4, 256, 128, seed=ctx + batch)
+
+
+def test_attention_with_real_layer3_scales(native_ops, device):
+    """The reference's real layer-3 K/V scales (test_hif8_kv_npu.py:427-436;
+    the exporter's convention, near amax / 12 rather than amax / 32768) on
+    K ~ 3 N(0, 1), V ~ 1.5 N(0, 1): codes in HiF8's 3-bit-mantissa core and
+    the tapered ends, against the float64 and bf16-rounding oracles.  q is
+    scaled by 0.35 so that the logits keep a standard deviation near 1, where
+    the bf16 logit rounding of the second oracle stays below the tolerance."""
+    for lens, seed in (([4096] * 4, 31), ([16384, 700, 1], 32)):
+        _check_attention(device, lens, 16, 4, 256, 128, seed=seed, q_mul=0.35,
+                         scales=(KEY_SCALES_L3, VALUE_SCALES_L3), kv_mul=(3.0, 1.5))
 
 
 def test_attention_ragged_lengths_and_empty_requests(native_ops, device):

@@ -20,7 +20,7 @@ import numpy as np
 import pytest
 import torch
 
-from _kv import build_cache, randn
+from _kv import KEY_SCALES_L3, VALUE_SCALES_L3, build_cache, randn
 from oracle import hif8_oracle as o
 
 pytestmark = pytest.mark.gpu
@@ -37,10 +37,11 @@ def _run_op(device, q, kc, vc, table, lens, qlens, scale, causal, max_query_len=
 
 
 def _check(device, lens, qlens, hq, hkv, d, bs, *, causal=True, dtype=torch.bfloat16, bt_dtype=torch.int32,
-           seed=0, dv=None, mixed=False, bound=2e-2, q_mul=1.0, via_api=False):
+           seed=0, dv=None, mixed=False, bound=2e-2, q_mul=1.0, via_api=False, scales=None, kv_mul=(1.0, 1.0)):
     from hif8_rocm import kv_cache
 
-    kc, vc, table = build_cache(device, lens, hkv, d, bs, seed, dv=dv, bt_dtype=bt_dtype, mixed=mixed)
+    kc, vc, table = build_cache(device, lens, hkv, d, bs, seed, dv=dv, bt_dtype=bt_dtype, mixed=mixed,
+                                scales=scales, kv_mul=kv_mul)
     q = randn((sum(qlens), hq, d), seed + 1, q_mul, dtype)
     scale = 1.0 / math.sqrt(d)
     print(f"case lens={lens[:4]} qlens={qlens[:4]} hq={hq} hkv={hkv} d={d} bs={bs} causal={causal}", flush=True)
@@ -114,6 +115,16 @@ def test_prefill_rows_before_the_first_key_are_zero(native_ops, device):
     # the kernel gives the rows at negative positions zeros, like the oracle).
     got, _ = _check(device, [5, 40], [9, 40], 16, 4, 256, 128, seed=17)
     assert not got[:4].any()
+
+
+@pytest.mark.parametrize("q_len", [17, 512])
+def test_prefill_with_real_layer3_scales(native_ops, device, q_len):
+    """The reference's real layer-3 K/V scales (test_hif8_kv_npu.py:427-436;
+    near amax / 12, not amax / 32768) on K ~ 3 N(0, 1), V ~ 1.5 N(0, 1), over
+    4096 cached keys: 17 rows run the in-kernel page decode, 512 the tile
+    images."""
+    _check(device, [4096, 1200], [q_len, min(q_len, 300)], 16, 4, 256, 128, seed=40 + q_len,
+           scales=(KEY_SCALES_L3, VALUE_SCALES_L3), kv_mul=(3.0, 1.5))
 
 
 def test_prefill_mixed_row_scales(native_ops, device):
