@@ -8,8 +8,8 @@ runs the static W8A8 linear method (hif8_rocm.scheme): hif8_static_quant of
 the bf16 activation, then soft_hif8_gemm, which runs the HBM-streaming GEMV
 kernel for M <= 4.  The fused single-launch variant (soft_hif8_static_fused_gemm)
 is reported beside it, and so is the scheme with the MI355X opt-in
-HIF8_STATIC_FUSED_SINGLE_ROW=1 (one-row projections in one fused launch,
-equal outputs).  One step = that sweep over one layer's
+HIF8_STATIC_FUSED_SINGLE_ROW=1 (one-row projections through the fused op,
+one launch for K <= 4096, equal outputs).  One step = that sweep over one layer's
 weights; five distinct weight copies (966 MB) are
 rotated so the 256 MB Infinity Cache cannot serve them.  Steps are captured
 in HIP graphs and replayed, so host launch overhead is not timed.
@@ -699,8 +699,8 @@ def e2e_decode(torch, device) -> dict:
     g = torch.Generator(device=device).manual_seed(9)
     # b1_single_row_fusion: batch 1 again with HIF8_STATIC_FUSED_SINGLE_ROW=1
     # and the glue-kernel input quant off, so every one-row projection (qkv /
-    # qkvz, gate_up, o / out, down) runs the fused static-quant GEMV in one
-    # launch (same tokens).
+    # qkvz, gate_up, o / out, down) goes through the fused static-quant op,
+    # one launch for K <= 4096 (same tokens).
     for b, key, single in ((1, "b1", False), (4, "b4", False), (1, "b1_single_row_fusion", True)):
         prompt = torch.randint(0, cfg.vocab, (b, E2E_PROMPT), generator=g, device=device)
         if single:
@@ -906,7 +906,8 @@ def main() -> None:
         "decode_sweep_fused_GBps": round(fused_gbs, 1),
         "decode_sweep_single_row_fusion": {"GBps": round(single_gbs, 1), "us_per_step": round(single_ms * 1e3, 1),
                                            "routing": "scheme apply with HIF8_STATIC_FUSED_SINGLE_ROW=1: M=1 "
-                                                      "fused (one launch), M=4 as the headline; outputs equal"},
+                                                      "through the fused op (one launch for K <= 4096), M=4 as "
+                                                      "the headline; outputs equal"},
         "gemv_all_launches_GBps": round(all_gemv_gbs, 1),
         "gemm_per_layer": gemm_layer,
         "gemm_decoded_weights": {"routing": "HIF8_PREFILL_BF16_WEIGHTS=1: weights kept decoded to bf16 "

@@ -289,13 +289,15 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
   const void *bias_ptr = bias.has_value() ? bias->data_ptr() : nullptr;
   const int bias_dtype = bias.has_value() ? DtypeCode(bias->scalar_type()) : HIF8_DTYPE_NONE;
   const int64_t m = activation.size(0), n = weight.size(0), k = activation.size(1);
-  if (m >= 2) {
+  if (m >= 2 || k > 4096) {
     // Every block of the single-launch kernel encodes its whole activation
     // chunk, which costs more than a separate quant launch once there are
     // several rows (measured on MI355X in graphs at M = 4: q 4096x4096 14.3
-    // vs 9.9 us, gate_up 24576x4096 38.1 vs 26.6).  One row is faster fused
-    // at every layer shape (q 6.5 vs 9.0 us, k/v 2048x4096 5.0 vs 7.6, o 6.7
-    // vs 8.3, gate_up 19.7 vs 20.5, down 4096x12288 14.0 vs 14.4-16.0).  The
+    // vs 9.9 us, gate_up 24576x4096 38.1 vs 26.6).  One row with K <= 4096
+    // (one chunk per thread, loaded before the table set-up) is faster fused
+    // (q 6.5 vs 8.7-9.0 us, k/v 2048x4096 5.0 vs 7.6, o 6.7 vs 8.3, gate_up
+    // 19.7-19.9 vs 20.5-20.9); with K = 12288 (down) the chunk loop measured
+    // either way (14.0-14.7 vs 13.7-16.0 us), so it keeps two launches.  The
     // two launches give the same codes and the same GEMV, hence equal
     // outputs.
     auto codes = at::empty({m, k}, activation.options().dtype(at::ScalarType::Byte));

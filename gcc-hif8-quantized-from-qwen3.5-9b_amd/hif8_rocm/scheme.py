@@ -11,13 +11,14 @@ static-quant GEMV only when ``HIF8_STATIC_FUSED_GENERATION=1``, M <= 4 and
 K < 1024, because on its hardware the fused kernel pays a global barrier.
 The MI355X fused kernel has none (every block encodes its own activation
 chunk) and its outputs equal quant -> GEMM bit for bit.  Measured on
-MI355X in HIP graphs, one token row is faster fused at every layer shape
-(q 6.5 vs 9.0 us, fused k/v 5.0 vs 7.6, o 6.7 vs 8.3, gate_up 19.7 vs
-20.5, down 14.0 vs 14.4-16.0: the separate quant launch costs 3-4 us of
-launch and cold-cache latency), while four rows are faster separate (each
-block re-encodes M*K values: q 14.3 vs 9.9 us).
-``HIF8_STATIC_FUSED_SINGLE_ROW=1`` opts into fusing one token row; it
-changes which kernels run, not the outputs.
+MI355X in HIP graphs, one token row with K <= 4096 is faster fused (q 6.5
+vs 8.7-9.0 us, fused k/v 5.0 vs 7.6, o 6.7 vs 8.3, gate_up 19.7-19.9 vs
+20.5-20.9: the separate quant launch costs 3-4 us of launch and cold-cache
+latency), while four rows are faster separate (each block re-encodes M*K
+values: q 14.3 vs 9.9 us) and K = 12288 measured either way, so the fused
+op itself runs those as quant + GEMV.
+``HIF8_STATIC_FUSED_SINGLE_ROW=1`` opts into the fused op for one token
+row; it changes which kernels run, not the outputs.
 
 ``HIF8_PREFILL_BF16_WEIGHTS=1`` (read in ``process_weights_after_loading``)
 keeps each weight decoded to bf16 beside its codes (2 bytes per element;

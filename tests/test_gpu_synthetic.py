@@ -95,7 +95,7 @@ def test_single_row_fusion_generates_the_same_tokens(model, device, monkeypatch)
     on one-row projections; the logits, hence the tokens, are unchanged.  The
     glue-kernel input quant is switched off, so that every one-row projection
     (qkv / qkvz, gate_up, o / out, down) goes through the scheme and the fused
-    kernel, not only the o / out projections."""
+    op, not only the o / out projections."""
     from hif8_rocm.synthetic_model import generate
 
     g = torch.Generator(device=device).manual_seed(21)
