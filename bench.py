@@ -9,7 +9,7 @@ the bf16 activation, then soft_hif8_gemm, which runs the HBM-streaming GEMV
 kernel for M <= 4.  The fused single-launch variant (soft_hif8_static_fused_gemm)
 is reported beside it, and so is the scheme with the MI355X opt-in
 HIF8_STATIC_FUSED_SINGLE_ROW=1 (one-row projections through the fused op,
-one launch for K <= 4096, equal outputs).  One step = that sweep over one layer's
+one launch for K <= 4096 and N < 12288, equal outputs).  One step = that sweep over one layer's
 weights; five distinct weight copies (966 MB) are
 rotated so the 256 MB Infinity Cache cannot serve them.  Steps are captured
 in HIP graphs and replayed, so host launch overhead is not timed.
@@ -700,7 +700,7 @@ def e2e_decode(torch, device) -> dict:
     # b1_single_row_fusion: batch 1 again with HIF8_STATIC_FUSED_SINGLE_ROW=1
     # and the glue-kernel input quant off, so every one-row projection (qkv /
     # qkvz, gate_up, o / out, down) goes through the fused static-quant op,
-    # one launch for K <= 4096 (same tokens).
+    # one launch for K <= 4096 and N < 12288 (same tokens).
     for b, key, single in ((1, "b1", False), (4, "b4", False), (1, "b1_single_row_fusion", True)):
         prompt = torch.randint(0, cfg.vocab, (b, E2E_PROMPT), generator=g, device=device)
         if single:
@@ -906,7 +906,7 @@ def main() -> None:
         "decode_sweep_fused_GBps": round(fused_gbs, 1),
         "decode_sweep_single_row_fusion": {"GBps": round(single_gbs, 1), "us_per_step": round(single_ms * 1e3, 1),
                                            "routing": "scheme apply with HIF8_STATIC_FUSED_SINGLE_ROW=1: M=1 "
-                                                      "through the fused op (one launch for K <= 4096), M=4 as "
+                                                      "through the fused op (one launch for K <= 4096, N < 12288), M=4 as "
                                                       "the headline; outputs equal"},
         "gemv_all_launches_GBps": round(all_gemv_gbs, 1),
         "gemm_per_layer": gemm_layer,

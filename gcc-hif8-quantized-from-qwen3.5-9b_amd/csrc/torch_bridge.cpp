@@ -289,16 +289,18 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
   const void *bias_ptr = bias.has_value() ? bias->data_ptr() : nullptr;
   const int bias_dtype = bias.has_value() ? DtypeCode(bias->scalar_type()) : HIF8_DTYPE_NONE;
   const int64_t m = activation.size(0), n = weight.size(0), k = activation.size(1);
-  if (m >= 2 || k > 4096) {
+  if (m >= 2 || k > 4096 || n >= 12288) {
     // Every block of the single-launch kernel encodes its whole activation
     // chunk, which costs more than a separate quant launch once there are
     // several rows (measured on MI355X in graphs at M = 4: q 4096x4096 14.3
     // vs 9.9 us, gate_up 24576x4096 38.1 vs 26.6).  One row with K <= 4096
-    // (one chunk per thread, loaded before the table set-up) is faster fused
-    // (q 6.5 vs 8.7-9.0 us, k/v 2048x4096 5.0 vs 7.6, o 6.7 vs 8.3, gate_up
-    // 19.7-19.9 vs 20.5-20.9); with K = 12288 (down) the chunk loop measured
-    // either way (14.0-14.7 vs 13.7-16.0 us), so it keeps two launches.  The
-    // two launches give the same codes and the same GEMV, hence equal
+    // and N < 12288 (one chunk per thread, loaded before the table set-up,
+    // at most 1536 blocks) is faster fused every time (q 6.5 vs 8.7-9.0 us,
+    // k/v 2048x4096 5.0-5.2 vs 7.6, o 6.6-6.7 vs 8.3-8.8); gate_up
+    // (N = 24576: 3072 blocks, each re-encoding) and down (K = 12288, the
+    // chunk loop) measured either way across runs (gate_up 19.7-21.4 vs
+    // 20.4-21.4 us, down 13.6-14.7 vs 13.7-16.0), so they keep two launches.
+    // The two launches give the same codes and the same GEMV, hence equal
     // outputs.
     auto codes = at::empty({m, k}, activation.options().dtype(at::ScalarType::Byte));
     auto row_scale = at::empty({m}, activation.options().dtype(at::ScalarType::Float));

@@ -11,12 +11,13 @@ static-quant GEMV only when ``HIF8_STATIC_FUSED_GENERATION=1``, M <= 4 and
 K < 1024, because on its hardware the fused kernel pays a global barrier.
 The MI355X fused kernel has none (every block encodes its own activation
 chunk) and its outputs equal quant -> GEMM bit for bit.  Measured on
-MI355X in HIP graphs, one token row with K <= 4096 is faster fused (q 6.5
-vs 8.7-9.0 us, fused k/v 5.0 vs 7.6, o 6.7 vs 8.3, gate_up 19.7-19.9 vs
-20.5-20.9: the separate quant launch costs 3-4 us of launch and cold-cache
+MI355X in HIP graphs, one token row of the q, fused k/v and o shapes is
+faster fused (q 6.5 vs 8.7-9.0 us, k/v 5.0-5.2 vs 7.6, o 6.6-6.7 vs
+8.3-8.8: the separate quant launch costs 2-3 us of launch and cold-cache
 latency), while four rows are faster separate (each block re-encodes M*K
-values: q 14.3 vs 9.9 us) and K = 12288 measured either way, so the fused
-op itself runs those as quant + GEMV.
+values: q 14.3 vs 9.9 us) and gate_up and down measured either way, so the
+fused op itself runs those (M >= 2, K > 4096 or N >= 12288) as
+quant + GEMV.
 ``HIF8_STATIC_FUSED_SINGLE_ROW=1`` opts into the fused op for one token
 row; it changes which kernels run, not the outputs.
 
