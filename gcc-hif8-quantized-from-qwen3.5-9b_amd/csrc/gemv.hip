@@ -650,7 +650,7 @@ void dispatch_m(const LinearArgs &a) {
 }  // namespace
 
 // Kernel selection knob, read once: HIF8_GEMV_KERNEL=valu|mfma (default valu),
-// HIF8_GEMV_ROWS=4|8|16 forces the VALU kernel's rows per block.
+// HIF8_GEMV_ROWS=4|8|12|16 forces the VALU kernel's rows per block (12: M = 1 only).
 // Measured on MI355X (gate_up 24576x4096, M=1): one-shot VALU kernel with 8
 // rows per block 20.0 us; the MFMA kernel 29.3 us (its 16-rows x 64-byte load
 // pattern alone reads ~20% slower than 1 KiB-contiguous rows); a persistent
@@ -683,11 +683,14 @@ int launch_gemv(const LinearArgs &a) {
         a.act, a.act_kind, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out,
         a.out_dtype, int(a.m), int(a.n), int(a.k));
   } else {
-    // 8 rows per block; M = 4 over wide weights (N >= 16384: at least 1024
-    // blocks) streams faster with 16 (gate_up 24576 x 4096: 24.8 vs 25.7-26.5
-    // us on MI355X; q/o/k-v and down are slower with 16, M = 1 too).
-    const int rows = knobs.rows ? knobs.rows : (a.m == 4 && a.n >= 16384 ? 16 : 8);
+    // 8 rows per block; over wide weights (N >= 16384) M = 4 streams faster
+    // with 16 (gate_up 24576 x 4096: 24.8 vs 25.7-26.5 us on MI355X) and
+    // M = 1 with 12, 2048 blocks (17.4-17.6 vs 17.8 us; 6 rows 17.6-18.3).
+    // q/o/k-v and down are fastest with 8.
+    const bool wide = a.n >= 16384;
+    const int rows = knobs.rows ? knobs.rows : (wide && a.m == 4 ? 16 : wide && a.m == 1 ? 12 : 8);
     if (rows >= 16) dispatch_m<16>(a);
+    else if (rows == 12 && a.m == 1) dispatch_src<1, 12>(a, dim3(unsigned((a.n + 11) / 12)));
     else if (rows >= 8) dispatch_m<8>(a);
     else dispatch_m<4>(a);
   }
