@@ -26,7 +26,7 @@
 //     LDS in wavefront order, so every wavefront runs the same softmax;
 //   * V slices are copied raw into LDS by DMA (global_load_lds_dwordx4) and
 //     read transposed (8 tokens x 4 dims per lane), and O^T += V^T P' runs on
-//     the same MFMA with the softmax weights P' rounded to bf16;
+//     the same MFMA with the softmax weights P' rounded to the query dtype;
 //   * both operands are decoded through per-wave LDS tables that hold
 //     dtype(dec(c) * s) for the tile's row scale s - which is how the
 //     reference decodes K and V before its attention
@@ -252,7 +252,7 @@ __global__ __launch_bounds__(kWave * (kD / 64), 4) void paged_decode_attention_k
 
   struct Smem {
     uint16_t k_tab[kWd][256];      // query dtype(dec(c) * k_tab_scale), per wavefront
-    uint16_t v_tab[kWd][256];      // bf16(dec(c) * v_tab_scale), per wavefront
+    uint16_t v_tab[kWd][256];      // query dtype(dec(c) * v_tab_scale) or (mixed scales) bf16(dec(c))
     float scl[kWd][64];            // K | V factors of the tile's tokens (0 = masked)
     f32x4_t sx[2][kWd][2][kWave];  // partial scores [tile parity][wavefront][16-token block][lane]
     uint8_t vtile[2][kWd][kSlice]; // double-buffered V slices
@@ -429,10 +429,19 @@ __global__ __launch_bounds__(kWave * (kD / 64), 4) void paged_decode_attention_k
       for (int i = 0; i < 4; ++i) smem.k_tab[wv][lane + 64 * i] = float_to_half_bits<kQBf16>(decf[i] * k_want);
       k_tab_scale = k_want;
     }
-    if (!(v_want == v_tab_scale)) {
+    // V and P' go through the MFMA in the query dtype when the tile's V rows
+    // share a scale (the reference rounds V and the softmax weights to
+    // query.dtype, kv_cache.py:355-356 and :370-371); with mixed scales the
+    // table holds the exact dec(c) in bf16 and P' = P * row scale stays bf16
+    // (fp16 would lose P' * scale below 2^-14 to subnormals).  The sentinel
+    // -1 marks the exact bf16 table of an fp16-query kernel.
+    const float v_key = kQBf16 || v_uniform ? v_want : -1.f;
+    if (!(v_key == v_tab_scale)) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) smem.v_tab[wv][lane + 64 * i] = float_to_bf16_bits(decf[i] * v_want);
-      v_tab_scale = v_want;
+      for (int i = 0; i < 4; ++i)
+        smem.v_tab[wv][lane + 64 * i] =
+            v_uniform ? float_to_half_bits<kQBf16>(decf[i] * v_want) : float_to_bf16_bits(decf[i] * v_want);
+      v_tab_scale = v_key;
     }
     sc[lane] = valid ? ((lane < 32 ? k_uniform : v_uniform) ? 1.f : s_cur) : 0.f;
     if (!__all(valid)) {
@@ -506,17 +515,23 @@ __global__ __launch_bounds__(kWave * (kD / 64), 4) void paged_decode_attention_k
       for (int q = 0; q < 4; ++q) oacc[q] *= alpha;
     }
     m = m_new;
-    const u32x4 pb{pack_half2<true>(pw[0] * vs0[0], pw[1] * vs0[1]), pack_half2<true>(pw[2] * vs0[2], pw[3] * vs0[3]),
-                   pack_half2<true>(pw[4] * vs1[0], pw[5] * vs1[1]), pack_half2<true>(pw[6] * vs1[2], pw[7] * vs1[3])};
-
     // O^T += V^T P' over this wavefront's 64 dims: word j holds dims
     // dim0 + 4n + [0, 4) of token 4g + j (j < 4) or 16 + 4g + j - 4.
     uint32_t w[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j)
       w[j] = *reinterpret_cast<const uint32_t *>(vt + 1024 * (j >> 2) + 256 * (j & 3) + 64 * g + 4 * n);
+    // P' = P * (1 for a valid row of a uniform tile, the row scale for mixed
+    // tiles, 0 for a masked row).
+    auto pv = [&](auto bf16_mma) {
+      constexpr bool kB = decltype(bf16_mma)::value;
+      const u32x4 pb{pack_half2<kB>(pw[0] * vs0[0], pw[1] * vs0[1]), pack_half2<kB>(pw[2] * vs0[2], pw[3] * vs0[3]),
+                     pack_half2<kB>(pw[4] * vs1[0], pw[5] * vs1[1]), pack_half2<kB>(pw[6] * vs1[2], pw[7] * vs1[3])};
 #pragma unroll
-    for (int q = 0; q < 4; ++q) oacc[q] = mfma16<true>(decode_column(vl, w, q), pb, oacc[q]);
+      for (int q = 0; q < 4; ++q) oacc[q] = mfma16<kB>(decode_column(vl, w, q), pb, oacc[q]);
+    };
+    if (kQBf16 || !v_uniform) pv(std::true_type{});
+    else pv(std::false_type{});
   }
   float lt = l + __shfl_xor(l, 16, kWave);
   lt += __shfl_xor(lt, 32, kWave);
@@ -639,26 +654,33 @@ __global__ __launch_bounds__(kWave) void paged_decode_attention_simple(const Att
     const int64_t slot = blk * p.block_size + t % p.block_size;
     const uint8_t *kr = p.key_cache + (slot * p.hkv + h) * krow;
     const uint8_t *vr = p.value_cache + (slot * p.hkv + h) * vrow;
+    // K and V rows decoded to the query dtype, dtype(dec(c) * row scale)
+    // (kv_cache.py:355-356), as in the MFMA kernel.
+    const float ksc = *reinterpret_cast<const float *>(kr + p.d);
+    const float vsc = *reinterpret_cast<const float *>(vr + p.dv);
     float dot = 0.f;
 #pragma unroll
     for (int i = 0; i < kMaxPerLane; ++i) {
       const int dim = lane + kWave * i;
-      if (dim < p.d) dot = fmaf(qv[i], __uint_as_float(kDeviceTables.decode_f32[kr[dim]]), dot);
+      if (dim < p.d)
+        dot = fmaf(qv[i], half_bits_to_float<kQBf16>(float_to_half_bits<kQBf16>(
+                              __uint_as_float(kDeviceTables.decode_f32[kr[dim]]) * ksc)), dot);
     }
     dot = wave_sum(dot);
-    const float x = dot * *reinterpret_cast<const float *>(kr + p.d) * p.scale_log2;
+    const float x = dot * p.scale_log2;
     const float m_new = fmaxf(m, x);
     const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
     const float alpha = __builtin_amdgcn_exp2f(m - m_use);
     const float pw = __builtin_amdgcn_exp2f(x - m_use);
     l = l * alpha + pw;
     m = m_new;
-    const float pv = pw * *reinterpret_cast<const float *>(vr + p.dv);
 #pragma unroll
     for (int i = 0; i < kMaxPerLane; ++i) {
       const int dim = lane + kWave * i;
       acc[i] *= alpha;
-      if (dim < p.dv) acc[i] = fmaf(pv, __uint_as_float(kDeviceTables.decode_f32[vr[dim]]), acc[i]);
+      if (dim < p.dv)
+        acc[i] = fmaf(pw, half_bits_to_float<kQBf16>(float_to_half_bits<kQBf16>(
+                              __uint_as_float(kDeviceTables.decode_f32[vr[dim]]) * vsc)), acc[i]);
     }
   }
   const float inv = l > 0.f ? 1.f / l : 0.f;

@@ -81,9 +81,58 @@ struct PrefillParams {
   int tokens_per_tile, q_tiles, num_splits, split_tiles, batch, max_len, causal;
   int total_q;                    // rows of query / out; rows at or past it are never touched
   float scale_log2;               // softmax scale * log2(e)
-  uint8_t *img;                   // decoded tile images [batch][hkv][img_tiles] (tile-image path)
+  uint8_t *img;                   // decoded tile images [slots][hkv][img_tiles] (tile-image path)
   int img_tiles;                  // 64-key tiles per (request, KV head) in img
+  int slots;                      // image slots (0: no request takes the tile-image path)
+  int long_rows;                  // a request is long when its (token, head) rows exceed this
 };
+
+// Requests whose query covers more than p.long_rows (token, head) rows take
+// the tile-image path when one of the p.slots image slots is theirs: slot s
+// belongs to the s-th long request in request order, so short requests in
+// the same batch (decode rows of a chunked-prefill step) neither get images
+// nor cost image bytes.  Every wavefront of a workgroup evaluates these
+// itself from query_start_loc; the results are uniform.
+__device__ __forceinline__ bool request_is_long(const PrefillParams &p, int b) {
+  const int q_begin = max(p.query_start_loc[b], 0);
+  const int ql = min(p.query_start_loc[b + 1], p.total_q) - q_begin;
+  return ql > 0 && int64_t(ql) * p.group > int64_t(p.long_rows);
+}
+
+// Long requests among 0 .. b - 1 (64 requests per round of the wavefront).
+__device__ int long_requests_before(const PrefillParams &p, int b) {
+  const int lane = threadIdx.x & 63;
+  int count = 0;
+  for (int base = 0; base < b; base += 64) {
+    const int i = base + lane;
+    count += __popcll(__ballot(i < b && request_is_long(p, i)));
+  }
+  return count;
+}
+
+// True when request b runs on the tile-image path.
+__device__ __forceinline__ bool request_has_images(const PrefillParams &p, int b) {
+  return p.slots > 0 && request_is_long(p, b) && long_requests_before(p, b) < p.slots;
+}
+
+// The request holding image slot s, or -1 when fewer requests are long.
+__device__ int request_of_slot(const PrefillParams &p, int s) {
+  const int lane = threadIdx.x & 63;
+  int seen = 0;
+  for (int base = 0; base < p.batch; base += 64) {
+    const int i = base + lane;
+    const bool lg = i < p.batch && request_is_long(p, i);
+    const uint64_t mask = __ballot(lg);
+    const int c = __popcll(mask);
+    if (seen + c > s) {  // the (s - seen)-th long request of this round
+      const int rank = __popcll(mask & ((uint64_t(1) << lane) - 1));
+      const uint64_t hit = __ballot(lg && rank == s - seen);
+      return base + __ffsll(static_cast<unsigned long long>(hit)) - 1;
+    }
+    seen += c;
+  }
+  return -1;
+}
 
 template <bool kBf16>
 __device__ __forceinline__ f32x4_t mfma16(u32x4 a, u32x4 b, f32x4_t c) {
@@ -295,6 +344,7 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
   const int rb = rest / p.hkv;
   const int b = rb % p.batch;
   const int qt = p.q_tiles - 1 - rb / p.batch;
+  if (request_has_images(p, b)) return;  // that request runs on the tile-image path (uniform)
   // A request's rows, clipped to the query tensor (query_start_loc is caller data).
   const int q_begin = max(p.query_start_loc[b], 0);
   const int ql = min(p.query_start_loc[b + 1], p.total_q) - q_begin;
@@ -421,9 +471,10 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
 
 // Tile images for the prefill path (long query ranges, where every query tile
 // of a (request, KV head) would decode the same pages again): workgroup
-// (b, h, tile) decodes keys 64 tile .. + 63 of request b, KV head h once into
-// global memory in exactly the layout the attention step copies into LDS.
-// Tiles at or past the request's length are not written (never read).
+// (s, h, tile) decodes keys 64 tile .. + 63 of the request holding image slot
+// s, KV head h, once into global memory in exactly the layout the attention
+// step copies into LDS.  Tiles at or past the request's length are not
+// written (never read).
 template <int kD, bool kBf16, typename BtT>
 __global__ __launch_bounds__(kPThreads) void prefill_decode_tiles_kernel(const PrefillParams p) {
   constexpr int kKPT = kD / 64;
@@ -434,7 +485,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_decode_tiles_kernel(const P
   const int tid = threadIdx.x;
   const int tile = int(blockIdx.x) % p.img_tiles;
   const int bh = int(blockIdx.x) / p.img_tiles;
-  const int h = bh % p.hkv, b = bh / p.hkv;
+  const int h = bh % p.hkv, slot = bh / p.hkv;
+  const int b = request_of_slot(p, slot);
+  if (b < 0) return;  // an unused slot (uniform)
   const int kl = clamp_len(p.seq_lens[b], p.max_len);
   const int k0 = tile * kKT;
   if (k0 >= kl) return;  // uniform
@@ -463,14 +516,14 @@ __global__ __launch_bounds__(kPThreads) void prefill_decode_tiles_kernel(const P
   }
   dec[tid] = __uint_as_float(decode_bits(uint32_t(tid)));
   lds_barrier();
-  uint8_t *im = p.img + ((size_t(b) * p.hkv + h) * p.img_tiles + tile) * kImg;
+  uint8_t *im = p.img + ((size_t(slot) * p.hkv + h) * p.img_tiles + tile) * kImg;
   uint16_t *ks = reinterpret_cast<uint16_t *>(im);
   decode_tile<kD, kBf16>(dec, kraw, vraw, kscl, vscl, ok, kq, dc, ks, ks + kKT * kD,
                          reinterpret_cast<float *>(im + 4 * kKT * kD));
 }
 
-// Prefill over tile images: a workgroup of kWaves wavefronts owns (request,
-// KV head, query tile of 128 / G tokens, key split), 128 rows, kRB blocks of
+// Prefill over tile images: a workgroup of kWaves wavefronts owns (image
+// slot, KV head, query tile of 128 / G tokens, key split), 128 rows, kRB blocks of
 // 16 per wavefront (every K / V^T fragment read from LDS feeds kRB MFMAs); per
 // 64-key tile it copies the image into one of two LDS stages by DMA
 // (global_load_lds_dwordx4, 1 KiB per instruction) while the previous tile's
@@ -492,8 +545,10 @@ __global__ __launch_bounds__(kWaves * 64) void paged_prefill_attention_img_kerne
   const int rest = int(blockIdx.x) / p.num_splits;
   const int h = rest % p.hkv;
   const int rq = rest / p.hkv;
-  const int b = rq % p.batch;
-  const int qt = p.q_tiles - 1 - rq / p.batch;
+  const int slot = rq % p.slots;
+  const int qt = p.q_tiles - 1 - rq / p.slots;
+  const int b = request_of_slot(p, slot);
+  if (b < 0) return;  // an unused slot (uniform)
   const int q_begin = max(p.query_start_loc[b], 0);
   const int ql = min(p.query_start_loc[b + 1], p.total_q) - q_begin;
   const int tok0 = qt * p.tokens_per_tile;
@@ -504,7 +559,7 @@ __global__ __launch_bounds__(kWaves * 64) void paged_prefill_attention_img_kerne
   const int s_k0 = split * p.split_tiles * kKT;
   const int s_k1 = min(s_k0 + p.split_tiles * kKT, k_vis);
   const int ntiles = s_k1 > s_k0 ? (s_k1 - s_k0 + kKT - 1) / kKT : 0;
-  const size_t item = (size_t(b) * p.q_tiles + qt) * p.hkv + h;
+  const size_t item = (size_t(slot) * p.q_tiles + qt) * p.hkv + h;
   // Row block rb of this wavefront: rows 16 (kRB wave + rb) + n.
   int r[kRB], tok[kRB], lim[kRB];
   bool row_ok[kRB];
@@ -521,7 +576,7 @@ __global__ __launch_bounds__(kWaves * 64) void paged_prefill_attention_img_kerne
 
   // Tile t of this (request, KV head) lands in stage s: copy instruction j
   // (wavefront j % kWaves) moves bytes 1024 j .. + 1023, lane i 16 of them.
-  const uint8_t *img = p.img + (size_t(b) * p.hkv + h) * p.img_tiles * kImg + 16 * lane;
+  const uint8_t *img = p.img + (size_t(slot) * p.hkv + h) * p.img_tiles * kImg + 16 * lane;
   const uint32_t lds0 = lds_address(smem_raw);
   const int t0 = s_k0 / kKT;
   auto copy = [&](int t, int stage) {
@@ -593,14 +648,18 @@ __global__ __launch_bounds__(kWaves * 64) void paged_prefill_attention_img_kerne
 // wavefronts measured 11.7 us for 8192 rows of 4 splits.)
 constexpr int kMaxCombineSplits = 64;
 
-template <bool kBf16, int kRows>
+// kSlots: the items are (image slot, query tile, KV head) of the tile-image
+// path; otherwise (request, query tile, KV head) of the in-kernel path.
+template <bool kBf16, int kRows, bool kSlots>
 __global__ __launch_bounds__(kPThreads) void prefill_combine_kernel(const PrefillParams p) {
   const int item = blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int r = int(blockIdx.y) * (kPThreads / kWave) + (threadIdx.x >> 6);
   const int h = item % p.hkv;
   const int qt = (item / p.hkv) % p.q_tiles;
-  const int b = item / (p.hkv * p.q_tiles);
+  const int rq = item / (p.hkv * p.q_tiles);
+  const int b = kSlots ? request_of_slot(p, rq) : rq;
+  if (b < 0 || (!kSlots && request_has_images(p, b))) return;  // uniform
   const int q_begin = max(p.query_start_loc[b], 0);
   const int ql = min(p.query_start_loc[b + 1], p.total_q) - q_begin;
   const int tok = qt * p.tokens_per_tile + (r >> p.log2_group);
@@ -728,36 +787,22 @@ bool prefill_mfma_shape(int64_t d, int64_t dv, int64_t group, int64_t block_size
 
 struct PrefillPlan {
   int tokens_per_tile, q_tiles, num_splits, split_tiles;
-  bool img;       // tile-image path: pages decoded once, then attention over the images
-  int img_tiles;  // 64-key tiles per (request, KV head) in the images
-  int rows;       // (token, head) rows per workgroup
+  int rows;  // (token, head) rows per workgroup
 };
 
-// The in-kernel decode path when at most two query tiles of 64 rows cover
-// the longest query (every page is decoded at most twice; measured on
-// MI355X, 17 rows x 4 heads over 4096 keys: B=1 29.6 vs 29.1 us, B=4 47.1 vs
-// 55.6 us with images); beyond that each query tile would decode the same
-// pages again, and the pages are decoded once into tile images first (64
-// rows per workgroup -> 128; 512 rows over 4096 keys: B=4 461 -> 214 us).
-// Query tiles of rows / G tokens; key splits while the (request, query tile,
-// KV head) items leave fewer than ~512 (in-kernel) or ~256 (images, one
-// eight-wave workgroup per CU) workgroups, each split at least two 64-key
-// tiles.
-PrefillPlan plan_prefill(int64_t batch, int64_t hkv, int64_t group, int64_t max_query_len, int64_t max_len) {
+// One path's plan over `requests` request slots of the grid whose longest
+// query has q_cover tokens: query tiles of rows / G tokens; key splits while
+// the (request, query tile, KV head) items leave fewer than ~512 (in-kernel
+// path) or ~256 (images, one eight-wave workgroup per CU) workgroups, each
+// split at least two 64-key tiles.
+PrefillPlan plan_path(int64_t requests, int64_t hkv, int64_t group, int64_t q_cover, int64_t max_len, bool img) {
   PrefillPlan pl{};
   const int64_t kv_tiles = std::max<int64_t>((max_len + kKT - 1) / kKT, 1);
-  static const int img_env = [] {
-    const char *v = getenv("HIF8_PREFILL_IMAGES");  // tuning: 0 never, 1 for every multi-tile query
-    return v && *v ? atoi(v) : -1;
-  }();
-  pl.img = img_env == 0 ? false
-                       : std::max<int64_t>(max_query_len, 1) * group > (img_env == 1 ? 1 : 2) * kPRows;
-  pl.rows = pl.img ? kIRows : kPRows;
-  pl.img_tiles = pl.img ? int(kv_tiles) : 0;
+  pl.rows = img ? kIRows : kPRows;
   pl.tokens_per_tile = int(pl.rows / group);
-  pl.q_tiles = int((std::max<int64_t>(max_query_len, 1) + pl.tokens_per_tile - 1) / pl.tokens_per_tile);
-  const int64_t items = batch * pl.q_tiles * hkv;
-  const int64_t target = pl.img ? kITargetBlocks : kTargetBlocks;
+  pl.q_tiles = int((std::max<int64_t>(q_cover, 1) + pl.tokens_per_tile - 1) / pl.tokens_per_tile);
+  const int64_t items = std::max<int64_t>(requests, 1) * pl.q_tiles * hkv;
+  const int64_t target = img ? kITargetBlocks : kTargetBlocks;
   int64_t splits = (target + items - 1) / items;
   if (splits > kv_tiles) splits = kv_tiles;
   if (splits < 1) splits = 1;
@@ -767,6 +812,68 @@ PrefillPlan plan_prefill(int64_t batch, int64_t hkv, int64_t group, int64_t max_
   pl.split_tiles = int(per);
   pl.num_splits = int((kv_tiles + per - 1) / per);
   return pl;
+}
+
+// Image bytes the tile-image path may hold per call (512 MiB, or
+// HIF8_PREFILL_IMAGE_CAP_MB, read at every call); long requests beyond the
+// slots this buys take the in-kernel path.
+int64_t image_cap_bytes() {
+  const char *v = getenv("HIF8_PREFILL_IMAGE_CAP_MB");
+  const int64_t mb = v && *v ? atoll(v) : 512;
+  return (mb > 0 ? mb : 0) << 20;
+}
+
+// Both paths of one call.  A request runs on the tile-image path when its
+// query covers more than two 64-row tiles (every page would otherwise be
+// decoded once per query tile; measured on MI355X, 512 rows over 4096 keys:
+// B=4 461 -> 214 us) and it gets an image slot; up to two tiles the
+// in-kernel decode is as fast or faster (17 rows x 4 heads over 4096 keys:
+// B=1 29.6 vs 29.1 us, B=4 47.1 vs 55.6 us with images).  Slots: at most one
+// per request that can be long (total_q / (long_rows / G + 1) of them), within
+// image_cap_bytes().  When every long request has a slot, the in-kernel path
+// covers only the short ones (two query tiles).
+struct PrefillPlans {
+  PrefillPlan in, img;
+  int slots, long_rows, img_tiles;
+};
+
+PrefillPlans plan_prefill(int64_t batch, int64_t hkv, int64_t group, int64_t total_q, int64_t max_query_len,
+                          int64_t max_len, int d) {
+  static const int img_env = [] {
+    const char *v = getenv("HIF8_PREFILL_IMAGES");  // tuning: 0 never, 1 for every multi-tile query
+    return v && *v ? atoi(v) : -1;
+  }();
+  PrefillPlans pp{};
+  const int64_t kv_tiles = std::max<int64_t>((max_len + kKT - 1) / kKT, 1);
+  pp.long_rows = img_env == 1 ? kPRows : 2 * kPRows;
+  int64_t long_max = 0;
+  if (img_env != 0 && std::max<int64_t>(max_query_len, 1) * group > pp.long_rows) {
+    long_max = std::min<int64_t>(batch, total_q / (pp.long_rows / group + 1));
+    const int64_t per_slot = hkv * kv_tiles * int64_t(img_bytes(d));
+    pp.slots = int(std::min<int64_t>(long_max, std::max<int64_t>(1, image_cap_bytes() / per_slot)));
+  }
+  pp.img_tiles = pp.slots > 0 ? int(kv_tiles) : 0;
+  if (pp.slots > 0) pp.img = plan_path(pp.slots, hkv, group, max_query_len, max_len, true);
+  const int64_t in_cover =
+      pp.slots > 0 && pp.slots >= long_max ? std::min<int64_t>(max_query_len, pp.long_rows / group) : max_query_len;
+  pp.in = plan_path(batch, hkv, group, in_cover, max_len, false);
+  return pp;
+}
+
+// Workspace bytes: images, the image path's split partials, the in-kernel
+// path's split partials (each partial region: outputs, then (max, sum)).
+struct PrefillWorkspace {
+  size_t images, img_parts, in_parts;
+};
+
+PrefillWorkspace prefill_workspace(const PrefillPlans &pp, int64_t batch, int64_t hkv, int d, int dv) {
+  PrefillWorkspace w{};
+  w.images = size_t(pp.slots) * hkv * pp.img_tiles * img_bytes(d);
+  if (pp.slots > 0 && pp.img.num_splits > 1)
+    w.img_parts = size_t(pp.slots) * pp.img.q_tiles * hkv * pp.img.num_splits * pp.img.rows * size_t(dv + 2) * 4;
+  if (pp.in.num_splits > 1)
+    w.in_parts = size_t(batch) * pp.in.q_tiles * hkv * pp.in.num_splits * pp.in.rows * size_t(dv + 2) * 4;
+  return w;
 }
 
 size_t prefill_smem(int d) { return size_t(256 + kKT) * 4 + size_t(2) * kKT * d * 2; }
@@ -779,7 +886,7 @@ int launch_prefill_mfma(const PrefillParams &p, hipStream_t stream) {
   const unsigned blocks = unsigned(int64_t(p.q_tiles) * p.batch * p.hkv * p.num_splits);
   paged_prefill_attention_kernel<kD, kBf16, BtT><<<blocks, kPThreads, smem, stream>>>(p);
   if (p.num_splits > 1)
-    prefill_combine_kernel<kBf16, kPRows>
+    prefill_combine_kernel<kBf16, kPRows, false>
         <<<dim3(unsigned(int64_t(p.batch) * p.q_tiles * p.hkv), kPRows / (kPThreads / kWave)), kPThreads, 0, stream>>>(p);
   return HIF8_OK;
 }
@@ -787,39 +894,44 @@ int launch_prefill_mfma(const PrefillParams &p, hipStream_t stream) {
 template <int kD, bool kBf16, typename BtT>
 int launch_prefill_img(const PrefillParams &p, hipStream_t stream) {
   prefill_decode_tiles_kernel<kD, kBf16, BtT>
-      <<<unsigned(int64_t(p.batch) * p.hkv * p.img_tiles), kPThreads, 0, stream>>>(p);
+      <<<unsigned(int64_t(p.slots) * p.hkv * p.img_tiles), kPThreads, 0, stream>>>(p);
   // Eight wavefronts of one 16-row block each.  Four wavefronts of two
   // blocks (half the LDS fragment reads per row, one wavefront per SIMD)
   // measured slower on MI355X: 512 rows over 4096 keys, B=4 310 vs 214 us.
   const size_t smem = 2 * size_t(img_bytes(kD));
-  const unsigned blocks = unsigned(int64_t(p.q_tiles) * p.batch * p.hkv * p.num_splits);
+  const unsigned blocks = unsigned(int64_t(p.q_tiles) * p.slots * p.hkv * p.num_splits);
   const auto kern = &paged_prefill_attention_img_kernel<kD, kBf16, kIWaves, 1>;
   if (const int st = reserve_dynamic_lds(reinterpret_cast<const void *>(kern), smem, "hif8_paged_prefill_attention"))
     return st;
   kern<<<blocks, kIThreads, smem, stream>>>(p);
   if (p.num_splits > 1)
-    prefill_combine_kernel<kBf16, kIRows>
-        <<<dim3(unsigned(int64_t(p.batch) * p.q_tiles * p.hkv), kIRows / (kPThreads / kWave)), kPThreads, 0, stream>>>(p);
+    prefill_combine_kernel<kBf16, kIRows, true>
+        <<<dim3(unsigned(int64_t(p.slots) * p.q_tiles * p.hkv), kIRows / (kPThreads / kWave)), kPThreads, 0, stream>>>(p);
   return HIF8_OK;
 }
 
+// p_in: the in-kernel path (every request without an image slot); p_img
+// (p_img.slots > 0): the tile-image path.  The two write disjoint rows.
 template <bool kBf16, typename BtT>
-int launch_prefill(const PrefillParams &p, bool mfma, int64_t total_q, hipStream_t stream) {
+int launch_prefill(const PrefillParams &p_in, const PrefillParams &p_img, bool mfma, int64_t total_q,
+                   hipStream_t stream) {
   if (!mfma) {
-    paged_prefill_attention_simple<kBf16, BtT><<<unsigned(total_q * p.hq), kWave, 0, stream>>>(p, int(total_q));
+    paged_prefill_attention_simple<kBf16, BtT><<<unsigned(total_q * p_in.hq), kWave, 0, stream>>>(p_in, int(total_q));
     return HIF8_OK;
   }
-  if (p.img) {
-    switch (p.d) {
-      case 64: return launch_prefill_img<64, kBf16, BtT>(p, stream);
-      case 128: return launch_prefill_img<128, kBf16, BtT>(p, stream);
-      default: return launch_prefill_img<256, kBf16, BtT>(p, stream);
+  if (p_img.slots > 0) {
+    int st;
+    switch (p_img.d) {
+      case 64: st = launch_prefill_img<64, kBf16, BtT>(p_img, stream); break;
+      case 128: st = launch_prefill_img<128, kBf16, BtT>(p_img, stream); break;
+      default: st = launch_prefill_img<256, kBf16, BtT>(p_img, stream); break;
     }
+    if (st) return st;
   }
-  switch (p.d) {
-    case 64: return launch_prefill_mfma<64, kBf16, BtT>(p, stream);
-    case 128: return launch_prefill_mfma<128, kBf16, BtT>(p, stream);
-    default: return launch_prefill_mfma<256, kBf16, BtT>(p, stream);
+  switch (p_in.d) {
+    case 64: return launch_prefill_mfma<64, kBf16, BtT>(p_in, stream);
+    case 128: return launch_prefill_mfma<128, kBf16, BtT>(p_in, stream);
+    default: return launch_prefill_mfma<256, kBf16, BtT>(p_in, stream);
   }
 }
 
@@ -830,17 +942,17 @@ using namespace hif8;
 
 extern "C" size_t hif8_paged_prefill_attention_workspace_size(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
                                                               int64_t head_size, int64_t head_size_v,
-                                                              int64_t max_query_len, int64_t max_seq_len) {
+                                                              int64_t total_query_tokens, int64_t max_query_len,
+                                                              int64_t max_seq_len) {
   if (batch <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_size <= 0 || head_size_v <= 0 ||
-      max_query_len <= 0 || max_seq_len <= 0 || num_heads % num_kv_heads)
+      total_query_tokens <= 0 || max_query_len <= 0 || max_seq_len <= 0 || num_heads % num_kv_heads)
     return 0;
   const int64_t group = num_heads / num_kv_heads;
   if (!prefill_mfma_shape(head_size, head_size_v, group, 4)) return 0;  // the simple kernel needs none
-  const PrefillPlan pl = plan_prefill(batch, num_kv_heads, group, max_query_len, max_seq_len);
-  const size_t images = pl.img ? size_t(batch) * num_kv_heads * pl.img_tiles * img_bytes(int(head_size)) : 0;
-  if (pl.num_splits <= 1) return images;
-  const size_t parts = size_t(batch) * pl.q_tiles * num_kv_heads * pl.num_splits * pl.rows;
-  return images + parts * size_t(head_size_v + 2) * sizeof(float);
+  const PrefillPlans pp =
+      plan_prefill(batch, num_kv_heads, group, total_query_tokens, max_query_len, max_seq_len, int(head_size));
+  const PrefillWorkspace w = prefill_workspace(pp, batch, num_kv_heads, int(head_size), int(head_size_v));
+  return w.images + w.img_parts + w.in_parts;
 }
 
 extern "C" int hif8_paged_prefill_attention(const void *query, int q_dtype, const uint8_t *key_cache,
@@ -908,20 +1020,29 @@ extern "C" int hif8_paged_prefill_attention(const void *query, int q_dtype, cons
   p.scale_log2 = scale * 1.4426950408889634f;
   const bool mfma = prefill_mfma_shape(head_size, head_size_v, p.group, block_size) && aligned(query, 16) &&
                     aligned(out, 16);
+  PrefillParams pi = p;  // the tile-image path
+  p.log2_group = log2_exact(p.group);
   if (mfma) {
-    const PrefillPlan pl = plan_prefill(batch, num_kv_heads, p.group, max_query_len, max_seq_len);
-    p.log2_group = log2_exact(p.group);
-    p.tokens_per_tile = pl.tokens_per_tile;
-    p.q_tiles = pl.q_tiles;
-    p.num_splits = pl.num_splits;
-    p.split_tiles = pl.split_tiles;
-    p.img = nullptr;
-    p.img_tiles = pl.img_tiles;
+    const PrefillPlans pp =
+        plan_prefill(batch, num_kv_heads, p.group, total_query_tokens, max_query_len, max_seq_len, int(head_size));
+    auto apply = [](PrefillParams &q, const PrefillPlan &pl) {
+      q.tokens_per_tile = pl.tokens_per_tile;
+      q.q_tiles = pl.q_tiles;
+      q.num_splits = pl.num_splits;
+      q.split_tiles = pl.split_tiles;
+    };
+    p.slots = pp.slots;
+    p.long_rows = pp.long_rows;
+    apply(p, pp.in);
+    pi = p;
+    if (pp.slots > 0) apply(pi, pp.img);
+    pi.img_tiles = pp.img_tiles;
     if (int64_t(p.q_tiles) * batch * num_kv_heads * p.num_splits > 0x7FFFFFFFll ||
-        batch * num_kv_heads * int64_t(pl.img_tiles) > 0x7FFFFFFFll)
+        int64_t(pi.q_tiles) * pp.slots * num_kv_heads * pi.num_splits > 0x7FFFFFFFll ||
+        int64_t(pp.slots) * num_kv_heads * pp.img_tiles > 0x7FFFFFFFll)
       return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: too many query tiles");
-    const size_t need = hif8_paged_prefill_attention_workspace_size(batch, num_heads, num_kv_heads, head_size,
-                                                                    head_size_v, max_query_len, max_seq_len);
+    const PrefillWorkspace w = prefill_workspace(pp, batch, num_kv_heads, int(head_size), int(head_size_v));
+    const size_t need = w.images + w.img_parts + w.in_parts;
     if (need > 0) {
       if (!workspace || workspace_bytes < need)
         return fail(HIF8_ERR_INVALID_ARGUMENT,
@@ -930,11 +1051,14 @@ extern "C" int hif8_paged_prefill_attention(const void *query, int q_dtype, cons
       if (!aligned(workspace, 16))
         return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_paged_prefill_attention: workspace must be 16-byte aligned");
       uint8_t *ws = static_cast<uint8_t *>(workspace);
-      const size_t images = pl.img ? size_t(batch) * num_kv_heads * pl.img_tiles * img_bytes(int(head_size)) : 0;
-      if (pl.img) p.img = ws;
-      if (pl.num_splits > 1) {
-        p.part_o = reinterpret_cast<float *>(ws + images);
-        p.part_ml = p.part_o + size_t(batch) * pl.q_tiles * num_kv_heads * pl.num_splits * pl.rows * head_size_v;
+      if (pp.slots > 0) pi.img = ws;
+      if (w.img_parts) {
+        pi.part_o = reinterpret_cast<float *>(ws + w.images);
+        pi.part_ml = pi.part_o + size_t(pp.slots) * pi.q_tiles * num_kv_heads * pi.num_splits * kIRows * head_size_v;
+      }
+      if (w.in_parts) {
+        p.part_o = reinterpret_cast<float *>(ws + w.images + w.img_parts);
+        p.part_ml = p.part_o + size_t(batch) * p.q_tiles * num_kv_heads * p.num_splits * kPRows * head_size_v;
       }
     }
   } else {
@@ -947,10 +1071,10 @@ extern "C" int hif8_paged_prefill_attention(const void *query, int q_dtype, cons
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const bool bf16 = q_dtype == HIF8_DTYPE_BF16, i64 = block_table_dtype == HIF8_INDEX_INT64;
   int st;
-  if (bf16 && i64) st = launch_prefill<true, int64_t>(p, mfma, total_query_tokens, s);
-  else if (bf16) st = launch_prefill<true, int32_t>(p, mfma, total_query_tokens, s);
-  else if (i64) st = launch_prefill<false, int64_t>(p, mfma, total_query_tokens, s);
-  else st = launch_prefill<false, int32_t>(p, mfma, total_query_tokens, s);
+  if (bf16 && i64) st = launch_prefill<true, int64_t>(p, pi, mfma, total_query_tokens, s);
+  else if (bf16) st = launch_prefill<true, int32_t>(p, pi, mfma, total_query_tokens, s);
+  else if (i64) st = launch_prefill<false, int64_t>(p, pi, mfma, total_query_tokens, s);
+  else st = launch_prefill<false, int32_t>(p, pi, mfma, total_query_tokens, s);
   if (st) return st;
   return check_launch("hif8_paged_prefill_attention");
 }

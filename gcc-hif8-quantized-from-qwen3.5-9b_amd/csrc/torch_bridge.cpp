@@ -534,8 +534,8 @@ at::Tensor Hif8PagedPrefillAttention(const at::Tensor &query, const at::Tensor &
   const c10::OptionalDeviceGuard guard(device);
   auto out = at::empty({tokens, heads, dv}, query.options());
   if (batch == 0 || tokens == 0 || max_query_len == 0) return out;
-  const size_t ws_bytes = hif8_paged_prefill_attention_workspace_size(batch, heads, kv_heads, d, dv, max_query_len,
-                                                                      max_seq_len > 0 ? max_seq_len : 1);
+  const size_t ws_bytes = hif8_paged_prefill_attention_workspace_size(batch, heads, kv_heads, d, dv, tokens,
+                                                                      max_query_len, max_seq_len > 0 ? max_seq_len : 1);
   at::Tensor workspace;
   if (ws_bytes) workspace = at::empty({int64_t(ws_bytes)}, query.options().dtype(at::ScalarType::Byte));
   CheckStatus(hif8_paged_prefill_attention(
@@ -829,6 +829,50 @@ at::Tensor Hif8EmbeddingLookupMeta(const at::Tensor &ids, const at::Tensor &weig
   return at::empty(shape, weight.options().dtype(at::kBFloat16));
 }
 
+// The decode glue ops (shapes and dtypes of the CUDA implementations above).
+at::Tensor Hif8AddRmsNormMeta(at::Tensor &h, const c10::optional<at::Tensor> &, const at::Tensor &, double) {
+  return at::empty_like(h);
+}
+
+at::Tensor Hif8SiluMulMeta(const at::Tensor &gate_up) {
+  std::vector<int64_t> shape(gate_up.sizes().begin(), gate_up.sizes().end());
+  shape.back() /= 2;
+  return at::empty(shape, gate_up.options());
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor> Hif8AddRmsNormQuantMeta(at::Tensor &h, const c10::optional<at::Tensor> &,
+                                                                       const at::Tensor &, double, const at::Tensor &) {
+  return {at::empty_like(h), at::empty(h.sizes(), h.options().dtype(at::kByte)),
+          at::empty(LeadingShape(h), h.options().dtype(at::kFloat))};
+}
+
+std::tuple<at::Tensor, at::Tensor> Hif8SiluMulQuantMeta(const at::Tensor &gate_up, const at::Tensor &) {
+  std::vector<int64_t> shape(gate_up.sizes().begin(), gate_up.sizes().end());
+  shape.back() /= 2;
+  return {at::empty(shape, gate_up.options().dtype(at::kByte)),
+          at::empty(LeadingShape(gate_up), gate_up.options().dtype(at::kFloat))};
+}
+
+at::Tensor Hif8Bf16GemvMeta(const at::Tensor &x, const at::Tensor &weight) {
+  return at::empty({x.size(0), weight.size(0)}, x.options());
+}
+
+std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> Hif8QkNormRopeMeta(
+    const at::Tensor &qkv, const at::Tensor &, const at::Tensor &, const at::Tensor &, const at::Tensor &,
+    const at::Tensor &, int64_t, int64_t num_heads, int64_t num_kv_heads, int64_t head_size, double) {
+  const int64_t batch = qkv.size(0);
+  return {at::empty({batch, num_heads, head_size}, qkv.options()),
+          at::empty({batch, num_kv_heads, head_size}, qkv.options()),
+          at::empty({batch, num_kv_heads, head_size}, qkv.options()),
+          at::empty({batch}, qkv.options().dtype(at::kLong))};
+}
+
+at::Tensor Hif8GdnDecodeStepMeta(const at::Tensor &mixed, const at::Tensor &, const at::Tensor &, at::Tensor &,
+                                 const at::Tensor &, const at::Tensor &, at::Tensor &, const at::Tensor &, int64_t,
+                                 int64_t v_heads, int64_t, int64_t v_dim, double) {
+  return at::empty({mixed.size(0), v_heads * v_dim}, mixed.options());
+}
+
 }  // namespace
 
 TORCH_LIBRARY(vllm_ascend_hif8, m) {
@@ -892,6 +936,13 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
   m.impl("soft_hif8_fused_gemm", &FusedLinearMeta);
   m.impl("soft_hif8_gemm_decoded_weight", &LinearMeta);
   m.impl("hif8_decode_bf16", &Hif8DecodeBf16Meta);
+  m.impl("hif8_add_rms_norm", &Hif8AddRmsNormMeta);
+  m.impl("hif8_silu_mul", &Hif8SiluMulMeta);
+  m.impl("hif8_add_rms_norm_quant", &Hif8AddRmsNormQuantMeta);
+  m.impl("hif8_silu_mul_quant", &Hif8SiluMulQuantMeta);
+  m.impl("hif8_bf16_gemv", &Hif8Bf16GemvMeta);
+  m.impl("hif8_qk_norm_rope", &Hif8QkNormRopeMeta);
+  m.impl("hif8_gdn_decode_step", &Hif8GdnDecodeStepMeta);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {

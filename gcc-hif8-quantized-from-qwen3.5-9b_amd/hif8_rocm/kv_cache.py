@@ -270,8 +270,10 @@ def paged_attention(
     reference's oracle takes them; rows must add up to T) or from
     ``query_start_loc`` (an int32 device tensor ``[B + 1]``, the cumulative
     form of the reference's ``actual_seq_lengths_q`` with a leading 0; pass
-    ``max_query_len`` to avoid a host synchronisation).  One query row per
-    request runs the decode kernel; otherwise the multi-token kernel.
+    ``max_query_len`` to avoid a host synchronisation, and ``validate=False``
+    as well, since validation checks it against ``query_start_loc``).  One
+    query row per request runs the decode kernel; otherwise the multi-token
+    kernel.
     """
     _check_caches(key_cache, value_cache)
     if query.ndim != 3:
@@ -336,6 +338,12 @@ def paged_attention(
     if table.dtype not in (torch.int32, torch.int64):
         table = table.to(torch.int64)
     table = table.to(query.device).contiguous()
+    if validate and batch:
+        # A max_query_len below the longest request would leave that request's
+        # later rows unwritten (the grid is sized by it).
+        longest = int((loc[1:batch + 1] - loc[:batch]).max().item())
+        if longest > max_query_len:
+            raise ValueError(f"max_query_len ({max_query_len}) is smaller than a request's query length ({longest})")
     if validate and batch and max_seq_len > 0:
         if bool((lens_dev[:batch] > max_seq_len).any()):
             raise ValueError("max_seq_len is smaller than a sequence length")

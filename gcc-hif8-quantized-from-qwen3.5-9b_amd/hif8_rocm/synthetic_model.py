@@ -462,6 +462,14 @@ class HybridModel:
         c = self.cfg
         if decode:
             return self._forward_decode(st, ids, pos)
+        # A prefill is never graph-captured, so the lengths can be checked
+        # here: the T rows are the last T positions of st.seq_lens, so each
+        # length must be the last position + 1 (a stale st.seq_lens would give
+        # rows that see no keys, i.e. silent zero attention).
+        want = pos[:, -1].to(torch.int64) + 1
+        if st.seq_lens is None or not torch.equal(st.seq_lens[:pos.shape[0]].to(torch.int64), want):
+            raise ValueError("st.seq_lens must hold each request's length including these tokens "
+                             "(the last position + 1) before a prefill forward")
         h = self.embed_method.embedding(self.embed, ids)
         attn_i = lin_i = 0
         for i, L in enumerate(self.layers):

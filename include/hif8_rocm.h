@@ -302,12 +302,16 @@ int hif8_paged_decode_attention_noalloc(const void *query, int q_dtype, const ui
 
 /*
  * Bytes of workspace hif8_paged_prefill_attention needs for these sizes (0 if none);
- * the key-split plan depends only on these arguments (ACLNN GetWorkspaceSize phase,
- * csrc/extension/hif8_native.cpp:202-239).
+ * the plan (image slots, key splits) depends only on these arguments (ACLNN
+ * GetWorkspaceSize phase, csrc/extension/hif8_native.cpp:202-239).  Requests whose
+ * query covers more than two 64-row tiles (rows = tokens x query heads per KV head)
+ * get decoded tile images while the images of all such requests fit 512 MiB; the
+ * others decode their pages inside the attention kernel.
  */
 size_t hif8_paged_prefill_attention_workspace_size(int64_t batch, int64_t num_heads, int64_t num_kv_heads,
                                                    int64_t head_size, int64_t head_size_v,
-                                                   int64_t max_query_len, int64_t max_seq_len);
+                                                   int64_t total_query_tokens, int64_t max_query_len,
+                                                   int64_t max_seq_len);
 
 /*
  * Paged HiF8 attention for several query tokens per request: prefill and chunked

@@ -509,7 +509,8 @@ def decode_kv_rows(data: np.ndarray, scale: np.ndarray) -> np.ndarray:
 
 def paged_attention_reference(query: np.ndarray, key_cache: np.ndarray, value_cache: np.ndarray,
                               block_table: np.ndarray, seq_lens, block_size: int, scale: float,
-                              rounding: str = "bf16", query_lens=None, causal: bool = True) -> np.ndarray:
+                              rounding: str = "bf16", query_lens=None, causal: bool = True,
+                              dtype: str = "bf16") -> np.ndarray:
     """Paged attention over HiF8 pages (kv_cache.py:314-372).
 
     ``query`` holds bf16 values as float32.  Without ``query_lens`` it is
@@ -521,16 +522,22 @@ def paged_attention_reference(query: np.ndarray, key_cache: np.ndarray, value_ca
     right-aligned mask of kv_cache.py:365-369; sparse_mode=3 in
     kv_runtime.py:1526-1540).  Without ``causal`` every row sees every key.
 
-    K/V rows are gathered, decoded as bf16_RNE(dec(b) * s_row) and query head
-    h attends KV head h // (Hq / Hkv), the head ``repeat_interleave`` gives it
-    (kv_cache.py:355-363).  ``rounding="bf16"`` reproduces the reference's
-    bf16 intermediate roundings (logits, probabilities and output are bf16
-    tensors in kv_cache.py:364-371); ``rounding="f64"`` keeps every
-    intermediate in float64.  A query row that sees no key (an empty request,
+    ``dtype`` is the query dtype ("bf16" or "f16"): K/V rows are gathered,
+    decoded as dtype_RNE(dec(b) * s_row) (``decode_kv_rows(...).to(
+    query.dtype)``) and query head h attends KV head h // (Hq / Hkv), the head
+    ``repeat_interleave`` gives it (kv_cache.py:355-363).  ``rounding="bf16"``
+    reproduces the reference's intermediate roundings to the query dtype
+    (logits, probabilities and output are query-dtype tensors in
+    kv_cache.py:364-371; the name is kept from when only bf16 queries were
+    covered); ``rounding="f64"`` keeps every intermediate after the K/V
+    decode in float64.  A query row that sees no key (an empty request,
     or a row whose position is negative because query_lens[b] > seq_lens[b],
     which the reference's attention plan rejects, kv_runtime.py:626-633)
     yields zeros.
     """
+    if dtype not in ("bf16", "f16"):
+        raise ValueError("dtype must be 'bf16' or 'f16'")
+    rnd = round_bf16 if dtype == "bf16" else round_f16
     q = np.asarray(query, dtype=np.float64)
     rows_total, hq, d = q.shape
     lengths = [int(v) for v in seq_lens]
@@ -559,8 +566,8 @@ def paged_attention_reference(query: np.ndarray, key_cache: np.ndarray, value_ca
             continue
         kd, ks = unpack_kv_rows(krows[b], kw)
         vd, vs = unpack_kv_rows(vrows[b], vw)
-        keys = round_bf16(decode_kv_rows(kd, ks)).astype(np.float64)      # [L, Hkv, D]
-        vals = round_bf16(decode_kv_rows(vd, vs)).astype(np.float64)
+        keys = rnd(decode_kv_rows(kd, ks)).astype(np.float64)             # [L, Hkv, D]
+        vals = rnd(decode_kv_rows(vd, vs)).astype(np.float64)
         qg = q[rows].reshape(ql, hkv, group, d)                           # head h = j * group + g
         logits = np.einsum("qjgd,kjd->qjgk", qg, keys, optimize=True)     # [ql, Hkv, G, L]
         visible = np.ones((ql, kl), dtype=bool)
@@ -570,17 +577,17 @@ def paged_attention_reference(query: np.ndarray, key_cache: np.ndarray, value_ca
         mask = visible[:, None, None, :]
         seen = visible.any(axis=1)                                        # rows with at least one key
         if rounding == "bf16":
-            logits = round_bf16(logits).astype(np.float64)
-            logits = round_bf16(logits * np.float32(scale)).astype(np.float64)
+            logits = rnd(logits).astype(np.float64)
+            logits = rnd(logits * np.float32(scale)).astype(np.float64)
             logits = np.where(mask, logits, -np.inf)
             mx = logits.max(axis=-1, keepdims=True)
             mx = np.where(np.isfinite(mx), mx, 0.0)
             with np.errstate(invalid="ignore"):
                 e = np.exp((logits - mx).astype(np.float32)).astype(np.float64)
-                probs = round_bf16(e / e.sum(axis=-1, keepdims=True)).astype(np.float64)
+                probs = rnd(e / e.sum(axis=-1, keepdims=True)).astype(np.float64)
             probs = np.where(mask, probs, 0.0)
             res = np.einsum("qjgk,kjd->qjgd", probs, vals, optimize=True).reshape(ql, hq, vw)
-            res = round_bf16(res)
+            res = rnd(res)
         else:
             logits = np.where(mask, logits * scale, -np.inf)
             mx = logits.max(axis=-1, keepdims=True)

@@ -137,25 +137,36 @@ def test_gemm_workspace_query_follows_the_split_plan(lib):
 
 
 def test_prefill_attention_contract_and_workspace_plan(lib):
-    """Multi-token paged attention: the workspace follows the plan (up to two
-    query tiles of 64 / G tokens: in-kernel page decode, key splits while the
-    tiles leave < 512 workgroups; more: tile images of every 64-key tile,
-    66560 bytes each at D=256, and 128 / G tokens per query tile with splits
-    below 256 workgroups; two or more 64-key tiles per split), and invalid
-    arguments are rejected before any launch."""
+    """Multi-token paged attention: the workspace follows the plan and invalid
+    arguments are rejected before any launch.  Plan: a request whose query
+    covers more than two query tiles of 64 rows (rows = tokens x G query heads
+    per KV head) is long and takes an image slot - the decoded images of its
+    64-key tiles, 66560 bytes each at D=256 - while slots are left: at most
+    total_q / (128 / G + 1) of them and as many as fit 512 MiB.  The tile-image
+    path runs 128 / G tokens per query tile and splits keys below 256
+    workgroups; the in-kernel path runs 64 / G tokens per tile (only the short
+    requests' two tiles when every long request has a slot) and splits below
+    512 workgroups; two or more 64-key tiles per split; each split partial row
+    holds Dv outputs + (max, sum) in fp32."""
     size = lib.hif8_paged_prefill_attention_workspace_size
-    size.argtypes = [ctypes.c_int64] * 7
+    size.argtypes = [ctypes.c_int64] * 8
     size.restype = ctypes.c_size_t
-    # B=1, q 17, ctx 4096, G 4: 2 query tiles x 4 heads, 64 key tiles in 32 splits of 2.
-    assert size(1, 16, 4, 256, 256, 17, 4096) == 1 * 2 * 4 * 32 * 64 * (256 + 2) * 4
-    # B=4, q 512: tile images (4 x 4 heads x 64 tiles); 16 query tiles x 4 heads x 4 fill
-    # the 256 workgroups, no split.
-    assert size(4, 16, 4, 256, 256, 512, 4096) == 4 * 4 * 64 * 66560
-    # B=1, q 512: images + 4 splits of 16 tiles for 16 query tiles x 4 heads of 128 rows.
-    assert size(1, 16, 4, 256, 256, 512, 4096) == 4 * 64 * 66560 + 16 * 4 * 4 * 128 * (256 + 2) * 4
+    part = (256 + 2) * 4
+    # B=1, q 17, ctx 4096, G 4: no long request; 2 query tiles x 4 heads, 64 key tiles in 32 splits of 2.
+    assert size(1, 16, 4, 256, 256, 17, 17, 4096) == 1 * 2 * 4 * 32 * 64 * part
+    # B=4, q 512: four image slots (4 x 4 heads x 64 tiles); 16 query tiles x 4 heads x 4 fill the
+    # 256 workgroups, no split; the in-kernel path keeps 2 query tiles x 4 heads x 4 in 16 splits.
+    assert size(4, 16, 4, 256, 256, 2048, 512, 4096) == 4 * 4 * 64 * 66560 + 4 * 2 * 4 * 16 * 64 * part
+    # B=1, q 512: one slot + 4 splits of 16 tiles for 16 query tiles x 4 heads of 128 rows.
+    assert size(1, 16, 4, 256, 256, 512, 512, 4096) == (4 * 64 * 66560 + 16 * 4 * 4 * 128 * part
+                                                         + 1 * 2 * 4 * 32 * 64 * part)
+    # Chunked prefill at ctx 16384: one 512-token chunk + 63 decode rows.  At most 575 / 33 = 17
+    # requests can be long, 7 slots of 68,157,440 bytes fit 512 MiB; long requests past them run
+    # in-kernel, so that path covers all 32 query tiles (8192 items: no split).
+    assert size(64, 16, 4, 256, 256, 575, 512, 16384) == 7 * 4 * 256 * 66560
     # Shapes for the one-wavefront kernel need none.
-    assert size(1, 12, 4, 64, 64, 17, 4096) == 0 and size(1, 16, 4, 24, 24, 17, 4096) == 0
-    assert size(0, 16, 4, 256, 256, 17, 4096) == 0 and size(1, 15, 4, 256, 256, 17, 4096) == 0
+    assert size(1, 12, 4, 64, 64, 17, 17, 4096) == 0 and size(1, 16, 4, 24, 24, 17, 17, 4096) == 0
+    assert size(0, 16, 4, 256, 256, 17, 17, 4096) == 0 and size(1, 15, 4, 256, 256, 17, 17, 4096) == 0
     f = lib.hif8_paged_prefill_attention
     f.argtypes = ([ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int64] * 5 +
                   [ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p, ctypes.c_void_p] +

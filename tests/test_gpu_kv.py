@@ -146,8 +146,13 @@ def _check_attention(device, lens, hq, hkv, d, bs, *, dtype=torch.bfloat16, bt_d
     torch.cuda.synchronize()
     got = out.float().cpu().numpy()
     kcn, vcn, tn = kc.cpu().numpy(), vc.cpu().numpy(), table.numpy()
-    ref = o.paged_attention_reference(q.float().numpy(), kcn, vcn, tn, lens, bs, scale, rounding="f64")
-    ref16 = o.paged_attention_reference(q.float().numpy(), kcn, vcn, tn, lens, bs, scale, rounding="bf16")
+    # K/V (and, in the second oracle, every intermediate) rounded to the query dtype.
+    qdt = "f16" if dtype == torch.float16 else "bf16"
+    ref = o.paged_attention_reference(q.float().numpy(), kcn, vcn, tn, lens, bs, scale, rounding="f64", dtype=qdt)
+    ref16 = o.paged_attention_reference(q.float().numpy(), kcn, vcn, tn, lens, bs, scale, rounding="bf16",
+                                        dtype=qdt)
+    if dtype == torch.float16:
+        bound = min(bound, 5e-3)  # fp16 keeps 11 bits: V, P and the output round 8x finer than bf16
     assert np.isfinite(got).all()
     np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-2)
     if q_mul <= 1.0:
@@ -233,7 +238,34 @@ def test_attention_other_shapes(native_ops, device, hq, hkv, d, bs, lens, bt_dty
 
 
 def test_attention_fp16_query(native_ops, device):
+    """fp16 queries: K, V and the softmax weights round to fp16 (the reference's
+    query.dtype), against the fp16-rounding oracles with a bound 4x tighter
+    than bf16's; a mixed-scale cache keeps P' * row scale in bf16 and is held to
+    the same bound; the any-shape kernel rounds K/V to fp16 too."""
     _check_attention(device, [513, 2000], 16, 4, 256, 128, dtype=torch.float16, seed=6)
+    _check_attention(device, [3000, 129, 64], 16, 4, 256, 128, dtype=torch.float16, seed=9, mixed=True)
+    _check_attention(device, [40, 17], 4, 2, 64, 8, dtype=torch.float16, dv=32, seed=10)
+
+
+def test_attention_fp16_decode_and_multi_token_kernels_agree(native_ops, device):
+    """One query row per request through the decode kernel and through the
+    multi-token kernel (the op paged_attention routes q_len = 1 batches away
+    from): both round V and P to fp16 for fp16 queries, so they agree to fp16
+    resolution, not just to the 1e-2 tolerance."""
+    lens = [700, 4096, 33]
+    kc, vc, table = _build_cache(device, lens, 4, 256, 128, 41)
+    q = _randn((len(lens), 16, 256), 42, 1.0, torch.float16).to(device)
+    loc = torch.arange(len(lens) + 1, dtype=torch.int32, device=device)
+    lens_d = torch.tensor(lens, dtype=torch.int32, device=device)
+    dec = torch.ops.vllm_ascend_hif8.hif8_paged_decode_attention(q, kc, vc, table.to(device), lens_d, 0.0625,
+                                                                  max(lens))
+    pre = torch.ops.vllm_ascend_hif8.hif8_paged_prefill_attention(q, kc, vc, table.to(device), loc, lens_d, 0.0625,
+                                                                   1, max(lens), True)
+    torch.cuda.synchronize()
+    a, b = dec.float().cpu(), pre.float().cpu()
+    rel = float(((a - b).abs().amax(dim=-1) / b.abs().amax(dim=-1).clamp_min(1e-3)).max())
+    print(f"fp16 decode vs multi-token kernel: max err/|out| {rel:.2e}", flush=True)
+    assert rel < 2e-3, rel
 
 
 @pytest.mark.parametrize("hq,hkv,d,dv,bs,lens", [

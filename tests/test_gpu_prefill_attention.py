@@ -54,8 +54,11 @@ def _check(device, lens, qlens, hq, hkv, d, bs, *, causal=True, dtype=torch.bflo
     got = out.float().cpu().numpy()
     kcn, vcn, tn = kc.cpu().numpy(), vc.cpu().numpy(), table.numpy()
     qn = q.float().numpy()
+    qdt = "f16" if dtype == torch.float16 else "bf16"   # K/V rounded to the query dtype
+    if dtype == torch.float16:
+        bound = min(bound, 5e-3)  # fp16 keeps 11 bits: V, P and the output round 8x finer than bf16
     ref = o.paged_attention_reference(qn, kcn, vcn, tn, lens, bs, scale, rounding="f64", query_lens=qlens,
-                                      causal=causal)
+                                      causal=causal, dtype=qdt)
     assert np.isfinite(got).all()
     np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-2)
     if q_mul <= 1.0:
@@ -64,7 +67,7 @@ def _check(device, lens, qlens, hq, hkv, d, bs, *, causal=True, dtype=torch.bflo
         # weight changes of several percent, so each element may also differ
         # by the gap between the two oracles themselves.
         ref16 = o.paged_attention_reference(qn, kcn, vcn, tn, lens, bs, scale, rounding="bf16", query_lens=qlens,
-                                            causal=causal)
+                                            causal=causal, dtype=qdt)
         slack = np.abs(ref16 - ref)
         bad = np.abs(got - ref16) > 1e-2 + 1e-2 * np.abs(ref16) + slack
         assert not bad.any(), (int(bad.sum()), float(np.abs(got - ref16)[bad].max()))
@@ -159,6 +162,26 @@ def test_prefill_other_shapes(native_ops, device, hq, hkv, d, bs, lens, qlens, b
 ])
 def test_prefill_any_shape_kernel(native_ops, device, hq, hkv, d, dv, bs, lens, qlens):
     _check(device, lens, qlens, hq, hkv, d, bs, dv=dv, seed=d + dv + hq)
+
+
+def test_prefill_mixed_chunked_batch(native_ops, device):
+    """A chunked-prefill step: decode rows (one token) beside long chunks and
+    short ones.  Only the long requests (more than 128 (token, head) rows:
+    200, 40 and 50 tokens at G = 4) get tile images; the decode rows and the
+    17-token chunk run the in-kernel page decode in the same call, in
+    whatever order the batch lists them."""
+    _check(device, [900, 2000, 600, 4096, 700, 50], [1, 200, 17, 1, 40, 50], 16, 4, 256, 128, seed=25)
+    _check(device, [4096, 900, 3000], [300, 1, 1], 16, 4, 256, 128, seed=26)
+
+
+def test_prefill_long_requests_past_the_image_slots(native_ops, device, monkeypatch):
+    """With the image budget capped at 1 MiB only one long request gets a slot
+    (at least one always does); the other long requests run the in-kernel
+    path, which then covers all of their query tiles."""
+    monkeypatch.setenv("HIF8_PREFILL_IMAGE_CAP_MB", "1")
+    _check(device, [600, 300, 640, 90, 500], [100, 1, 64, 90, 33], 16, 4, 256, 128, seed=27)
+    monkeypatch.setenv("HIF8_PREFILL_IMAGE_CAP_MB", "0")
+    _check(device, [1000, 700], [70, 700], 16, 4, 256, 128, seed=28)
 
 
 def test_prefill_is_deterministic(native_ops, device):

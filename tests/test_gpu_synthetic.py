@@ -57,6 +57,18 @@ def test_decode_steps_agree_with_prefill(model, device):
     assert float(cos.min()) > 0.995, cos
 
 
+def test_prefill_rejects_stale_sequence_lengths(model, device):
+    # seq_lens must cover the prefill's rows (last position + 1); a stale value
+    # would make rows see no keys, so the forward refuses it.
+    st = model.new_state(2, 16)
+    ids = torch.zeros(2, 8, dtype=torch.int64, device=device)
+    pos = torch.arange(8, device=device).expand(2, 8).contiguous()
+    with pytest.raises(ValueError, match="seq_lens"):
+        model.forward(st, ids, pos, decode=False)
+    st.seq_lens.fill_(8)
+    assert bool(torch.isfinite(model.forward(st, ids, pos, decode=False)).all())
+
+
 def test_chunked_prefill_continues_the_cached_request(model, device):
     """A prompt prefilled in two chunks (the second chunk's rows attend the
     first chunk's cached pages through the right-aligned causal mask, and the

@@ -75,6 +75,12 @@ def test_write_and_attention_reject_bad_arguments_before_launch():
         kv_cache.paged_decode_attention(q, kc, vc, table, [9], scale=0.25)
     with pytest.raises(ValueError, match="divisible"):
         kv_cache.paged_decode_attention(torch.zeros(1, 3, 16, dtype=torch.bfloat16), kc, vc, table, [2], scale=0.25)
+    # A caller-supplied max_query_len below the longest request is caught by validation.
+    q3 = torch.zeros(5, 4, 16, dtype=torch.bfloat16)
+    loc = torch.tensor([0, 2, 5], dtype=torch.int32)
+    with pytest.raises(ValueError, match="max_query_len"):
+        kv_cache.paged_attention(q3, kc, vc, torch.tensor([[0], [1]]), [3, 4], scale=0.25, query_start_loc=loc,
+                                 max_query_len=2)
 
 
 @pytest.fixture(scope="module")

@@ -83,6 +83,36 @@ def test_meta_shapes():
     assert e.shape == (2, 3, 64) and e.dtype == torch.bfloat16
 
 
+def test_decode_glue_meta_shapes():
+    native.load_extension()
+    ops = torch.ops.vllm_ascend_hif8
+    meta = dict(device="meta")
+    h = torch.empty(3, 64, dtype=torch.bfloat16, **meta)
+    w = torch.empty(64, dtype=torch.bfloat16, **meta)
+    s = torch.empty(1, **meta)
+    assert ops.hif8_add_rms_norm(h, None, w, 1e-6).shape == (3, 64)
+    y, codes, rs = ops.hif8_add_rms_norm_quant(h, h, w, 1e-6, s)
+    assert y.shape == (3, 64) and codes.dtype == torch.uint8 and codes.shape == (3, 64) and rs.shape == (3,)
+    gu = torch.empty(2, 5, 96, dtype=torch.bfloat16, **meta)
+    assert ops.hif8_silu_mul(gu).shape == (2, 5, 48)
+    c2, r2 = ops.hif8_silu_mul_quant(gu, s)
+    assert c2.shape == (2, 5, 48) and c2.dtype == torch.uint8 and r2.shape == (2, 5) and r2.dtype == torch.float32
+    g = ops.hif8_bf16_gemv(torch.empty(4, 64, dtype=torch.bfloat16, **meta),
+                           torch.empty(9, 64, dtype=torch.bfloat16, **meta))
+    assert g.shape == (4, 9) and g.dtype == torch.bfloat16
+    q, k, v, slots = ops.hif8_qk_norm_rope(
+        torch.empty(2, (8 + 2 * 2) * 32, dtype=torch.bfloat16, **meta), torch.empty(32, dtype=torch.bfloat16, **meta),
+        torch.empty(32, dtype=torch.bfloat16, **meta), torch.empty(2, dtype=torch.int64, **meta),
+        torch.empty(8, **meta), torch.empty(2, 4, dtype=torch.int32, **meta), 16, 8, 2, 32, 1e-6)
+    assert q.shape == (2, 8, 32) and k.shape == (2, 2, 32) and v.shape == (2, 2, 32) and slots.dtype == torch.int64
+    out = ops.hif8_gdn_decode_step(
+        torch.empty(2, 320, dtype=torch.bfloat16, **meta), torch.empty(2, 8, dtype=torch.bfloat16, **meta),
+        torch.empty(320, 4, dtype=torch.bfloat16, **meta), torch.empty(2, 320, 3, dtype=torch.bfloat16, **meta),
+        torch.empty(4, **meta), torch.empty(4, **meta), torch.empty(2, 4, 32, 48, **meta),
+        torch.empty(48, dtype=torch.bfloat16, **meta), 2, 4, 32, 48, 1e-6)
+    assert out.shape == (2, 4 * 48) and out.dtype == torch.bfloat16
+
+
 def test_embedding_method_validates_weights_without_a_gpu(monkeypatch):
     from hif8_rocm import scheme
 

@@ -5,6 +5,7 @@ static KV quant against the static codec with per-head scales
 head-mapping check and a per-token loop."""
 
 import math
+import struct
 
 import numpy as np
 import pytest
@@ -106,6 +107,11 @@ def _bf16(x: float) -> float:
     return float(o.round_bf16(np.array([x], np.float32))[0])
 
 
+def _f16(x: float) -> float:
+    """IEEE half, round to nearest even, by the struct module (no numpy)."""
+    return struct.unpack("<e", struct.pack("<e", float(x)))[0]
+
+
 def test_attention_matches_per_token_loop_and_empty_requests():
     rng = np.random.default_rng(5)
     hkv, group, d, bs, nb = 2, 2, 8, 4, 6
@@ -143,7 +149,7 @@ def test_attention_matches_per_token_loop_and_empty_requests():
 
 # ---------------------------------------------------------------- multi-token (prefill / chunked prefill)
 
-def _attention_loop(query, kc, vc, table, lens, bs, scale, query_lens, causal):
+def _attention_loop(query, kc, vc, table, lens, bs, scale, query_lens, causal, kv_round=_bf16):
     """Per query row and head, keys walked through the block table one token
     at a time and the softmax written out by hand (no array code shared with
     the oracle): query row i of request b sits at position lens[b] -
@@ -164,8 +170,8 @@ def _attention_loop(query, kc, vc, table, lens, bs, scale, query_lens, causal):
                     slot = table[b, t // bs] * bs + t % bs
                     kd, ksc = o.unpack_kv_rows(flat_k[slot:slot + 1], d)
                     vd, vsc = o.unpack_kv_rows(flat_v[slot:slot + 1], d)
-                    k = [_bf16(o.decode_scalar(int(c)) * ksc[0, j]) for c in kd[0, j]]
-                    rows.append([_bf16(o.decode_scalar(int(c)) * vsc[0, j]) for c in vd[0, j]])
+                    k = [kv_round(o.decode_scalar(int(c)) * ksc[0, j]) for c in kd[0, j]]
+                    rows.append([kv_round(o.decode_scalar(int(c)) * vsc[0, j]) for c in vd[0, j]])
                     logits.append(scale * sum(float(a) * b_ for a, b_ in zip(query[r, h], k)))
                 if not logits:
                     heads.append([0.0] * d)
@@ -206,6 +212,31 @@ def test_multi_token_attention_matches_per_row_loop(causal):
     bf = o.paged_attention_reference(q, kc, vc, table, lens, bs, 0.35, rounding="bf16", query_lens=qlens,
                                      causal=causal)
     assert np.allclose(bf, out, rtol=0, atol=3e-2)
+
+
+def test_fp16_queries_round_kv_and_intermediates_to_fp16():
+    """dtype="f16": K/V rows rounded to fp16 (decode_kv_rows(...).to(query.dtype),
+    kv_cache.py:355-356), checked against the per-row loop with a struct-module
+    fp16 rounding; the query-dtype intermediates stay within fp16 resolution of
+    the float64 path, and differ from the bf16 ones."""
+    rng = np.random.default_rng(23)
+    hkv, group, d, bs, nb = 2, 2, 8, 4, 8
+    kc, vc = _random_paged_cache(rng, nb, bs, hkv, d)
+    table = np.array([[6, 1, 3, -1], [0, 7, 2, 5]])
+    lens, qlens = [9, 14], [4, 3]
+    q = rng.standard_normal((sum(qlens), hkv * group, d)).astype(np.float32)
+    f64 = o.paged_attention_reference(q, kc, vc, table, lens, bs, 0.35, rounding="f64", query_lens=qlens,
+                                      dtype="f16")
+    want = _attention_loop(q, kc, vc, table, lens, bs, 0.35, qlens, True, kv_round=_f16)
+    assert np.allclose(f64, want, rtol=1e-12, atol=1e-12)
+    b16 = o.paged_attention_reference(q, kc, vc, table, lens, bs, 0.35, rounding="f64", query_lens=qlens)
+    assert not np.allclose(f64, b16, rtol=1e-9, atol=1e-9)
+    r16 = o.paged_attention_reference(q, kc, vc, table, lens, bs, 0.35, rounding="bf16", query_lens=qlens,
+                                      dtype="f16")
+    assert np.allclose(r16, f64, rtol=0, atol=4e-3)
+    assert np.array_equal(r16, r16.astype(np.float16).astype(np.float64))   # outputs are fp16 values
+    with pytest.raises(ValueError, match="dtype"):
+        o.paged_attention_reference(q, kc, vc, table, lens, bs, 0.35, query_lens=qlens, dtype="fp8")
 
 
 def test_right_aligned_causal_mask_closed_form():

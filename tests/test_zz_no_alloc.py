@@ -3,8 +3,9 @@ pointers) against hif8_paged_decode_attention with a caller workspace: the
 same kernels and split plan, so the outputs are equal bit for bit.  Two calls
 in a row, the second with a smaller input (the shared scratch array keeps the
 first call's partials, which the second must not read), then the first size
-again; sizes whose partials exceed the scratch array are rejected before any
-launch; a size without splits needs no scratch."""
+again; the first call made under HIP graph capture and replayed; sizes whose
+partials exceed the scratch array are rejected before any launch; a size
+without splits needs no scratch."""
 
 import ctypes
 import math
@@ -67,6 +68,42 @@ def _run_both(lib, device, lens, seed):
     torch.cuda.synchronize()
     assert torch.equal(got, want)
     return got
+
+
+def test_noalloc_first_call_captured_in_a_graph(lib, device):
+    """The process's first call of the entry point (defined first here; no other
+    test calls it) is made under HIP graph capture, so the scratch address is
+    resolved inside the capture.  The graph is replayed three times with eager
+    work in between - a smaller eager call that overwrites the shared scratch,
+    and the output reset - and every replay equals the workspace entry point
+    bit for bit."""
+    kc, vc, table, q, lens_dev = _case(device, [16384, 3000, 700], 44)
+    max_len = 16384
+    need = lib.hif8_paged_decode_attention_workspace_size(3, 16, 4, 256, 256, max_len)
+    assert 0 < need <= SCRATCH_BYTES
+    ws = torch.empty(need, dtype=torch.uint8, device=device)
+    want = torch.empty(3, 16, 256, dtype=torch.bfloat16, device=device)
+    got = torch.full_like(want, float("nan"))
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    assert lib.hif8_paged_decode_attention(*_args(kc, vc, table, q, lens_dev, max_len, want), _ptr(ws), need,
+                                           stream) == 0, lib.hif8_last_error()
+    torch.cuda.synchronize()
+    print("noalloc capture: recording the first call", flush=True)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        cap = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        st = lib.hif8_paged_decode_attention_noalloc(*_args(kc, vc, table, q, lens_dev, max_len, got), cap)
+    assert st == 0, lib.hif8_last_error()
+    other = _case(device, [5000, 64], 45)
+    other_out = torch.empty(2, 16, 256, dtype=torch.bfloat16, device=device)
+    for rep in range(3):
+        got.fill_(float("nan"))
+        assert lib.hif8_paged_decode_attention_noalloc(*_args(*other, 5000, other_out), stream) == 0
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        print(f"noalloc capture: replay {rep}", flush=True)
+        assert torch.equal(got, want), rep
 
 
 def test_noalloc_matches_the_workspace_entry_point_twice_then_smaller(lib, device):
