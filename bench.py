@@ -4,15 +4,17 @@
 Headline (``value``): the decode GEMV sweep of BASELINE configs[1] - for
 M in {1, 4}, every projection of one 9B-class decoder layer (q 4096x4096,
 fused k+v 2048x4096, o 4096x4096, fused gate+up 24576x4096, down 4096x12288)
-runs the static W8A8 linear method (hif8_rocm.scheme): hif8_static_quant of
-the bf16 activation, then soft_hif8_gemm, which runs the HBM-streaming GEMV
-kernel for M <= 4.  The fused single-launch variant (soft_hif8_static_fused_gemm)
-is reported beside it, and so is the scheme with the MI355X opt-in
-HIF8_STATIC_FUSED_SINGLE_ROW=1 (one-row projections through the fused op,
-one launch for K <= 4096 and N < 12288, equal outputs).  One step = that sweep over one layer's
-weights; five distinct weight copies (966 MB) are
-rotated so the 256 MB Infinity Cache cannot serve them.  Steps are captured
-in HIP graphs and replayed, so host launch overhead is not timed.
+runs the static W8A8 linear method (hif8_rocm.scheme) with its default
+routing: four token rows as hif8_static_quant of the bf16 activation, then
+soft_hif8_gemm (the HBM-streaming GEMV kernel for M <= 4); one token row
+through the fused op soft_hif8_static_fused_gemm (one launch for K <= 4096
+and N < 12288, static quant + GEMV inside the op otherwise; outputs equal to
+the two-stage route).  The reference's routing (every projection two-stage,
+HIF8_STATIC_FUSED_SINGLE_ROW=0) and every projection through the fused op
+are reported beside it.  One step = that sweep over one layer's weights; five
+distinct weight copies (966 MB) are rotated so the 256 MB Infinity Cache
+cannot serve them.  Steps are captured in HIP graphs and replayed, so host
+launch overhead is not timed.
 
 ``value`` = algorithmic bytes of the step (weights + activations + scales +
 outputs of every quant and GEMV launch) / wall time per step, in GB/s.
@@ -48,6 +50,9 @@ LAYER = [("q", 4096, 4096), ("kv", 2048, 4096), ("o", 4096, 4096), ("gate_up", 2
 DECODE_M = (1, 4)
 PREFILL_M = (512, 4096)
 N_COPIES = 5
+ROTATE_BYTES = 768 * 2 ** 20   # weight bytes rotated per per-kernel row (> 3x the 256 MB Infinity Cache)
+MIN_TIMED_LAUNCHES = 100        # per-kernel rows: median over at least this many launches
+HOST_LIB = PKG_ROOT / "hif8_rocm" / "libhif8_rocm.so"
 # KV8 decode attention: 16 query heads, 4 KV heads, head_dim 256, 128-token pages.
 KV_HQ, KV_HKV, KV_D, KV_BS = 16, 4, 256, 128
 KV_CTX = (512, 4096, 16384)
@@ -92,6 +97,7 @@ class Setup:
                 x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
                 s = (x.float().abs().amax() / HIF8_MAX).reshape(1).contiguous()
                 self.x[(m, k)] = (x, s)
+        self.rot = {}      # name -> rotated weight copies of >= ROTATE_BYTES (per-kernel rows)
         self.weights = []  # [copy][name] -> (codes u8 [N,K], scale f32 [N])
         self.layers = []   # [copy][name] -> module with weight / weight_scale / input_scale
         for _ in range(N_COPIES):
@@ -261,6 +267,60 @@ def time_graphs(torch, graphs, reps: int) -> float:
     return e0.elapsed_time(e1) / reps
 
 
+def time_rotated(torch, launch, count: int, per: int = 20, min_launches: int = MIN_TIMED_LAUNCHES):
+    """Per-launch time (ms) of launch(i) for i over `count` rotated operand
+    copies: graphs of `per` launches covering every copy once per cycle,
+    replayed (after one warm-up replay each) until >= min_launches launches
+    ran, each replay timed with HIP events on the replay stream.  Returns
+    (median, mean) over the replays."""
+    graphs = []
+    for g0 in range(0, count, per):
+        def fn(g0=g0):
+            for i in range(per):
+                launch((g0 + i) % count)
+        graphs.append(capture(torch, fn))
+    for g in graphs:
+        g.replay()
+    torch.cuda.synchronize()
+    reps = max(len(graphs), -(-min_launches // per))
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for r, (a, b) in enumerate(ev):
+        a.record()
+        graphs[r % len(graphs)].replay()
+        b.record()
+    torch.cuda.synchronize()
+    times = sorted(a.elapsed_time(b) / per for a, b in ev)
+    return times[len(times) // 2], sum(times) / len(times)
+
+
+def rotation(st: "Setup", name: str):
+    """Weight copies (codes, channel scale) of one projection totalling >= ROTATE_BYTES:
+    the Setup's N_COPIES plus clones, made once and kept."""
+    if name not in st.rot:
+        base = [st.weights[c][name] for c in range(N_COPIES)]
+        n, k = base[0][0].shape
+        need = max(N_COPIES, -(-ROTATE_BYTES // (n * k)))
+        st.rot[name] = base + [(base[i % N_COPIES][0].clone(), base[i % N_COPIES][1]) for i in range(need - N_COPIES)]
+    return st.rot[name]
+
+
+def gemv_plan(m: int, n: int, k: int, kind: int = 0):
+    """(kernel name, grid) of the GEMV the library launches for these sizes
+    (hif8_gemv_launch_plan; kind 0 = code activations, 2 = bf16 x with a
+    fixed scale)."""
+    import ctypes
+
+    lib = ctypes.CDLL(str(HOST_LIB))
+    f = lib.hif8_gemv_launch_plan
+    f.argtypes = [ctypes.c_int64] * 3 + [ctypes.c_int, ctypes.c_char_p, ctypes.c_size_t,
+                                         ctypes.POINTER(ctypes.c_int64)]
+    buf = ctypes.create_string_buffer(160)
+    grid = ctypes.c_int64()
+    if f(m, n, k, kind, buf, len(buf), ctypes.byref(grid)) != 0:
+        raise RuntimeError("hif8_gemv_launch_plan failed")
+    return buf.value.decode(), grid.value
+
+
 def decode_step_fn(st: Setup, copy: int, fused: bool = False):
     """One decode sweep through the scheme, or through the fused static-quant GEMV."""
     native, torch = st.native, st.torch
@@ -277,62 +337,63 @@ def decode_step_fn(st: Setup, copy: int, fused: bool = False):
     return step
 
 
-def per_kernel_table(st: Setup, launches: int = 20) -> dict:
-    """Per-launch time of each GEMV / GEMM / quant, from graphs of back-to-back launches.
+def per_kernel_table(st: Setup) -> dict:
+    """Per-launch time of each GEMV / GEMM / quant: the median over >= 100
+    launches (graphs of 20, or 5 above M = 4) rotating >= 768 MB of weight
+    copies, so the Infinity Cache cannot serve them.
 
-    Each fused static-quant GEMV row also carries ``quant_then_gemv_us``: the
-    same projection as static quant + GEMV, two launches per call in one graph."""
+    GEMV rows name the kernel and grid the library launches (and every
+    one-row projection also has a ``_fused`` row: the scheme's default route
+    for one token row, the fused static-quant op).  Each fused row carries
+    ``quant_then_gemv_us``: the same projection as static quant + GEMV, two
+    launches per call."""
     torch, native = st.torch, st.native
     table = {}
     for m in DECODE_M + PREFILL_M:
         for name, n, k in LAYER:
             x, s = st.x[(m, k)]
             q, rs = native.static_quant(x, s)
-            per = max(1, launches if m <= 4 else 5)
+            rot = rotation(st, name)
+            per = 20 if m <= 4 else 5
 
-            def fn(q=q, rs=rs, name=name):
-                for i in range(per):
-                    w, ws = st.weights[i % N_COPIES][name]
-                    native.soft_linear(q, w, rs, ws, None, output_dtype=torch.bfloat16)
-            ms = time_graphs(torch, [capture(torch, fn)], 3) / per
-            entry = {"us": round(ms * 1e3, 3)}
+            def lin(i, q=q, rs=rs, rot=rot):
+                native.soft_linear(q, rot[i][0], rs, rot[i][1], None, output_dtype=torch.bfloat16)
+            med, mean = time_rotated(torch, lin, len(rot), per)
+            entry = {"us": round(med * 1e3, 3), "us_mean": round(mean * 1e3, 3), "copies": len(rot)}
             if m <= 4:
-                gbs = gemv_bytes(m, n, k) / (ms * 1e-3) / 1e9
-                entry.update(kernel="gemv", bytes=gemv_bytes(m, n, k), GBps=round(gbs, 1),
+                gbs = gemv_bytes(m, n, k) / (med * 1e-3) / 1e9
+                kern, grid = gemv_plan(m, n, k)
+                entry.update(kernel="gemv", launch=kern, grid=grid, bytes=gemv_bytes(m, n, k), GBps=round(gbs, 1),
                              frac_hbm=round(gbs / HBM_PEAK_GBS, 4))
             else:
-                tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
+                tf = 2.0 * m * n * k / (med * 1e-3) / 1e12
                 entry.update(kernel="gemm", flops=2 * m * n * k, TFLOPs=round(tf, 1),
                              frac_bf16=round(tf / BF16_PEAK_TFLOPS, 4))
             table[f"{name}_m{m}"] = entry
             if m <= 4:
-                def ff(x=x, s=s, name=name):
-                    for i in range(per):
-                        w, ws = st.weights[i % N_COPIES][name]
-                        native.soft_static_fused_linear(x, w, s, ws, None, output_dtype=torch.bfloat16)
-                ms = time_graphs(torch, [capture(torch, ff)], 3) / per
+                def fused(i, x=x, s=s, rot=rot):
+                    native.soft_static_fused_linear(x, rot[i][0], s, rot[i][1], None, output_dtype=torch.bfloat16)
+                med, _ = time_rotated(torch, fused, len(rot), per)
 
-                # The same work as two launches (static quant, then the GEMV) in one graph.
-                def f2(x=x, s=s, name=name):
-                    for i in range(per):
-                        w, ws = st.weights[i % N_COPIES][name]
-                        qq, rr = native.static_quant(x, s)
-                        native.soft_linear(qq, w, rr, ws, None, output_dtype=torch.bfloat16)
-                ms2 = time_graphs(torch, [capture(torch, f2)], 3) / per
+                def two(i, x=x, s=s, rot=rot):  # the same work as two launches (static quant, then the GEMV)
+                    qq, rr = native.static_quant(x, s)
+                    native.soft_linear(qq, rot[i][0], rr, rot[i][1], None, output_dtype=torch.bfloat16)
+                med2, _ = time_rotated(torch, two, len(rot), per)
                 fb = gemv_bytes(m, n, k) + m * k  # bf16 x instead of u8 codes
-                gbs = fb / (ms * 1e-3) / 1e9
-                table[f"{name}_m{m}_fused"] = {"kernel": "fused_quant_gemv", "us": round(ms * 1e3, 3), "bytes": fb,
+                gbs = fb / (med * 1e-3) / 1e9
+                kern, grid = gemv_plan(m, n, k, 2)
+                table[f"{name}_m{m}_fused"] = {"kernel": "fused_quant_gemv", "us": round(med * 1e3, 3), "bytes": fb,
                                                "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
-                                               "quant_then_gemv_us": round(ms2 * 1e3, 3)}
+                                               "quant_then_gemv_us": round(med2 * 1e3, 3),
+                                               "launch": kern if m == 1 and k <= 4096 and n < 12288
+                                               else "hif8_static_quant + code GEMV", "grid": grid}
     for m, k in ((4096, 4096), (4096, 12288), (512, 4096), (1, 4096), (4, 12288)):
         x, s = st.x[(m, k)]
-
-        def fq(x=x, s=s):
-            for _ in range(10):
-                native.static_quant(x, s)
-        ms = time_graphs(torch, [capture(torch, fq)], 3) / 10
-        gbs = quant_bytes(m, k) / (ms * 1e-3) / 1e9
-        table[f"static_quant_m{m}_k{k}"] = {"kernel": "static_quant", "us": round(ms * 1e3, 3),
+        xs = [x] + [x.clone() for _ in range(-(-ROTATE_BYTES // (2 * m * k)) - 1)] if m > 4 else [x]
+        med, _ = time_rotated(torch, lambda i, xs=xs, s=s: native.static_quant(xs[i], s), len(xs), 10)
+        del xs
+        gbs = quant_bytes(m, k) / (med * 1e-3) / 1e9
+        table[f"static_quant_m{m}_k{k}"] = {"kernel": "static_quant", "us": round(med * 1e3, 3),
                                             "bytes": quant_bytes(m, k), "GBps": round(gbs, 1),
                                             "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
     return table
@@ -341,35 +402,32 @@ def per_kernel_table(st: Setup, launches: int = 20) -> dict:
 def decoded_weight_gemm(st: Setup) -> dict:
     """Prefill GEMMs with the weight kept decoded to bf16 (the opt-in
     HIF8_PREFILL_BF16_WEIGHTS=1 route, soft_hif8_gemm_decoded_weight): per
-    shape and per layer at M in PREFILL_M, same graphs of 5 launches over the
-    rotated copies as the code-weight table.  The one-time decodes are made
-    before timing (they happen once per model load)."""
+    shape and per layer at M in PREFILL_M, median over >= 100 launches in
+    graphs of 5 rotating >= 768 MB of decoded copies.  The one-time decodes
+    are made before timing (they happen once per model load)."""
     torch, native = st.torch, st.native
-    decoded = [{name: native.decode_weight(st.weights[c][name][0]) for name, _, _ in LAYER} for c in range(N_COPIES)]
     res = {}
-    for m in PREFILL_M:
-        fl_total = us_total = 0.0
-        for name, n, k in LAYER:
+    for name, n, k in LAYER:
+        rot = rotation(st, name)
+        decoded = [native.decode_weight(rot[i][0]) for i in range(-(-ROTATE_BYTES // (2 * n * k)))]
+        for m in PREFILL_M:
             x, s = st.x[(m, k)]
             q, rs = native.static_quant(x, s)
-            per = 5
 
-            def fn(q=q, rs=rs, name=name):
-                for i in range(per):
-                    ws = st.weights[i % N_COPIES][name][1]
-                    native.soft_linear_decoded_weight(q, decoded[i % N_COPIES][name], rs, ws, None,
-                                                      output_dtype=torch.bfloat16)
-            ms = time_graphs(torch, [capture(torch, fn)], 3) / per
-            tf = 2.0 * m * n * k / (ms * 1e-3) / 1e12
-            res[f"{name}_m{m}"] = {"us": round(ms * 1e3, 3), "TFLOPs": round(tf, 1),
-                                   "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 4)}
-            fl_total += 2.0 * m * n * k
-            us_total += ms * 1e3
+            def fn(i, q=q, rs=rs, rot=rot, decoded=decoded):
+                native.soft_linear_decoded_weight(q, decoded[i], rs, rot[i][1], None, output_dtype=torch.bfloat16)
+            med, _ = time_rotated(torch, fn, len(decoded), 5)
+            tf = 2.0 * m * n * k / (med * 1e-3) / 1e12
+            res[f"{name}_m{m}"] = {"us": round(med * 1e3, 3), "TFLOPs": round(tf, 1),
+                                   "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 4), "copies": len(decoded)}
+        del decoded
+        torch.cuda.empty_cache()
+    for m in PREFILL_M:
+        fl_total = sum(2.0 * m * n * k for _, n, k in LAYER)
+        us_total = sum(res[f"{name}_m{m}"]["us"] for name, _, _ in LAYER)
         tf = fl_total / (us_total * 1e-6) / 1e12
         res[f"layer_m{m}"] = {"TFLOPs": round(tf, 1), "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 4),
                               "us_per_layer": round(us_total, 1)}
-    del decoded
-    torch.cuda.empty_cache()
     return res
 
 
@@ -551,32 +609,37 @@ def c1_gpu(torch, native, device) -> dict:
     K 4096 -> the GEMV kernel) on the seeded weights, 6 weight copies (302 MB)
     rotated past the Infinity Cache; graphs of 20 launches."""
     x, s, wq, ws = c1_operands()
-    copies = [(wq.to(device), ws.to(device)) for _ in range(6)]
+    wd = wq.to(device)
+    copies = [(wd if i == 0 else wd.clone(), ws.to(device)) for i in range(-(-ROTATE_BYTES // wq.numel()))]
     xd, sd = x.to(device), s.to(device)
     q, rs = native.static_quant(xd, sd)
-    per = 20
 
-    def both():
-        for i in range(per):
-            qq, rr = native.static_quant(xd, sd)
-            w, sc = copies[i % len(copies)]
-            native.soft_linear(qq, w, rr, sc, None, output_dtype=torch.bfloat16)
+    def both(i):
+        qq, rr = native.static_quant(xd, sd)
+        native.soft_linear(qq, copies[i][0], rr, copies[i][1], None, output_dtype=torch.bfloat16)
 
-    def gemv():
-        for i in range(per):
-            w, sc = copies[i % len(copies)]
-            native.soft_linear(q, w, rs, sc, None, output_dtype=torch.bfloat16)
-    ms_both = time_graphs(torch, [capture(torch, both)], 3) / per
-    ms_gemv = time_graphs(torch, [capture(torch, gemv)], 3) / per
+    def gemv(i):
+        native.soft_linear(q, copies[i][0], rs, copies[i][1], None, output_dtype=torch.bfloat16)
+
+    def fused(i):
+        native.soft_static_fused_linear(xd, copies[i][0], sd, copies[i][1], None, output_dtype=torch.bfloat16)
+    ms_both, _ = time_rotated(torch, both, len(copies))
+    ms_gemv, _ = time_rotated(torch, gemv, len(copies))
+    ms_fused, _ = time_rotated(torch, fused, len(copies))
+    kern, grid = gemv_plan(1, C1_N, C1_K)
     gb = gemv_bytes(1, C1_N, C1_K)
     qb = quant_bytes(1, C1_K)
     res = {"workload": "BASELINE configs[0]: M=1 GEMV, N 12288, K 4096, seeded fp32 N(0,0.02) weights encoded "
                        "with per-row absmax/32768 scales, x ~ N(0,1) bf16 with a static absmax/32768 scale",
+           "gemv_launch": kern, "gemv_grid": grid, "weight_copies": len(copies),
            "gemv_us": round(ms_gemv * 1e3, 3), "gemv_bytes": gb,
            "gemv_GBps": round(gb / (ms_gemv * 1e-3) / 1e9, 1),
            "gemv_frac_hbm": round(gb / (ms_gemv * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
            "quant_plus_gemv_us": round(ms_both * 1e3, 3),
-           "quant_plus_gemv_GBps": round((gb + qb) / (ms_both * 1e-3) / 1e9, 1)}
+           "quant_plus_gemv_GBps": round((gb + qb) / (ms_both * 1e-3) / 1e9, 1),
+           "scheme_route_us": round(ms_fused * 1e3, 3),
+           "scheme_route": "the scheme's default for one token row: the fused static-quant op (static quant + "
+                           "GEMV inside it at N >= 12288)"}
     del copies
     return res
 
@@ -620,7 +683,8 @@ def profile_pass(st: Setup, reps: int = 3) -> None:
     Known-size calibration kernels first: a torch copy of 64 MiB (read + write)
     and an fp32 sum over the same 64 MiB (a plain streaming read with 16-byte
     vector loads, the load width of the GEMV).  Then every decode GEMV, static
-    quant and prefill GEMM launch `reps` times."""
+    quant and prefill GEMM launch `reps` times, and the one-row fused op per
+    shape `reps` times."""
     torch, native = st.torch, st.native
     src = torch.empty(64 << 20, dtype=torch.uint8, device=st.device).fill_(3)
     dst = torch.empty_like(src)
@@ -637,6 +701,13 @@ def profile_pass(st: Setup, reps: int = 3) -> None:
                 q, rs = native.static_quant(x, s)
                 w, ws = st.weights[i % N_COPIES][name]
                 native.soft_linear(q, w, rs, ws, None, output_dtype=torch.bfloat16)
+    torch.cuda.synchronize()
+    # The one-row fused op (the scheme's default for one token row), `reps` times per shape.
+    for name, n, k in LAYER:
+        x, s = st.x[(1, k)]
+        for i in range(reps):
+            w, ws = st.weights[i % N_COPIES][name]
+            native.soft_static_fused_linear(x, w, s, ws, None, output_dtype=torch.bfloat16)
     torch.cuda.synchronize()
     log("profile pass: linear done")
     # KV path: decode attention (b4 ctx16384, b1 ctx512), the fused cache write
@@ -665,13 +736,111 @@ def profile_pass(st: Setup, reps: int = 3) -> None:
     log("profile pass done")
 
 
-def committed_traffic(kernel_key: str):
-    """HBM bytes per launch measured with rocprofv3 --pmc (profiles/pmc_traffic.json), if present."""
+def committed_traffic(row: str, kernel: str, grid: int):
+    """HBM bytes per launch of `row` measured with rocprofv3 --pmc
+    (profiles/pmc_traffic.json) and a note; None unless the profile was taken
+    on the same kernel (name with template arguments) and grid as the launch
+    timed here."""
     path = REPO / "profiles" / "pmc_traffic.json"
     if not path.exists():
-        return None
-    entry = json.loads(path.read_text()).get("kernels", {}).get(kernel_key)
-    return None if entry is None else entry.get("traffic_bytes")
+        return None, "no committed PMC profile"
+    entry = json.loads(path.read_text()).get("kernels", {}).get(row)
+    if entry is None:
+        return None, f"no PMC entry for {row}"
+    if entry.get("kernel") != kernel or int(entry.get("grid", -1)) != int(grid):
+        log(f"PMC profile of {row} is for {entry.get('kernel')} x {entry.get('grid')}, the bench times {kernel} x {grid}")
+        return None, (f"refused: the committed profile measured {entry.get('kernel')} x {entry.get('grid')} "
+                      f"workgroups, the bench times {kernel} x {grid}")
+    return entry.get("traffic_bytes"), (f"profiles/pmc_traffic.json: FETCH_SIZE x {json.loads(path.read_text())['fetch_scale']:.3f} "
+                                        f"+ WRITE_SIZE of {kernel} x {grid}")
+
+
+def _median_time(fn, threads: int, runs: int, warmup: int) -> float:
+    import torch
+
+    torch.set_num_threads(threads)
+    times = []
+    for i in range(warmup + runs):
+        t0 = time.perf_counter()
+        fn()
+        if i >= warmup:
+            times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2]
+
+
+def gemm_cpu_baseline(threads: int, runs: int = 5, warmup: int = 2) -> dict:
+    """BASELINE configs[2] on the host, the q projection at M = 512 (512 x 4096
+    x 4096): the torch-CPU port of the reference's CPU path - static encode of
+    x, then decode-LUT weights x channel scale and one fp32 matmul with the
+    decoded activation (tests/test_npu_ops.py:334-336).  Median of `runs`
+    after `warmup`, at `threads` torch threads and at one."""
+    import torch
+
+    from oracle import torch_cpu
+
+    m, n, k = 512, 4096, 4096
+    g = torch.Generator().manual_seed(C1_SEED + 2)
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16)
+    s = torch.tensor([float(x.float().abs().max()) / HIF8_MAX], dtype=torch.float32)
+    w = torch.randn(n, k, generator=g) * 0.02
+    ws = (w.abs().amax(dim=1) / HIF8_MAX).to(torch.float32)
+    wq = torch_cpu.static_quant(w, ws.reshape(-1, 1))
+
+    def run():
+        xq = torch_cpu.static_quant(x.float(), float(s[0]))
+        torch_cpu.soft_gemv(xq, s.expand(m), wq, ws)
+    out = {}
+    for t in (threads, 1):
+        med = _median_time(run, t, runs, warmup)
+        out[t] = {"value": round(2.0 * m * n * k / med / 1e12, 4), "unit": "TFLOP/s", "ms_per_gemm": round(med * 1e3, 2),
+                  "cores": t}
+    torch.set_num_threads(threads)
+    return {"value": out[threads]["value"], "unit": "TFLOP/s", "cores": threads, "kind": "port",
+            "sample": f"BASELINE configs[2] q projection at M=512 (512x4096x4096, 17.2 GFLOP): torch-CPU port of the "
+                      f"reference CPU path (static encode of x, decode-LUT weights x scale, fp32 matmul), median of "
+                      f"{runs} after {warmup} warm-up runs, {out[threads]['ms_per_gemm']} ms per GEMM at {threads} "
+                      f"threads", "nproc": os.cpu_count(), "cpu_model": cpu_model(), "single_thread": out[1]}
+
+
+def kv_cpu_baseline_torch(threads: int, runs: int = 5, warmup: int = 2) -> dict:
+    """BASELINE configs[3] at batch 4, ctx 4096 on the host: the torch-CPU port
+    of the reference's paged_attention_reference (kv_cache.py:314-372; gather,
+    decode x row scale to bf16, GQA repeat, bf16 einsums, fp32 softmax) over a
+    HiF8 cache written by the numpy oracle.  Median of `runs` after `warmup`
+    at `threads` torch threads and at one; us per token = step time / 4."""
+    import numpy as np
+    import torch
+
+    from oracle import hif8_oracle as o
+    from oracle import torch_cpu
+
+    batch, ctx = 4, 4096
+    pages = batch * ctx // KV_BS
+    rng = np.random.default_rng(2)
+    kc = np.zeros((pages, KV_BS, KV_HKV, KV_D + 4), np.uint8)
+    vc = np.zeros_like(kc)
+    for c in (kc, vc):
+        vals = rng.standard_normal((pages * KV_BS, KV_HKV, KV_D)).astype(np.float32)
+        data, sc = o.quantize_kv_rows_static(vals, (np.abs(vals).max(axis=(0, 2)) / HIF8_MAX).astype(np.float32))
+        o.scatter_kv_rows(c, o.pack_kv_rows(data, sc), np.arange(pages * KV_BS), KV_BS)
+    table = torch.from_numpy(rng.permutation(pages).reshape(batch, ctx // KV_BS))
+    q = torch.randn(batch, KV_HQ, KV_D, generator=torch.Generator().manual_seed(2)).to(torch.bfloat16)
+    kct, vct = torch.from_numpy(kc), torch.from_numpy(vc)
+
+    def run():
+        torch_cpu.paged_decode_attention(q, kct, vct, table, [ctx] * batch, KV_D ** -0.5)
+    out = {}
+    for t in (threads, 1):
+        med = _median_time(run, t, runs, warmup)
+        out[t] = {"value": round(med * 1e6 / batch, 1), "unit": "us/token", "ms_per_step": round(med * 1e3, 2),
+                  "cores": t}
+    torch.set_num_threads(threads)
+    return {"value": out[threads]["value"], "unit": "us/token", "cores": threads, "kind": "port",
+            "sample": f"BASELINE configs[3] batch 4, ctx 4096 (Hq 16, Hkv 4, D 256, 128-token pages): torch-CPU port of "
+                      f"the reference's paged_attention_reference, one decode step, median of {runs} after {warmup} "
+                      f"warm-up runs, {out[threads]['ms_per_step']} ms per step at {threads} threads",
+            "nproc": os.cpu_count(), "cpu_model": cpu_model(), "single_thread": out[1]}
 
 
 E2E_PROMPT, E2E_NEW = 512, 256
@@ -740,7 +909,7 @@ def main() -> None:
               file=sys.stderr)
         sys.exit(2)
 
-    cpu = kv_cpu = None
+    cpu = kv_cpu = gemm_cpu = None
     # The host's thread share: OMP_NUM_THREADS where the pool sets it (16 per GPU
     # on the GPU boxes), else every CPU; never more than the CPUs present.
     nproc = os.cpu_count() or 1
@@ -762,6 +931,14 @@ def main() -> None:
                          f"after 2 warm-up runs, {c1[threads]['us_per_gemv']} us per GEMV at {threads} threads",
                "nproc": nproc, "cpu_model": model, "single_thread": c1[1], "decode_sweep_numpy_1thread": sweep_cpu}
         log(f"cpu baseline C1: {c1[threads]['value']} GB/s at {threads} threads, {c1[1]['value']} GB/s at 1")
+        gemm_cpu = gemm_cpu_baseline(threads)
+        log(f"cpu baseline GEMM q M=512: {gemm_cpu['value']} TFLOP/s at {threads} threads, "
+            f"{gemm_cpu['single_thread']['value']} at 1")
+        kv_cpu_t = kv_cpu_baseline_torch(threads)
+        log(f"cpu baseline KV b4 ctx4096: {kv_cpu_t['value']} us/token at {threads} threads, "
+            f"{kv_cpu_t['single_thread']['value']} at 1")
+        kv_cpu_t["numpy_oracle_1thread_b1_ctx4096"] = kv_cpu
+        kv_cpu = kv_cpu_t
 
     import torch
 
@@ -798,15 +975,16 @@ def main() -> None:
     fused_gbs = step_bytes / (fused_ms * 1e-3) / 1e9
     log(f"fused single-launch sweep: {fused_ms * 1e3:.1f} us/step, {fused_gbs:.1f} GB/s")
 
-    # The scheme with the MI355X opt-in HIF8_STATIC_FUSED_SINGLE_ROW=1 (one token
-    # row fused; equal outputs).  apply() routes at capture time.
-    os.environ["HIF8_STATIC_FUSED_SINGLE_ROW"] = "1"
-    single = [capture(torch, decode_step_fn(st, c)) for c in range(N_COPIES)]
+    # The scheme with the reference's routing (HIF8_STATIC_FUSED_SINGLE_ROW=0:
+    # every projection as static quant + GEMV; equal outputs).  apply() routes
+    # at capture time.
+    os.environ["HIF8_STATIC_FUSED_SINGLE_ROW"] = "0"
+    two = [capture(torch, decode_step_fn(st, c)) for c in range(N_COPIES)]
     del os.environ["HIF8_STATIC_FUSED_SINGLE_ROW"]
-    single_ms = time_graphs(torch, single, args.steps)
-    single_gbs = step_bytes / (single_ms * 1e-3) / 1e9
-    del single
-    log(f"sweep with single-row fusion: {single_ms * 1e3:.1f} us/step, {single_gbs:.1f} GB/s")
+    two_ms = time_graphs(torch, two, args.steps)
+    two_gbs = step_bytes / (two_ms * 1e-3) / 1e9
+    del two
+    log(f"sweep with two-stage one-row projections: {two_ms * 1e3:.1f} us/step, {two_gbs:.1f} GB/s")
 
     log("per-kernel table ...")
     table = per_kernel_table(st)
@@ -815,7 +993,16 @@ def main() -> None:
     log(f"decoded-weight layer: m512 {gemm_decoded['layer_m512']['us_per_layer']} us, "
         f"m4096 {gemm_decoded['layer_m4096']['us_per_layer']} us")
     gemv = [v for v in table.values() if v["kernel"] == "gemv"]
-    dom = table["gate_up_m1"]
+    # The launches of the headline step: M = 4 static quant + the code GEMV;
+    # one row through the fused op (one launch for K <= 4096, N < 12288,
+    # else static quant + the code GEMV inside the op).  The dominant launch
+    # is the longest of them.
+    step_rows = [(f"{name}_m1_fused" if m == 1 and k <= 4096 and n < 12288 else f"{name}_m{m}")
+                 for m in DECODE_M for name, n, k in LAYER]
+    dom_key = max(step_rows, key=lambda r: table[r]["us"])
+    best_key = max(step_rows, key=lambda r: table[r]["frac_hbm"])
+    dom, best = table[dom_key], table[best_key]
+    traffic, traffic_note = committed_traffic(dom_key, dom["launch"], dom["grid"])
     gemm_layer = {}
     for m in PREFILL_M:
         fl = sum(table[f"{n}_m{m}"]["flops"] for n, _, _ in LAYER)
@@ -824,7 +1011,9 @@ def main() -> None:
         gemm_layer[f"m{m}"] = {"TFLOPs": round(tf, 1), "frac_bf16": round(tf / BF16_PEAK_TFLOPS, 4),
                                "us_per_layer": round(us, 1)}
     gdom = table["gate_up_m4096"]
-    gemm_layer["roofline"] = {"kernel": "activation + weight decode + gemm_dma_kernel<256,256> (gate_up 4096x24576x4096)",
+    gemm_layer["cpu_baseline"] = gemm_cpu
+    gemm_layer["roofline"] = {"kernel": "the GEMM call for gate_up 4096x24576x4096 (activation and weight decodes + "
+                                        "gemm_dma_kernel<256,256>)",
                               "bound": "mfma", "achieved": gdom["TFLOPs"], "peak": BF16_PEAK_TFLOPS,
                               "unit": "TFLOP/s", "frac": gdom["frac_bf16"], "flops_per_launch": gdom["flops"],
                               "us_per_launch": gdom["us"]}
@@ -874,15 +1063,20 @@ def main() -> None:
             "step_bytes": step_bytes,
         },
         "roofline": {
-            "kernel": "gemv_kernel (gate_up 24576x4096, M=1)",
+            "kernel": f"{dom['launch']} x {dom['grid']} workgroups ({dom_key}: the longest launch of the step)",
             "bound": "hbm",
             "achieved": dom["GBps"],
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom["GBps"] / HBM_PEAK_GBS, 4),
-            "traffic": committed_traffic("gate_up_m1"),
+            "traffic": traffic,
+            "traffic_source": traffic_note,
             "bytes_per_launch": dom["bytes"],
             "us_per_launch": dom["us"],
+            "timing": f"median over >= {MIN_TIMED_LAUNCHES} launches, graphs of 20 rotating {dom.get('copies')} "
+                      f"weight copies, HIP events on the replay stream",
+            "best_launch": {"row": best_key, "kernel": f"{best['launch']} x {best['grid']}", "GBps": best["GBps"],
+                            "frac": best["frac_hbm"], "us": best["us"]},
         },
         "cpu_baseline": cpu,
         "kv_decode_attention": {
@@ -904,10 +1098,9 @@ def main() -> None:
         },
         "c1_gemv": c1,
         "decode_sweep_fused_GBps": round(fused_gbs, 1),
-        "decode_sweep_single_row_fusion": {"GBps": round(single_gbs, 1), "us_per_step": round(single_ms * 1e3, 1),
-                                           "routing": "scheme apply with HIF8_STATIC_FUSED_SINGLE_ROW=1: M=1 "
-                                                      "through the fused op (one launch for K <= 4096, N < 12288), M=4 as "
-                                                      "the headline; outputs equal"},
+        "decode_sweep_two_stage": {"GBps": round(two_gbs, 1), "us_per_step": round(two_ms * 1e3, 1),
+                                   "routing": "scheme apply with HIF8_STATIC_FUSED_SINGLE_ROW=0 (the reference's "
+                                              "routing): every projection static quant + GEMV; outputs equal"},
         "gemv_all_launches_GBps": round(all_gemv_gbs, 1),
         "gemm_per_layer": gemm_layer,
         "gemm_decoded_weights": {"routing": "HIF8_PREFILL_BF16_WEIGHTS=1: weights kept decoded to bf16 "

@@ -18,7 +18,10 @@
 // fixed scale (soft_hif8_fused_gemm.cpp:449-534 with HIF8_FUSED_STATIC_SCALE)
 // or with each row's dynamic scale max(finite amax, 1e-12), which every block
 // reduces from the whole row first (soft_hif8_fused_gemm.cpp:536-571).
+#include <stdio.h>
 #include <stdlib.h>
+
+#include <type_traits>
 
 #include "linear.h"
 
@@ -28,6 +31,7 @@ namespace {
 constexpr int kThreads = 256;
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a),
@@ -384,6 +388,192 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
   }
 }
 
+// ------------------------------------------------------------------------
+// MFMA-4 GEMV for 2 <= M <= 4 (code activations, k % 16 == 0, 16-byte aligned
+// operands).  v_mfma_f32_4x4x4_16b_bf16 runs 16 independent 4 x 4 x 4
+// products per wavefront, product b on lanes 4b .. 4b + 3: A row r comes from
+// lane 4b + r, B column j from lane 4b + j, and D[r][j] lands in lane 4b + j,
+// element r.  Lane 4b + j of wavefront w loads the 16-byte chunks
+// b + 16 s + 64 w + 256 p (s = 0..3, pass p) of weight row 4g + j of each
+// row group g of the block, and of activation row j: a load instruction
+// covers four rows x 256 contiguous bytes (measured on MI355X, one-shot
+// blocks over 100 MB: 5.85 TB/s, against 6.0 TB/s for 1 KiB of one row and
+// 5.3 TB/s for sixteen rows x 64 bytes), and the four lanes of each product
+// hold the same k positions, so A (four weight rows) and B (the activation
+// rows, zero past M) feed the MFMA without any data movement.  The MFMA does
+// the M products and the k sums; the VALU only decodes (one table lookup per
+// code) - against the dot2 kernel's M / 2 products per weight code plus the
+// lane reduction of kR x M partials, which bound it at M = 4.  At the end
+// each lane holds kR partial sums of its product's 64-code k range; lane
+// bits 5 and 4 are summed by permlane swaps that halve the values per lane,
+// bits 3 and 2 by DPP rotations (bits 1..0 are the activation row), and the
+// four wavefronts meet in LDS.
+typedef short s16x4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f32x4_t mfma4(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, f32x4_t c) {
+  typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_mfma_f32_4x4x4bf16_1k(__builtin_bit_cast(s16x4_t, u32x2_t{a0, a1}),
+                                                 __builtin_bit_cast(s16x4_t, u32x2_t{b0, b1}), c, 0, 0, 0);
+}
+
+// Sum of v over the lanes that share bits 0-1 of the lane index and bits 2-3
+// (one 16-lane row): DPP rotations by 8 and 4 within the row.
+__device__ __forceinline__ float row_quad_sum(float v) {
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x128, 0xF, 0xF, false));  // row_ror:8
+  v += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), 0x124, 0xF, 0xF, false));  // row_ror:4
+  return v;
+}
+
+// kPasses: 1..3 passes of 4096 k bytes per block, unrolled (k <= 4096 kPasses),
+// or 0 for any k (a loop without prefetch).
+template <int kM, int kR, int kPasses>
+__global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
+    const uint8_t *act, const float *__restrict__ act_scale, const uint8_t *weight, const float *__restrict__ cs,
+    const void *__restrict__ bias, int bias_dtype, void *__restrict__ out, int out_dtype, int n, int k) {
+  static_assert(kR % 4 == 0 && kR <= 16 && kM >= 1 && kM <= 4, "row groups of four, up to four activation rows");
+  constexpr int kG = kR / 4;              // row groups
+  constexpr int kWaves = kThreads / kWave;
+  constexpr int kPass = 16 * kThreads;    // k bytes per pass of the block
+  // The decode table first, at LDS address 0: a lookup is one shift of the byte.
+  __shared__ __attribute__((aligned(16))) uint16_t dec_lut[256];
+  __shared__ __attribute__((aligned(16))) float red[kWaves][kR][4];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int b = lane >> 2, j = lane & 3;
+  const int n0 = blockIdx.x * kR;
+  const int chunks = k >> 4;
+  // This lane's weight rows (rows past n re-read row n - 1; never stored) and
+  // activation row (rows past M read row M - 1 and are zeroed after the load).
+  const uint8_t *wrow[kG];
+#pragma unroll
+  for (int g = 0; g < kG; ++g) wrow[g] = weight + size_t(min(n0 + 4 * g + j, n - 1)) * k;
+  const uint8_t *arow = act + size_t(min(j, kM - 1)) * k;
+  const bool act_lane = j < kM;
+
+  // Codes of one pass: weight rows [group][step s], activation [step s].
+  struct Pass {
+    u32x4 w[kG][4], a[4];
+  };
+  // Chunk of step s in the pass starting at chunk p0; past the last chunk the
+  // lane re-reads it and zeroes the codes (code 0 decodes to +0, and both
+  // operands are zeroed, so no 0 x Inf can appear).
+  auto load = [&](Pass &q, int p0) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int c = min(p0 + 64 * wave + 16 * s + b, chunks - 1);
+      q.a[s] = reinterpret_cast<const u32x4 *>(arow)[c];
+    }
+#pragma unroll
+    for (int g = 0; g < kG; ++g)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int c = min(p0 + 64 * wave + 16 * s + b, chunks - 1);
+        q.w[g][s] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(wrow[g]) + c);
+      }
+  };
+  Pass cur;
+  const uint16_t entry = uint16_t(decode_bits(uint32_t(tid)) >> 16);
+  load(cur, 0);
+  dec_lut[tid] = entry;
+  __builtin_amdgcn_sched_barrier(0);
+  lds_barrier();
+
+  f32x4_t acc[kG];
+#pragma unroll
+  for (int g = 0; g < kG; ++g) acc[g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // kTail: chunks past the end (a pass that is not full) become zero codes.
+  auto compute = [&](const Pass &q, int p0, auto tail) {
+    constexpr bool kTail = decltype(tail)::value;
+    bool cv[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) cv[s] = !kTail || p0 + 64 * wave + 16 * s + b < chunks;
+    uint32_t ad[4][8];  // activation row j as bf16 pairs, per step s
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const u32x4 a = act_lane && cv[s] ? q.a[s] : u32x4{0, 0, 0, 0};
+      decode16(dec_lut, a, ad[s]);
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+      for (int g = 0; g < kG; ++g) {
+        uint32_t p[8];
+        decode16(dec_lut, !kTail || cv[s] ? q.w[g][s] : u32x4{0, 0, 0, 0}, p);
+#pragma unroll
+        for (int d = 0; d < 4; ++d) acc[g] = mfma4(p[2 * d], p[2 * d + 1], ad[s][2 * d], ad[s][2 * d + 1], acc[g]);
+      }
+  };
+  const std::true_type tail;
+  const std::false_type no_tail;
+  constexpr int kStep = kPass / 16;  // chunks per pass
+  auto last = [&](const Pass &q, int p) {  // the last pass may be partial
+    if (p + kStep <= chunks) compute(q, p, no_tail);
+    else compute(q, p, tail);
+  };
+  if constexpr (kPasses == 1) {
+    last(cur, 0);
+  } else if constexpr (kPasses > 0) {
+    // kPasses passes, unrolled, so the wait counts stay exact: the next
+    // pass's loads are in flight while the current one is decoded and
+    // multiplied (two register sets).
+    Pass nxt;
+#pragma unroll
+    for (int p = 0; p < kPasses; ++p) {
+      Pass &q = (p & 1) ? nxt : cur;
+      if (p + 1 < kPasses) load((p & 1) ? cur : nxt, (p + 1) * kStep);
+      // All of the next pass's loads go out before this pass's math (left to
+      // itself the scheduler sinks some of them between the MFMAs and then
+      // waits for every load at once).
+      __builtin_amdgcn_sched_barrier(0);
+      if (p + 1 < kPasses) compute(q, p * kStep, no_tail);
+      else last(q, p * kStep);
+    }
+  } else {
+    // Any number of passes, one at a time.
+    int p0 = 0;
+    for (; p0 + kStep < chunks; p0 += kStep) {
+      if (p0) load(cur, p0);
+      compute(cur, p0, no_tail);
+    }
+    if (p0) load(cur, p0);
+    last(cur, p0);
+  }
+
+  // vals[4 g + r] = row 4 g + r of this lane's product, activation row j.
+  float vals[kR];
+#pragma unroll
+  for (int g = 0; g < kG; ++g)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) vals[4 * g + r] = acc[g][r];
+  constexpr int kQ = kR / 4;  // values per lane after the two halving levels
+#pragma unroll
+  for (int i = 0; i < kR / 2; ++i) vals[i] = exchange_add<5>(vals[i], vals[i + kR / 2], lane);
+#pragma unroll
+  for (int i = 0; i < kQ; ++i) vals[i] = exchange_add<4>(vals[i], vals[i + kQ], lane);
+  // Lane 16 q + 4 t + j now holds rows i + kQ q (i < kQ) summed over lane
+  // bits 4-5; the rotations add bits 2-3.
+#pragma unroll
+  for (int i = 0; i < kQ; ++i) vals[i] = row_quad_sum(vals[i]);
+  if (((lane >> 2) & 3) == 0) {
+#pragma unroll
+    for (int i = 0; i < kQ; ++i) red[wave][i + kQ * (lane >> 4)][j] = vals[i];
+  }
+  __syncthreads();
+  if (tid < kR * kM) {
+    const int r = tid / kM, m = tid - r * kM;
+    const int row = n0 + r;
+    if (row < n) {
+      float sum = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) sum += red[w][r][m];
+      float y = sum * act_scale[m] * cs[row];
+      if (bias) y += load_bias(bias, bias_dtype, row);
+      store_out(out, out_dtype, size_t(m) * n + row, y);
+    }
+  }
+}
+
 // Any shape or alignment: one wavefront per output row, byte-wise k loop.
 __global__ __launch_bounds__(64) void gemv_simple_kernel(
     const void *__restrict__ act, int act_kind, const float *__restrict__ act_scale,
@@ -646,17 +836,17 @@ void dispatch_m(const LinearArgs &a) {
   }
 }
 
-
-}  // namespace
-
-// Kernel selection knob, read once: HIF8_GEMV_KERNEL=valu|mfma (default valu),
-// HIF8_GEMV_ROWS=4|8|12|16 forces the VALU kernel's rows per block (12: M = 1 only).
-// Measured on MI355X (gate_up 24576x4096, M=1): one-shot VALU kernel with 8
-// rows per block 20.0 us; the MFMA kernel 29.3 us (its 16-rows x 64-byte load
-// pattern alone reads ~20% slower than 1 KiB-contiguous rows); a persistent
+// Kernel selection knobs, read once: HIF8_GEMV_KERNEL=d forces the dot2 VALU
+// kernel for every M (default: the MFMA-4 kernel for code activations at
+// M = 4, and M = 3 over wide weights), =4 the MFMA-4 kernel for every M >= 2,
+// =m the experimental 16x16x32 MFMA kernel; HIF8_GEMV_ROWS=4|8|12|16
+// forces the rows per block (12: M = 1 or the MFMA-4 kernel).  Measured on
+// MI355X (gate_up 24576x4096, M=1): the dot2 kernel with 8 rows per block
+// 20.0 us; the 16x16x32 MFMA kernel 29.3 us (its 16-rows x 64-byte load
+// pattern alone reads ~12 % slower than 1 KiB-contiguous rows); a persistent
 // double-buffered variant 24 us (2 blocks/CU keep too few bytes in flight).
 struct GemvKnobs {
-  char kernel = 'v';  // 'v' one-shot VALU (default), 'm' MFMA
+  char kernel = 'v';
   int rows = 0;
   GemvKnobs() {
     if (const char *v = getenv("HIF8_GEMV_KERNEL")) kernel = v[0];
@@ -664,37 +854,153 @@ struct GemvKnobs {
   }
 };
 
-int launch_gemv(const LinearArgs &a) {
-  if (a.m < 1 || a.m > 4) return fail(HIF8_ERR_UNSUPPORTED, "GEMV kernel handles 1 <= M <= 4, got %lld", (long long)a.m);
+enum GemvKind { kGemvDot2, kGemvMfma4, kGemvSimple, kGemvMfma16 };
+
+struct GemvPlan {
+  GemvKind kind;
+  int rows;        // weight rows per block
+  bool one_chunk;  // k <= 16 * 256: one 16-byte chunk (dot2) or one pass (MFMA-4) per thread
+  unsigned grid;
+  unsigned threads;
+};
+
+GemvPlan plan_gemv(int64_t m, int64_t n, int64_t k, int act_kind, bool vec) {
   static const GemvKnobs knobs;
-  const bool vec = a.k % 16 == 0 && aligned(a.weight, 16) && aligned(a.act, 16);
-  const bool dynamic = a.act_kind == kActF16Dyn || a.act_kind == kActBf16Dyn;
-  if (knobs.kernel == 'm' && !dynamic && mfma_gemv_smem(a)) {
-    int st = HIF8_OK;
-    switch (a.m) {
-      case 1: st = launch_mfma_src<1>(a); break;
-      case 2: st = launch_mfma_src<2>(a); break;
-      case 3: st = launch_mfma_src<3>(a); break;
-      default: st = launch_mfma_src<4>(a); break;
-    }
-    if (st) return st;
-  } else if (!vec) {
-    gemv_simple_kernel<<<dim3(unsigned(a.n)), 64, 0, a.stream>>>(
-        a.act, a.act_kind, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out,
-        a.out_dtype, int(a.m), int(a.n), int(a.k));
+  const bool dynamic = act_kind == kActF16Dyn || act_kind == kActBf16Dyn;
+  GemvPlan p{};
+  p.one_chunk = k <= 16 * kThreads;
+  p.threads = kThreads;
+  if (!vec) {
+    p.kind = kGemvSimple;
+    p.rows = 1;
+    p.threads = kWave;
+    p.grid = unsigned(n);
+    return p;
+  }
+  const bool wide = n >= 16384;
+  if (knobs.kernel == 'm' && !dynamic && k % 64 == 0) {
+    p.kind = kGemvMfma16;
+    p.rows = 16;
+    p.threads = kMfmaThreads;
+  } else if (knobs.kernel != 'd' && act_kind == kActCodes &&
+             ((k <= 16 * kThreads && (m == 4 || (m == 3 && wide))) || (knobs.kernel == '4' && m >= 2))) {
+    // Code activations, four rows (three over wide weights), k <= 4096: the
+    // MFMA does the products.  Measured on MI355X (graphs of 20 launches over
+    // >= 768 MB of weights), against the dot2 kernel: M = 4 gate_up 20.3 vs
+    // 23.2 us, q / o 6.4 vs 6.8, k+v 4.95 vs 5.1; M = 3 gate_up 20.2 vs 22.1;
+    // but M = 2, the narrow M = 3 shapes (q M = 2 6.0 vs 7.1) and the
+    // multi-pass down projection (k = 12288, M = 4: 14.8 vs 14.3, also with
+    // the next pass prefetched) are faster on dot2.
+    p.kind = kGemvMfma4;
+    const int r = knobs.rows;
+    p.rows = r == 4 || r == 8 || r == 12 || r == 16 ? r : (wide ? 16 : 8);
   } else {
     // 8 rows per block; over wide weights (N >= 16384) M = 4 streams faster
     // with 16 (gate_up 24576 x 4096: 24.8 vs 25.7-26.5 us on MI355X) and
     // M = 1 with 12, 2048 blocks (17.4-17.6 vs 17.8 us; 6 rows 17.6-18.3).
     // q/o/k-v and down are fastest with 8.
-    const bool wide = a.n >= 16384;
-    const int rows = knobs.rows ? knobs.rows : (wide && a.m == 4 ? 16 : wide && a.m == 1 ? 12 : 8);
-    if (rows >= 16) dispatch_m<16>(a);
-    else if (rows == 12 && a.m == 1) dispatch_src<1, 12>(a, dim3(unsigned((a.n + 11) / 12)));
-    else if (rows >= 8) dispatch_m<8>(a);
-    else dispatch_m<4>(a);
+    p.kind = kGemvDot2;
+    const int r = knobs.rows ? knobs.rows : (wide && m == 4 ? 16 : wide && m == 1 ? 12 : 8);
+    p.rows = r >= 16 ? 16 : r == 12 && m == 1 ? 12 : r >= 8 ? 8 : 4;
+  }
+  p.grid = unsigned((n + p.rows - 1) / p.rows);
+  return p;
+}
+
+// Passes of 4096 k bytes the MFMA-4 kernel unrolls for this k (0: a loop).
+int mfma4_passes(int64_t k) {
+  const int64_t passes = (k + 16 * kThreads - 1) / (16 * kThreads);
+  return passes <= 3 ? int(passes) : 0;
+}
+
+template <int kM, int kR>
+void launch_mfma4(const LinearArgs &a, const GemvPlan &p) {
+  const uint8_t *act = static_cast<const uint8_t *>(a.act);
+#define HIF8_MFMA4_LAUNCH(P)                                                                                \
+  gemv_mfma4_kernel<kM, kR, P><<<p.grid, kThreads, 0, a.stream>>>(act, a.act_scale, a.weight, a.channel_scale, \
+                                                                 a.bias, a.bias_dtype, a.out, a.out_dtype,   \
+                                                                 int(a.n), int(a.k))
+  // Two register sets of more than eight rows exceed the register file.
+  constexpr bool kTwoSets = kR <= 8;
+  switch (mfma4_passes(a.k)) {
+    case 1: HIF8_MFMA4_LAUNCH(1); break;
+    case 2: if constexpr (kTwoSets) { HIF8_MFMA4_LAUNCH(2); } else { HIF8_MFMA4_LAUNCH(0); } break;
+    case 3: if constexpr (kTwoSets) { HIF8_MFMA4_LAUNCH(3); } else { HIF8_MFMA4_LAUNCH(0); } break;
+    default: HIF8_MFMA4_LAUNCH(0); break;
+  }
+#undef HIF8_MFMA4_LAUNCH
+}
+
+template <int kR>
+void launch_mfma4_m(const LinearArgs &a, const GemvPlan &p) {
+  switch (a.m) {
+    case 2: launch_mfma4<2, kR>(a, p); break;
+    case 3: launch_mfma4<3, kR>(a, p); break;
+    default: launch_mfma4<4, kR>(a, p); break;
+  }
+}
+
+}  // namespace
+
+int launch_gemv(const LinearArgs &a) {
+  if (a.m < 1 || a.m > 4) return fail(HIF8_ERR_UNSUPPORTED, "GEMV kernel handles 1 <= M <= 4, got %lld", (long long)a.m);
+  const bool vec = a.k % 16 == 0 && aligned(a.weight, 16) && aligned(a.act, 16);
+  const GemvPlan p = plan_gemv(a.m, a.n, a.k, a.act_kind, vec);
+  switch (p.kind) {
+    case kGemvSimple:
+      gemv_simple_kernel<<<p.grid, kWave, 0, a.stream>>>(a.act, a.act_kind, a.act_scale, a.weight, a.channel_scale,
+                                                         a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.m),
+                                                         int(a.n), int(a.k));
+      break;
+    case kGemvMfma16: {
+      int st = HIF8_OK;
+      if (!mfma_gemv_smem(a)) return fail(HIF8_ERR_UNSUPPORTED, "soft_hif8 GEMV: the MFMA kernel cannot take this shape");
+      switch (a.m) {
+        case 1: st = launch_mfma_src<1>(a); break;
+        case 2: st = launch_mfma_src<2>(a); break;
+        case 3: st = launch_mfma_src<3>(a); break;
+        default: st = launch_mfma_src<4>(a); break;
+      }
+      if (st) return st;
+      break;
+    }
+    case kGemvMfma4:
+      switch (p.rows) {
+        case 4: launch_mfma4_m<4>(a, p); break;
+        case 8: launch_mfma4_m<8>(a, p); break;
+        case 12: launch_mfma4_m<12>(a, p); break;
+        default: launch_mfma4_m<16>(a, p); break;
+      }
+      break;
+    default:
+      if (p.rows >= 16) dispatch_m<16>(a);
+      else if (p.rows == 12) dispatch_src<1, 12>(a, dim3(p.grid));
+      else if (p.rows >= 8) dispatch_m<8>(a);
+      else dispatch_m<4>(a);
+      break;
   }
   return check_launch("soft_hif8 GEMV");
+}
+
+int describe_gemv(int64_t m, int64_t n, int64_t k, int act_kind, char *name, size_t name_len, int64_t *grid) {
+  const GemvPlan p = plan_gemv(m, n, k, act_kind, k % 16 == 0);
+  if (grid) *grid = p.grid;
+  if (name && name_len) {
+    switch (p.kind) {
+      case kGemvSimple: snprintf(name, name_len, "gemv_simple_kernel"); break;
+      case kGemvMfma16: snprintf(name, name_len, "gemv_mfma_kernel<%lld, %d>", (long long)m, act_kind); break;
+      case kGemvMfma4:
+        snprintf(name, name_len, "gemv_mfma4_kernel<%lld, %d, %d>", (long long)m, p.rows,
+                 p.rows > 8 && mfma4_passes(k) > 1 ? 0 : mfma4_passes(k));
+        break;
+      default: {
+        const bool dyn = act_kind == kActF16Dyn || act_kind == kActBf16Dyn;
+        snprintf(name, name_len, "gemv_kernel<%lld, %d, %d, %s>", (long long)m, p.rows, act_kind,
+                 p.one_chunk && !dyn ? "true" : "false");
+      }
+    }
+  }
+  return HIF8_OK;
 }
 
 }  // namespace hif8

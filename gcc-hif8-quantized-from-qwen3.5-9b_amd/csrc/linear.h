@@ -32,6 +32,9 @@ struct LinearArgs {
 
 // HBM-streaming GEMV for m <= 4 (gemv.hip).  Returns a status.
 int launch_gemv(const LinearArgs &a);
+// The kernel launch_gemv picks for these sizes and activation kind (16-byte
+// aligned operands): its name as profilers print it, and its grid.
+int describe_gemv(int64_t m, int64_t n, int64_t k, int act_kind, char *name, size_t name_len, int64_t *grid);
 // bf16-MFMA GEMM for any m (gemm.hip).  Returns a status.  With a workspace of
 // gemm_workspace_size(m, n, k) bytes, shapes with too few output tiles to fill
 // the chip split K over several blocks; without one they run unsplit.

@@ -173,3 +173,15 @@ extern "C" int soft_hif8_fused_gemm(const void *x, int x_dtype, const uint8_t *w
   a.act_kind = x_dtype == HIF8_DTYPE_BF16 ? kActBf16Dyn : kActF16Dyn;
   return launch_gemv(a);
 }
+
+extern "C" int hif8_gemv_launch_plan(int64_t m, int64_t n, int64_t k, int activation_kind, char *kernel,
+                                     size_t kernel_len, int64_t *grid) {
+  clear_error();
+  if (m < 1 || m > 4 || n <= 0 || k <= 0 || n > 0x7FFFFFFFll || k > 0x7FFFFFFFll)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gemv_launch_plan: needs 1 <= M <= 4 and positive N, K");
+  if (activation_kind < HIF8_ACT_CODES || activation_kind > HIF8_ACT_BF16_STATIC)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gemv_launch_plan: unknown activation kind %d", activation_kind);
+  static_assert(HIF8_ACT_CODES == kActCodes && HIF8_ACT_F16_STATIC == kActF16 && HIF8_ACT_BF16_STATIC == kActBf16,
+                "activation kind codes");
+  return describe_gemv(m, n, k, activation_kind, kernel, kernel_len, grid);
+}

@@ -18,8 +18,11 @@ latency), while four rows are faster separate (each block re-encodes M*K
 values: q 14.3 vs 9.9 us) and gate_up and down measured either way, so the
 fused op itself runs those (M >= 2, K > 4096 or N >= 12288) as
 quant + GEMV.
-``HIF8_STATIC_FUSED_SINGLE_ROW=1`` opts into the fused op for one token
-row; it changes which kernels run, not the outputs.
+One token row therefore goes through the fused op by default (one launch
+for K <= 4096 and N < 12288); ``HIF8_STATIC_FUSED_SINGLE_ROW=0`` restores
+the reference's routing (static_quant -> soft_linear unless
+``HIF8_STATIC_FUSED_GENERATION=1``, M <= 4, K < 1024, scheme.py:183-190).
+It changes which kernels run, not the outputs (equal bit for bit).
 
 ``HIF8_PREFILL_BF16_WEIGHTS=1`` (read in ``process_weights_after_loading``)
 keeps each weight decoded to bf16 beside its codes (2 bytes per element;
@@ -127,14 +130,14 @@ class W8A8HiFloat8StaticLinearMethod:
         """static_quant -> soft_linear, or the fused kernel (scheme.py:174-211).
 
         Fused when the reference would fuse (``HIF8_STATIC_FUSED_GENERATION=1``,
-        M <= 4, K < 1024) and, with ``HIF8_STATIC_FUSED_SINGLE_ROW=1``, for
-        one token row; the two routes give equal outputs."""
+        M <= 4, K < 1024) and for one token row unless
+        ``HIF8_STATIC_FUSED_SINGLE_ROW=0``; the two routes give equal outputs."""
         del tp_rank
         token_rows = x.numel() // x.shape[-1]
         k = x.shape[-1]
         use_fused = (
             token_rows <= 4 and os.environ.get(_STATIC_FUSED_GENERATION_ENV) == "1" and k < 1024
-        ) or (token_rows == 1 and os.environ.get(_STATIC_FUSED_SINGLE_ROW_ENV) == "1")
+        ) or (token_rows == 1 and os.environ.get(_STATIC_FUSED_SINGLE_ROW_ENV, "1") != "0")
         scale_factor = _static_scale_factor()
         fixed_scale = layer.input_scale
         if scale_factor != 1.0:

@@ -216,6 +216,21 @@ int soft_hif8_fused_gemm(const void *x, int x_dtype, const uint8_t *weight, cons
                          int64_t k, hif8_stream_t stream);
 
 /*
+ * Introspection, no counterpart in the reference: the GEMV kernel that soft_hif8_gemm
+ * (activation_kind HIF8_ACT_CODES) or soft_hif8_static_fused_gemm (HIF8_ACT_F16_STATIC /
+ * HIF8_ACT_BF16_STATIC, M = 1; the op itself runs static quant + the code kernel at
+ * M >= 2) launches for these sizes with 16-byte aligned operands: its name as profilers
+ * print it (template arguments included) into kernel[kernel_len], and its grid in
+ * workgroups.  For benchmarks that must match their timing to a profile of the same
+ * kernel.  Returns HIF8_OK or an error status; launches nothing.
+ */
+#define HIF8_ACT_CODES 0
+#define HIF8_ACT_F16_STATIC 1
+#define HIF8_ACT_BF16_STATIC 2
+int hif8_gemv_launch_plan(int64_t m, int64_t n, int64_t k, int activation_kind, char *kernel, size_t kernel_len,
+                          int64_t *grid);
+
+/*
  * Fused static KV-cache write (quantise + pack + scatter in one launch).
  * Replaces the static branch of _write_hif8_cache
  * (src/vllm_ascend_hif8/kv_runtime.py:1222-1339): _quantize_kv with checkpoint

@@ -42,6 +42,35 @@ def test_gemv_propagates_special_codes(native_ops, device):
             assert (math.isnan(got) and math.isnan(want)) or got == want
 
 
+@pytest.mark.parametrize("rows", [2, 3, 4])
+def test_multi_row_gemv_propagates_special_codes(native_ops, device, rows):
+    """M = 2..4 (the MFMA GEMV): NaN and +-Inf codes in the activation or the
+    weight reach exactly the outputs they feed, in either output dtype."""
+    one = o.encode_scalar(1.0)
+    k, n = 64, 8
+    act = np.zeros((rows, k), np.uint8)
+    act[:, 5] = one
+    weight = np.zeros((n, k), np.uint8)
+    weight[:, 5] = one
+    weight[1, 9] = 0x6F          # +Inf weight: meets activation zeros -> NaN in row 1 of every m
+    act[rows - 1, 9] = one       # ... and 1.0 in the last activation row -> +Inf there
+    weight[2, 5] = 0xEF          # -Inf weight times activation 1.0 -> -Inf
+    act[0, 20] = 0x80            # NaN activation code: all of row m = 0 is NaN (NaN x 0 is NaN)
+    weight[3, 20] = one
+    ts = np.full(rows, 0.5, np.float32)
+    cs = np.full(n, 2.0, np.float32)
+    with np.errstate(all="ignore"):
+        want = o.linear_u8_u8(act, ts, weight, cs)
+    for out_dtype in (torch.float16, torch.bfloat16):
+        y = native_ops.soft_hif8_gemm(_t(act, device), _t(weight, device), _t(ts, device), _t(cs, device), None,
+                                      out_dtype)
+        torch.cuda.synchronize()
+        got = y.cpu().float().numpy()
+        assert np.array_equal(np.isnan(got), np.isnan(want)), (got, want)
+        fin = ~np.isnan(want)
+        assert np.array_equal(got[fin], want[fin].astype(np.float32)), (got, want)
+
+
 @pytest.mark.parametrize("rows", [1, 2, 3, 4, 5])
 def test_soft_linear_matches_reference_small(native_ops, device, rows):
     from hif8_rocm import native as api
@@ -195,8 +224,9 @@ def test_nonzero_storage_offset_is_rejected(native_ops, device):
 
 @pytest.mark.parametrize("n,k", LAYER_SHAPES)
 def test_single_row_fusion_equals_the_two_stage_apply(native_ops, device, monkeypatch, n, k):
-    """The scheme's HIF8_STATIC_FUSED_SINGLE_ROW route gives the two-stage
-    route's outputs bit for bit at every decode projection shape."""
+    """The scheme's default one-row route (the fused op) gives the two-stage
+    route's outputs (HIF8_STATIC_FUSED_SINGLE_ROW=0) bit for bit at every
+    decode projection shape."""
     import torch.nn as nn
 
     from hif8_rocm import scheme
@@ -209,9 +239,9 @@ def test_single_row_fusion_equals_the_two_stage_apply(native_ops, device, monkey
     layer.input_scale = nn.Parameter(input_scale_of(x).to(device), requires_grad=False)
     method = scheme.W8A8HiFloat8StaticLinearMethod()
     method.process_weights_after_loading(layer)
-    monkeypatch.delenv("HIF8_STATIC_FUSED_SINGLE_ROW", raising=False)
+    monkeypatch.setenv("HIF8_STATIC_FUSED_SINGLE_ROW", "0")
     two_stage = method.apply(layer, x.to(device))
-    monkeypatch.setenv("HIF8_STATIC_FUSED_SINGLE_ROW", "1")
+    monkeypatch.delenv("HIF8_STATIC_FUSED_SINGLE_ROW", raising=False)
     fused = method.apply(layer, x.to(device))
     torch.cuda.synchronize()
     assert torch.equal(fused, two_stage)

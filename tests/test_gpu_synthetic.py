@@ -103,8 +103,9 @@ def test_graph_replay_matches_eager_decode(model, device):
 
 
 def test_single_row_fusion_generates_the_same_tokens(model, device, monkeypatch):
-    """HIF8_STATIC_FUSED_SINGLE_ROW=1 swaps quant -> GEMV for the fused kernel
-    on one-row projections; the logits, hence the tokens, are unchanged.  The
+    """One-row projections through the fused kernel (the default) and through
+    quant -> GEMV (HIF8_STATIC_FUSED_SINGLE_ROW=0) give the same logits,
+    hence the same tokens.  The
     glue-kernel input quant is switched off, so that every one-row projection
     (qkv / qkvz, gate_up, o / out, down) goes through the scheme and the fused
     op, not only the o / out projections."""
@@ -112,10 +113,11 @@ def test_single_row_fusion_generates_the_same_tokens(model, device, monkeypatch)
 
     g = torch.Generator(device=device).manual_seed(21)
     prompt = torch.randint(0, model.cfg.vocab, (1, 12), generator=g, device=device)
+    monkeypatch.setenv("HIF8_STATIC_FUSED_SINGLE_ROW", "0")
     glue, _ = generate(model, prompt, 6, graph=True)
     monkeypatch.setattr(model, "fuse_input_quant", False)
     plain, _ = generate(model, prompt, 6, graph=True)
-    monkeypatch.setenv("HIF8_STATIC_FUSED_SINGLE_ROW", "1")
+    monkeypatch.delenv("HIF8_STATIC_FUSED_SINGLE_ROW", raising=False)
     fused, _ = generate(model, prompt, 6, graph=True)
     assert torch.equal(plain, fused)
     assert torch.equal(glue, plain)

@@ -251,6 +251,9 @@ def test_apply_defaults_to_standalone_static_quant(clean_env):
 
 
 def test_fused_generation_is_opt_in_and_limited_to_small_shapes(clean_env):
+    # The reference's routing contract (test_static_scheme.py:105-192), which
+    # HIF8_STATIC_FUSED_SINGLE_ROW=0 restores for one-row inputs too.
+    os.environ["HIF8_STATIC_FUSED_SINGLE_ROW"] = "0"
     os.environ["HIF8_STATIC_FUSED_GENERATION"] = "1"
     method = W8A8HiFloat8StaticLinearMethod()
     layer = _layer()
@@ -276,13 +279,15 @@ def test_fused_generation_is_opt_in_and_limited_to_small_shapes(clean_env):
         fused.assert_not_called()
 
 
-def test_single_row_fusion_is_an_opt_in(clean_env):
-    """HIF8_STATIC_FUSED_SINGLE_ROW=1 fuses one token row, whatever K, and
-    nothing else; unset, routing is the reference's."""
+def test_single_row_fusion_is_the_default_with_an_opt_out(clean_env):
+    """One token row goes through the fused op by default, whatever K, and
+    nothing else does; HIF8_STATIC_FUSED_SINGLE_ROW=0 restores the
+    reference's two-stage routing."""
     method = W8A8HiFloat8StaticLinearMethod()
     out = torch.randn(1, 5)
-    cases = [(None, (1, 4096), False), ("1", (1, 4096), True), ("1", (1, 8), True), ("1", (2, 4096), False),
-             ("1", (1, 12288), True), (None, (1, 12288), False), ("0", (1, 64), False)]
+    cases = [(None, (1, 4096), True), ("1", (1, 4096), True), ("0", (1, 4096), False), (None, (1, 8), True),
+             (None, (2, 4096), False), ("1", (3, 64), False), (None, (1, 12288), True), ("0", (1, 12288), False),
+             ("0", (1, 64), False)]
     for flag, shape, want_fused in cases:
         if flag is None:
             os.environ.pop("HIF8_STATIC_FUSED_SINGLE_ROW", None)
@@ -303,7 +308,9 @@ def test_single_row_fusion_is_an_opt_in(clean_env):
 
 
 def test_prefill_bf16_weights_route_only_large_m(clean_env):
-    """A layer holding a decoded weight runs M > 4 on it; M <= 4 keeps the codes."""
+    """A layer holding a decoded weight runs M > 4 on it; M <= 4 keeps the codes
+    (two-stage routing, so that one row is not fused)."""
+    os.environ["HIF8_STATIC_FUSED_SINGLE_ROW"] = "0"
     method = W8A8HiFloat8StaticLinearMethod()
     layer = _layer(k=64)
     method.process_weights_after_loading(layer)
@@ -341,11 +348,15 @@ def test_scale_factor_env_multiplies_the_checkpoint_scale(clean_env):
     method = W8A8HiFloat8StaticLinearMethod()
     layer = _layer(0.25)
     method.process_weights_after_loading(layer)
-    x = torch.zeros((1, 8), dtype=torch.bfloat16)
-    with patch("hif8_rocm.scheme.native.static_quant", return_value=(x.to(torch.uint8), torch.ones(1))) as sq, \
-         patch("hif8_rocm.scheme.native.soft_linear", return_value=torch.zeros(1, 5)):
+    x = torch.zeros((2, 8), dtype=torch.bfloat16)
+    with patch("hif8_rocm.scheme.native.static_quant", return_value=(x.to(torch.uint8), torch.ones(2))) as sq, \
+         patch("hif8_rocm.scheme.native.soft_linear", return_value=torch.zeros(2, 5)):
         method.apply(layer, x)
     assert float(sq.call_args[0][1]) == 0.5
+    # One row takes the fused op, with the same scaled fixed scale.
+    with patch("hif8_rocm.scheme.native.soft_static_fused_linear", return_value=torch.zeros(1, 5)) as fused:
+        method.apply(layer, x[:1])
+    assert float(fused.call_args[0][2]) == 0.5
     os.environ["HIF8_STATIC_SCALE_FACTOR"] = "-1"
     with pytest.raises(ValueError, match="positive finite"):
         method.apply(layer, x)

@@ -47,3 +47,27 @@ def test_static_quant_with_per_row_scales():
     got = torch_cpu.static_quant(torch.from_numpy(w), torch.from_numpy(ws).reshape(-1, 1)).numpy()
     want, _ = o.static_quant_rows(w, ws)
     assert np.array_equal(got, want)
+
+
+def test_paged_decode_attention_matches_the_numpy_oracle():
+    """The torch-CPU attention port against paged_attention_reference: within
+    bf16 resolution of the float64 variant and closer still to the variant
+    that rounds like the reference's bf16 tensors; empty requests give zeros."""
+    rng = np.random.default_rng(9)
+    hkv, group, d, bs, nb = 2, 4, 32, 8, 12
+    kc = np.zeros((nb, bs, hkv, d + 4), np.uint8)
+    vc = np.zeros_like(kc)
+    for c in (kc, vc):
+        vals = rng.standard_normal((nb * bs, hkv, d)).astype(np.float32)
+        data, sc = o.quantize_kv_rows_static(vals, (np.abs(vals).max(axis=(0, 2)) / 32768.0).astype(np.float32))
+        o.scatter_kv_rows(c, o.pack_kv_rows(data, sc), np.arange(nb * bs), bs)
+    table = np.array([[3, 7, 1, 0], [11, 2, 5, 9], [4, 6, 8, 10]])
+    lens = [29, 7, 0]
+    q = torch.randn(3, hkv * group, d, generator=torch.Generator().manual_seed(3)).to(torch.bfloat16)
+    got = torch_cpu.paged_decode_attention(q, torch.from_numpy(kc), torch.from_numpy(vc), torch.from_numpy(table),
+                                           lens, 0.2).float().numpy()
+    f64 = o.paged_attention_reference(q.float().numpy(), kc, vc, table, lens, bs, 0.2, rounding="f64")
+    b16 = o.paged_attention_reference(q.float().numpy(), kc, vc, table, lens, bs, 0.2, rounding="bf16")
+    assert not got[2].any()
+    np.testing.assert_allclose(got, f64, rtol=2e-2, atol=2e-2)
+    np.testing.assert_allclose(got, b16, rtol=1e-2, atol=1e-2)
