@@ -8,7 +8,7 @@ runs the static W8A8 linear method (hif8_rocm.scheme) with its default
 routing: four token rows as hif8_static_quant of the bf16 activation, then
 soft_hif8_gemm (the HBM-streaming GEMV kernel for M <= 4); one token row
 through the fused op soft_hif8_static_fused_gemm (one launch for K <= 4096
-and N < 12288, static quant + GEMV inside the op otherwise; outputs equal to
+and N < 16384, static quant + GEMV inside the op otherwise; outputs equal to
 the two-stage route).  The reference's routing (every projection two-stage,
 HIF8_STATIC_FUSED_SINGLE_ROW=0) and every projection through the fused op
 are reported beside it.  One step = that sweep over one layer's weights; five
@@ -385,7 +385,7 @@ def per_kernel_table(st: Setup) -> dict:
                 table[f"{name}_m{m}_fused"] = {"kernel": "fused_quant_gemv", "us": round(med * 1e3, 3), "bytes": fb,
                                                "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                                                "quant_then_gemv_us": round(med2 * 1e3, 3),
-                                               "launch": kern if m == 1 and k <= 4096 and n < 12288
+                                               "launch": kern if m == 1 and k <= 4096 and n < 16384
                                                else "hif8_static_quant + code GEMV", "grid": grid}
     for m, k in ((4096, 4096), (4096, 12288), (512, 4096), (1, 4096), (4, 12288)):
         x, s = st.x[(m, k)]
@@ -869,7 +869,7 @@ def e2e_decode(torch, device) -> dict:
     # b1_single_row_fusion: batch 1 again with HIF8_STATIC_FUSED_SINGLE_ROW=1
     # and the glue-kernel input quant off, so every one-row projection (qkv /
     # qkvz, gate_up, o / out, down) goes through the fused static-quant op,
-    # one launch for K <= 4096 and N < 12288 (same tokens).
+    # one launch for K <= 4096 and N < 16384 (same tokens).
     for b, key, single in ((1, "b1", False), (4, "b4", False), (1, "b1_single_row_fusion", True)):
         prompt = torch.randint(0, cfg.vocab, (b, E2E_PROMPT), generator=g, device=device)
         if single:
@@ -994,10 +994,10 @@ def main() -> None:
         f"m4096 {gemm_decoded['layer_m4096']['us_per_layer']} us")
     gemv = [v for v in table.values() if v["kernel"] == "gemv"]
     # The launches of the headline step: M = 4 static quant + the code GEMV;
-    # one row through the fused op (one launch for K <= 4096, N < 12288,
+    # one row through the fused op (one launch for K <= 4096, N < 16384,
     # else static quant + the code GEMV inside the op).  The dominant launch
     # is the longest of them.
-    step_rows = [(f"{name}_m1_fused" if m == 1 and k <= 4096 and n < 12288 else f"{name}_m{m}")
+    step_rows = [(f"{name}_m1_fused" if m == 1 and k <= 4096 and n < 16384 else f"{name}_m{m}")
                  for m in DECODE_M for name, n, k in LAYER]
     dom_key = max(step_rows, key=lambda r: table[r]["us"])
     best_key = max(step_rows, key=lambda r: table[r]["frac_hbm"])

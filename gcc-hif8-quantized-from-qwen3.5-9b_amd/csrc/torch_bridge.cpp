@@ -10,6 +10,7 @@
 // Two operators are new: the fused KV-cache write and the paged decode
 // attention that replace the reference's quant + pack + index_copy_ and
 // gather + decode + fused-attention sequences (kv_runtime.py:1222-1563).
+#include <cstdlib>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
@@ -289,17 +290,22 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
   const void *bias_ptr = bias.has_value() ? bias->data_ptr() : nullptr;
   const int bias_dtype = bias.has_value() ? DtypeCode(bias->scalar_type()) : HIF8_DTYPE_NONE;
   const int64_t m = activation.size(0), n = weight.size(0), k = activation.size(1);
-  if (m >= 2 || k > 4096 || n >= 12288) {
+  // Widest N fused into one launch (tuning knob HIF8_FUSED_MAX_N, read once).
+  static const int64_t max_n = [] {
+    const char *v = getenv("HIF8_FUSED_MAX_N");
+    return v && *v ? int64_t(atoll(v)) : int64_t(16383);
+  }();
+  if (m >= 2 || k > 4096 || n > max_n) {
     // Every block of the single-launch kernel encodes its whole activation
     // chunk, which costs more than a separate quant launch once there are
     // several rows (measured on MI355X in graphs at M = 4: q 4096x4096 14.3
     // vs 9.9 us, gate_up 24576x4096 38.1 vs 26.6).  One row with K <= 4096
-    // and N < 12288 (one chunk per thread, loaded before the table set-up,
-    // at most 1536 blocks) is faster fused every time (q 6.5 vs 8.7-9.0 us,
-    // k/v 2048x4096 5.0-5.2 vs 7.6, o 6.6-6.7 vs 8.3-8.8); gate_up
-    // (N = 24576: 3072 blocks, each re-encoding) and down (K = 12288, the
-    // chunk loop) measured either way across runs (gate_up 19.7-21.4 vs
-    // 20.4-21.4 us, down 13.6-14.7 vs 13.7-16.0), so they keep two launches.
+    // and N < 16384 (one chunk per thread, loaded before the table set-up,
+    // at most 2048 blocks) is faster fused every time (q 6.5 vs 8.7-9.0 us,
+    // k/v 2048x4096 5.0-5.2 vs 7.6, o 6.6-6.7 vs 8.3-8.8, 12288x4096 12.4 vs
+    // 14.0); gate_up (N = 24576, each of 2048 blocks re-encoding: 21.5-22.9
+    // vs 21.5-21.7 us) and down (K = 12288, the chunk loop: 13.6-14.7 vs
+    // 13.7-16.0) keep two launches.
     // The two launches give the same codes and the same GEMV, hence equal
     // outputs.
     auto codes = at::empty({m, k}, activation.options().dtype(at::ScalarType::Byte));

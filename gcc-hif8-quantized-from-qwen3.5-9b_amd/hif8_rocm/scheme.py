@@ -16,10 +16,10 @@ faster fused (q 6.5 vs 8.7-9.0 us, k/v 5.0-5.2 vs 7.6, o 6.6-6.7 vs
 8.3-8.8: the separate quant launch costs 2-3 us of launch and cold-cache
 latency), while four rows are faster separate (each block re-encodes M*K
 values: q 14.3 vs 9.9 us) and gate_up and down measured either way, so the
-fused op itself runs those (M >= 2, K > 4096 or N >= 12288) as
+fused op itself runs those (M >= 2, K > 4096 or N >= 16384) as
 quant + GEMV.
 One token row therefore goes through the fused op by default (one launch
-for K <= 4096 and N < 12288); ``HIF8_STATIC_FUSED_SINGLE_ROW=0`` restores
+for K <= 4096 and N < 16384); ``HIF8_STATIC_FUSED_SINGLE_ROW=0`` restores
 the reference's routing (static_quant -> soft_linear unless
 ``HIF8_STATIC_FUSED_GENERATION=1``, M <= 4, K < 1024, scheme.py:183-190).
 It changes which kernels run, not the outputs (equal bit for bit).
