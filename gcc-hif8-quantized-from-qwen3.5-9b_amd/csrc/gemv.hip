@@ -7,9 +7,9 @@
 //     1 KiB of contiguous row bytes and a thread has kR 16-byte loads in flight;
 //   * the activation chunk (m <= 4 rows) is decoded once per chunk into packed
 //     bf16 pairs and stays in VGPRs for all kR weight rows;
-//   * weight bytes are decoded with a 256-entry bf16 table in LDS (HiF8 is a
-//     subset of bf16, so decode is exact) and multiplied with v_dot2_f32_bf16,
-//     FP32 accumulation;
+//   * weight bytes are decoded with a bf16 table in LDS (HiF8 is a subset of
+//     bf16, so decode is exact; replicated per lane for small grids, see
+//     RepLut) and multiplied with v_dot2_f32_bf16, FP32 accumulation;
 //   * each wavefront sums its kR*kM partials over its 64 lanes in registers
 //     (permlane swaps and DPP, halving the values per lane at each level),
 //     the four wavefront totals meet in LDS, and the epilogue applies token
@@ -40,21 +40,91 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
 
 typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
 
-// Two table entries packed as one bf16 pair (compiles to one v_perm_b32).
-__device__ __forceinline__ uint32_t lut_pair(const uint16_t *lut, uint32_t lo, uint32_t hi) {
-  u16x2 v;
-  v.x = lut[lo];
-  v.y = lut[hi];
-  return __builtin_bit_cast(uint32_t, v);
+// Decode-table lookups.  LDS serves a DS instruction 32 lanes at a time from
+// 32 four-byte banks.  The plain 256-entry bf16 table (CompactLut) spans 128
+// dwords, four per bank, and lanes holding codes in different dwords of one
+// bank are served one after another: measured on MI355X, a wavefront of
+// lookups takes 2.3x the conflict-free time for codes quantised from Gaussian
+// weights (1.7x for codes uniform in 0..110).
+//
+// RepLut is the conflict-free form: code c owns the 128-byte row at byte
+// 256 c, 32 dwords each holding bf16(dec(c)) in both halves, and lane l reads
+// dword l % 32 of the row, so the 32 lanes served together always hit 32
+// distinct banks.  The address is one v_perm_b32 of the code byte and the
+// lane's column, as the plain table's is one shift; but the table takes 64 KiB
+// of LDS (half of it unused), which leaves room for two blocks per CU.  The
+// GEMV therefore uses it only when its grid fits the chip in one round of two
+// blocks per CU (kRepMaxBlocks): there the blocks' latency sets the time and
+// the faster lookups shorten it (MI355X, graphs of 20 launches over >= 768 MB
+// of weights quantised from Gaussian rows, M = 1: q 4096 x 4096 5.27 vs 5.50
+// us, k+v 3.98 vs 4.18, o 5.36 vs 5.59; M = 4: down 4096 x 12288 13.6 vs
+// 14.4).  Larger grids
+// stream as fast as the memory pipeline allows with four blocks per CU and
+// the plain table, and lose 5-10 % with the big one (gate_up 24576 x 4096, M
+// = 4: 22.0-22.9 vs 20.6-21.0 us, also as 512-thread blocks of two 4-wave
+// teams sharing one table), though their lookups wait far less (rocprofv3
+// SQ_WAIT_INST_LDS down 3x, SQ_LDS_BANK_CONFLICT 0).
+constexpr uint32_t kRepLutBytes = 256 * 256;
+constexpr int64_t kRepMaxBlocks = 2 * 256;
+
+struct RepLut {
+  const uint8_t *t;  // LDS, kRepLutBytes
+  uint32_t col;      // 4 * (lane % 32)
+  // Entry of byte kByte of the word w.
+  template <int kByte>
+  __device__ __forceinline__ uint16_t byte(uint32_t w) const {
+    const uint32_t off = __builtin_amdgcn_perm(col, w, 0x0C0C0004u | (uint32_t(kByte) << 8));
+    return *reinterpret_cast<const uint16_t *>(t + off);
+  }
+  __device__ __forceinline__ uint16_t code(uint32_t c) const { return byte<0>(c); }
+};
+
+struct CompactLut {
+  const uint16_t *t;  // LDS, 256 entries, at LDS address 0 (a lookup address is one shift of the byte)
+  template <int kByte>
+  __device__ __forceinline__ uint16_t byte(uint32_t w) const { return t[(w >> (8 * kByte)) & 0xFFu]; }
+  __device__ __forceinline__ uint16_t code(uint32_t c) const { return t[c]; }
+};
+
+// The decode table of a block of 256 threads, in LDS at `tab` (kRep: RepLut,
+// else CompactLut).  Replicated, thread t writes row t as eight 16-byte stores
+// at column quads rotated by t, so the lanes of one store instruction cover
+// distinct banks.
+template <bool kRep>
+__device__ __forceinline__ void fill_decode_table(uint8_t *tab, int tid) {
+  const uint32_t e = decode_bits(uint32_t(tid)) >> 16;
+  if constexpr (kRep) {
+    const uint32_t v = e | (e << 16);
+    u32x4 *row = reinterpret_cast<u32x4 *>(tab + 256u * uint32_t(tid));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) row[(j + tid) & 7] = u32x4{v, v, v, v};
+  } else {
+    reinterpret_cast<uint16_t *>(tab)[tid] = uint16_t(e);
+  }
 }
 
-// 16 HiF8 bytes -> 8 packed bf16 pairs through the LDS decode table.
-__device__ __forceinline__ void decode16(const uint16_t *lut, const u32x4 q, uint32_t (&p)[8]) {
+template <bool kRep>
+using DecodeLut = std::conditional_t<kRep, RepLut, CompactLut>;
+
+template <bool kRep>
+__device__ __forceinline__ DecodeLut<kRep> decode_lut(const uint8_t *tab, int lane) {
+  if constexpr (kRep) return RepLut{tab, 4u * uint32_t(lane & 31)};
+  else return CompactLut{reinterpret_cast<const uint16_t *>(tab)};
+}
+
+// 16 HiF8 bytes -> 8 packed bf16 pairs (each pair packs with one v_perm_b32).
+template <class Lut>
+__device__ __forceinline__ void decode16(const Lut &lut, const u32x4 q, uint32_t (&p)[8]) {
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const uint32_t w = q[i];
-    p[2 * i] = lut_pair(lut, w & 0xFFu, (w >> 8) & 0xFFu);
-    p[2 * i + 1] = lut_pair(lut, (w >> 16) & 0xFFu, w >> 24);
+    u16x2 lo, hi;
+    lo.x = lut.template byte<0>(w);
+    lo.y = lut.template byte<1>(w);
+    hi.x = lut.template byte<2>(w);
+    hi.y = lut.template byte<3>(w);
+    p[2 * i] = __builtin_bit_cast(uint32_t, lo);
+    p[2 * i + 1] = __builtin_bit_cast(uint32_t, hi);
   }
 }
 
@@ -71,9 +141,9 @@ __device__ __forceinline__ bool near_index_boundary(float q) {
 // MI355X, rounding the quotient's bits arithmetically instead (about 20 VALU
 // operations per element) made the fused GEMV 20-30 % slower, since every
 // block re-encodes its activation chunk.
-template <bool kBf16>
+template <bool kBf16, class Lut>
 __device__ __forceinline__ void fast_encode_decode16(const u32x4 a, const u32x4 b, float s, float r,
-                                                     const uint8_t *enc, const uint16_t *dec, u32x4 &lo,
+                                                     const uint8_t *enc, const Lut &dec, u32x4 &lo,
                                                      u32x4 &hi) {
   uint32_t p[8];
 #pragma unroll
@@ -91,7 +161,7 @@ __device__ __forceinline__ void fast_encode_decode16(const u32x4 a, const u32x4 
       c0 = enc[__float_as_uint(q0) >> 19];
       c1 = enc[__float_as_uint(q1) >> 19];
     }
-    p[i] = uint32_t(dec[c0]) | (uint32_t(dec[c1]) << 16);
+    p[i] = uint32_t(dec.code(c0)) | (uint32_t(dec.code(c1)) << 16);
   }
   lo = u32x4{p[0], p[1], p[2], p[3]};
   hi = u32x4{p[4], p[5], p[6], p[7]};
@@ -190,7 +260,7 @@ constexpr int gemv_min_waves(int m, int rows) { return rows > 8 ? 2 : m == 1 ? 6
 // loads count as invariant, and the compiler sinks the one-chunk preload below
 // the LDS barrier to its first use, serialising the set-up and the weight
 // fetch that the preload exists to overlap.
-template <int kM, int kR, int kSrc, bool kOneChunk>
+template <int kM, int kR, int kSrc, bool kOneChunk, bool kRep>
 __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
     const void *act, const float *__restrict__ act_scale,
     const uint8_t *weight, const float *__restrict__ cs,
@@ -203,11 +273,13 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
   constexpr bool kDynamic = kSrc == kActF16Dyn || kSrc == kActBf16Dyn;
   constexpr bool kInBf16 = kSrc == kActBf16 || kSrc == kActBf16Dyn;
   constexpr int kActWords = kFused ? 2 : 1;  // 16-byte words of activation per row per chunk
-  __shared__ __attribute__((aligned(16))) uint16_t dec_lut[256];
+  // The decode table first, at LDS address 0.
+  __shared__ __attribute__((aligned(16))) uint8_t dec_tab[kRep ? kRepLutBytes : 512];
   __shared__ __attribute__((aligned(16))) uint8_t enc_lut[kFused ? 8192 : 16];
   __shared__ __attribute__((aligned(16))) float red[kWaves][kVp];
 
   const int tid = threadIdx.x;
+  const auto dec_lut = decode_lut<kRep>(dec_tab, tid & 63);
   const int n0 = blockIdx.x * kR;
   const int chunks = k >> 4;
 
@@ -255,9 +327,8 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
     enc_part[0] = src[tid];
     enc_part[1] = src[tid + kThreads];
   }
-  const uint16_t entry = uint16_t(decode_bits(uint32_t(tid)) >> 16);
   if constexpr (kOneChunk) load(min(tid, chunks - 1));
-  dec_lut[tid] = entry;
+  fill_decode_table<kRep>(dec_tab, tid);
   if constexpr (kFused) {
     u32x4 *dst = reinterpret_cast<u32x4 *>(enc_lut);
     dst[tid] = enc_part[0];
@@ -426,7 +497,7 @@ __device__ __forceinline__ float row_quad_sum(float v) {
 
 // kPasses: 1..3 passes of 4096 k bytes per block, unrolled (k <= 4096 kPasses),
 // or 0 for any k (a loop without prefetch).
-template <int kM, int kR, int kPasses>
+template <int kM, int kR, int kPasses, bool kRep>
 __global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
     const uint8_t *act, const float *__restrict__ act_scale, const uint8_t *weight, const float *__restrict__ cs,
     const void *__restrict__ bias, int bias_dtype, void *__restrict__ out, int out_dtype, int n, int k) {
@@ -434,11 +505,12 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
   constexpr int kG = kR / 4;              // row groups
   constexpr int kWaves = kThreads / kWave;
   constexpr int kPass = 16 * kThreads;    // k bytes per pass of the block
-  // The decode table first, at LDS address 0: a lookup is one shift of the byte.
-  __shared__ __attribute__((aligned(16))) uint16_t dec_lut[256];
+  // The decode table first, at LDS address 0.
+  __shared__ __attribute__((aligned(16))) uint8_t dec_tab[kRep ? kRepLutBytes : 512];
   __shared__ __attribute__((aligned(16))) float red[kWaves][kR][4];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const auto dec_lut = decode_lut<kRep>(dec_tab, lane);
   const int b = lane >> 2, j = lane & 3;
   const int n0 = blockIdx.x * kR;
   const int chunks = k >> 4;
@@ -472,9 +544,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
       }
   };
   Pass cur;
-  const uint16_t entry = uint16_t(decode_bits(uint32_t(tid)) >> 16);
   load(cur, 0);
-  dec_lut[tid] = entry;
+  fill_decode_table<kRep>(dec_tab, tid);
   __builtin_amdgcn_sched_barrier(0);
   lds_barrier();
 
@@ -658,8 +729,9 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemv_mfma_kernel(
   constexpr bool kFused = kSrc != kActCodes;
   // Static LDS first: the decode table sits at LDS address 0, so a table
   // address is one SDWA shift of the weight byte.
-  __shared__ __attribute__((aligned(16))) uint16_t dec_lut[256];
+  __shared__ __attribute__((aligned(16))) uint16_t dec_tab[256];
   __shared__ __attribute__((aligned(16))) uint32_t zero_block[8];
+  const CompactLut dec_lut{dec_tab};
   __shared__ __attribute__((aligned(16))) float red[kMfmaWaves * 16 * 4];
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   uint16_t *xs = reinterpret_cast<uint16_t *>(smem);                       // [kM][k] bf16
@@ -677,7 +749,7 @@ __global__ __launch_bounds__(kMfmaThreads, 1) void gemv_mfma_kernel(
   for (int u = 0; u < kMfmaUnroll; ++u)
     if (s_begin + u < s_end) wq[u] = *reinterpret_cast<const u32x4 *>(wptr + size_t(s_begin + u) * 64);
 
-  if (tid < 128) reinterpret_cast<uint32_t *>(dec_lut)[tid] = reinterpret_cast<const uint32_t *>(kDeviceTables.decode_bf16)[tid];
+  if (tid < 128) reinterpret_cast<uint32_t *>(dec_tab)[tid] = reinterpret_cast<const uint32_t *>(kDeviceTables.decode_bf16)[tid];
   if (tid < 8) zero_block[tid] = 0u;
   if constexpr (kFused) reinterpret_cast<u32x4 *>(enc_lut)[tid] = reinterpret_cast<const u32x4 *>(kDeviceTables.static_encode)[tid];
   lds_barrier();
@@ -786,74 +858,6 @@ size_t mfma_gemv_smem(const LinearArgs &a) {
   return smem <= 160 * 1024 ? smem : 0;
 }
 
-template <int kM, int kR>
-void dispatch_src(const LinearArgs &a, dim3 grid) {
-  const int n = int(a.n), k = int(a.k);
-  switch (a.act_kind) {
-    case kActCodes:
-      if (k <= 16 * kThreads)
-        gemv_kernel<kM, kR, kActCodes, true><<<grid, kThreads, 0, a.stream>>>(
-            a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
-      else
-        gemv_kernel<kM, kR, kActCodes, false><<<grid, kThreads, 0, a.stream>>>(
-            a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
-      break;
-    case kActF16:
-      if (k <= 16 * kThreads)
-        gemv_kernel<kM, kR, kActF16, true><<<grid, kThreads, 0, a.stream>>>(
-            a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
-      else
-        gemv_kernel<kM, kR, kActF16, false><<<grid, kThreads, 0, a.stream>>>(
-            a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
-      break;
-    case kActBf16:
-      if (k <= 16 * kThreads)
-        gemv_kernel<kM, kR, kActBf16, true><<<grid, kThreads, 0, a.stream>>>(
-            a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
-      else
-        gemv_kernel<kM, kR, kActBf16, false><<<grid, kThreads, 0, a.stream>>>(
-            a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
-      break;
-    case kActF16Dyn:
-      gemv_kernel<kM, kR, kActF16Dyn, false><<<grid, kThreads, 0, a.stream>>>(
-          a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
-      break;
-    default:
-      gemv_kernel<kM, kR, kActBf16Dyn, false><<<grid, kThreads, 0, a.stream>>>(
-          a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k);
-      break;
-  }
-}
-
-template <int kR>
-void dispatch_m(const LinearArgs &a) {
-  const dim3 grid(unsigned((a.n + kR - 1) / kR));
-  switch (a.m) {
-    case 1: dispatch_src<1, kR>(a, grid); break;
-    case 2: dispatch_src<2, kR>(a, grid); break;
-    case 3: dispatch_src<3, kR>(a, grid); break;
-    default: dispatch_src<4, kR>(a, grid); break;
-  }
-}
-
-// Kernel selection knobs, read once: HIF8_GEMV_KERNEL=d forces the dot2 VALU
-// kernel for every M (default: the MFMA-4 kernel for code activations at
-// M = 4, and M = 3 over wide weights), =4 the MFMA-4 kernel for every M >= 2,
-// =m the experimental 16x16x32 MFMA kernel; HIF8_GEMV_ROWS=4|8|12|16
-// forces the rows per block (12: M = 1 or the MFMA-4 kernel).  Measured on
-// MI355X (gate_up 24576x4096, M=1): the dot2 kernel with 8 rows per block
-// 20.0 us; the 16x16x32 MFMA kernel 29.3 us (its 16-rows x 64-byte load
-// pattern alone reads ~12 % slower than 1 KiB-contiguous rows); a persistent
-// double-buffered variant 24 us (2 blocks/CU keep too few bytes in flight).
-struct GemvKnobs {
-  char kernel = 'v';
-  int rows = 0;
-  GemvKnobs() {
-    if (const char *v = getenv("HIF8_GEMV_KERNEL")) kernel = v[0];
-    if (const char *v = getenv("HIF8_GEMV_ROWS")) rows = atoi(v);
-  }
-};
-
 enum GemvKind { kGemvDot2, kGemvMfma4, kGemvSimple, kGemvMfma16 };
 
 struct GemvPlan {
@@ -862,6 +866,74 @@ struct GemvPlan {
   bool one_chunk;  // k <= 16 * 256: one 16-byte chunk (dot2) or one pass (MFMA-4) per thread
   unsigned grid;
   unsigned threads;
+  bool rep;        // replicated (conflict-free) decode table
+};
+
+template <int kM, int kR, bool kRep>
+void dispatch_src(const LinearArgs &a, dim3 grid) {
+  const int n = int(a.n), k = int(a.k);
+#define HIF8_DOT2_LAUNCH(SRC, ONE, REP)                                                                    \
+  gemv_kernel<kM, kR, SRC, ONE, REP><<<grid, kThreads, 0, a.stream>>>(                                   \
+      a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k)
+  const bool one = k <= 16 * kThreads;
+  switch (a.act_kind) {
+    case kActCodes:
+      if (one) HIF8_DOT2_LAUNCH(kActCodes, true, kRep);
+      else HIF8_DOT2_LAUNCH(kActCodes, false, kRep);
+      break;
+    case kActF16:
+      if (one) HIF8_DOT2_LAUNCH(kActF16, true, kRep);
+      else HIF8_DOT2_LAUNCH(kActF16, false, kRep);
+      break;
+    case kActBf16:
+      if (one) HIF8_DOT2_LAUNCH(kActBf16, true, kRep);
+      else HIF8_DOT2_LAUNCH(kActBf16, false, kRep);
+      break;
+    case kActF16Dyn: HIF8_DOT2_LAUNCH(kActF16Dyn, false, kRep); break;
+    default: HIF8_DOT2_LAUNCH(kActBf16Dyn, false, kRep); break;
+  }
+#undef HIF8_DOT2_LAUNCH
+}
+
+template <int kR>
+void dispatch_m(const LinearArgs &a, const GemvPlan &p) {
+  const dim3 grid(p.grid);
+  if (p.rep) {
+    switch (a.m) {
+      case 1: dispatch_src<1, kR, true>(a, grid); break;
+      case 2: dispatch_src<2, kR, true>(a, grid); break;
+      case 3: dispatch_src<3, kR, true>(a, grid); break;
+      default: dispatch_src<4, kR, true>(a, grid); break;
+    }
+    return;
+  }
+  switch (a.m) {
+    case 1: dispatch_src<1, kR, false>(a, grid); break;
+    case 2: dispatch_src<2, kR, false>(a, grid); break;
+    case 3: dispatch_src<3, kR, false>(a, grid); break;
+    default: dispatch_src<4, kR, false>(a, grid); break;
+  }
+}
+
+// Kernel selection knobs, read once: HIF8_GEMV_KERNEL=d forces the dot2 VALU
+// kernel for every M (default: the MFMA-4 kernel for code activations at
+// M = 4, and M = 3 over wide weights), =4 the MFMA-4 kernel for every M >= 2,
+// =m the experimental 16x16x32 MFMA kernel; HIF8_GEMV_ROWS=4|8|12|16
+// forces the rows per block (12: M = 1 or the MFMA-4 kernel);
+// HIF8_GEMV_LUT=r|c forces the replicated or the compact decode table.  Measured on
+// MI355X (gate_up 24576x4096, M=1): the dot2 kernel with 8 rows per block
+// 20.0 us; the 16x16x32 MFMA kernel 29.3 us (its 16-rows x 64-byte load
+// pattern alone reads ~12 % slower than 1 KiB-contiguous rows); a persistent
+// double-buffered variant 24 us (2 blocks/CU keep too few bytes in flight).
+struct GemvKnobs {
+  char kernel = 'v';
+  int rows = 0;
+  char lut = 0;  // 'r' replicated, 'c' compact, else by grid size
+  GemvKnobs() {
+    if (const char *v = getenv("HIF8_GEMV_KERNEL")) kernel = v[0];
+    if (const char *v = getenv("HIF8_GEMV_ROWS")) rows = atoi(v);
+    if (const char *v = getenv("HIF8_GEMV_LUT")) lut = v[0];
+  }
 };
 
 GemvPlan plan_gemv(int64_t m, int64_t n, int64_t k, int act_kind, bool vec) {
@@ -904,6 +976,10 @@ GemvPlan plan_gemv(int64_t m, int64_t n, int64_t k, int act_kind, bool vec) {
     p.rows = r >= 16 ? 16 : r == 12 && m == 1 ? 12 : r >= 8 ? 8 : 4;
   }
   p.grid = unsigned((n + p.rows - 1) / p.rows);
+  // The replicated table for grids of one round, except the single-row k
+  // loop (down 4096 x 12288 at M = 1: 11.07 vs 10.85 us on MI355X).
+  p.rep = knobs.lut == 'r' ||
+          (knobs.lut != 'c' && p.grid <= kRepMaxBlocks && !(m == 1 && p.kind == kGemvDot2 && !p.one_chunk));
   return p;
 }
 
@@ -913,13 +989,12 @@ int mfma4_passes(int64_t k) {
   return passes <= 3 ? int(passes) : 0;
 }
 
-template <int kM, int kR>
-void launch_mfma4(const LinearArgs &a, const GemvPlan &p) {
+template <int kM, int kR, bool kRep>
+void launch_mfma4_t(const LinearArgs &a, const GemvPlan &p) {
   const uint8_t *act = static_cast<const uint8_t *>(a.act);
-#define HIF8_MFMA4_LAUNCH(P)                                                                                \
-  gemv_mfma4_kernel<kM, kR, P><<<p.grid, kThreads, 0, a.stream>>>(act, a.act_scale, a.weight, a.channel_scale, \
-                                                                 a.bias, a.bias_dtype, a.out, a.out_dtype,   \
-                                                                 int(a.n), int(a.k))
+#define HIF8_MFMA4_LAUNCH(P)                                                                              \
+  gemv_mfma4_kernel<kM, kR, P, kRep><<<p.grid, kThreads, 0, a.stream>>>(                                \
+      act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.n), int(a.k))
   // Two register sets of more than eight rows exceed the register file.
   constexpr bool kTwoSets = kR <= 8;
   switch (mfma4_passes(a.k)) {
@@ -929,6 +1004,12 @@ void launch_mfma4(const LinearArgs &a, const GemvPlan &p) {
     default: HIF8_MFMA4_LAUNCH(0); break;
   }
 #undef HIF8_MFMA4_LAUNCH
+}
+
+template <int kM, int kR>
+void launch_mfma4(const LinearArgs &a, const GemvPlan &p) {
+  if (p.rep) launch_mfma4_t<kM, kR, true>(a, p);
+  else launch_mfma4_t<kM, kR, false>(a, p);
 }
 
 template <int kR>
@@ -973,10 +1054,11 @@ int launch_gemv(const LinearArgs &a) {
       }
       break;
     default:
-      if (p.rows >= 16) dispatch_m<16>(a);
-      else if (p.rows == 12) dispatch_src<1, 12>(a, dim3(p.grid));
-      else if (p.rows >= 8) dispatch_m<8>(a);
-      else dispatch_m<4>(a);
+      if (p.rows >= 16) dispatch_m<16>(a, p);
+      else if (p.rows == 12 && p.rep) dispatch_src<1, 12, true>(a, dim3(p.grid));
+      else if (p.rows == 12) dispatch_src<1, 12, false>(a, dim3(p.grid));
+      else if (p.rows >= 8) dispatch_m<8>(a, p);
+      else dispatch_m<4>(a, p);
       break;
   }
   return check_launch("soft_hif8 GEMV");
@@ -990,13 +1072,13 @@ int describe_gemv(int64_t m, int64_t n, int64_t k, int act_kind, char *name, siz
       case kGemvSimple: snprintf(name, name_len, "gemv_simple_kernel"); break;
       case kGemvMfma16: snprintf(name, name_len, "gemv_mfma_kernel<%lld, %d>", (long long)m, act_kind); break;
       case kGemvMfma4:
-        snprintf(name, name_len, "gemv_mfma4_kernel<%lld, %d, %d>", (long long)m, p.rows,
-                 p.rows > 8 && mfma4_passes(k) > 1 ? 0 : mfma4_passes(k));
+        snprintf(name, name_len, "gemv_mfma4_kernel<%lld, %d, %d, %s>", (long long)m, p.rows,
+                 p.rows > 8 && mfma4_passes(k) > 1 ? 0 : mfma4_passes(k), p.rep ? "true" : "false");
         break;
       default: {
         const bool dyn = act_kind == kActF16Dyn || act_kind == kActBf16Dyn;
-        snprintf(name, name_len, "gemv_kernel<%lld, %d, %d, %s>", (long long)m, p.rows, act_kind,
-                 p.one_chunk && !dyn ? "true" : "false");
+        snprintf(name, name_len, "gemv_kernel<%lld, %d, %d, %s, %s>", (long long)m, p.rows, act_kind,
+                 p.one_chunk && !dyn ? "true" : "false", p.rep ? "true" : "false");
       }
     }
   }
