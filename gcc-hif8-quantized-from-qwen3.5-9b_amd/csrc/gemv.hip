@@ -86,13 +86,15 @@ struct CompactLut {
   __device__ __forceinline__ uint16_t code(uint32_t c) const { return t[c]; }
 };
 
+// Entry `tid` of the decode table: bf16 bits of dec(tid).
+__device__ __forceinline__ uint32_t decode_entry(int tid) { return decode_bits(uint32_t(tid)) >> 16; }
+
 // The decode table of a block of 256 threads, in LDS at `tab` (kRep: RepLut,
-// else CompactLut).  Replicated, thread t writes row t as eight 16-byte stores
-// at column quads rotated by t, so the lanes of one store instruction cover
-// distinct banks.
+// else CompactLut); thread t passes e = decode_entry(t).  Replicated, thread t
+// writes row t as eight 16-byte stores at column quads rotated by t, so the
+// lanes of one store instruction cover distinct banks.
 template <bool kRep>
-__device__ __forceinline__ void fill_decode_table(uint8_t *tab, int tid) {
-  const uint32_t e = decode_bits(uint32_t(tid)) >> 16;
+__device__ __forceinline__ void fill_decode_table(uint8_t *tab, int tid, uint32_t e) {
   if constexpr (kRep) {
     const uint32_t v = e | (e << 16);
     u32x4 *row = reinterpret_cast<u32x4 *>(tab + 256u * uint32_t(tid));
@@ -327,8 +329,12 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
     enc_part[0] = src[tid];
     enc_part[1] = src[tid + kThreads];
   }
+  // The plain table's entry is computed before the chunk loads, the
+  // replicated table's after them (each order measured faster for its table).
+  uint32_t entry = kRep ? 0u : decode_entry(tid);
   if constexpr (kOneChunk) load(min(tid, chunks - 1));
-  fill_decode_table<kRep>(dec_tab, tid);
+  if constexpr (kRep) entry = decode_entry(tid);
+  fill_decode_table<kRep>(dec_tab, tid, entry);
   if constexpr (kFused) {
     u32x4 *dst = reinterpret_cast<u32x4 *>(enc_lut);
     dst[tid] = enc_part[0];
@@ -544,8 +550,10 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
       }
   };
   Pass cur;
+  uint32_t entry = kRep ? 0u : decode_entry(tid);  // order as in gemv_kernel
   load(cur, 0);
-  fill_decode_table<kRep>(dec_tab, tid);
+  if constexpr (kRep) entry = decode_entry(tid);
+  fill_decode_table<kRep>(dec_tab, tid, entry);
   __builtin_amdgcn_sched_barrier(0);
   lds_barrier();
 
