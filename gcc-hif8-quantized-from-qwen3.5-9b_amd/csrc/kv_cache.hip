@@ -251,8 +251,10 @@ __global__ __launch_bounds__(kWave * (kD / 64), 4) void paged_decode_attention_k
   static_assert(kD % 64 == 0 && kWd >= 1 && kWd <= 4, "64-dim slices");
 
   struct Smem {
-    uint16_t k_tab[kWd][256];      // query dtype(dec(c) * k_tab_scale), per wavefront
-    uint16_t v_tab[kWd][256];      // query dtype(dec(c) * v_tab_scale) or (mixed scales) bf16(dec(c))
+    // The decode tables first (Smem is the kernel's only LDS object): at fixed
+    // LDS addresses 0 and 512 a lookup address is one shift of the code byte.
+    uint16_t k_tab[256];           // query dtype(dec(c) * k_tab_scale)
+    uint16_t v_tab[256];           // query dtype(dec(c) * v_tab_scale) or (mixed scales) bf16(dec(c))
     float scl[kWd][64];            // K | V factors of the tile's tokens (0 = masked)
     f32x4_t sx[2][kWd][2][kWave];  // partial scores [tile parity][wavefront][16-token block][lane]
     uint8_t vtile[2][kWd][kSlice]; // double-buffered V slices
@@ -369,9 +371,11 @@ __global__ __launch_bounds__(kWave * (kD / 64), 4) void paged_decode_attention_k
     qf[0] = head_ok ? q[0] : u32x4{0, 0, 0, 0};
     qf[1] = head_ok ? q[1] : u32x4{0, 0, 0, 0};
   }
-  float decf[4];
+  // Each wavefront writes a quarter of the shared tables (entries 64 wv + lane;
+  // a D = 128 / D = 64 workgroup's wavefronts write two / four quarters each).
+  float decf[4 / kWd];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) decf[i] = __uint_as_float(kDeviceTables.decode_f32[lane + 64 * i]);
+  for (int i = 0; i < 4 / kWd; ++i) decf[i] = __uint_as_float(kDeviceTables.decode_f32[lane + 64 * (wv + kWd * i)]);
   // The scales the tables currently hold (NaN: not built yet).
   float k_tab_scale = __builtin_nanf(""), v_tab_scale = __builtin_nanf("");
 
@@ -393,8 +397,8 @@ __global__ __launch_bounds__(kWave * (kD / 64), 4) void paged_decode_attention_k
   for (int q = 0; q < 4; ++q) oacc[q] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   float m = -__builtin_inff(), l = 0.f;
   float *sc = smem.scl[wv];
-  const uint16_t *kl = smem.k_tab[wv];
-  const uint16_t *vl = smem.v_tab[wv];
+  const uint16_t *kl = smem.k_tab;
+  const uint16_t *vl = smem.v_tab;
 
   for (int it = 0; it < ntiles; ++it) {
     const int t0 = t_begin + it * kTile;
@@ -424,11 +428,6 @@ __global__ __launch_bounds__(kWave * (kD / 64), 4) void paged_decode_attention_k
     const bool k_uniform = (same & 0xFFFFFFFFull) == 0xFFFFFFFFull;
     const bool v_uniform = (same >> 32) == 0xFFFFFFFFull;
     const float k_want = k_uniform ? k_one : 1.f, v_want = v_uniform ? v_one : 1.f;
-    if (!(k_want == k_tab_scale)) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) smem.k_tab[wv][lane + 64 * i] = float_to_half_bits<kQBf16>(decf[i] * k_want);
-      k_tab_scale = k_want;
-    }
     // V and P' go through the MFMA in the query dtype when the tile's V rows
     // share a scale (the reference rounds V and the softmax weights to
     // query.dtype, kv_cache.py:355-356 and :370-371); with mixed scales the
@@ -436,12 +435,24 @@ __global__ __launch_bounds__(kWave * (kD / 64), 4) void paged_decode_attention_k
     // (fp16 would lose P' * scale below 2^-14 to subnormals).  The sentinel
     // -1 marks the exact bf16 table of an fp16-query kernel.
     const float v_key = kQBf16 || v_uniform ? v_want : -1.f;
-    if (!(v_key == v_tab_scale)) {
+    // The tables are shared by the workgroup's wavefronts, which all see the
+    // same tile scales: a rebuild (once per workgroup for a cache with static
+    // per-head scales) waits until every wavefront is done with the old
+    // tables, and the lookups wait until every quarter is written.
+    const bool k_new = !(k_want == k_tab_scale), v_new = !(v_key == v_tab_scale);
+    if (k_new || v_new) {
+      if (it > 0) lds_barrier();
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        smem.v_tab[wv][lane + 64 * i] =
-            v_uniform ? float_to_half_bits<kQBf16>(decf[i] * v_want) : float_to_bf16_bits(decf[i] * v_want);
+      for (int i = 0; i < 4 / kWd; ++i) {
+        const int e = lane + 64 * (wv + kWd * i);
+        if (k_new) smem.k_tab[e] = float_to_half_bits<kQBf16>(decf[i] * k_want);
+        if (v_new)
+          smem.v_tab[e] =
+              v_uniform ? float_to_half_bits<kQBf16>(decf[i] * v_want) : float_to_bf16_bits(decf[i] * v_want);
+      }
+      k_tab_scale = k_want;
       v_tab_scale = v_key;
+      lds_barrier();
     }
     sc[lane] = valid ? ((lane < 32 ? k_uniform : v_uniform) ? 1.f : s_cur) : 0.f;
     if (!__all(valid)) {
