@@ -22,8 +22,13 @@ reference, where they are not part of the W8A8 set
 (docs/checkpoint-format.md:23-37).
 
 Static scales come from a calibration prefill of the same model (activation
-absmax / 32768 per Linear input, per KV head for K and V), the scheme the
-reference's calibrator produces offline.
+absmax / ``act_scale_div`` per Linear input, per KV head for K and V), as the
+reference's calibrator produces them offline.  The default convention maps
+every amax to 32768, HiF8's largest power of two (weights too); the
+reference's own maps a weight row's amax to 1.0 (codec.py:212-224) and
+calibrates activation scales near amax / 12 (its calibration JSON: the
+searched max_abs / scale targets are 0.5 ... 64), ``weight_scale_div=1`` and
+``act_scale_div=12`` here.
 """
 
 from __future__ import annotations
@@ -57,6 +62,8 @@ class HybridConfig:
     vocab: int = 151_936
     rms_eps: float = 1e-6
     block_size: int = 128
+    weight_scale_div: float = HIF8_MAX  # weight row scale = row amax / this
+    act_scale_div: float = HIF8_MAX     # Linear input / KV head scale = calibrated amax / this
 
     def is_full_attention(self, layer: int) -> bool:
         return layer % self.full_attention_interval == self.full_attention_interval - 1
@@ -149,13 +156,14 @@ class StaticLinear:
     During calibration each call sets the input scale from the running
     activation absmax before applying the scheme."""
 
-    def __init__(self, n: int, k: int, device, generator: torch.Generator, std: float = 0.02):
+    def __init__(self, n: int, k: int, device, generator: torch.Generator, std: float = 0.02,
+                 weight_div: float = HIF8_MAX, act_div: float = HIF8_MAX):
         codes = torch.empty(n, k, dtype=torch.uint8, device=device)
         scales = torch.empty(n, dtype=torch.float32, device=device)
         step = max(1, (64 << 20) // (k * 2))
         for r in range(0, n, step):
             w = (torch.randn(min(step, n - r), k, generator=generator, device=device) * std).to(torch.bfloat16)
-            s = (w.float().abs().amax(dim=1) / HIF8_MAX).clamp_min(1e-30)
+            s = (w.float().abs().amax(dim=1) / weight_div).clamp_min(1e-30)
             c, _ = native.static_quant(w, s)
             codes[r:r + w.shape[0]] = c
             scales[r:r + w.shape[0]] = s
@@ -167,12 +175,13 @@ class StaticLinear:
         self.method = scheme.W8A8HiFloat8StaticLinearMethod()
         self.method.process_weights_after_loading(self.layer)
         self.amax = torch.zeros((), dtype=torch.float32, device=device)
+        self.act_div = act_div
         self.calibrating = False
 
     def __call__(self, x: torch.Tensor) -> torch.Tensor:
         if self.calibrating:
             self.amax = torch.maximum(self.amax, x.float().abs().amax())
-            self.layer.input_scale.data.copy_((self.amax / HIF8_MAX).clamp_min(1e-30).reshape(1))
+            self.layer.input_scale.data.copy_((self.amax / self.act_div).clamp_min(1e-30).reshape(1))
         return self.method.apply(self.layer, x)
 
     def from_codes(self, codes: torch.Tensor, row_scale: torch.Tensor) -> torch.Tensor:
@@ -211,8 +220,9 @@ class HybridModel:
         self.device = torch.device(device)
         g = torch.Generator(device=self.device).manual_seed(seed)
         c = cfg
+        div = {"weight_div": c.weight_scale_div, "act_div": c.act_scale_div}
         # SOFT embedding: HiF8 rows + per-row scales.
-        emb = StaticLinear(c.vocab, c.hidden, device, g)
+        emb = StaticLinear(c.vocab, c.hidden, device, g, **div)
         self.embed = torch.nn.Module()
         self.embed.weight = emb.layer.weight
         self.embed.weight_scale = emb.layer.weight_scale
@@ -223,11 +233,11 @@ class HybridModel:
         for i in range(c.layers):
             L = {"input_norm": torch.ones(c.hidden, dtype=torch.bfloat16, device=device),
                  "post_norm": torch.ones(c.hidden, dtype=torch.bfloat16, device=device),
-                 "gate_up": StaticLinear(2 * c.intermediate, c.hidden, device, g),
-                 "down": StaticLinear(c.hidden, c.intermediate, device, g)}
+                 "gate_up": StaticLinear(2 * c.intermediate, c.hidden, device, g, **div),
+                 "down": StaticLinear(c.hidden, c.intermediate, device, g, **div)}
             if c.is_full_attention(i):
-                L["qkv"] = StaticLinear((c.heads + 2 * c.kv_heads) * c.head_dim, c.hidden, device, g)
-                L["o"] = StaticLinear(c.hidden, c.heads * c.head_dim, device, g)
+                L["qkv"] = StaticLinear((c.heads + 2 * c.kv_heads) * c.head_dim, c.hidden, device, g, **div)
+                L["o"] = StaticLinear(c.hidden, c.heads * c.head_dim, device, g, **div)
                 L["q_norm"] = torch.ones(c.head_dim, dtype=torch.bfloat16, device=device)
                 L["k_norm"] = torch.ones(c.head_dim, dtype=torch.bfloat16, device=device)
                 L["k_scale"] = torch.ones(c.kv_heads, dtype=torch.float32, device=device)
@@ -235,7 +245,7 @@ class HybridModel:
                 L["k_amax"] = torch.zeros(c.kv_heads, dtype=torch.float32, device=device)
                 L["v_amax"] = torch.zeros(c.kv_heads, dtype=torch.float32, device=device)
             else:
-                L["qkvz"] = StaticLinear(2 * c.lin_qk_width + 2 * c.lin_v_width, c.hidden, device, g)
+                L["qkvz"] = StaticLinear(2 * c.lin_qk_width + 2 * c.lin_v_width, c.hidden, device, g, **div)
                 L["ba"] = (torch.randn(2 * c.lin_v_heads, c.hidden, generator=g, device=device) * 0.02).to(
                     torch.bfloat16)
                 L["conv"] = (torch.randn(2 * c.lin_qk_width + c.lin_v_width, c.conv_kernel, generator=g,
@@ -243,7 +253,7 @@ class HybridModel:
                 L["A_log"] = torch.log(torch.empty(c.lin_v_heads, device=device).uniform_(1, 16, generator=g))
                 L["dt_bias"] = torch.ones(c.lin_v_heads, device=device)
                 L["out_norm"] = torch.ones(c.lin_v_dim, dtype=torch.bfloat16, device=device)
-                L["out"] = StaticLinear(c.hidden, c.lin_v_width, device, g)
+                L["out"] = StaticLinear(c.hidden, c.lin_v_width, device, g, **div)
             self.layers.append(L)
         self.final_norm = torch.ones(c.hidden, dtype=torch.bfloat16, device=device)
         self.lm_head = (torch.randn(c.vocab, c.hidden, generator=g, device=device) * 0.02).to(torch.bfloat16)
@@ -327,8 +337,8 @@ class HybridModel:
         if self.calibrating:
             L["k_amax"] = torch.maximum(L["k_amax"], k.float().abs().amax(dim=(0, 1, 3)))
             L["v_amax"] = torch.maximum(L["v_amax"], v.float().abs().amax(dim=(0, 1, 3)))
-            L["k_scale"] = (L["k_amax"] / HIF8_MAX).clamp_min(1e-30)
-            L["v_scale"] = (L["v_amax"] / HIF8_MAX).clamp_min(1e-30)
+            L["k_scale"] = (L["k_amax"] / c.act_scale_div).clamp_min(1e-30)
+            L["v_scale"] = (L["v_amax"] / c.act_scale_div).clamp_min(1e-30)
         kc, vc = st.key_caches[idx], st.value_caches[idx]
         kv_cache.write_kv_cache(k.reshape(b * t, c.kv_heads, c.head_dim).contiguous(),
                                 v.reshape(b * t, c.kv_heads, c.head_dim).contiguous(), kc, vc,
