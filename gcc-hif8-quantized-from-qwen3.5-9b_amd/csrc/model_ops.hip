@@ -238,6 +238,17 @@ __global__ __launch_bounds__(256) void silu_mul_quant_kernel(const uint16_t *__r
 // chunks t, t + 256, ... of each; k % 8 == 0, 16-byte aligned rows.
 // kSmallRows output rows per block: 4, or 1 for M >= 3 (more blocks for the
 // few outputs: 64 x 4096 at M = 4 took 7.1 us with 4 rows per block).
+// acc + the products of eight bf16 pairs (one 16-byte chunk of x and of a
+// weight row), in the order every bf16 GEMV here sums them.
+__device__ __forceinline__ float bf16_dot8(float acc, const uint4 xv, const uint4 wv) {
+  const uint32_t xw[4] = {xv.x, xv.y, xv.z, xv.w}, ww[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    acc += __uint_as_float(xw[e] << 16) * __uint_as_float(ww[e] << 16) +
+           __uint_as_float(xw[e] & 0xFFFF0000u) * __uint_as_float(ww[e] & 0xFFFF0000u);
+  return acc;
+}
+
 template <int kM, int kSmallRows>
 __global__ __launch_bounds__(kNormThreads) void bf16_gemv_kernel(const uint16_t *__restrict__ x,
                                                                  const uint16_t *__restrict__ w,
@@ -257,17 +268,9 @@ __global__ __launch_bounds__(kNormThreads) void bf16_gemv_kernel(const uint16_t 
     for (int r = 0; r < kSmallRows; ++r)
       wv[r] = reinterpret_cast<const uint4 *>(w + size_t(min(n0 + r, n - 1)) * k)[c];
 #pragma unroll
-    for (int r = 0; r < kSmallRows; ++r) {
-      const uint32_t ww[4] = {wv[r].x, wv[r].y, wv[r].z, wv[r].w};
+    for (int r = 0; r < kSmallRows; ++r)
 #pragma unroll
-      for (int m = 0; m < kM; ++m) {
-        const uint32_t xw[4] = {xv[m].x, xv[m].y, xv[m].z, xv[m].w};
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-          acc[r][m] += __uint_as_float(xw[e] << 16) * __uint_as_float(ww[e] << 16) +
-                       __uint_as_float(xw[e] & 0xFFFF0000u) * __uint_as_float(ww[e] & 0xFFFF0000u);
-      }
-    }
+      for (int m = 0; m < kM; ++m) acc[r][m] = bf16_dot8(acc[r][m], xv[m], wv[r]);
   }
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
 #pragma unroll
@@ -417,6 +420,135 @@ __global__ __launch_bounds__(kGdnWideThreads) void gdn_delta_wide_kernel(
   if (lead && col_ok) {
     const float z = bf(mixed[size_t(b) * ld + 2 * qk_width + v_heads * dv + hv * dv + j]);
     out[(size_t(b) * v_heads + hv) * dv + j] = to_bf(o * r * bf(w_out[j]) * (z / (1.f + expf(-z))));
+  }
+}
+
+// One decode token of the linear-attention mixer for the value heads of KV
+// group (request b, key head hk), fused with the b/a projection and the conv:
+// the kRep = v_heads / k_heads value heads of the group share its q and k, so
+// the block owns every conv channel it reads (q and k of hk, v of its value
+// heads) and shifts that channel's state alone.  The b/a rows are summed as
+// hif8_bf16_gemv sums them (one 256-thread team per row, chunks t, t + 256,
+// ..., then the four wavefront totals in order), the conv as gdn_conv_kernel,
+// and each value head runs gdn_delta_wide_kernel's arithmetic in turn, so the
+// outputs and states equal hif8_bf16_gemv + hif8_gdn_decode_step bit for bit
+// in three launches fewer.  Requires kRep <= 2, dk % 8 == 0, dk <= 128,
+// dv <= 128, 2 dk + kRep dv <= 1024, hidden % 8 == 0.
+template <int kRep>
+__global__ __launch_bounds__(kGdnWideThreads) void gdn_token_kernel(
+    const uint16_t *__restrict__ mixed, int64_t ld, const uint16_t *__restrict__ x,
+    const uint16_t *__restrict__ w_ba, int hidden, const uint16_t *__restrict__ conv_w,
+    uint16_t *__restrict__ conv_state, int kw, const float *__restrict__ a_log, const float *__restrict__ dt_bias,
+    float *__restrict__ state, const uint16_t *__restrict__ w_out, uint16_t *__restrict__ out, int k_heads,
+    int v_heads, int dk, int dv, float eps) {
+  static_assert(kRep >= 1 && kRep <= 2, "one or two value heads per key head");
+  __shared__ float cbuf[(2 + kRep) * kGdnCols];  // conv outputs: q | k | v of each value head
+  __shared__ float qs[kGdnCols], ks[kGdnCols];
+  __shared__ float pa[kGdnParts][kGdnCols], pc[kGdnParts][kGdnCols];
+  __shared__ float red[kGdnWideThreads / kWave];
+  __shared__ float ba_red[2 * kRep][kNormThreads / kWave];
+  const int b = blockIdx.x / k_heads, hk = blockIdx.x - b * k_heads;
+  const int qk_width = k_heads * dk, channels = 2 * qk_width + v_heads * dv;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int j = tid % kGdnCols, part = tid / kGdnCols;
+  const int rows = dk / kGdnParts, r0 = part * rows;
+  const bool col_ok = j < dv;
+  // State rows of every value head first (the longest loads).
+  float sv[kRep][kGdnRows];
+#pragma unroll
+  for (int i = 0; i < kRep; ++i) {
+    const float *S = state + (size_t(b) * v_heads + kRep * hk + i) * dk * dv;
+#pragma unroll
+    for (int r = 0; r < kGdnRows; ++r) sv[i][r] = (r < rows && col_ok) ? S[size_t(r0 + r) * dv + j] : 0.f;
+  }
+  // b/a projection: team t sums row b (t even) or a (t odd) of value head t / 2.
+  {
+    const int team = tid / kNormThreads, tt = tid % kNormThreads;
+    if (team < 2 * kRep) {
+      const int hv = kRep * hk + team / 2;
+      const uint4 *wr = reinterpret_cast<const uint4 *>(w_ba + size_t(team % 2 ? v_heads + hv : hv) * hidden);
+      const uint4 *xr = reinterpret_cast<const uint4 *>(x + size_t(b) * hidden);
+      float acc = 0.f;
+      for (int c = tt; c < hidden / 8; c += kNormThreads) acc = bf16_dot8(acc, xr[c], wr[c]);
+      const float v = wave_sum(acc);
+      if (lane == 0) ba_red[team][tt / kWave] = v;
+    }
+  }
+  // Conv of the group's channels (thread t: q of hk, then k of hk, then v of
+  // the value heads), as gdn_conv_kernel.
+  const int nch = 2 * dk + kRep * dv;
+  if (tid < nch) {
+    const int c = tid < dk ? hk * dk + tid
+                           : tid < 2 * dk ? qk_width + hk * dk + (tid - dk) : 2 * qk_width + kRep * hk * dv + (tid - 2 * dk);
+    uint16_t *st = conv_state + (size_t(b) * channels + c) * (kw - 1);
+    const uint16_t xc = mixed[size_t(b) * ld + c];
+    float acc = 0.f;
+    for (int t = 0; t < kw - 1; ++t) acc += bf(st[t]) * bf(conv_w[size_t(c) * kw + t]);
+    acc += bf(xc) * bf(conv_w[size_t(c) * kw + kw - 1]);
+    for (int t = 0; t + 1 < kw - 1; ++t) st[t] = st[t + 1];
+    st[kw - 2] = xc;
+    cbuf[tid] = acc / (1.f + expf(-acc));
+  }
+  __syncthreads();
+  const bool lead = part == 0;
+  const float qi = lead && j < dk ? cbuf[j] : 0.f;
+  const float ki = lead && j < dk ? cbuf[dk + j] : 0.f;
+  // F.normalize: x / max(||x||, 1e-12); q also scaled by 1 / sqrt(dk).
+  const float qn = fmaxf(sqrtf(block_sum<kGdnWideThreads>(qi * qi, red)), 1e-12f);
+  const float kn = fmaxf(sqrtf(block_sum<kGdnWideThreads>(ki * ki, red)), 1e-12f);
+  const float qv = qi / qn / sqrtf(float(dk)), kv = ki / kn;
+  if (lead) {
+    qs[j] = qv;
+    ks[j] = kv;
+  }
+  const float kq = block_sum<kGdnWideThreads>(kv * qv, red);  // also orders the qs / ks stores
+#pragma unroll
+  for (int i = 0; i < kRep; ++i) {
+    const int hv = kRep * hk + i;
+    float bsum = 0.f, asum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kNormThreads / kWave; ++w) {
+      bsum += ba_red[2 * i][w];
+      asum += ba_red[2 * i + 1][w];
+    }
+    const float braw = bf(to_bf(bsum));
+    const float araw = bf(to_bf(asum)) + dt_bias[hv];
+    const float vj = col_ok ? cbuf[2 * dk + i * dv + j] : 0.f;
+    const float beta = 1.f / (1.f + expf(-braw));
+    const float softplus = araw > 20.f ? araw : log1pf(expf(araw));
+    const float decay = expf(-expf(a_log[hv]) * softplus);
+    float a = 0.f, c = 0.f;
+#pragma unroll
+    for (int r = 0; r < kGdnRows; ++r) {
+      if (r < rows) {
+        a += sv[i][r] * ks[r0 + r];
+        c += sv[i][r] * qs[r0 + r];
+      }
+    }
+    pa[part][j] = a;
+    pc[part][j] = c;
+    __syncthreads();
+    a = 0.f;
+    c = 0.f;
+#pragma unroll
+    for (int p = 0; p < kGdnParts; ++p) {
+      a += pa[p][j];
+      c += pc[p][j];
+    }
+    const float delta = beta * (vj - decay * a);
+    const float o = decay * c + delta * kq;
+    if (col_ok) {
+      float *S = state + (size_t(b) * v_heads + hv) * dk * dv;
+#pragma unroll
+      for (int r = 0; r < kGdnRows; ++r)
+        if (r < rows) S[size_t(r0 + r) * dv + j] = decay * sv[i][r] + ks[r0 + r] * delta;
+    }
+    // The norm's first barrier also retires this head's pa / pc reads.
+    const float rn = rsqrtf(block_sum<kGdnWideThreads>(lead && col_ok ? o * o : 0.f, red) / float(dv) + eps);
+    if (lead && col_ok) {
+      const float z = bf(mixed[size_t(b) * ld + 2 * qk_width + v_heads * dv + hv * dv + j]);
+      out[(size_t(b) * v_heads + hv) * dv + j] = to_bf(o * rn * bf(w_out[j]) * (z / (1.f + expf(-z))));
+    }
   }
 }
 
@@ -578,6 +710,40 @@ extern "C" int hif8_bf16_gemv(const uint16_t *x, const uint16_t *weight, uint16_
     default: bf16_gemv_kernel<4, 1><<<grid1, kNormThreads, 0, s>>>(x, weight, out, int(n), int(k)); break;
   }
   return check_launch("hif8_bf16_gemv");
+}
+
+extern "C" int hif8_gdn_decode_token(const uint16_t *mixed_qkvz, int64_t ld, const uint16_t *x,
+                                     const uint16_t *ba_weight, int64_t hidden, const uint16_t *conv_weight,
+                                     uint16_t *conv_state, const float *a_log, const float *dt_bias,
+                                     float *rec_state, const uint16_t *out_norm, uint16_t *out, int64_t batch,
+                                     int64_t k_heads, int64_t v_heads, int64_t k_dim, int64_t v_dim,
+                                     int64_t conv_width, float eps, hif8_stream_t stream) {
+  clear_error();
+  if (!mixed_qkvz || !x || !ba_weight || !conv_weight || !conv_state || !a_log || !dt_bias || !rec_state ||
+      !out_norm || !out)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gdn_decode_token: null pointer argument");
+  if (batch <= 0 || k_heads <= 0 || v_heads <= 0 || v_heads % k_heads || k_dim <= 0 || v_dim <= 0 ||
+      hidden <= 0 || hidden > 0x7FFFFFFFll || conv_width < 2 || conv_width > 16 || batch * k_heads > 0x7FFFFFFFll)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gdn_decode_token: unsupported dimensions");
+  const int64_t channels = 2 * k_heads * k_dim + v_heads * v_dim;
+  if (ld < channels + v_heads * v_dim)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gdn_decode_token: mixed_qkvz row too short");
+  const int64_t rep = v_heads / k_heads;
+  if (rep > 2 || k_dim % kGdnParts || k_dim > kGdnParts * kGdnRows || v_dim > kGdnCols ||
+      2 * k_dim + rep * v_dim > kGdnWideThreads || hidden % 8 || !aligned(x, 16) || !aligned(ba_weight, 16))
+    return fail(HIF8_ERR_UNSUPPORTED, "hif8_gdn_decode_token: needs v_heads / k_heads <= 2, k_dim %% 8 == 0, "
+                                      "k_dim, v_dim <= 128, hidden %% 8 == 0 and 16-byte aligned x / ba_weight");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(unsigned(batch * k_heads));
+#define HIF8_GDN_TOKEN(R)                                                                                     \
+  gdn_token_kernel<R><<<grid, kGdnWideThreads, 0, s>>>(mixed_qkvz, ld, x, ba_weight, int(hidden), conv_weight, \
+                                                       conv_state, int(conv_width), a_log, dt_bias, rec_state,   \
+                                                       out_norm, out, int(k_heads), int(v_heads), int(k_dim),    \
+                                                       int(v_dim), eps)
+  if (rep == 2) HIF8_GDN_TOKEN(2);
+  else HIF8_GDN_TOKEN(1);
+#undef HIF8_GDN_TOKEN
+  return check_launch("hif8_gdn_decode_token");
 }
 
 extern "C" int hif8_gdn_decode_step(const uint16_t *mixed_qkvz, int64_t ld, const uint16_t *ba,

@@ -749,6 +749,56 @@ at::Tensor Hif8GdnDecodeStep(const at::Tensor &mixed, const at::Tensor &ba, cons
   return out;
 }
 
+// hif8_gdn_decode_step with the b/a projection of x folded in; shapes the
+// fused kernel does not take run hif8_bf16_gemv + hif8_gdn_decode_step.
+at::Tensor Hif8GdnDecodeToken(const at::Tensor &mixed, const at::Tensor &x, const at::Tensor &ba_weight,
+                              const at::Tensor &conv_weight, at::Tensor &conv_state, const at::Tensor &a_log,
+                              const at::Tensor &dt_bias, at::Tensor &rec_state, const at::Tensor &out_norm,
+                              int64_t k_heads, int64_t v_heads, int64_t k_dim, int64_t v_dim, double eps) {
+  CheckContiguousDevice(x, "x");
+  CheckContiguousDevice(ba_weight, "ba_weight");
+  TORCH_CHECK(x.scalar_type() == at::kBFloat16 && ba_weight.scalar_type() == at::kBFloat16,
+              "hif8_gdn_decode_token takes bfloat16 x and ba_weight");
+  TORCH_CHECK(x.dim() == 2 && ba_weight.dim() == 2 && x.size(0) == mixed.size(0) && x.size(1) == ba_weight.size(1) &&
+                  ba_weight.size(0) == 2 * v_heads,
+              "hif8_gdn_decode_token needs x [batch, hidden] and ba_weight [2 v_heads, hidden]");
+  for (auto *t : {&mixed, &conv_weight, &a_log, &dt_bias, &out_norm}) CheckContiguousDevice(*t, "operand");
+  CheckContiguousDevice(conv_state, "conv_state");
+  CheckContiguousDevice(rec_state, "rec_state");
+  TORCH_CHECK(mixed.dim() == 2 && conv_weight.dim() == 2 && conv_state.dim() == 3 && rec_state.dim() == 4,
+              "hif8_gdn_decode_token: operand ranks");
+  const int64_t batch = mixed.size(0);
+  const int64_t channels = 2 * k_heads * k_dim + v_heads * v_dim;
+  TORCH_CHECK(mixed.scalar_type() == at::kBFloat16 && conv_weight.scalar_type() == at::kBFloat16 &&
+                  conv_state.scalar_type() == at::kBFloat16 && out_norm.scalar_type() == at::kBFloat16,
+              "hif8_gdn_decode_token: bf16 operands expected");
+  TORCH_CHECK(a_log.scalar_type() == at::kFloat && dt_bias.scalar_type() == at::kFloat &&
+                  rec_state.scalar_type() == at::kFloat, "hif8_gdn_decode_token: float32 a_log / dt_bias / state");
+  TORCH_CHECK(conv_weight.size(0) == channels && conv_state.size(0) == batch && conv_state.size(1) == channels &&
+                  conv_state.size(2) == conv_weight.size(1) - 1, "conv weight / state shapes");
+  TORCH_CHECK(rec_state.size(0) == batch && rec_state.size(1) == v_heads && rec_state.size(2) == k_dim &&
+                  rec_state.size(3) == v_dim, "rec_state must be [batch, v_heads, k_dim, v_dim]");
+  TORCH_CHECK(a_log.numel() == v_heads && dt_bias.numel() == v_heads && out_norm.numel() == v_dim,
+              "per-head parameters");
+  const c10::OptionalDeviceGuard guard(mixed.device());
+  auto out = at::empty({batch, v_heads * v_dim}, mixed.options());
+  const int st = hif8_gdn_decode_token(
+      reinterpret_cast<const uint16_t *>(mixed.data_ptr()), mixed.size(1),
+      reinterpret_cast<const uint16_t *>(x.data_ptr()), reinterpret_cast<const uint16_t *>(ba_weight.data_ptr()),
+      x.size(1), reinterpret_cast<const uint16_t *>(conv_weight.data_ptr()),
+      reinterpret_cast<uint16_t *>(conv_state.data_ptr()), a_log.data_ptr<float>(), dt_bias.data_ptr<float>(),
+      rec_state.data_ptr<float>(), reinterpret_cast<const uint16_t *>(out_norm.data_ptr()),
+      reinterpret_cast<uint16_t *>(out.data_ptr()), batch, k_heads, v_heads, k_dim, v_dim, conv_weight.size(1),
+      float(eps), CurrentStream(mixed.device()));
+  if (st != HIF8_ERR_UNSUPPORTED) {
+    CheckStatus(st, "hif8_gdn_decode_token");
+    return out;
+  }
+  const at::Tensor ba = Hif8Bf16Gemv(x, ba_weight);
+  return Hif8GdnDecodeStep(mixed, ba, conv_weight, conv_state, a_log, dt_bias, rec_state, out_norm, k_heads, v_heads,
+                           k_dim, v_dim, eps);
+}
+
 std::tuple<at::Tensor, at::Tensor, at::Tensor, at::Tensor> Hif8QkNormRope(
     const at::Tensor &qkv, const at::Tensor &q_norm, const at::Tensor &k_norm, const at::Tensor &pos,
     const at::Tensor &inv_freq, const at::Tensor &block_table, int64_t block_size, int64_t num_heads,
@@ -879,6 +929,13 @@ at::Tensor Hif8GdnDecodeStepMeta(const at::Tensor &mixed, const at::Tensor &, co
   return at::empty({mixed.size(0), v_heads * v_dim}, mixed.options());
 }
 
+at::Tensor Hif8GdnDecodeTokenMeta(const at::Tensor &mixed, const at::Tensor &, const at::Tensor &,
+                                  const at::Tensor &, at::Tensor &, const at::Tensor &, const at::Tensor &,
+                                  at::Tensor &, const at::Tensor &, int64_t, int64_t v_heads, int64_t, int64_t v_dim,
+                                  double) {
+  return at::empty({mixed.size(0), v_heads * v_dim}, mixed.options());
+}
+
 }  // namespace
 
 TORCH_LIBRARY(vllm_ascend_hif8, m) {
@@ -903,6 +960,7 @@ TORCH_LIBRARY(vllm_ascend_hif8, m) {
   m.def("soft_hif8_gemm_decoded_weight(Tensor activation, Tensor weight_bf16, Tensor token_scale, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
   m.def("hif8_decode_bf16(Tensor codes) -> Tensor");
   m.def("hif8_gdn_decode_step(Tensor mixed_qkvz, Tensor ba, Tensor conv_weight, Tensor(a!) conv_state, Tensor a_log, Tensor dt_bias, Tensor(b!) rec_state, Tensor out_norm, int k_heads, int v_heads, int k_dim, int v_dim, float eps) -> Tensor");
+  m.def("hif8_gdn_decode_token(Tensor mixed_qkvz, Tensor x, Tensor ba_weight, Tensor conv_weight, Tensor(a!) conv_state, Tensor a_log, Tensor dt_bias, Tensor(b!) rec_state, Tensor out_norm, int k_heads, int v_heads, int k_dim, int v_dim, float eps) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
@@ -924,6 +982,7 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
   m.impl("hif8_bf16_gemv", &Hif8Bf16Gemv);
   m.impl("hif8_qk_norm_rope", &Hif8QkNormRope);
   m.impl("hif8_gdn_decode_step", &Hif8GdnDecodeStep);
+  m.impl("hif8_gdn_decode_token", &Hif8GdnDecodeToken);
   m.impl("soft_hif8_gemm_decoded_weight", &SoftHif8GemmDecodedWeight);
   m.impl("hif8_decode_bf16", &Hif8DecodeBf16);
 }
@@ -949,6 +1008,7 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
   m.impl("hif8_bf16_gemv", &Hif8Bf16GemvMeta);
   m.impl("hif8_qk_norm_rope", &Hif8QkNormRopeMeta);
   m.impl("hif8_gdn_decode_step", &Hif8GdnDecodeStepMeta);
+  m.impl("hif8_gdn_decode_token", &Hif8GdnDecodeTokenMeta);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {

@@ -395,14 +395,14 @@ class HybridModel:
 
     def _linear_attention_decode(self, L, idx: int, st: RequestState, x: torch.Tensor, xq=None) -> torch.Tensor:
         """One decode token of the linear-attention mixer with the fused glue
-        kernel (conv + recurrence + gated norm in two launches); x [B, H];
-        xq: x already quantized for the qkvz projection."""
+        kernel (b/a projection + conv + recurrence + gated norm in one launch
+        where the head shapes allow it); x [B, H]; xq: x already quantized
+        for the qkvz projection."""
         c = self.cfg
         qkvz = L["qkvz"](x) if xq is None else L["qkvz"].from_codes(*xq)
-        ba = torch.ops.vllm_ascend_hif8.hif8_bf16_gemv(x, L["ba"])
-        o = torch.ops.vllm_ascend_hif8.hif8_gdn_decode_step(
-            qkvz, ba, L["conv"], st.conv_states[idx], L["A_log"], L["dt_bias"], st.rec_states[idx], L["out_norm"],
-            c.lin_k_heads, c.lin_v_heads, c.lin_k_dim, c.lin_v_dim, c.rms_eps)
+        o = torch.ops.vllm_ascend_hif8.hif8_gdn_decode_token(
+            qkvz, x, L["ba"], L["conv"], st.conv_states[idx], L["A_log"], L["dt_bias"], st.rec_states[idx],
+            L["out_norm"], c.lin_k_heads, c.lin_v_heads, c.lin_k_dim, c.lin_v_dim, c.rms_eps)
         return L["out"](o)
 
     def _fuse_input_quant(self) -> bool:

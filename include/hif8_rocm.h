@@ -417,6 +417,17 @@ int hif8_gdn_decode_step(const uint16_t *mixed_qkvz, int64_t ld, const uint16_t 
                          const float *dt_bias, float *rec_state, const uint16_t *out_norm, uint16_t *out,
                          float *conv_scratch, int64_t batch, int64_t k_heads, int64_t v_heads, int64_t k_dim,
                          int64_t v_dim, int64_t conv_width, float eps, hif8_stream_t stream);
+/* hif8_gdn_decode_step with the b/a projection folded in (glue, no reference
+ * counterpart): ba = hif8_bf16_gemv(x [batch, hidden], ba_weight [2 v_heads,
+ * hidden]) computed inside, one launch instead of three, outputs and states
+ * equal to the two calls bit for bit.  Needs v_heads / k_heads <= 2,
+ * k_dim % 8 == 0, k_dim, v_dim <= 128, hidden % 8 == 0 and 16-byte aligned x
+ * and ba_weight, else HIF8_ERR_UNSUPPORTED (run the two calls). */
+int hif8_gdn_decode_token(const uint16_t *mixed_qkvz, int64_t ld, const uint16_t *x, const uint16_t *ba_weight,
+                          int64_t hidden, const uint16_t *conv_weight, uint16_t *conv_state, const float *a_log,
+                          const float *dt_bias, float *rec_state, const uint16_t *out_norm, uint16_t *out,
+                          int64_t batch, int64_t k_heads, int64_t v_heads, int64_t k_dim, int64_t v_dim,
+                          int64_t conv_width, float eps, hif8_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -209,6 +209,42 @@ def test_fused_add_rms_norm_silu_mul_and_bf16_gemv_match_torch(native_ops, devic
     torch.testing.assert_close(act.float(), ref.float(), rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("shape", [
+    # batch, k_heads, v_heads, k_dim, v_dim, hidden, conv width
+    (1, 16, 32, 128, 128, 4096, 4),  # the full-size model
+    (4, 16, 32, 128, 128, 4096, 4),
+    (3, 2, 4, 32, 32, 256, 4),       # the tiny model
+    (2, 3, 3, 64, 96, 520, 3),       # one value head per key head
+    (2, 2, 6, 32, 32, 256, 4),       # three per key head: the two-launch fallback
+])
+def test_fused_decode_token_equals_bf16_gemv_plus_decode_step(shape, native_ops, device):
+    """hif8_gdn_decode_token folds the b/a projection and the conv into the
+    delta-rule kernel; its outputs and both states equal hif8_bf16_gemv +
+    hif8_gdn_decode_step bit for bit, step after step."""
+    b, kh, vh, dk, dv, hidden, kw = shape
+    ops = torch.ops.vllm_ascend_hif8
+    g = torch.Generator(device=device).manual_seed(sum(shape))
+    channels = 2 * kh * dk + vh * dv
+    bf = torch.bfloat16
+    ba_w = (torch.randn(2 * vh, hidden, generator=g, device=device) * 0.05).to(bf)
+    conv_w = (torch.randn(channels, kw, generator=g, device=device) * 0.5).to(bf)
+    a_log = torch.randn(vh, generator=g, device=device) * 0.5
+    dt_bias = torch.randn(vh, generator=g, device=device) * 0.5
+    out_norm = (torch.rand(dv, generator=g, device=device) + 0.5).to(bf)
+    conv_a = torch.randn(b, channels, kw - 1, generator=g, device=device).to(bf)
+    rec_a = torch.randn(b, vh, dk, dv, generator=g, device=device) * 0.1
+    conv_b, rec_b = conv_a.clone(), rec_a.clone()
+    for step in range(3):
+        mixed = torch.randn(b, channels + vh * dv, generator=g, device=device).to(bf)
+        x = torch.randn(b, hidden, generator=g, device=device).to(bf)
+        got = ops.hif8_gdn_decode_token(mixed, x, ba_w, conv_w, conv_a, a_log, dt_bias, rec_a, out_norm,
+                                        kh, vh, dk, dv, 1e-6)
+        want = ops.hif8_gdn_decode_step(mixed, ops.hif8_bf16_gemv(x, ba_w), conv_w, conv_b, a_log, dt_bias, rec_b,
+                                        out_norm, kh, vh, dk, dv, 1e-6)
+        assert torch.equal(got, want), (shape, step)
+        assert torch.equal(conv_a, conv_b) and torch.equal(rec_a, rec_b), (shape, step)
+
+
 @pytest.fixture(scope="module")
 def odd_model(native_ops, device):
     """Linear-attention head sizes the wide delta-rule kernel does not take

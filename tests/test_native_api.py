@@ -111,6 +111,12 @@ def test_decode_glue_meta_shapes():
         torch.empty(4, **meta), torch.empty(4, **meta), torch.empty(2, 4, 32, 48, **meta),
         torch.empty(48, dtype=torch.bfloat16, **meta), 2, 4, 32, 48, 1e-6)
     assert out.shape == (2, 4 * 48) and out.dtype == torch.bfloat16
+    out = ops.hif8_gdn_decode_token(
+        torch.empty(2, 320, dtype=torch.bfloat16, **meta), torch.empty(2, 64, dtype=torch.bfloat16, **meta),
+        torch.empty(8, 64, dtype=torch.bfloat16, **meta), torch.empty(320, 4, dtype=torch.bfloat16, **meta),
+        torch.empty(2, 320, 3, dtype=torch.bfloat16, **meta), torch.empty(4, **meta), torch.empty(4, **meta),
+        torch.empty(2, 4, 32, 48, **meta), torch.empty(48, dtype=torch.bfloat16, **meta), 2, 4, 32, 48, 1e-6)
+    assert out.shape == (2, 4 * 48) and out.dtype == torch.bfloat16
 
 
 def test_embedding_method_validates_weights_without_a_gpu(monkeypatch):
