@@ -267,7 +267,7 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
     const void *act, const float *__restrict__ act_scale,
     const uint8_t *weight, const float *__restrict__ cs,
     const void *__restrict__ bias, int bias_dtype, void *__restrict__ out, int out_dtype,
-    int n, int k) {
+    int n, int k, const GemvPair pair) {
   constexpr int kV = kR * kM;
   constexpr int kVp = pow2_ceil(kV);  // partial sums per lane, zero-padded
   constexpr int kWaves = kThreads / kWave;
@@ -284,6 +284,15 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
   const auto dec_lut = decode_lut<kRep>(dec_tab, tid & 63);
   const int n0 = blockIdx.x * kR;
   const int chunks = k >> 4;
+  // Weight row of block row r: consecutive rows, or (pair.inter > 0) gate
+  // rows i0 + r and up rows inter + i0 + r - kR / 2.
+  const bool paired = pair.inter > 0;
+  constexpr int kHalf = kR / 2;
+  auto row_of = [&](int r) -> int {
+    if (!paired) return n0 + r;
+    const int i = blockIdx.x * kHalf + (r < kHalf ? r : r - kHalf);
+    return r < kHalf ? i : pair.inter + i;
+  };
 
   // Raw operands of one 16-byte column chunk: kR weight rows + kM activation rows.
   u32x4 wq[kR];
@@ -304,7 +313,7 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
 #pragma unroll
     for (int r = 0; r < kR; ++r) {
       // Rows past n re-read row n-1; their sums are never stored.
-      const int row = min(n0 + r, n - 1);
+      const int row = min(row_of(r), n - 1);
       // Weights are read once per call: non-temporal (streaming) loads.
       wq[r] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(weight + size_t(row) * k) + c);
     }
@@ -450,7 +459,7 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
   }
   if (v < kV) {
     const int r = v / kM, m = v % kM;
-    const int row = n0 + r;
+    const int row = paired ? min(row_of(r), n - 1) : n0 + r;
     if (row < n) {
       float ts = kFused ? row_s[0] : act_scale[m];
       if constexpr (kFused) {
@@ -460,8 +469,33 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
       }
       float y = s * ts * cs[row];
       if (bias) y += load_bias(bias, bias_dtype, row);
-      store_out(out, out_dtype, size_t(m) * n + row, y);
+      if (paired) red[0][v] = half_bits_to_float<true>(float_to_bf16_bits(y));  // the bf16 GEMV output
+      else store_out(out, out_dtype, size_t(m) * n + row, y);
     }
+  }
+  if (paired) {
+    // Every wave has read red above (the sums before the barrier); the
+    // gate / up pairs meet in red[0] after this one.
+    __syncthreads();
+    if (v < kHalf * kM) {
+      const int r = v / kM, m = v % kM;
+      const int i = blockIdx.x * kHalf + r;
+      if (i < pair.inter) {
+        const float g = red[0][v], u = red[0][v + kHalf * kM];
+        const float act = half_bits_to_float<true>(float_to_bf16_bits(g / (1.f + expf(-g)) * u));
+        const float qs = pair.qs[0];
+        const float q = act * __builtin_amdgcn_rcpf(qs);
+        uint32_t code;
+        if (__builtin_expect(near_index_boundary(q), 0)) {
+          const float x = act / qs;
+          code = __builtin_isnan(x) ? uint32_t(kNan) : kDeviceTables.static_encode[__float_as_uint(x) >> 19];
+        } else {
+          code = kDeviceTables.static_encode[__float_as_uint(q) >> 19];
+        }
+        pair.codes[size_t(m) * pair.inter + i] = uint8_t(code);
+      }
+    }
+    if (blockIdx.x == 0 && v < kM) pair.row_scale[v] = pair.qs[0];
   }
 }
 
@@ -882,7 +916,7 @@ void dispatch_src(const LinearArgs &a, dim3 grid) {
   const int n = int(a.n), k = int(a.k);
 #define HIF8_DOT2_LAUNCH(SRC, ONE, REP)                                                                    \
   gemv_kernel<kM, kR, SRC, ONE, REP><<<grid, kThreads, 0, a.stream>>>(                                   \
-      a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k)
+      a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k, a.pair)
   const bool one = k <= 16 * kThreads;
   switch (a.act_kind) {
     case kActCodes:
@@ -1035,6 +1069,9 @@ int launch_gemv(const LinearArgs &a) {
   if (a.m < 1 || a.m > 4) return fail(HIF8_ERR_UNSUPPORTED, "GEMV kernel handles 1 <= M <= 4, got %lld", (long long)a.m);
   const bool vec = a.k % 16 == 0 && aligned(a.weight, 16) && aligned(a.act, 16);
   const GemvPlan p = plan_gemv(a.m, a.n, a.k, a.act_kind, vec);
+  if (a.pair.inter > 0 && (p.kind != kGemvDot2 || a.n != 2 * int64_t(a.pair.inter) || a.bias))
+    return fail(HIF8_ERR_UNSUPPORTED, "gate_up + SiLU-mul GEMV: the plan for M=%lld N=%lld K=%lld is not the dot2 kernel",
+                (long long)a.m, (long long)a.n, (long long)a.k);
   switch (p.kind) {
     case kGemvSimple:
       gemv_simple_kernel<<<p.grid, kWave, 0, a.stream>>>(a.act, a.act_kind, a.act_scale, a.weight, a.channel_scale,

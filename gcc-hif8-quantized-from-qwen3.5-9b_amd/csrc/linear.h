@@ -13,6 +13,19 @@ enum ActKind : int {
   kActBf16Dyn = 4,  // bfloat16 x, likewise
 };
 
+// The gate_up projection of an MLP fused with SiLU-mul and the down
+// projection's static input quant (inter > 0): weight rows [0, inter) are the
+// gates, [inter, 2 inter) the ups; a GEMV block takes kR / 2 gate rows and the
+// matching up rows, and writes codes[m, i] = static HiF8 code of
+// bf16(silu(bf16 gate) * bf16 up) with the fixed scale qs[0] (the arithmetic of
+// hif8_silu_mul_quant over the bf16 GEMV output) and row_scale[m] = qs[0].
+struct GemvPair {
+  int inter = 0;
+  const float *qs = nullptr;
+  uint8_t *codes = nullptr;
+  float *row_scale = nullptr;
+};
+
 struct LinearArgs {
   const void *act;        // [m, k] codes or fp16/bf16 x
   int act_kind;           // ActKind
@@ -28,9 +41,11 @@ struct LinearArgs {
   void *workspace = nullptr;    // split-K partials (GEMM only), may be null
   size_t workspace_bytes = 0;
   const uint16_t *weight_bf16 = nullptr;  // [n, k] weight decoded beforehand (GEMM), else null
+  GemvPair pair;                          // GEMV only: gate_up + SiLU-mul + quant epilogue
 };
 
-// HBM-streaming GEMV for m <= 4 (gemv.hip).  Returns a status.
+// HBM-streaming GEMV for m <= 4 (gemv.hip).  Returns a status; with a.pair
+// set, HIF8_ERR_UNSUPPORTED where the plan is not the dot2 kernel.
 int launch_gemv(const LinearArgs &a);
 // The kernel launch_gemv picks for these sizes and activation kind (16-byte
 // aligned operands): its name as profilers print it, and its grid.

@@ -61,6 +61,26 @@ extern "C" int soft_hif8_gemv(const uint8_t *activation, const uint8_t *weight,
                                 out, out_dtype, m, n, k, stream));
 }
 
+extern "C" int hif8_gate_up_silu_mul_quant(const uint8_t *activation, const uint8_t *weight,
+                                           const float *token_scale, const float *channel_scale,
+                                           const float *input_scale, uint8_t *codes, float *row_scale, int64_t m,
+                                           int64_t inter, int64_t k, hif8_stream_t stream) {
+  clear_error();
+  int st = validate("hif8_gate_up_silu_mul_quant", activation, weight, token_scale, channel_scale, nullptr,
+                    HIF8_DTYPE_NONE, codes, HIF8_DTYPE_BF16, m, 2 * inter, k);
+  if (st) return st;
+  if (!input_scale || !row_scale) return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gate_up_silu_mul_quant: null pointer argument");
+  if (m > 4 || inter > 0x3FFFFFFFll)
+    return fail(HIF8_ERR_UNSUPPORTED, "hif8_gate_up_silu_mul_quant takes 1 <= M <= 4 and inter < 2^30");
+  LinearArgs a = codes_args(activation, weight, token_scale, channel_scale, nullptr, HIF8_DTYPE_NONE, nullptr,
+                            HIF8_DTYPE_BF16, m, 2 * inter, k, stream);
+  a.pair.inter = int(inter);
+  a.pair.qs = input_scale;
+  a.pair.codes = codes;
+  a.pair.row_scale = row_scale;
+  return launch_gemv(a);
+}
+
 extern "C" size_t soft_hif8_gemm_workspace_size(int64_t m, int64_t n, int64_t k) {
   return gemm_workspace_size(m, n, k);
 }

@@ -692,6 +692,36 @@ std::tuple<at::Tensor, at::Tensor> Hif8SiluMulQuant(const at::Tensor &gate_up, c
   return {codes, row_scale};
 }
 
+// The gate_up projection over activation codes fused with SiLU-mul and the
+// down projection's static input quant (no reference counterpart); where the
+// fused GEMV does not take the shape, soft_hif8_gemm + hif8_silu_mul_quant.
+std::tuple<at::Tensor, at::Tensor> Hif8GateUpSiluMulQuant(const at::Tensor &activation, const at::Tensor &weight,
+                                                          const at::Tensor &token_scale,
+                                                          const at::Tensor &channel_scale,
+                                                          const at::Tensor &input_scale) {
+  ValidateSoftLinear(activation, weight, token_scale, channel_scale, c10::nullopt, at::ScalarType::BFloat16, false);
+  TORCH_CHECK(weight.size(0) % 2 == 0, "hif8_gate_up_silu_mul_quant needs an even number of weight rows");
+  CheckContiguousDevice(input_scale, "input_scale");
+  TORCH_CHECK(input_scale.scalar_type() == at::kFloat && input_scale.numel() == 1,
+              "input_scale must be one float32 value");
+  const c10::OptionalDeviceGuard guard(activation.device());
+  const int64_t m = activation.size(0), inter = weight.size(0) / 2, k = activation.size(1);
+  auto codes = at::empty({m, inter}, activation.options());
+  auto row_scale = at::empty({m}, activation.options().dtype(at::kFloat));
+  const int st = hif8_gate_up_silu_mul_quant(activation.data_ptr<uint8_t>(), weight.data_ptr<uint8_t>(),
+                                             token_scale.data_ptr<float>(), channel_scale.data_ptr<float>(),
+                                             input_scale.data_ptr<float>(), codes.data_ptr<uint8_t>(),
+                                             row_scale.data_ptr<float>(), m, inter, k,
+                                             CurrentStream(activation.device()));
+  if (st != HIF8_ERR_UNSUPPORTED) {
+    CheckStatus(st, "hif8_gate_up_silu_mul_quant");
+    return {codes, row_scale};
+  }
+  return Hif8SiluMulQuant(SoftHif8Gemm(activation, weight, token_scale, channel_scale, c10::nullopt,
+                                       at::ScalarType::BFloat16),
+                          input_scale);
+}
+
 at::Tensor Hif8Bf16Gemv(const at::Tensor &x, const at::Tensor &weight) {
   CheckContiguousDevice(x, "x");
   CheckContiguousDevice(weight, "weight");
@@ -929,6 +959,13 @@ at::Tensor Hif8GdnDecodeStepMeta(const at::Tensor &mixed, const at::Tensor &, co
   return at::empty({mixed.size(0), v_heads * v_dim}, mixed.options());
 }
 
+std::tuple<at::Tensor, at::Tensor> Hif8GateUpSiluMulQuantMeta(const at::Tensor &activation, const at::Tensor &weight,
+                                                              const at::Tensor &, const at::Tensor &,
+                                                              const at::Tensor &) {
+  return {at::empty({activation.size(0), weight.size(0) / 2}, activation.options()),
+          at::empty({activation.size(0)}, activation.options().dtype(at::kFloat))};
+}
+
 at::Tensor Hif8GdnDecodeTokenMeta(const at::Tensor &mixed, const at::Tensor &, const at::Tensor &,
                                   const at::Tensor &, at::Tensor &, const at::Tensor &, const at::Tensor &,
                                   at::Tensor &, const at::Tensor &, int64_t, int64_t v_heads, int64_t, int64_t v_dim,
@@ -960,6 +997,7 @@ TORCH_LIBRARY(vllm_ascend_hif8, m) {
   m.def("soft_hif8_gemm_decoded_weight(Tensor activation, Tensor weight_bf16, Tensor token_scale, Tensor channel_scale, Tensor? bias, ScalarType output_dtype) -> Tensor");
   m.def("hif8_decode_bf16(Tensor codes) -> Tensor");
   m.def("hif8_gdn_decode_step(Tensor mixed_qkvz, Tensor ba, Tensor conv_weight, Tensor(a!) conv_state, Tensor a_log, Tensor dt_bias, Tensor(b!) rec_state, Tensor out_norm, int k_heads, int v_heads, int k_dim, int v_dim, float eps) -> Tensor");
+  m.def("hif8_gate_up_silu_mul_quant(Tensor activation, Tensor weight, Tensor token_scale, Tensor channel_scale, Tensor input_scale) -> (Tensor, Tensor)");
   m.def("hif8_gdn_decode_token(Tensor mixed_qkvz, Tensor x, Tensor ba_weight, Tensor conv_weight, Tensor(a!) conv_state, Tensor a_log, Tensor dt_bias, Tensor(b!) rec_state, Tensor out_norm, int k_heads, int v_heads, int k_dim, int v_dim, float eps) -> Tensor");
 }
 
@@ -983,6 +1021,7 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
   m.impl("hif8_qk_norm_rope", &Hif8QkNormRope);
   m.impl("hif8_gdn_decode_step", &Hif8GdnDecodeStep);
   m.impl("hif8_gdn_decode_token", &Hif8GdnDecodeToken);
+  m.impl("hif8_gate_up_silu_mul_quant", &Hif8GateUpSiluMulQuant);
   m.impl("soft_hif8_gemm_decoded_weight", &SoftHif8GemmDecodedWeight);
   m.impl("hif8_decode_bf16", &Hif8DecodeBf16);
 }
@@ -1009,6 +1048,7 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
   m.impl("hif8_qk_norm_rope", &Hif8QkNormRopeMeta);
   m.impl("hif8_gdn_decode_step", &Hif8GdnDecodeStepMeta);
   m.impl("hif8_gdn_decode_token", &Hif8GdnDecodeTokenMeta);
+  m.impl("hif8_gate_up_silu_mul_quant", &Hif8GateUpSiluMulQuantMeta);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {

@@ -195,6 +195,16 @@ class StaticLinear:
         return native.soft_linear(codes, self.layer.weight, row_scale, self.layer.weight_scale, None,
                                   output_dtype=torch.bfloat16)
 
+    def silu_mul_quant_from_codes(self, codes: torch.Tensor, row_scale: torch.Tensor,
+                                  next_input_scale: torch.Tensor):
+        """For a gate_up projection (gate rows, then up rows): the static
+        HiF8 codes and row scales of silu(gate) * up for the next projection,
+        from activation codes of at most four rows, in one GEMV launch where
+        the kernel plan allows it (the same codes as ``from_codes`` followed
+        by ``hif8_silu_mul_quant``)."""
+        return torch.ops.vllm_ascend_hif8.hif8_gate_up_silu_mul_quant(
+            codes, self.layer.weight, row_scale.reshape(-1), self.layer.weight_scale.reshape(-1), next_input_scale)
+
 
 @dataclass
 class RequestState:
@@ -444,8 +454,7 @@ class HybridModel:
             if fuse:
                 _, codes, rs = ops.hif8_add_rms_norm_quant(h, mix, L["post_norm"], c.rms_eps,
                                                            L["gate_up"].layer.input_scale)
-                gu = L["gate_up"].from_codes(codes, rs)
-                codes, rs = ops.hif8_silu_mul_quant(gu, L["down"].layer.input_scale)
+                codes, rs = L["gate_up"].silu_mul_quant_from_codes(codes, rs, L["down"].layer.input_scale)
                 pending = L["down"].from_codes(codes, rs)
             else:
                 x2 = ops.hif8_add_rms_norm(h, mix, L["post_norm"], c.rms_eps)

@@ -407,6 +407,16 @@ int hif8_add_rms_norm_quant(uint16_t *h, const uint16_t *delta, const uint16_t *
                             float eps, hif8_stream_t stream);
 int hif8_silu_mul_quant(const uint16_t *gate_up, const float *input_scale, uint8_t *codes, float *row_scale,
                         int64_t rows, int64_t n, hif8_stream_t stream);
+/* The gate_up projection and hif8_silu_mul_quant in one GEMV launch (glue, no
+ * reference counterpart): weight [2 inter, k] (gate rows, then up rows) and
+ * channel_scale [2 inter] as for soft_hif8_gemm over activation codes [m, k]
+ * with token_scale [m]; codes [m, inter] and row_scale [m] equal
+ * hif8_silu_mul_quant(soft_hif8_gemm(...) in bf16, input_scale) bit for bit.
+ * 1 <= m <= 4; HIF8_ERR_UNSUPPORTED where the GEMV plan for (m, 2 inter, k)
+ * is not the dot2 kernel (then run the two calls). */
+int hif8_gate_up_silu_mul_quant(const uint8_t *activation, const uint8_t *weight, const float *token_scale,
+                                const float *channel_scale, const float *input_scale, uint8_t *codes,
+                                float *row_scale, int64_t m, int64_t inter, int64_t k, hif8_stream_t stream);
 int hif8_qk_norm_rope(const uint16_t *qkv, const uint16_t *q_norm, const uint16_t *k_norm, const int64_t *pos,
                       const float *inv_freq, const int32_t *block_table, int64_t max_blocks, int64_t block_size,
                       uint16_t *q_out, uint16_t *k_out, uint16_t *v_out, int64_t *slots, int64_t batch,

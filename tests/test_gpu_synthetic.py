@@ -209,6 +209,34 @@ def test_fused_add_rms_norm_silu_mul_and_bf16_gemv_match_torch(native_ops, devic
     torch.testing.assert_close(act.float(), ref.float(), rtol=1e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("m,inter,k", [(1, 12288, 4096), (2, 12288, 4096), (4, 12288, 4096), (1, 37, 64),
+                                       (3, 500, 256), (1, 2048, 12288)])
+def test_fused_gate_up_silu_mul_quant_equals_gemv_then_silu_mul_quant(m, inter, k, native_ops, device):
+    """hif8_gate_up_silu_mul_quant: the gate_up GEMV whose blocks pair gate
+    and up rows and finish with SiLU-mul and the static quant gives the codes
+    of soft_hif8_gemm (bf16) + SiLU-mul + static quant bit for bit (where the
+    GEMV plan is not the dot2 kernel, e.g. M = 4 over wide weights, the op
+    runs soft_hif8_gemm + hif8_silu_mul_quant itself)."""
+    ops = torch.ops.vllm_ascend_hif8
+    g = torch.Generator(device=device).manual_seed(m * 7 + inter + k)
+    w = torch.randn(2 * inter, k, generator=g, device=device).to(torch.bfloat16)
+    from hif8_rocm import native
+    ws = (w.float().abs().amax(dim=1) / 32768.0).contiguous()
+    wq, _ = native.static_quant(w, ws)
+    x = torch.randn(m, k, generator=g, device=device).to(torch.bfloat16)
+    xs = (x.float().abs().amax() / 32768.0).reshape(1)
+    a, rs = native.static_quant(x, xs)
+    a[0, :3] = torch.tensor([0x80, 0x6F, 0xEF], dtype=torch.uint8, device=device)  # NaN, +Inf, -Inf codes
+    for sv in (1e-6, 0.01, 3.0):
+        s = torch.tensor([sv], device=device)
+        codes, out_rs = ops.hif8_gate_up_silu_mul_quant(a, wq, rs, ws, s)
+        gu = ops.soft_hif8_gemm(a, wq, rs, ws, None, torch.bfloat16)
+        # hif8_silu_mul_quant takes widths % 8 == 0 only; its codes equal these
+        want, want_rs = native.static_quant(ops.hif8_silu_mul(gu), s)
+        assert torch.equal(codes, want), (m, inter, k, sv)
+        assert torch.equal(out_rs, want_rs.reshape(-1))
+
+
 @pytest.mark.parametrize("shape", [
     # batch, k_heads, v_heads, k_dim, v_dim, hidden, conv width
     (1, 16, 32, 128, 128, 4096, 4),  # the full-size model

@@ -111,6 +111,10 @@ def test_decode_glue_meta_shapes():
         torch.empty(4, **meta), torch.empty(4, **meta), torch.empty(2, 4, 32, 48, **meta),
         torch.empty(48, dtype=torch.bfloat16, **meta), 2, 4, 32, 48, 1e-6)
     assert out.shape == (2, 4 * 48) and out.dtype == torch.bfloat16
+    c3, r3 = ops.hif8_gate_up_silu_mul_quant(torch.empty(3, 64, dtype=torch.uint8, **meta),
+                                             torch.empty(10, 64, dtype=torch.uint8, **meta), torch.empty(3, **meta),
+                                             torch.empty(10, **meta), torch.empty(1, **meta))
+    assert c3.shape == (3, 5) and c3.dtype == torch.uint8 and r3.shape == (3,)
     out = ops.hif8_gdn_decode_token(
         torch.empty(2, 320, dtype=torch.bfloat16, **meta), torch.empty(2, 64, dtype=torch.bfloat16, **meta),
         torch.empty(8, 64, dtype=torch.bfloat16, **meta), torch.empty(320, 4, dtype=torch.bfloat16, **meta),
