@@ -866,10 +866,10 @@ def e2e_decode(torch, device) -> dict:
                        "HiF8 SOFT, norms / conv / recurrence / LM head in bf16-fp32 torch; greedy, random ids",
            "prompt_tokens": E2E_PROMPT, "new_tokens": E2E_NEW, "build_and_calibrate_s": round(time.perf_counter() - t0, 2)}
     g = torch.Generator(device=device).manual_seed(9)
-    # b1_single_row_fusion: batch 1 again with HIF8_STATIC_FUSED_SINGLE_ROW=1
-    # and the glue-kernel input quant off, so every one-row projection (qkv /
-    # qkvz, gate_up, o / out, down) goes through the fused static-quant op,
-    # one launch for K <= 4096 and N < 16384 (same tokens).
+    # b1_single_row_fusion: batch 1 again with the glue-kernel input quant
+    # off, so every one-row projection (qkv / qkvz, gate_up, o / out, down)
+    # goes through the scheme's fused static-quant op (HIF8_STATIC_FUSED_SINGLE_ROW,
+    # the default), one launch for K <= 4096 and N < 16384 (same tokens).
     for b, key, single in ((1, "b1", False), (4, "b4", False), (1, "b1_single_row_fusion", True)):
         prompt = torch.randint(0, cfg.vocab, (b, E2E_PROMPT), generator=g, device=device)
         if single:
