@@ -863,7 +863,8 @@ def e2e_decode(torch, device) -> dict:
     res = {"workload": "BASELINE configs[4]: random-init Qwen3.5-9B-shaped hybrid (32 layers, hidden 4096, "
                        "full attention every 4th layer with HiF8 KV, gated-delta-rule layers, intermediate "
                        "12288, vocab 151936); every projection W8A8 HiF8 static through the scheme, embedding "
-                       "HiF8 SOFT, norms / conv / recurrence / LM head in bf16-fp32 torch; greedy, random ids",
+                       "HiF8 SOFT, norms / conv / recurrence in bf16-fp32 glue kernels, bf16 LM head (library bf16 GEMV up "
+                       "to 4 rows); greedy, random ids",
            "prompt_tokens": E2E_PROMPT, "new_tokens": E2E_NEW, "build_and_calibrate_s": round(time.perf_counter() - t0, 2)}
     g = torch.Generator(device=device).manual_seed(9)
     # b1_single_row_fusion: batch 1 again with the glue-kernel input quant

@@ -460,6 +460,15 @@ class HybridModel:
                 x2 = ops.hif8_add_rms_norm(h, mix, L["post_norm"], c.rms_eps)
                 pending = L["down"](ops.hif8_silu_mul(L["gate_up"](x2)))
         last = ops.hif8_add_rms_norm(h, pending, self.final_norm, c.rms_eps)
+        return self._lm_head(last)
+
+    def _lm_head(self, last: torch.Tensor) -> torch.Tensor:
+        """bf16 logits of the last positions [B, H] -> float32 [B, vocab]: up to
+        four rows through the library's bf16 GEMV (the 1.24 GB head streamed
+        at 6.2 TB/s, 202 us at B = 1 against 250 us for torch's GEMM on
+        MI355X), more through torch."""
+        if last.shape[0] <= 4:
+            return torch.ops.vllm_ascend_hif8.hif8_bf16_gemv(last.contiguous(), self.lm_head).float()
         return torch.nn.functional.linear(last, self.lm_head).float()
 
     def _mlp(self, L, h: torch.Tensor) -> torch.Tensor:
@@ -501,7 +510,7 @@ class HybridModel:
                 lin_i += 1
             h = h + self._mlp(L, rms_norm(h, L["post_norm"], c.rms_eps))
         last = rms_norm(h[:, -1], self.final_norm, c.rms_eps)
-        return torch.nn.functional.linear(last, self.lm_head).float()
+        return self._lm_head(last)
 
     def calibrate(self, batch: int = 1, tokens: int = 64, seed: int = 1) -> None:
         """Static scales from one prefill of random tokens: each Linear's input
