@@ -251,6 +251,31 @@ __device__ __forceinline__ void store_out(void *out, int dtype, size_t i, float 
       dtype == HIF8_DTYPE_BF16 ? float_to_bf16_bits(y) : float_to_f16_bits(y);
 }
 
+// The causal-conv epilogue (GemvConv) of output (m, c), y its fp32 value
+// before the bf16 store.  Loads take clamped tap indices so they issue
+// together; the taps past kw are read and ignored.
+__device__ __forceinline__ void conv_epilogue(const GemvConv &cv, int m, int c, float y) {
+  const uint32_t xb = float_to_bf16_bits(y);
+  uint16_t *st = cv.state + (size_t(m) * cv.channels + c) * (cv.kw - 1);
+  const uint16_t *w = cv.weight + size_t(c) * cv.kw;
+  uint32_t sv[3], wv[4];
+#pragma unroll
+  for (int t = 0; t < 3; ++t) sv[t] = st[min(t, cv.kw - 2)];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) wv[t] = w[min(t, cv.kw - 1)];
+  float acc = 0.f;
+#pragma unroll
+  for (int t = 0; t < 3; ++t)
+    if (t < cv.kw - 1) acc += half_bits_to_float<true>(sv[t]) * half_bits_to_float<true>(wv[t]);
+  const uint32_t wl = cv.kw == 2 ? wv[1] : cv.kw == 3 ? wv[2] : wv[3];
+  acc += half_bits_to_float<true>(xb) * half_bits_to_float<true>(wl);
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+    if (t + 1 < cv.kw - 1) st[t] = uint16_t(sv[t + 1]);
+  st[cv.kw - 2] = uint16_t(xb);
+  cv.out[size_t(m) * cv.channels + c] = acc / (1.f + expf(-acc));
+}
+
 // Waves per SIMD the register allocation must allow.  Tighter bounds than
 // these make the compiler spill (M = 2 at 5 waves, M = 4 at 4 waves).
 constexpr int gemv_min_waves(int m, int rows) { return rows > 8 ? 2 : m == 1 ? 6 : m == 2 ? 4 : 2; }
@@ -267,7 +292,7 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
     const void *act, const float *__restrict__ act_scale,
     const uint8_t *weight, const float *__restrict__ cs,
     const void *__restrict__ bias, int bias_dtype, void *__restrict__ out, int out_dtype,
-    int n, int k, const GemvPair pair) {
+    int n, int k, const GemvPair pair, const GemvConv conv) {
   constexpr int kV = kR * kM;
   constexpr int kVp = pow2_ceil(kV);  // partial sums per lane, zero-padded
   constexpr int kWaves = kThreads / kWave;
@@ -469,8 +494,12 @@ __global__ __launch_bounds__(kThreads, gemv_min_waves(kM, kR)) void gemv_kernel(
       }
       float y = s * ts * cs[row];
       if (bias) y += load_bias(bias, bias_dtype, row);
-      if (paired) red[0][v] = half_bits_to_float<true>(float_to_bf16_bits(y));  // the bf16 GEMV output
-      else store_out(out, out_dtype, size_t(m) * n + row, y);
+      if (paired) {
+        red[0][v] = half_bits_to_float<true>(float_to_bf16_bits(y));  // the bf16 GEMV output
+      } else {
+        store_out(out, out_dtype, size_t(m) * n + row, y);
+        if (row < conv.channels) conv_epilogue(conv, m, row, y);
+      }
     }
   }
   if (paired) {
@@ -540,7 +569,8 @@ __device__ __forceinline__ float row_quad_sum(float v) {
 template <int kM, int kR, int kPasses, bool kRep>
 __global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
     const uint8_t *act, const float *__restrict__ act_scale, const uint8_t *weight, const float *__restrict__ cs,
-    const void *__restrict__ bias, int bias_dtype, void *__restrict__ out, int out_dtype, int n, int k) {
+    const void *__restrict__ bias, int bias_dtype, void *__restrict__ out, int out_dtype, int n, int k,
+    const GemvConv conv) {
   static_assert(kR % 4 == 0 && kR <= 16 && kM >= 1 && kM <= 4, "row groups of four, up to four activation rows");
   constexpr int kG = kR / 4;              // row groups
   constexpr int kWaves = kThreads / kWave;
@@ -683,6 +713,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
       float y = sum * act_scale[m] * cs[row];
       if (bias) y += load_bias(bias, bias_dtype, row);
       store_out(out, out_dtype, size_t(m) * n + row, y);
+      if (row < conv.channels) conv_epilogue(conv, m, row, y);
     }
   }
 }
@@ -916,7 +947,7 @@ void dispatch_src(const LinearArgs &a, dim3 grid) {
   const int n = int(a.n), k = int(a.k);
 #define HIF8_DOT2_LAUNCH(SRC, ONE, REP)                                                                    \
   gemv_kernel<kM, kR, SRC, ONE, REP><<<grid, kThreads, 0, a.stream>>>(                                   \
-      a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k, a.pair)
+      a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, n, k, a.pair, a.conv)
   const bool one = k <= 16 * kThreads;
   switch (a.act_kind) {
     case kActCodes:
@@ -1036,7 +1067,8 @@ void launch_mfma4_t(const LinearArgs &a, const GemvPlan &p) {
   const uint8_t *act = static_cast<const uint8_t *>(a.act);
 #define HIF8_MFMA4_LAUNCH(P)                                                                              \
   gemv_mfma4_kernel<kM, kR, P, kRep><<<p.grid, kThreads, 0, a.stream>>>(                                \
-      act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.n), int(a.k))
+      act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.n), int(a.k), \
+      a.conv)
   // Two register sets of more than eight rows exceed the register file.
   constexpr bool kTwoSets = kR <= 8;
   switch (mfma4_passes(a.k)) {
@@ -1063,7 +1095,24 @@ void launch_mfma4_m(const LinearArgs &a, const GemvPlan &p) {
   }
 }
 
+__global__ __launch_bounds__(256) void conv_rows_kernel(const GemvConv conv, const uint16_t *__restrict__ y,
+                                                        int64_t ld, int m_rows) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= m_rows * conv.channels) return;
+  const int m = idx / conv.channels, c = idx - m * conv.channels;
+  conv_epilogue(conv, m, c, half_bits_to_float<true>(y[size_t(m) * ld + c]));
+}
+
 }  // namespace
+
+int launch_conv_rows(const GemvConv &conv, const uint16_t *y, int64_t ld, int64_t m, hipStream_t stream) {
+  if (conv.channels <= 0 || conv.kw < 2 || conv.kw > 4 || m <= 0 || ld < conv.channels ||
+      m * conv.channels > 0x7FFFFFFFll || !y || !conv.weight || !conv.state || !conv.out)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "conv epilogue: invalid arguments");
+  const int64_t items = m * conv.channels;
+  conv_rows_kernel<<<unsigned((items + 255) / 256), 256, 0, stream>>>(conv, y, ld, int(m));
+  return check_launch("conv epilogue");
+}
 
 int launch_gemv(const LinearArgs &a) {
   if (a.m < 1 || a.m > 4) return fail(HIF8_ERR_UNSUPPORTED, "GEMV kernel handles 1 <= M <= 4, got %lld", (long long)a.m);
@@ -1071,6 +1120,11 @@ int launch_gemv(const LinearArgs &a) {
   const GemvPlan p = plan_gemv(a.m, a.n, a.k, a.act_kind, vec);
   if (a.pair.inter > 0 && (p.kind != kGemvDot2 || a.n != 2 * int64_t(a.pair.inter) || a.bias))
     return fail(HIF8_ERR_UNSUPPORTED, "gate_up + SiLU-mul GEMV: the plan for M=%lld N=%lld K=%lld is not the dot2 kernel",
+                (long long)a.m, (long long)a.n, (long long)a.k);
+  if (a.conv.channels > 0 && ((p.kind != kGemvDot2 && p.kind != kGemvMfma4) || a.pair.inter > 0 ||
+                              a.out_dtype != HIF8_DTYPE_BF16 || a.conv.channels > a.n || a.conv.kw < 2 ||
+                              a.conv.kw > 4 || !a.conv.weight || !a.conv.state || !a.conv.out))
+    return fail(HIF8_ERR_UNSUPPORTED, "conv-epilogue GEMV: the plan for M=%lld N=%lld K=%lld has no conv epilogue",
                 (long long)a.m, (long long)a.n, (long long)a.k);
   switch (p.kind) {
     case kGemvSimple:

@@ -26,6 +26,19 @@ struct GemvPair {
   float *row_scale = nullptr;
 };
 
+// Causal depthwise-conv epilogue of a decode token's qkvz projection: for
+// output rows c < channels of activation row m, with x = the bf16 output
+// value, out[m, c] = SiLU(sum_t bf(state[m, c, t]) bf(weight[c, t]) +
+// x bf(weight[c, kw - 1])) in fp32 (t = 0 .. kw - 2 in order), and
+// state[m, c] shifts by one with x appended.  2 <= kw <= 4, bf16 output.
+struct GemvConv {
+  int channels = 0;
+  int kw = 0;
+  const uint16_t *weight = nullptr;  // [channels, kw] bf16
+  uint16_t *state = nullptr;         // [m, channels, kw - 1] bf16
+  float *out = nullptr;              // [m, channels]
+};
+
 struct LinearArgs {
   const void *act;        // [m, k] codes or fp16/bf16 x
   int act_kind;           // ActKind
@@ -42,11 +55,17 @@ struct LinearArgs {
   size_t workspace_bytes = 0;
   const uint16_t *weight_bf16 = nullptr;  // [n, k] weight decoded beforehand (GEMM), else null
   GemvPair pair;                          // GEMV only: gate_up + SiLU-mul + quant epilogue
+  GemvConv conv;                          // GEMV only: causal-conv epilogue
 };
 
 // HBM-streaming GEMV for m <= 4 (gemv.hip).  Returns a status; with a.pair
-// set, HIF8_ERR_UNSUPPORTED where the plan is not the dot2 kernel.
+// set, HIF8_ERR_UNSUPPORTED where the plan is not the dot2 kernel; with
+// a.conv set, HIF8_ERR_UNSUPPORTED where it is neither the dot2 nor the
+// MFMA-4 kernel.
 int launch_gemv(const LinearArgs &a);
+// The conv epilogue of a.conv as a kernel of its own over y [m, ld] bf16 (the
+// projection output), for plans without the epilogue.
+int launch_conv_rows(const GemvConv &conv, const uint16_t *y, int64_t ld, int64_t m, hipStream_t stream);
 // The kernel launch_gemv picks for these sizes and activation kind (16-byte
 // aligned operands): its name as profilers print it, and its grid.
 int describe_gemv(int64_t m, int64_t n, int64_t k, int act_kind, char *name, size_t name_len, int64_t *grid);

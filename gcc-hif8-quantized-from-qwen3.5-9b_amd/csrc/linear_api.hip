@@ -81,6 +81,41 @@ extern "C" int hif8_gate_up_silu_mul_quant(const uint8_t *activation, const uint
   return launch_gemv(a);
 }
 
+extern "C" int hif8_linear_conv(const uint8_t *activation, const uint8_t *weight, const float *token_scale,
+                                const float *channel_scale, uint16_t *out, const uint16_t *conv_weight,
+                                uint16_t *conv_state, float *conv_out, int64_t m, int64_t n, int64_t k,
+                                int64_t channels, int64_t conv_width, hif8_stream_t stream) {
+  clear_error();
+  int st = validate("hif8_linear_conv", activation, weight, token_scale, channel_scale, nullptr, HIF8_DTYPE_NONE,
+                    out, HIF8_DTYPE_BF16, m, n, k);
+  if (st) return st;
+  if (!conv_weight || !conv_state || !conv_out)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_linear_conv: null pointer argument");
+  if (channels <= 0 || channels > n || conv_width < 2 || conv_width > 4 || m * channels > 0x7FFFFFFFll)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_linear_conv: needs 0 < channels <= n and 2 <= conv_width <= 4");
+  LinearArgs a = codes_args(activation, weight, token_scale, channel_scale, nullptr, HIF8_DTYPE_NONE, out,
+                            HIF8_DTYPE_BF16, m, n, k, stream);
+  GemvConv conv;
+  conv.channels = int(channels);
+  conv.kw = int(conv_width);
+  conv.weight = conv_weight;
+  conv.state = conv_state;
+  conv.out = conv_out;
+  if (m <= 4) {
+    a.conv = conv;
+    st = launch_gemv(a);
+    if (st != HIF8_ERR_UNSUPPORTED) return st;
+    // The plan has no conv epilogue: the projection, then the conv on its own.
+    clear_error();
+    a.conv = GemvConv();
+    st = launch_gemv(a);
+  } else {
+    st = launch_gemm(a);
+  }
+  if (st) return st;
+  return launch_conv_rows(conv, out, n, m, reinterpret_cast<hipStream_t>(stream));
+}
+
 extern "C" size_t soft_hif8_gemm_workspace_size(int64_t m, int64_t n, int64_t k) {
   return gemm_workspace_size(m, n, k);
 }

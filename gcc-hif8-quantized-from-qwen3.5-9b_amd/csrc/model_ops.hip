@@ -95,11 +95,14 @@ __global__ __launch_bounds__(256) void gdn_conv_kernel(const uint16_t *__restric
   out[idx] = acc / (1.f + expf(-acc));
 }
 
-// Rows of n % 8 == 0, n <= 8 * kNormThreads * kNormChunks, 16-byte aligned:
-// thread t owns 16-byte chunks t + kNormThreads * c, loads all of them at
+// Rows of n % 8 == 0, n <= 8 * kRowThreads * kRowChunks, 16-byte aligned:
+// thread t owns 16-byte chunks t + kRowThreads * c, loads all of them at
 // once and keeps the row in registers (the scalar loop above waits on one
-// 2-byte load per iteration and re-reads the row: ~10 us for n = 4096).
-constexpr int kNormChunks = 4;
+// 2-byte load per iteration and re-reads the row: ~10 us for n = 4096).  A
+// decode row runs on one block, so its latency is the block's: 512 threads
+// (one chunk each at n = 4096) take 3.2 us per add + norm + quant on MI355X
+// where 256 threads take 4.3 us and 1024 threads 3.4 us.
+constexpr int kRowThreads = 512, kRowChunks = 2;
 
 // Static HiF8 codes of eight bf16 values (four packed pairs) divided by s,
 // as hif8_static_quant encodes them: the product with the reciprocal, or the
@@ -127,26 +130,26 @@ __device__ __forceinline__ uint2 static_encode8(const uint32_t (&pairs)[4], floa
 // kQuant: also the static HiF8 codes of out with the fixed scale qs[0] (the
 // next projection's input quant) and row_scale[row] = qs[0].
 template <bool kResidual, bool kQuant = false>
-__global__ __launch_bounds__(kNormThreads) void add_rms_norm_vec_kernel(uint16_t *__restrict__ h,
+__global__ __launch_bounds__(kRowThreads) void add_rms_norm_vec_kernel(uint16_t *__restrict__ h,
                                                                         const uint16_t *__restrict__ delta,
                                                                         const uint16_t *__restrict__ w,
                                                                         uint16_t *__restrict__ out, int n,
                                                                         float eps, const float *__restrict__ qs = nullptr,
                                                                         uint8_t *__restrict__ codes = nullptr,
                                                                         float *__restrict__ row_scale = nullptr) {
-  __shared__ float red[kNormThreads / kWave];
+  __shared__ float red[kRowThreads / kWave];
   __shared__ __attribute__((aligned(16))) uint8_t lut[kQuant ? 8192 : 16];
   // The table copy is visible after the barriers of the row sum.
-  if constexpr (kQuant) stage_static_encode_table(lut, threadIdx.x, kNormThreads);
+  if constexpr (kQuant) stage_static_encode_table(lut, threadIdx.x, kRowThreads);
   const int chunks = n / 8;
   uint4 *hr = reinterpret_cast<uint4 *>(h + size_t(blockIdx.x) * n);
   const uint4 *dr = kResidual ? reinterpret_cast<const uint4 *>(delta + size_t(blockIdx.x) * n) : nullptr;
   const uint4 *wr = reinterpret_cast<const uint4 *>(w);
   uint4 *orow = reinterpret_cast<uint4 *>(out + size_t(blockIdx.x) * n);
-  uint4 hv[kNormChunks], dv[kNormChunks], wv[kNormChunks];
+  uint4 hv[kRowChunks], dv[kRowChunks], wv[kRowChunks];
 #pragma unroll
-  for (int c = 0; c < kNormChunks; ++c) {
-    const int i = threadIdx.x + kNormThreads * c;
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int i = threadIdx.x + kRowThreads * c;
     if (i < chunks) {
       hv[c] = hr[i];
       if constexpr (kResidual) dv[c] = dr[i];
@@ -155,8 +158,8 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_vec_kernel(uint16_t
   }
   float ss = 0.f;
 #pragma unroll
-  for (int c = 0; c < kNormChunks; ++c) {
-    const int i = threadIdx.x + kNormThreads * c;
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int i = threadIdx.x + kRowThreads * c;
     if (i < chunks) {
       uint32_t hw[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
 #pragma unroll
@@ -176,10 +179,10 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_vec_kernel(uint16_t
       if constexpr (kResidual) hr[i] = hv[c];
     }
   }
-  const float r = rsqrtf(block_sum<kNormThreads>(ss, red) / float(n) + eps);
+  const float r = rsqrtf(block_sum<kRowThreads>(ss, red) / float(n) + eps);
 #pragma unroll
-  for (int c = 0; c < kNormChunks; ++c) {
-    const int i = threadIdx.x + kNormThreads * c;
+  for (int c = 0; c < kRowChunks; ++c) {
+    const int i = threadIdx.x + kRowThreads * c;
     if (i < chunks) {
       const uint32_t hw[4] = {hv[c].x, hv[c].y, hv[c].z, hv[c].w};
       const uint32_t ww[4] = {wv[c].x, wv[c].y, wv[c].z, wv[c].w};
@@ -427,128 +430,321 @@ __global__ __launch_bounds__(kGdnWideThreads) void gdn_delta_wide_kernel(
 // group (request b, key head hk), fused with the b/a projection and the conv:
 // the kRep = v_heads / k_heads value heads of the group share its q and k, so
 // the block owns every conv channel it reads (q and k of hk, v of its value
-// heads) and shifts that channel's state alone.  The b/a rows are summed as
-// hif8_bf16_gemv sums them (one 256-thread team per row, chunks t, t + 256,
-// ..., then the four wavefront totals in order), the conv as gdn_conv_kernel,
-// and each value head runs gdn_delta_wide_kernel's arithmetic in turn, so the
-// outputs and states equal hif8_bf16_gemv + hif8_gdn_decode_step bit for bit
-// in three launches fewer.  Requires kRep <= 2, dk % 8 == 0, dk <= 128,
-// dv <= 128, 2 dk + kRep dv <= 1024, hidden % 8 == 0.
-template <int kRep>
+// heads) and shifts that channel's state alone.  The kRep heads run side by
+// side, each on 1024 / kRep threads: thread (head, part, j) owns rows
+// [part * R, part * R + R) of state column j, R = dk * kRep / 8 (<= 32),
+// loaded at kernel entry into registers.  Four barriers in all: after the
+// conv and the b/a row sums (one 256-thread team per row, as hif8_bf16_gemv
+// sums a row, so b and a round to the same bf16 values); after the q / k
+// sums (|q|^2, |k|^2 and q.k from the raw conv outputs in one pass; the
+// normalisation is applied to the dot products afterwards, S^T k = (S^T
+// k_raw) / |k|, so only one reduction precedes the state dot products);
+// after the column partials of S^T k and S^T q; after the output norm.  The
+// b/a values equal hif8_bf16_gemv's bit for bit; the state and output agree
+// with hif8_gdn_decode_step to FP32 rounding (the dot products are scaled
+// after the sum instead of before).  Requires kRep <= 2, dk % 8 == 0,
+// dk <= 128, dv <= 128, 2 dk + kRep dv <= 1024, hidden % 8 == 0,
+// hidden <= 8192.
+template <int kRep, int kKw>
 __global__ __launch_bounds__(kGdnWideThreads) void gdn_token_kernel(
     const uint16_t *__restrict__ mixed, int64_t ld, const uint16_t *__restrict__ x,
     const uint16_t *__restrict__ w_ba, int hidden, const uint16_t *__restrict__ conv_w,
-    uint16_t *__restrict__ conv_state, int kw, const float *__restrict__ a_log, const float *__restrict__ dt_bias,
+    uint16_t *__restrict__ conv_state, const float *__restrict__ a_log, const float *__restrict__ dt_bias,
     float *__restrict__ state, const uint16_t *__restrict__ w_out, uint16_t *__restrict__ out, int k_heads,
     int v_heads, int dk, int dv, float eps) {
   static_assert(kRep >= 1 && kRep <= 2, "one or two value heads per key head");
-  __shared__ float cbuf[(2 + kRep) * kGdnCols];  // conv outputs: q | k | v of each value head
-  __shared__ float qs[kGdnCols], ks[kGdnCols];
-  __shared__ float pa[kGdnParts][kGdnCols], pc[kGdnParts][kGdnCols];
-  __shared__ float red[kGdnWideThreads / kWave];
+  constexpr int kHeadT = kGdnWideThreads / kRep;  // threads per value head
+  constexpr int kParts = kHeadT / kGdnCols;       // row parts per head
+  constexpr int kRows = kGdnRows * kRep;          // rows per part, at most
+  // Conv outputs: q | k | v of each value head, then one slot per other
+  // thread (every thread stores its conv, so its loads issue first).
+  __shared__ float cbuf[kGdnWideThreads];
+  __shared__ float pa[kRep][kParts][kGdnCols], pc[kRep][kParts][kGdnCols];
   __shared__ float ba_red[2 * kRep][kNormThreads / kWave];
+  __shared__ float qk_red[2][3];                 // waves 0-1: |q|^2, |k|^2, q.k
+  __shared__ float o_red[kRep][2];               // the two lead waves of each head: |o|^2
   const int b = blockIdx.x / k_heads, hk = blockIdx.x - b * k_heads;
   const int qk_width = k_heads * dk, channels = 2 * qk_width + v_heads * dv;
-  const int tid = threadIdx.x, lane = tid % kWave;
-  const int j = tid % kGdnCols, part = tid / kGdnCols;
-  const int rows = dk / kGdnParts, r0 = part * rows;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int head = tid / kHeadT, ht = tid % kHeadT;
+  const int j = ht % kGdnCols, part = ht / kGdnCols;
+  const int rows = dk / kParts, r0 = part * rows;
   const bool col_ok = j < dv;
-  // State rows of every value head first (the longest loads).
-  float sv[kRep][kGdnRows];
+  const int hv = kRep * hk + head;
+  // Every load is issued up front, in the order the values are consumed:
+  // the conv inputs, the b/a chunks, the state rows, the output-gate values.
+  // Conv thread t < nch owns channel q[t] of hk, then k of hk, then v of the
+  // value heads.
+  const int nch = 2 * dk + kRep * dv;
+  const bool conv_thread = tid < nch;
+  const int cch = !conv_thread     ? 0
+                  : tid < dk       ? hk * dk + tid
+                  : tid < 2 * dk   ? qk_width + hk * dk + (tid - dk)
+                                   : 2 * qk_width + kRep * hk * dv + (tid - 2 * dk);
+  // Loads take clamped indices instead of predicates and land in 32-bit
+  // registers, so they issue back to back with no wait between them; lanes
+  // and taps past the end read in-bounds values they ignore.
+  uint16_t *cst = conv_state + (size_t(b) * channels + cch) * (kKw - 1);
+  uint32_t stv[kKw - 1], cwv[kKw];
+  const uint32_t xc = mixed[size_t(b) * ld + cch];
 #pragma unroll
-  for (int i = 0; i < kRep; ++i) {
-    const float *S = state + (size_t(b) * v_heads + kRep * hk + i) * dk * dv;
+  for (int t = 0; t < kKw - 1; ++t) stv[t] = cst[t];
 #pragma unroll
-    for (int r = 0; r < kGdnRows; ++r) sv[i][r] = (r < rows && col_ok) ? S[size_t(r0 + r) * dv + j] : 0.f;
-  }
-  // b/a projection: team t sums row b (t even) or a (t odd) of value head t / 2.
-  {
-    const int team = tid / kNormThreads, tt = tid % kNormThreads;
-    if (team < 2 * kRep) {
-      const int hv = kRep * hk + team / 2;
-      const uint4 *wr = reinterpret_cast<const uint4 *>(w_ba + size_t(team % 2 ? v_heads + hv : hv) * hidden);
-      const uint4 *xr = reinterpret_cast<const uint4 *>(x + size_t(b) * hidden);
-      float acc = 0.f;
-      for (int c = tt; c < hidden / 8; c += kNormThreads) acc = bf16_dot8(acc, xr[c], wr[c]);
-      const float v = wave_sum(acc);
-      if (lane == 0) ba_red[team][tt / kWave] = v;
+  for (int t = 0; t < kKw; ++t) cwv[t] = conv_w[size_t(cch) * kKw + t];
+  // b/a projection: team t (256 threads) sums row b (t even) or a (t odd) of
+  // value head t / 2.
+  const int team = tid / kNormThreads, tt = tid % kNormThreads;
+  constexpr int kMaxChunks = 4;  // hidden <= 8 * 256 * 4
+  uint4 xv[kMaxChunks], wv[kMaxChunks];
+  const int chunks = hidden / 8;
+  if (team < 2 * kRep) {
+    const int hvt = kRep * hk + team / 2;
+    const uint4 *wr = reinterpret_cast<const uint4 *>(w_ba + size_t(team % 2 ? v_heads + hvt : hvt) * hidden);
+    const uint4 *xr = reinterpret_cast<const uint4 *>(x + size_t(b) * hidden);
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c) {
+      const int i = min(tt + kNormThreads * c, chunks - 1);
+      xv[c] = xr[i];
+      wv[c] = wr[i];
     }
   }
-  // Conv of the group's channels (thread t: q of hk, then k of hk, then v of
-  // the value heads), as gdn_conv_kernel.
-  const int nch = 2 * dk + kRep * dv;
-  if (tid < nch) {
-    const int c = tid < dk ? hk * dk + tid
-                           : tid < 2 * dk ? qk_width + hk * dk + (tid - dk) : 2 * qk_width + kRep * hk * dv + (tid - 2 * dk);
-    uint16_t *st = conv_state + (size_t(b) * channels + c) * (kw - 1);
-    const uint16_t xc = mixed[size_t(b) * ld + c];
+  float sv[kRows];
+  {
+    const float *S = state + (size_t(b) * v_heads + hv) * dk * dv;
+#pragma unroll
+    for (int r = 0; r < kRows; ++r) sv[r] = S[size_t(r0 + min(r, rows - 1)) * dv + min(j, dv - 1)];
+  }
+  const bool lead = part == 0;
+  const uint32_t zraw = mixed[size_t(b) * ld + 2 * qk_width + v_heads * dv + hv * dv + min(j, dv - 1)];
+  const uint32_t wo = w_out[min(j, dv - 1)];
+  const float dtb = dt_bias[hv], alog = a_log[hv];
+  // Conv, as gdn_conv_kernel, on every thread; the conv threads shift the
+  // channel's state by one.
+  float cacc = 0.f;
+#pragma unroll
+  for (int t = 0; t < kKw - 1; ++t) cacc += bf(stv[t]) * bf(cwv[t]);
+  cacc += bf(xc) * bf(cwv[kKw - 1]);
+  cbuf[tid] = cacc / (1.f + expf(-cacc));
+  if (conv_thread) {
+#pragma unroll
+    for (int t = 0; t + 1 < kKw - 1; ++t) cst[t] = uint16_t(stv[t + 1]);
+    cst[kKw - 2] = uint16_t(xc);
+  }
+  if (team < 2 * kRep) {
     float acc = 0.f;
-    for (int t = 0; t < kw - 1; ++t) acc += bf(st[t]) * bf(conv_w[size_t(c) * kw + t]);
-    acc += bf(xc) * bf(conv_w[size_t(c) * kw + kw - 1]);
-    for (int t = 0; t + 1 < kw - 1; ++t) st[t] = st[t + 1];
-    st[kw - 2] = xc;
-    cbuf[tid] = acc / (1.f + expf(-acc));
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c)
+      if (tt + kNormThreads * c < chunks) acc = bf16_dot8(acc, xv[c], wv[c]);
+    const float v = wave_sum(acc);
+    if (lane == 0) ba_red[team][tt / kWave] = v;
   }
   __syncthreads();
-  const bool lead = part == 0;
-  const float qi = lead && j < dk ? cbuf[j] : 0.f;
-  const float ki = lead && j < dk ? cbuf[dk + j] : 0.f;
-  // F.normalize: x / max(||x||, 1e-12); q also scaled by 1 / sqrt(dk).
-  const float qn = fmaxf(sqrtf(block_sum<kGdnWideThreads>(qi * qi, red)), 1e-12f);
-  const float kn = fmaxf(sqrtf(block_sum<kGdnWideThreads>(ki * ki, red)), 1e-12f);
-  const float qv = qi / qn / sqrtf(float(dk)), kv = ki / kn;
-  if (lead) {
-    qs[j] = qv;
-    ks[j] = kv;
+  // |q|^2, |k|^2 and q.k over the dk channels (waves 0 and 1: threads 0..127).
+  if (wave < 2) {
+    const float qi = tid < dk ? cbuf[tid] : 0.f, ki = tid < dk ? cbuf[dk + tid] : 0.f;
+    const float s0 = wave_sum(qi * qi), s1 = wave_sum(ki * ki), s2 = wave_sum(qi * ki);
+    if (lane == 0) {
+      qk_red[wave][0] = s0;
+      qk_red[wave][1] = s1;
+      qk_red[wave][2] = s2;
+    }
   }
-  const float kq = block_sum<kGdnWideThreads>(kv * qv, red);  // also orders the qs / ks stores
+  // Column partials of S^T k_raw and S^T q_raw over this part's rows.
+  float a = 0.f, c = 0.f;
 #pragma unroll
-  for (int i = 0; i < kRep; ++i) {
-    const int hv = kRep * hk + i;
-    float bsum = 0.f, asum = 0.f;
+  for (int r = 0; r < kRows; ++r) {
+    if (r < rows) {
+      a += sv[r] * cbuf[dk + r0 + r];
+      c += sv[r] * cbuf[r0 + r];
+    }
+  }
+  pa[head][part][j] = a;
+  pc[head][part][j] = c;
+  __syncthreads();
+  // F.normalize: x / max(||x||, 1e-12); q also scaled by 1 / sqrt(dk).
+  const float qn = fmaxf(sqrtf(qk_red[0][0] + qk_red[1][0]), 1e-12f);
+  const float kn = fmaxf(sqrtf(qk_red[0][1] + qk_red[1][1]), 1e-12f);
+  const float qscale = 1.f / qn / sqrtf(float(dk)), kscale = 1.f / kn;
+  const float kq = (qk_red[0][2] + qk_red[1][2]) * qscale * kscale;
+  a = 0.f;
+  c = 0.f;
 #pragma unroll
-    for (int w = 0; w < kNormThreads / kWave; ++w) {
-      bsum += ba_red[2 * i][w];
-      asum += ba_red[2 * i + 1][w];
-    }
-    const float braw = bf(to_bf(bsum));
-    const float araw = bf(to_bf(asum)) + dt_bias[hv];
-    const float vj = col_ok ? cbuf[2 * dk + i * dv + j] : 0.f;
-    const float beta = 1.f / (1.f + expf(-braw));
-    const float softplus = araw > 20.f ? araw : log1pf(expf(araw));
-    const float decay = expf(-expf(a_log[hv]) * softplus);
-    float a = 0.f, c = 0.f;
+  for (int p = 0; p < kParts; ++p) {
+    a += pa[head][p][j];
+    c += pc[head][p][j];
+  }
+  a *= kscale;
+  c *= qscale;
+  float bsum = 0.f, asum = 0.f;
 #pragma unroll
-    for (int r = 0; r < kGdnRows; ++r) {
-      if (r < rows) {
-        a += sv[i][r] * ks[r0 + r];
-        c += sv[i][r] * qs[r0 + r];
-      }
-    }
-    pa[part][j] = a;
-    pc[part][j] = c;
-    __syncthreads();
-    a = 0.f;
-    c = 0.f;
+  for (int w = 0; w < kNormThreads / kWave; ++w) {
+    bsum += ba_red[2 * head][w];
+    asum += ba_red[2 * head + 1][w];
+  }
+  const float braw = bf(to_bf(bsum));
+  const float araw = bf(to_bf(asum)) + dtb;
+  const float vj = col_ok ? cbuf[2 * dk + head * dv + j] : 0.f;
+  const float beta = 1.f / (1.f + expf(-braw));
+  const float softplus = araw > 20.f ? araw : log1pf(expf(araw));
+  const float decay = expf(-expf(alog) * softplus);
+  const float delta = beta * (vj - decay * a);
+  const float o = decay * c + delta * kq;
+  if (col_ok) {
+    float *S = state + (size_t(b) * v_heads + hv) * dk * dv;
 #pragma unroll
-    for (int p = 0; p < kGdnParts; ++p) {
-      a += pa[p][j];
-      c += pc[p][j];
-    }
-    const float delta = beta * (vj - decay * a);
-    const float o = decay * c + delta * kq;
-    if (col_ok) {
-      float *S = state + (size_t(b) * v_heads + hv) * dk * dv;
+    for (int r = 0; r < kRows; ++r)
+      if (r < rows) S[size_t(r0 + r) * dv + j] = decay * sv[r] + cbuf[dk + r0 + r] * kscale * delta;
+  }
+  // Output RMSNorm over the head's dv columns (the part-0 threads of the
+  // head: its first two wavefronts).
+  const int hw = ht / kWave;  // wavefront within the head
+  if (hw < 2) {
+    const float v = wave_sum(lead && col_ok ? o * o : 0.f);
+    if (lane == 0) o_red[head][hw] = v;
+  }
+  __syncthreads();
+  if (lead && col_ok) {
+    const float rn = rsqrtf((o_red[head][0] + o_red[head][1]) / float(dv) + eps);
+    const float z = bf(zraw);
+    out[(size_t(b) * v_heads + hv) * dv + j] = to_bf(o * rn * bf(wo) * (z / (1.f + expf(-z))));
+  }
+}
+
+// One decode token of the linear-attention recurrence for one (request b,
+// value head hv), from conv [b, channels] (fp32, SiLU applied: q | k | v, as
+// the qkvz projection's conv epilogue writes them), fused with the b/a
+// projection of the head.  Thread (part, j) owns rows [part * kR, part * kR +
+// kR) of state column j (dk = 8 kR), loaded at kernel entry into registers
+// with every other load.  Three barriers: after the b/a row sums (two
+// 256-thread teams, as hif8_bf16_gemv sums a row, so b and a round to its bf16
+// values) and the q / k sums (|q|^2, |k|^2 and q.k over the raw conv outputs;
+// S^T k = (S^T k_raw) / |k|, S^T q likewise, so one reduction precedes the
+// state dot products); after the column partials; after the output norm.
+// The arithmetic per head is gdn_token_kernel's.  One head per block spreads
+// a step over batch * v_heads blocks where the group kernel puts two heads'
+// 32768 state elements on one CU, whose VALU then bounds it: on MI355X at
+// b = 1 (16 key heads, 32 value heads, dk = dv = 128) 6.8 us per call in the
+// decode step's kernel trace against 12.5 us for the group kernel.  Requires
+// dk = 8 kR, dv <= 128, hidden % 8 == 0, hidden <= 8192.
+template <int kR>
+__global__ __launch_bounds__(kGdnWideThreads) void gdn_head_kernel(
+    const float *__restrict__ conv, const uint16_t *__restrict__ mixed, int64_t ld, const uint16_t *__restrict__ x,
+    const uint16_t *__restrict__ w_ba, int hidden, const float *__restrict__ a_log,
+    const float *__restrict__ dt_bias, float *__restrict__ state, const uint16_t *__restrict__ w_out,
+    uint16_t *__restrict__ out, int k_heads, int v_heads, int dv, float eps) {
+  constexpr int dk = kGdnParts * kR;
+  __shared__ __attribute__((aligned(16))) float qs[dk], ks[dk];  // raw conv outputs of q and k
+  __shared__ float pa[kGdnParts][kGdnCols], pc[kGdnParts][kGdnCols];
+  __shared__ float ba_red[2][kNormThreads / kWave];
+  __shared__ float qk_red[2][3];  // waves 0-1: |q|^2, |k|^2, q.k
+  __shared__ float o_red[2];      // waves 0-1: |o|^2
+  const int b = blockIdx.x / v_heads, hv = blockIdx.x - b * v_heads;
+  const int hk = hv / (v_heads / k_heads);
+  const int qk_width = k_heads * dk, channels = 2 * qk_width + v_heads * dv;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int j = tid % kGdnCols, part = tid / kGdnCols, r0 = part * kR;
+  const bool col_ok = j < dv;
+  const int jc = min(j, dv - 1);
+  // Every load first, with clamped indices (no predicates, so they issue
+  // back to back; lanes past the end read in-bounds values they ignore).
+  const float *cr = conv + size_t(b) * channels;
+  const int qt = min(tid, dk - 1);
+  const float qraw = cr[hk * dk + qt], kraw = cr[qk_width + hk * dk + qt];
+  const int team = tid / kNormThreads, tt = tid % kNormThreads;
+  constexpr int kMaxChunks = 4;  // hidden <= 8 * 256 * 4
+  uint4 xv[kMaxChunks], wv[kMaxChunks];
+  const int chunks = hidden / 8;
+  if (team < 2) {
+    const uint4 *wr = reinterpret_cast<const uint4 *>(w_ba + size_t(team ? v_heads + hv : hv) * hidden);
+    const uint4 *xr = reinterpret_cast<const uint4 *>(x + size_t(b) * hidden);
 #pragma unroll
-      for (int r = 0; r < kGdnRows; ++r)
-        if (r < rows) S[size_t(r0 + r) * dv + j] = decay * sv[i][r] + ks[r0 + r] * delta;
+    for (int c = 0; c < kMaxChunks; ++c) {
+      const int i = min(tt + kNormThreads * c, chunks - 1);
+      xv[c] = xr[i];
+      wv[c] = wr[i];
     }
-    // The norm's first barrier also retires this head's pa / pc reads.
-    const float rn = rsqrtf(block_sum<kGdnWideThreads>(lead && col_ok ? o * o : 0.f, red) / float(dv) + eps);
-    if (lead && col_ok) {
-      const float z = bf(mixed[size_t(b) * ld + 2 * qk_width + v_heads * dv + hv * dv + j]);
-      out[(size_t(b) * v_heads + hv) * dv + j] = to_bf(o * rn * bf(w_out[j]) * (z / (1.f + expf(-z))));
+  }
+  float *S = state + (size_t(b) * v_heads + hv) * dk * dv;
+  float sv[kR];
+#pragma unroll
+  for (int r = 0; r < kR; ++r) sv[r] = S[size_t(r0 + r) * dv + jc];
+  const float vj = cr[2 * qk_width + hv * dv + jc];
+  const uint32_t zraw = mixed[size_t(b) * ld + 2 * qk_width + v_heads * dv + hv * dv + jc];
+  const uint32_t wo = w_out[jc];
+  const float dtb = dt_bias[hv], alog = a_log[hv];
+  if (tid < dk) {
+    qs[tid] = qraw;
+    ks[tid] = kraw;
+  }
+  if (wave < 2) {
+    const float qi = tid < dk ? qraw : 0.f, ki = tid < dk ? kraw : 0.f;
+    const float s0 = wave_sum(qi * qi), s1 = wave_sum(ki * ki), s2 = wave_sum(qi * ki);
+    if (lane == 0) {
+      qk_red[wave][0] = s0;
+      qk_red[wave][1] = s1;
+      qk_red[wave][2] = s2;
     }
+  }
+  if (team < 2) {
+    float acc = 0.f;
+#pragma unroll
+    for (int c = 0; c < kMaxChunks; ++c)
+      if (tt + kNormThreads * c < chunks) acc = bf16_dot8(acc, xv[c], wv[c]);
+    const float v = wave_sum(acc);
+    if (lane == 0) ba_red[team][tt / kWave] = v;
+  }
+  __syncthreads();
+  // Column partials of S^T k_raw and S^T q_raw over this part's rows.
+  float a = 0.f, c = 0.f;
+#pragma unroll
+  for (int r = 0; r < kR; ++r) {
+    a += sv[r] * ks[r0 + r];
+    c += sv[r] * qs[r0 + r];
+  }
+  pa[part][j] = a;
+  pc[part][j] = c;
+  __syncthreads();
+  // F.normalize: x / max(||x||, 1e-12); q also scaled by 1 / sqrt(dk).
+  const float qn = fmaxf(sqrtf(qk_red[0][0] + qk_red[1][0]), 1e-12f);
+  const float kn = fmaxf(sqrtf(qk_red[0][1] + qk_red[1][1]), 1e-12f);
+  const float qscale = 1.f / qn / sqrtf(float(dk)), kscale = 1.f / kn;
+  const float kq = (qk_red[0][2] + qk_red[1][2]) * qscale * kscale;
+  a = 0.f;
+  c = 0.f;
+#pragma unroll
+  for (int p = 0; p < kGdnParts; ++p) {
+    a += pa[p][j];
+    c += pc[p][j];
+  }
+  a *= kscale;
+  c *= qscale;
+  float bsum = 0.f, asum = 0.f;
+#pragma unroll
+  for (int w = 0; w < kNormThreads / kWave; ++w) {
+    bsum += ba_red[0][w];
+    asum += ba_red[1][w];
+  }
+  const float braw = bf(to_bf(bsum));
+  const float araw = bf(to_bf(asum)) + dtb;
+  const float beta = 1.f / (1.f + expf(-braw));
+  const float softplus = araw > 20.f ? araw : log1pf(expf(araw));
+  const float decay = expf(-expf(alog) * softplus);
+  const float delta = beta * ((col_ok ? vj : 0.f) - decay * a);
+  const float o = decay * c + delta * kq;
+  if (col_ok) {
+#pragma unroll
+    for (int r = 0; r < kR; ++r) S[size_t(r0 + r) * dv + j] = decay * sv[r] + ks[r0 + r] * kscale * delta;
+  }
+  // Output RMSNorm over the dv columns (the part-0 threads: waves 0-1).
+  if (wave < 2) {
+    const float v = wave_sum(col_ok ? o * o : 0.f);
+    if (lane == 0) o_red[wave] = v;
+  }
+  __syncthreads();
+  if (part == 0 && col_ok) {
+    const float rn = rsqrtf((o_red[0] + o_red[1]) / float(dv) + eps);
+    const float z = bf(uint16_t(zraw));
+    out[(size_t(b) * v_heads + hv) * dv + j] = to_bf(o * rn * bf(uint16_t(wo)) * (z / (1.f + expf(-z))));
   }
 }
 
@@ -634,12 +830,12 @@ extern "C" int hif8_add_rms_norm(uint16_t *h, const uint16_t *delta, const uint1
   if (rows <= 0 || n <= 0 || rows > 0x7FFFFFFFll || n > 0x7FFFFFFFll)
     return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_add_rms_norm: invalid dimensions");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const bool vec = n % 8 == 0 && n <= 8 * kNormThreads * kNormChunks && aligned(h, 16) && aligned(weight, 16) &&
+  const bool vec = n % 8 == 0 && n <= 8 * kRowThreads * kRowChunks && aligned(h, 16) && aligned(weight, 16) &&
                    aligned(out, 16) && (!delta || aligned(delta, 16));
   if (vec && delta)
-    add_rms_norm_vec_kernel<true><<<unsigned(rows), kNormThreads, 0, s>>>(h, delta, weight, out, int(n), eps);
+    add_rms_norm_vec_kernel<true><<<unsigned(rows), kRowThreads, 0, s>>>(h, delta, weight, out, int(n), eps);
   else if (vec)
-    add_rms_norm_vec_kernel<false><<<unsigned(rows), kNormThreads, 0, s>>>(h, nullptr, weight, out, int(n), eps);
+    add_rms_norm_vec_kernel<false><<<unsigned(rows), kRowThreads, 0, s>>>(h, nullptr, weight, out, int(n), eps);
   else if (delta)
     add_rms_norm_kernel<true><<<unsigned(rows), kNormThreads, 0, s>>>(h, delta, weight, out, int(n), eps);
   else
@@ -655,16 +851,16 @@ extern "C" int hif8_add_rms_norm_quant(uint16_t *h, const uint16_t *delta, const
     return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_add_rms_norm_quant: null pointer argument");
   if (rows <= 0 || n <= 0 || rows > 0x7FFFFFFFll || n > 0x7FFFFFFFll)
     return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_add_rms_norm_quant: invalid dimensions");
-  if (n % 8 || n > 8 * kNormThreads * kNormChunks || !aligned(h, 16) || !aligned(weight, 16) || !aligned(out, 16) ||
+  if (n % 8 || n > 8 * kRowThreads * kRowChunks || !aligned(h, 16) || !aligned(weight, 16) || !aligned(out, 16) ||
       (delta && !aligned(delta, 16)) || !aligned(codes, 8))
     return fail(HIF8_ERR_UNSUPPORTED, "hif8_add_rms_norm_quant: needs n %% 8 == 0, n <= %d and aligned rows",
-                8 * kNormThreads * kNormChunks);
+                8 * kRowThreads * kRowChunks);
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (delta)
-    add_rms_norm_vec_kernel<true, true><<<unsigned(rows), kNormThreads, 0, s>>>(h, delta, weight, out, int(n), eps,
+    add_rms_norm_vec_kernel<true, true><<<unsigned(rows), kRowThreads, 0, s>>>(h, delta, weight, out, int(n), eps,
                                                                                input_scale, codes, row_scale);
   else
-    add_rms_norm_vec_kernel<false, true><<<unsigned(rows), kNormThreads, 0, s>>>(h, nullptr, weight, out, int(n), eps,
+    add_rms_norm_vec_kernel<false, true><<<unsigned(rows), kRowThreads, 0, s>>>(h, nullptr, weight, out, int(n), eps,
                                                                                 input_scale, codes, row_scale);
   return check_launch("hif8_add_rms_norm_quant");
 }
@@ -739,20 +935,61 @@ extern "C" int hif8_gdn_decode_token(const uint16_t *mixed_qkvz, int64_t ld, con
     return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gdn_decode_token: mixed_qkvz row too short");
   const int64_t rep = v_heads / k_heads;
   if (rep > 2 || k_dim % kGdnParts || k_dim > kGdnParts * kGdnRows || v_dim > kGdnCols ||
-      2 * k_dim + rep * v_dim > kGdnWideThreads || hidden % 8 || !aligned(x, 16) || !aligned(ba_weight, 16))
+      2 * k_dim + rep * v_dim > kGdnWideThreads || hidden % 8 || hidden > 8 * kNormThreads * 4 ||
+      conv_width > 4 ||
+      !aligned(x, 16) || !aligned(ba_weight, 16))
     return fail(HIF8_ERR_UNSUPPORTED, "hif8_gdn_decode_token: needs v_heads / k_heads <= 2, k_dim %% 8 == 0, "
-                                      "k_dim, v_dim <= 128, hidden %% 8 == 0 and 16-byte aligned x / ba_weight");
+                                      "k_dim, v_dim <= 128, hidden %% 8 == 0, hidden <= 8192, conv_width <= 4 "
+                                      "and 16-byte aligned x / ba_weight");
   hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const dim3 grid(unsigned(batch * k_heads));
-#define HIF8_GDN_TOKEN(R)                                                                                     \
-  gdn_token_kernel<R><<<grid, kGdnWideThreads, 0, s>>>(mixed_qkvz, ld, x, ba_weight, int(hidden), conv_weight, \
-                                                       conv_state, int(conv_width), a_log, dt_bias, rec_state,   \
-                                                       out_norm, out, int(k_heads), int(v_heads), int(k_dim),    \
-                                                       int(v_dim), eps)
-  if (rep == 2) HIF8_GDN_TOKEN(2);
-  else HIF8_GDN_TOKEN(1);
+#define HIF8_GDN_TOKEN(R, W)                                                                                     \
+  gdn_token_kernel<R, W><<<grid, kGdnWideThreads, 0, s>>>(mixed_qkvz, ld, x, ba_weight, int(hidden), conv_weight, \
+                                                          conv_state, a_log, dt_bias, rec_state, out_norm, out,      \
+                                                          int(k_heads), int(v_heads), int(k_dim), int(v_dim), eps)
+#define HIF8_GDN_TOKEN_W(R)             \
+  switch (conv_width) {                 \
+    case 2: HIF8_GDN_TOKEN(R, 2); break; \
+    case 3: HIF8_GDN_TOKEN(R, 3); break; \
+    default: HIF8_GDN_TOKEN(R, 4); break; \
+  }
+  if (rep == 2) HIF8_GDN_TOKEN_W(2)
+  else HIF8_GDN_TOKEN_W(1)
+#undef HIF8_GDN_TOKEN_W
 #undef HIF8_GDN_TOKEN
   return check_launch("hif8_gdn_decode_token");
+}
+
+extern "C" int hif8_gdn_decode_head(const float *conv, const uint16_t *mixed_qkvz, int64_t ld, const uint16_t *x,
+                                    const uint16_t *ba_weight, int64_t hidden, const float *a_log,
+                                    const float *dt_bias, float *rec_state, const uint16_t *out_norm, uint16_t *out,
+                                    int64_t batch, int64_t k_heads, int64_t v_heads, int64_t k_dim, int64_t v_dim,
+                                    float eps, hif8_stream_t stream) {
+  clear_error();
+  if (!conv || !mixed_qkvz || !x || !ba_weight || !a_log || !dt_bias || !rec_state || !out_norm || !out)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gdn_decode_head: null pointer argument");
+  if (batch <= 0 || k_heads <= 0 || v_heads <= 0 || v_heads % k_heads || k_dim <= 0 || v_dim <= 0 ||
+      hidden <= 0 || hidden > 0x7FFFFFFFll || batch * v_heads > 0x7FFFFFFFll)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gdn_decode_head: unsupported dimensions");
+  const int64_t channels = 2 * k_heads * k_dim + v_heads * v_dim;
+  if (ld < channels + v_heads * v_dim)
+    return fail(HIF8_ERR_INVALID_ARGUMENT, "hif8_gdn_decode_head: mixed_qkvz row too short");
+  const int64_t rows = k_dim / kGdnParts;
+  if (k_dim % kGdnParts || (rows != 16 && rows != 8 && rows != 4) || v_dim > kGdnCols || hidden % 8 ||
+      hidden > 8 * kNormThreads * 4 || !aligned(x, 16) || !aligned(ba_weight, 16))
+    return fail(HIF8_ERR_UNSUPPORTED, "hif8_gdn_decode_head: needs k_dim in {32, 64, 128}, v_dim <= 128, "
+                                      "hidden %% 8 == 0, hidden <= 8192 and 16-byte aligned x / ba_weight");
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid(unsigned(batch * v_heads));
+#define HIF8_GDN_HEAD(R)                                                                                    \
+  gdn_head_kernel<R><<<grid, kGdnWideThreads, 0, s>>>(conv, mixed_qkvz, ld, x, ba_weight, int(hidden), a_log, \
+                                                      dt_bias, rec_state, out_norm, out, int(k_heads),        \
+                                                      int(v_heads), int(v_dim), eps)
+  if (rows == 16) HIF8_GDN_HEAD(16);
+  else if (rows == 8) HIF8_GDN_HEAD(8);
+  else HIF8_GDN_HEAD(4);
+#undef HIF8_GDN_HEAD
+  return check_launch("hif8_gdn_decode_head");
 }
 
 extern "C" int hif8_gdn_decode_step(const uint16_t *mixed_qkvz, int64_t ld, const uint16_t *ba,

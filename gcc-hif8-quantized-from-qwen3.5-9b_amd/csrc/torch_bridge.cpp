@@ -722,6 +722,38 @@ std::tuple<at::Tensor, at::Tensor> Hif8GateUpSiluMulQuant(const at::Tensor &acti
                           input_scale);
 }
 
+// The qkvz projection over activation codes with the linear-attention causal
+// conv in its epilogue (no reference counterpart): (bf16 projection [m, n],
+// float32 conv outputs [m, channels]), conv_state shifted in place.
+std::tuple<at::Tensor, at::Tensor> Hif8LinearConv(const at::Tensor &activation, const at::Tensor &weight,
+                                                  const at::Tensor &token_scale, const at::Tensor &channel_scale,
+                                                  const at::Tensor &conv_weight, at::Tensor &conv_state) {
+  ValidateSoftLinear(activation, weight, token_scale, channel_scale, c10::nullopt, at::ScalarType::BFloat16, false);
+  CheckContiguousDevice(conv_weight, "conv_weight");
+  CheckContiguousDevice(conv_state, "conv_state");
+  TORCH_CHECK(conv_weight.scalar_type() == at::kBFloat16 && conv_state.scalar_type() == at::kBFloat16,
+              "hif8_linear_conv takes bfloat16 conv_weight and conv_state");
+  const int64_t m = activation.size(0), n = weight.size(0), k = activation.size(1);
+  TORCH_CHECK(conv_weight.dim() == 2 && conv_weight.size(0) > 0 && conv_weight.size(0) <= n &&
+                  conv_weight.size(1) >= 2 && conv_weight.size(1) <= 4,
+              "hif8_linear_conv needs conv_weight [channels <= n, 2 <= conv_width <= 4]");
+  const int64_t channels = conv_weight.size(0), kw = conv_weight.size(1);
+  TORCH_CHECK(conv_state.dim() == 3 && conv_state.size(0) == m && conv_state.size(1) == channels &&
+                  conv_state.size(2) == kw - 1,
+              "hif8_linear_conv needs conv_state [m, channels, conv_width - 1]");
+  const c10::OptionalDeviceGuard guard(activation.device());
+  auto out = at::empty({m, n}, activation.options().dtype(at::kBFloat16));
+  auto conv = at::empty({m, channels}, activation.options().dtype(at::kFloat));
+  CheckStatus(hif8_linear_conv(activation.data_ptr<uint8_t>(), weight.data_ptr<uint8_t>(),
+                               token_scale.data_ptr<float>(), channel_scale.data_ptr<float>(),
+                               reinterpret_cast<uint16_t *>(out.data_ptr()),
+                               reinterpret_cast<const uint16_t *>(conv_weight.data_ptr()),
+                               reinterpret_cast<uint16_t *>(conv_state.data_ptr()), conv.data_ptr<float>(), m, n, k,
+                               channels, kw, CurrentStream(activation.device())),
+              "hif8_linear_conv");
+  return {out, conv};
+}
+
 at::Tensor Hif8Bf16Gemv(const at::Tensor &x, const at::Tensor &weight) {
   CheckContiguousDevice(x, "x");
   CheckContiguousDevice(weight, "weight");
@@ -776,6 +808,45 @@ at::Tensor Hif8GdnDecodeStep(const at::Tensor &mixed, const at::Tensor &ba, cons
                   scratch.data_ptr<float>(), batch, k_heads, v_heads, k_dim, v_dim, conv_weight.size(1), float(eps),
                   CurrentStream(mixed.device())),
               "hif8_gdn_decode_step");
+  return out;
+}
+
+// The recurrence of one decode token from hif8_linear_conv's conv outputs,
+// the b/a projection of x folded in, one block per (request, value head).
+at::Tensor Hif8GdnDecodeHead(const at::Tensor &conv, const at::Tensor &mixed, const at::Tensor &x,
+                             const at::Tensor &ba_weight, const at::Tensor &a_log, const at::Tensor &dt_bias,
+                             at::Tensor &rec_state, const at::Tensor &out_norm, int64_t k_heads, int64_t v_heads,
+                             int64_t k_dim, int64_t v_dim, double eps) {
+  for (auto *t : {&conv, &mixed, &x, &ba_weight, &a_log, &dt_bias, &out_norm}) CheckContiguousDevice(*t, "operand");
+  CheckContiguousDevice(rec_state, "rec_state");
+  TORCH_CHECK(conv.dim() == 2 && mixed.dim() == 2 && x.dim() == 2 && ba_weight.dim() == 2 && rec_state.dim() == 4,
+              "hif8_gdn_decode_head: operand ranks");
+  const int64_t batch = conv.size(0);
+  const int64_t channels = 2 * k_heads * k_dim + v_heads * v_dim;
+  TORCH_CHECK(conv.scalar_type() == at::kFloat && conv.size(1) == channels,
+              "hif8_gdn_decode_head needs float32 conv [batch, 2 k_heads k_dim + v_heads v_dim]");
+  TORCH_CHECK(mixed.scalar_type() == at::kBFloat16 && x.scalar_type() == at::kBFloat16 &&
+                  ba_weight.scalar_type() == at::kBFloat16 && out_norm.scalar_type() == at::kBFloat16,
+              "hif8_gdn_decode_head: bf16 mixed_qkvz / x / ba_weight / out_norm expected");
+  TORCH_CHECK(mixed.size(0) == batch && x.size(0) == batch && x.size(1) == ba_weight.size(1) &&
+                  ba_weight.size(0) == 2 * v_heads,
+              "hif8_gdn_decode_head needs mixed_qkvz [batch, .], x [batch, hidden], ba_weight [2 v_heads, hidden]");
+  TORCH_CHECK(a_log.scalar_type() == at::kFloat && dt_bias.scalar_type() == at::kFloat &&
+                  rec_state.scalar_type() == at::kFloat, "hif8_gdn_decode_head: float32 a_log / dt_bias / state");
+  TORCH_CHECK(rec_state.size(0) == batch && rec_state.size(1) == v_heads && rec_state.size(2) == k_dim &&
+                  rec_state.size(3) == v_dim, "rec_state must be [batch, v_heads, k_dim, v_dim]");
+  TORCH_CHECK(a_log.numel() == v_heads && dt_bias.numel() == v_heads && out_norm.numel() == v_dim,
+              "per-head parameters");
+  const c10::OptionalDeviceGuard guard(conv.device());
+  auto out = at::empty({batch, v_heads * v_dim}, mixed.options());
+  CheckStatus(hif8_gdn_decode_head(conv.data_ptr<float>(), reinterpret_cast<const uint16_t *>(mixed.data_ptr()),
+                                   mixed.size(1), reinterpret_cast<const uint16_t *>(x.data_ptr()),
+                                   reinterpret_cast<const uint16_t *>(ba_weight.data_ptr()), x.size(1),
+                                   a_log.data_ptr<float>(), dt_bias.data_ptr<float>(), rec_state.data_ptr<float>(),
+                                   reinterpret_cast<const uint16_t *>(out_norm.data_ptr()),
+                                   reinterpret_cast<uint16_t *>(out.data_ptr()), batch, k_heads, v_heads, k_dim,
+                                   v_dim, float(eps), CurrentStream(conv.device())),
+              "hif8_gdn_decode_head");
   return out;
 }
 
@@ -966,6 +1037,19 @@ std::tuple<at::Tensor, at::Tensor> Hif8GateUpSiluMulQuantMeta(const at::Tensor &
           at::empty({activation.size(0)}, activation.options().dtype(at::kFloat))};
 }
 
+std::tuple<at::Tensor, at::Tensor> Hif8LinearConvMeta(const at::Tensor &activation, const at::Tensor &weight,
+                                                      const at::Tensor &, const at::Tensor &,
+                                                      const at::Tensor &conv_weight, at::Tensor &) {
+  return {at::empty({activation.size(0), weight.size(0)}, activation.options().dtype(at::kBFloat16)),
+          at::empty({activation.size(0), conv_weight.size(0)}, activation.options().dtype(at::kFloat))};
+}
+
+at::Tensor Hif8GdnDecodeHeadMeta(const at::Tensor &conv, const at::Tensor &, const at::Tensor &, const at::Tensor &,
+                                 const at::Tensor &, const at::Tensor &, at::Tensor &, const at::Tensor &, int64_t,
+                                 int64_t v_heads, int64_t, int64_t v_dim, double) {
+  return at::empty({conv.size(0), v_heads * v_dim}, conv.options().dtype(at::kBFloat16));
+}
+
 at::Tensor Hif8GdnDecodeTokenMeta(const at::Tensor &mixed, const at::Tensor &, const at::Tensor &,
                                   const at::Tensor &, at::Tensor &, const at::Tensor &, const at::Tensor &,
                                   at::Tensor &, const at::Tensor &, int64_t, int64_t v_heads, int64_t, int64_t v_dim,
@@ -999,6 +1083,8 @@ TORCH_LIBRARY(vllm_ascend_hif8, m) {
   m.def("hif8_gdn_decode_step(Tensor mixed_qkvz, Tensor ba, Tensor conv_weight, Tensor(a!) conv_state, Tensor a_log, Tensor dt_bias, Tensor(b!) rec_state, Tensor out_norm, int k_heads, int v_heads, int k_dim, int v_dim, float eps) -> Tensor");
   m.def("hif8_gate_up_silu_mul_quant(Tensor activation, Tensor weight, Tensor token_scale, Tensor channel_scale, Tensor input_scale) -> (Tensor, Tensor)");
   m.def("hif8_gdn_decode_token(Tensor mixed_qkvz, Tensor x, Tensor ba_weight, Tensor conv_weight, Tensor(a!) conv_state, Tensor a_log, Tensor dt_bias, Tensor(b!) rec_state, Tensor out_norm, int k_heads, int v_heads, int k_dim, int v_dim, float eps) -> Tensor");
+  m.def("hif8_linear_conv(Tensor activation, Tensor weight, Tensor token_scale, Tensor channel_scale, Tensor conv_weight, Tensor(a!) conv_state) -> (Tensor, Tensor)");
+  m.def("hif8_gdn_decode_head(Tensor conv, Tensor mixed_qkvz, Tensor x, Tensor ba_weight, Tensor a_log, Tensor dt_bias, Tensor(a!) rec_state, Tensor out_norm, int k_heads, int v_heads, int k_dim, int v_dim, float eps) -> Tensor");
 }
 
 TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
@@ -1022,6 +1108,8 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, CUDA, m) {
   m.impl("hif8_gdn_decode_step", &Hif8GdnDecodeStep);
   m.impl("hif8_gdn_decode_token", &Hif8GdnDecodeToken);
   m.impl("hif8_gate_up_silu_mul_quant", &Hif8GateUpSiluMulQuant);
+  m.impl("hif8_linear_conv", &Hif8LinearConv);
+  m.impl("hif8_gdn_decode_head", &Hif8GdnDecodeHead);
   m.impl("soft_hif8_gemm_decoded_weight", &SoftHif8GemmDecodedWeight);
   m.impl("hif8_decode_bf16", &Hif8DecodeBf16);
 }
@@ -1049,6 +1137,8 @@ TORCH_LIBRARY_IMPL(vllm_ascend_hif8, Meta, m) {
   m.impl("hif8_gdn_decode_step", &Hif8GdnDecodeStepMeta);
   m.impl("hif8_gdn_decode_token", &Hif8GdnDecodeTokenMeta);
   m.impl("hif8_gate_up_silu_mul_quant", &Hif8GateUpSiluMulQuantMeta);
+  m.impl("hif8_linear_conv", &Hif8LinearConvMeta);
+  m.impl("hif8_gdn_decode_head", &Hif8GdnDecodeHeadMeta);
 }
 
 PYBIND11_MODULE(TORCH_EXTENSION_NAME, module) {

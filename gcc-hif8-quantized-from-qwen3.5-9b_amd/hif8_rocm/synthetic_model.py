@@ -205,6 +205,17 @@ class StaticLinear:
         return torch.ops.vllm_ascend_hif8.hif8_gate_up_silu_mul_quant(
             codes, self.layer.weight, row_scale.reshape(-1), self.layer.weight_scale.reshape(-1), next_input_scale)
 
+    def conv_from_codes(self, codes: torch.Tensor, row_scale: torch.Tensor, conv_weight: torch.Tensor,
+                        conv_state: torch.Tensor):
+        """For a qkvz projection of at most four rows: (the bf16 projection,
+        the float32 causal-conv outputs of its first conv_weight.shape[0]
+        columns), the conv state shifted in place; the conv runs in the GEMV
+        epilogue where the kernel plan allows it (the conv of
+        ``hif8_gdn_decode_step``)."""
+        return torch.ops.vllm_ascend_hif8.hif8_linear_conv(
+            codes, self.layer.weight, row_scale.reshape(-1), self.layer.weight_scale.reshape(-1), conv_weight,
+            conv_state)
+
 
 @dataclass
 class RequestState:
@@ -227,6 +238,10 @@ class HybridModel:
         # Decode quantizes projection inputs inside the glue kernels; False
         # runs the scheme's own quant per projection (same codes, more launches).
         self.fuse_input_quant = True
+        # Decode runs the linear-attention mixer as the conv-epilogue qkvz GEMV
+        # + one block per value head where the shapes allow; False keeps the
+        # per-group kernel that folds the conv in.
+        self.head_split = True
         self.device = torch.device(device)
         g = torch.Generator(device=self.device).manual_seed(seed)
         c = cfg
@@ -409,11 +424,28 @@ class HybridModel:
         where the head shapes allow it); x [B, H]; xq: x already quantized
         for the qkvz projection."""
         c = self.cfg
+        ops = torch.ops.vllm_ascend_hif8
+        if xq is not None and self._head_split_ok(x.shape[0]):
+            # Two launches: the qkvz GEMV with the conv in its epilogue, then
+            # one block per (request, value head) for the recurrence.
+            qkvz, conv = L["qkvz"].conv_from_codes(*xq, L["conv"], st.conv_states[idx])
+            o = ops.hif8_gdn_decode_head(conv, qkvz, x, L["ba"], L["A_log"], L["dt_bias"], st.rec_states[idx],
+                                         L["out_norm"], c.lin_k_heads, c.lin_v_heads, c.lin_k_dim, c.lin_v_dim,
+                                         c.rms_eps)
+            return L["out"](o)
         qkvz = L["qkvz"](x) if xq is None else L["qkvz"].from_codes(*xq)
-        o = torch.ops.vllm_ascend_hif8.hif8_gdn_decode_token(
+        o = ops.hif8_gdn_decode_token(
             qkvz, x, L["ba"], L["conv"], st.conv_states[idx], L["A_log"], L["dt_bias"], st.rec_states[idx],
             L["out_norm"], c.lin_k_heads, c.lin_v_heads, c.lin_k_dim, c.lin_v_dim, c.rms_eps)
         return L["out"](o)
+
+    def _head_split_ok(self, batch: int) -> bool:
+        """Whether the decode token's linear-attention mixer takes the
+        conv-epilogue GEMV + per-head kernel pair (the shapes that pair
+        handles; others run the fused per-group kernel)."""
+        c = self.cfg
+        return (self.head_split and batch <= 4 and 2 <= c.conv_kernel <= 4 and c.lin_k_dim in (32, 64, 128)
+                and c.lin_v_dim <= 128 and c.hidden % 8 == 0 and c.hidden <= 8192)
 
     def _fuse_input_quant(self) -> bool:
         """Whether the decode step quantizes projection inputs inside the

@@ -417,6 +417,32 @@ int hif8_silu_mul_quant(const uint16_t *gate_up, const float *input_scale, uint8
 int hif8_gate_up_silu_mul_quant(const uint8_t *activation, const uint8_t *weight, const float *token_scale,
                                 const float *channel_scale, const float *input_scale, uint8_t *codes,
                                 float *row_scale, int64_t m, int64_t inter, int64_t k, hif8_stream_t stream);
+/* The qkvz projection of a linear-attention decode token with the causal
+ * depthwise conv in its epilogue (glue, no reference counterpart): out [m, n]
+ * = soft_hif8_gemm(activation codes, weight, token_scale, channel_scale) in
+ * bf16, and for the first `channels` columns (q | k | v) conv_out [m,
+ * channels] (float32) = SiLU(sum_t bf(conv_state[m, c, t]) bf(conv_weight[c,
+ * t]) + out[m, c] bf(conv_weight[c, kw - 1])) (t = 0 .. kw - 2 in order), the
+ * conv of hif8_gdn_decode_step, with conv_state [m, channels, kw - 1] shifted
+ * by one and out[m, c] appended.  2 <= conv_width <= 4.  One launch where the
+ * GEMV plan for (m, n, k) is the dot2 or MFMA-4 kernel, else the projection
+ * and a conv kernel. */
+int hif8_linear_conv(const uint8_t *activation, const uint8_t *weight, const float *token_scale,
+                     const float *channel_scale, uint16_t *out, const uint16_t *conv_weight, uint16_t *conv_state,
+                     float *conv_out, int64_t m, int64_t n, int64_t k, int64_t channels, int64_t conv_width,
+                     hif8_stream_t stream);
+/* The recurrence of hif8_gdn_decode_token from the conv outputs of
+ * hif8_linear_conv (glue, no reference counterpart): conv [batch, channels]
+ * float32, mixed_qkvz [batch, ld] (the z gate columns after the channels),
+ * the b/a projection of x [batch, hidden] by ba_weight [2 v_heads, hidden]
+ * folded in; one block per (request, value head).  Outputs and states equal
+ * hif8_gdn_decode_token's given the same conv outputs.  Needs k_dim in
+ * {32, 64, 128}, v_dim <= 128, hidden % 8 == 0, hidden <= 8192 and 16-byte
+ * aligned x and ba_weight, else HIF8_ERR_UNSUPPORTED. */
+int hif8_gdn_decode_head(const float *conv, const uint16_t *mixed_qkvz, int64_t ld, const uint16_t *x,
+                         const uint16_t *ba_weight, int64_t hidden, const float *a_log, const float *dt_bias,
+                         float *rec_state, const uint16_t *out_norm, uint16_t *out, int64_t batch, int64_t k_heads,
+                         int64_t v_heads, int64_t k_dim, int64_t v_dim, float eps, hif8_stream_t stream);
 int hif8_qk_norm_rope(const uint16_t *qkv, const uint16_t *q_norm, const uint16_t *k_norm, const int64_t *pos,
                       const float *inv_freq, const int32_t *block_table, int64_t max_blocks, int64_t block_size,
                       uint16_t *q_out, uint16_t *k_out, uint16_t *v_out, int64_t *slots, int64_t batch,
@@ -429,10 +455,13 @@ int hif8_gdn_decode_step(const uint16_t *mixed_qkvz, int64_t ld, const uint16_t 
                          int64_t v_dim, int64_t conv_width, float eps, hif8_stream_t stream);
 /* hif8_gdn_decode_step with the b/a projection folded in (glue, no reference
  * counterpart): ba = hif8_bf16_gemv(x [batch, hidden], ba_weight [2 v_heads,
- * hidden]) computed inside, one launch instead of three, outputs and states
- * equal to the two calls bit for bit.  Needs v_heads / k_heads <= 2,
- * k_dim % 8 == 0, k_dim, v_dim <= 128, hidden % 8 == 0 and 16-byte aligned x
- * and ba_weight, else HIF8_ERR_UNSUPPORTED (run the two calls). */
+ * hidden]) computed inside, one launch instead of three; the conv state equals
+ * the two calls' bit for bit, b and a equal hif8_bf16_gemv's, the recurrent
+ * state and output agree to FP32 rounding (the state dot products are scaled
+ * by the q / k norms after the sum).  Needs v_heads / k_heads <= 2,
+ * k_dim % 8 == 0, k_dim, v_dim <= 128, hidden % 8 == 0, hidden <= 8192,
+ * conv_width <= 4 and 16-byte aligned x and ba_weight, else
+ * HIF8_ERR_UNSUPPORTED (run the two calls). */
 int hif8_gdn_decode_token(const uint16_t *mixed_qkvz, int64_t ld, const uint16_t *x, const uint16_t *ba_weight,
                           int64_t hidden, const uint16_t *conv_weight, uint16_t *conv_state, const float *a_log,
                           const float *dt_bias, float *rec_state, const uint16_t *out_norm, uint16_t *out,

@@ -121,6 +121,17 @@ def test_decode_glue_meta_shapes():
         torch.empty(2, 320, 3, dtype=torch.bfloat16, **meta), torch.empty(4, **meta), torch.empty(4, **meta),
         torch.empty(2, 4, 32, 48, **meta), torch.empty(48, dtype=torch.bfloat16, **meta), 2, 4, 32, 48, 1e-6)
     assert out.shape == (2, 4 * 48) and out.dtype == torch.bfloat16
+    y, conv = ops.hif8_linear_conv(torch.empty(2, 64, dtype=torch.uint8, **meta),
+                                   torch.empty(512, 64, dtype=torch.uint8, **meta), torch.empty(2, **meta),
+                                   torch.empty(512, **meta), torch.empty(320, 4, dtype=torch.bfloat16, **meta),
+                                   torch.empty(2, 320, 3, dtype=torch.bfloat16, **meta))
+    assert y.shape == (2, 512) and y.dtype == torch.bfloat16 and conv.shape == (2, 320) and conv.dtype == torch.float32
+    out = ops.hif8_gdn_decode_head(
+        torch.empty(2, 320, **meta), torch.empty(2, 512, dtype=torch.bfloat16, **meta),
+        torch.empty(2, 64, dtype=torch.bfloat16, **meta), torch.empty(8, 64, dtype=torch.bfloat16, **meta),
+        torch.empty(4, **meta), torch.empty(4, **meta), torch.empty(2, 4, 32, 48, **meta),
+        torch.empty(48, dtype=torch.bfloat16, **meta), 2, 4, 32, 48, 1e-6)
+    assert out.shape == (2, 4 * 48) and out.dtype == torch.bfloat16
 
 
 def test_embedding_method_validates_weights_without_a_gpu(monkeypatch):
