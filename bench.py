@@ -5,13 +5,12 @@ Headline (``value``): the decode GEMV sweep of BASELINE configs[1] - for
 M in {1, 4}, every projection of one 9B-class decoder layer (q 4096x4096,
 fused k+v 2048x4096, o 4096x4096, fused gate+up 24576x4096, down 4096x12288)
 runs the static W8A8 linear method (hif8_rocm.scheme) with its default
-routing: four token rows as hif8_static_quant of the bf16 activation, then
-soft_hif8_gemm (the HBM-streaming GEMV kernel for M <= 4); one token row
-through the fused op soft_hif8_static_fused_gemm (one launch for K <= 4096
-and N < 16384, static quant + GEMV inside the op otherwise; outputs equal to
-the two-stage route).  The reference's routing (every projection two-stage,
-HIF8_STATIC_FUSED_SINGLE_ROW=0) and every projection through the fused op
-are reported beside it.  One step = that sweep over one layer's weights; five
+routing: decode-sized inputs through the fused op soft_hif8_static_fused_gemm
+(one launch for one row with K <= 4096 and N < 16384, and for four rows with
+K <= 4096 on the MFMA-4 GEMV; hif8_static_quant then the code GEMV inside
+the op otherwise; outputs equal to the two-stage route).  The reference's
+routing (every projection as static quant + soft_hif8_gemm,
+HIF8_STATIC_FUSED_SINGLE_ROW=0) is reported beside it.  One step = that sweep over one layer's weights; five
 distinct weight copies (966 MB) are rotated so the 256 MB Infinity Cache
 cannot serve them.  Steps are captured in HIP graphs and replayed, so host
 launch overhead is not timed.
@@ -321,6 +320,15 @@ def gemv_plan(m: int, n: int, k: int, kind: int = 0):
     return buf.value.decode(), grid.value
 
 
+def fused_one_launch(m: int, n: int, k: int) -> bool:
+    """Whether soft_static_fused_linear runs one launch for these sizes (the
+    torch op's rule): one row with K <= 4096 and N < 16384, or several rows
+    whose fused-kind plan is the MFMA-4 GEMV; otherwise static quant + GEMV."""
+    if m == 1:
+        return k <= 4096 and n < 16384
+    return gemv_plan(m, n, k, 2)[0].startswith("gemv_mfma4_kernel")
+
+
 def decode_step_fn(st: Setup, copy: int, fused: bool = False):
     """One decode sweep through the scheme, or through the fused static-quant GEMV."""
     native, torch = st.native, st.torch
@@ -385,7 +393,7 @@ def per_kernel_table(st: Setup) -> dict:
                 table[f"{name}_m{m}_fused"] = {"kernel": "fused_quant_gemv", "us": round(med * 1e3, 3), "bytes": fb,
                                                "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                                                "quant_then_gemv_us": round(med2 * 1e3, 3),
-                                               "launch": kern if m == 1 and k <= 4096 and n < 16384
+                                               "launch": kern if fused_one_launch(m, n, k)
                                                else "hif8_static_quant + code GEMV", "grid": grid}
     for m, k in ((4096, 4096), (4096, 12288), (512, 4096), (1, 4096), (4, 12288)):
         x, s = st.x[(m, k)]
@@ -994,11 +1002,10 @@ def main() -> None:
     log(f"decoded-weight layer: m512 {gemm_decoded['layer_m512']['us_per_layer']} us, "
         f"m4096 {gemm_decoded['layer_m4096']['us_per_layer']} us")
     gemv = [v for v in table.values() if v["kernel"] == "gemv"]
-    # The launches of the headline step: M = 4 static quant + the code GEMV;
-    # one row through the fused op (one launch for K <= 4096, N < 16384,
-    # else static quant + the code GEMV inside the op).  The dominant launch
-    # is the longest of them.
-    step_rows = [(f"{name}_m1_fused" if m == 1 and k <= 4096 and n < 16384 else f"{name}_m{m}")
+    # The launches of the headline step: every projection through the fused
+    # op (one launch where fused_one_launch says so, else static quant + the
+    # code GEMV inside the op).  The dominant launch is the longest of them.
+    step_rows = [(f"{name}_m{m}_fused" if fused_one_launch(m, n, k) else f"{name}_m{m}")
                  for m in DECODE_M for name, n, k in LAYER]
     dom_key = max(step_rows, key=lambda r: table[r]["us"])
     best_key = max(step_rows, key=lambda r: table[r]["frac_hbm"])

@@ -143,30 +143,91 @@ __device__ __forceinline__ bool near_index_boundary(float q) {
 // MI355X, rounding the quotient's bits arithmetically instead (about 20 VALU
 // operations per element) made the fused GEMV 20-30 % slower, since every
 // block re-encodes its activation chunk.
+// All 16 take the multiply first; one branch (rarely taken) redoes the 16
+// with the division, so the kernel holds one copy of the division code per
+// 16 values instead of one per pair.
 template <bool kBf16, class Lut>
 __device__ __forceinline__ void fast_encode_decode16(const u32x4 a, const u32x4 b, float s, float r,
                                                      const uint8_t *enc, const Lut &dec, u32x4 &lo,
                                                      u32x4 &hi) {
-  uint32_t p[8];
+  uint32_t u[16];
+  bool redo = false;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
     const uint32_t w = i < 4 ? a[i] : b[i - 4];
-    const float x0 = lo_to_float<kBf16>(w), x1 = hi_to_float<kBf16>(w);
-    float q0 = x0 * r, q1 = x1 * r;
-    uint32_t c0, c1;
-    if (__builtin_expect(near_index_boundary(q0) || near_index_boundary(q1), 0)) {
-      q0 = x0 / s;
-      q1 = x1 / s;
-      c0 = __builtin_isnan(q0) ? uint32_t(kNan) : enc[__float_as_uint(q0) >> 19];
-      c1 = __builtin_isnan(q1) ? uint32_t(kNan) : enc[__float_as_uint(q1) >> 19];
-    } else {
-      c0 = enc[__float_as_uint(q0) >> 19];
-      c1 = enc[__float_as_uint(q1) >> 19];
-    }
-    p[i] = uint32_t(dec.code(c0)) | (uint32_t(dec.code(c1)) << 16);
+    const float q0 = lo_to_float<kBf16>(w) * r, q1 = hi_to_float<kBf16>(w) * r;
+    redo |= near_index_boundary(q0) | near_index_boundary(q1);
+    u[2 * i] = __float_as_uint(q0);
+    u[2 * i + 1] = __float_as_uint(q1);
   }
+  if (__builtin_expect(redo, 0)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w = i < 4 ? a[i] : b[i - 4];
+      const float q0 = lo_to_float<kBf16>(w) / s, q1 = hi_to_float<kBf16>(w) / s;
+      // NaN quotients index an entry of exponent 0xFF whose top mantissa bit
+      // is set, which encodes to the NaN code.
+      u[2 * i] = __builtin_isnan(q0) ? 0x7FC00000u : __float_as_uint(q0);
+      u[2 * i + 1] = __builtin_isnan(q1) ? 0x7FC00000u : __float_as_uint(q1);
+    }
+  }
+  uint32_t p[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    p[i] = uint32_t(dec.code(enc[u[2 * i] >> 19])) | (uint32_t(dec.code(enc[u[2 * i + 1] >> 19])) << 16);
   lo = u32x4{p[0], p[1], p[2], p[3]};
   hi = u32x4{p[4], p[5], p[6], p[7]};
+}
+
+// Quantise-dequantise table of the fused static kinds in the MFMA-4 GEMV:
+// entry i (the 13-bit sign / exponent / top-four-mantissa index of an FP32
+// quotient x / s, the index of Tables::static_encode) holds the bf16 bits of
+// dec(static_encode[i]).  One lookup instead of the encode and decode lookups;
+// 16 KiB, copied into LDS by each block.
+struct QdqTable {
+  uint16_t v[8192];
+};
+
+constexpr QdqTable make_qdq_table() {
+  QdqTable t{};
+  for (uint32_t i = 0; i < 8192; ++i) t.v[i] = uint16_t(decode_bits(static_encode_bits(i << 19)) >> 16);
+  return t;
+}
+
+static __device__ const QdqTable kQdqTable = make_qdq_table();
+
+// Static encode + decode of 16 fp16/bf16 values into bf16 pairs through the
+// quantise-dequantise table: the same reciprocal multiply, boundary test and
+// IEEE-division redo as fast_encode_decode16, so each value equals
+// dec(the standalone quant's code).  All 16 take the multiply first; one
+// branch (rarely taken: a quotient within 8 ulps of an index boundary, or
+// NaN) redoes the 16 with the division, so the kernel holds one copy of the
+// division code per 16 values instead of one per pair.
+template <bool kBf16>
+__device__ __forceinline__ void fast_qdq16(const u32x4 a, const u32x4 b, float s, float r, const uint16_t *qdq,
+                                           uint32_t (&p)[8]) {
+  uint32_t u[16];
+  bool redo = false;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t w = i < 4 ? a[i] : b[i - 4];
+    const float q0 = lo_to_float<kBf16>(w) * r, q1 = hi_to_float<kBf16>(w) * r;
+    redo |= near_index_boundary(q0) | near_index_boundary(q1);
+    u[2 * i] = __float_as_uint(q0);
+    u[2 * i + 1] = __float_as_uint(q1);
+  }
+  if (__builtin_expect(redo, 0)) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t w = i < 4 ? a[i] : b[i - 4];
+      const float q0 = lo_to_float<kBf16>(w) / s, q1 = hi_to_float<kBf16>(w) / s;
+      // NaN quotients index the NaN entries of exponent 0xFF.
+      u[2 * i] = __builtin_isnan(q0) ? 0x7FC00000u : __float_as_uint(q0);
+      u[2 * i + 1] = __builtin_isnan(q1) ? 0x7FC00000u : __float_as_uint(q1);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 8; ++i) p[i] = uint32_t(qdq[u[2 * i] >> 19]) | (uint32_t(qdq[u[2 * i + 1] >> 19]) << 16);
 }
 
 constexpr int pow2_floor(int v) {
@@ -566,18 +627,28 @@ __device__ __forceinline__ float row_quad_sum(float v) {
 
 // kPasses: 1..3 passes of 4096 k bytes per block, unrolled (k <= 4096 kPasses),
 // or 0 for any k (a loop without prefetch).
-template <int kM, int kR, int kPasses, bool kRep>
+// kSrc: code activations (kActCodes, act = uint8 [M, k], act_scale = the
+// token scales) or the fused static kinds (kActF16 / kActBf16, act = x [M, k],
+// act_scale = the fixed scale [1]): each lane encodes and decodes its own
+// activation chunks through the quantise-dequantise table (QdqTable), whose
+// 16 KiB copy is requested before the chunk loads, so the table stores wait
+// for its loads alone.
+template <int kM, int kR, int kPasses, bool kRep, int kSrc>
 __global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
-    const uint8_t *act, const float *__restrict__ act_scale, const uint8_t *weight, const float *__restrict__ cs,
+    const void *act, const float *__restrict__ act_scale, const uint8_t *weight, const float *__restrict__ cs,
     const void *__restrict__ bias, int bias_dtype, void *__restrict__ out, int out_dtype, int n, int k,
     const GemvConv conv) {
   static_assert(kR % 4 == 0 && kR <= 16 && kM >= 1 && kM <= 4, "row groups of four, up to four activation rows");
+  static_assert(kSrc == kActCodes || kSrc == kActF16 || kSrc == kActBf16, "codes or a fixed activation scale");
+  constexpr bool kFused = kSrc != kActCodes;
+  constexpr int kAW = kFused ? 2 : 1;     // 16-byte words of activation per chunk
   constexpr int kG = kR / 4;              // row groups
   constexpr int kWaves = kThreads / kWave;
   constexpr int kPass = 16 * kThreads;    // k bytes per pass of the block
   // The decode table first, at LDS address 0.
   __shared__ __attribute__((aligned(16))) uint8_t dec_tab[kRep ? kRepLutBytes : 512];
   __shared__ __attribute__((aligned(16))) float red[kWaves][kR][4];
+  __shared__ __attribute__((aligned(16))) uint16_t qdq[kFused ? 8192 : 8];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const auto dec_lut = decode_lut<kRep>(dec_tab, lane);
@@ -589,12 +660,14 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
   const uint8_t *wrow[kG];
 #pragma unroll
   for (int g = 0; g < kG; ++g) wrow[g] = weight + size_t(min(n0 + 4 * g + j, n - 1)) * k;
-  const uint8_t *arow = act + size_t(min(j, kM - 1)) * k;
+  // 16-byte words of the activation row: codes, or x (two words per chunk).
+  const u32x4 *arow = reinterpret_cast<const u32x4 *>(static_cast<const uint8_t *>(act) +
+                                                      size_t(min(j, kM - 1)) * k * (kFused ? 2 : 1));
   const bool act_lane = j < kM;
 
-  // Codes of one pass: weight rows [group][step s], activation [step s].
+  // Operands of one pass: weight codes [group][step s], activation [step s].
   struct Pass {
-    u32x4 w[kG][4], a[4];
+    u32x4 w[kG][4], a[4][kAW];
   };
   // Chunk of step s in the pass starting at chunk p0; past the last chunk the
   // lane re-reads it and zeroes the codes (code 0 decodes to +0, and both
@@ -603,7 +676,8 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const int c = min(p0 + 64 * wave + 16 * s + b, chunks - 1);
-      q.a[s] = reinterpret_cast<const u32x4 *>(arow)[c];
+#pragma unroll
+      for (int h = 0; h < kAW; ++h) q.a[s][h] = arow[kAW * c + h];
     }
 #pragma unroll
     for (int g = 0; g < kG; ++g)
@@ -614,10 +688,22 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
       }
   };
   Pass cur;
+  constexpr int kQdqWords = kFused ? 8192 * 2 / 16 / kThreads : 1;  // 16-byte table words per thread
+  u32x4 qdq_part[kQdqWords];
+  if constexpr (kFused) {
+#pragma unroll
+    for (int i = 0; i < kQdqWords; ++i) qdq_part[i] = reinterpret_cast<const u32x4 *>(kQdqTable.v)[tid + i * kThreads];
+  }
   uint32_t entry = kRep ? 0u : decode_entry(tid);  // order as in gemv_kernel
   load(cur, 0);
   if constexpr (kRep) entry = decode_entry(tid);
   fill_decode_table<kRep>(dec_tab, tid, entry);
+  if constexpr (kFused) {
+#pragma unroll
+    for (int i = 0; i < kQdqWords; ++i) reinterpret_cast<u32x4 *>(qdq)[tid + i * kThreads] = qdq_part[i];
+  }
+  const float fixed = kFused ? act_scale[0] : 0.f;
+  const float rcp = kFused ? __builtin_amdgcn_rcpf(fixed) : 0.f;
   __builtin_amdgcn_sched_barrier(0);
   lds_barrier();
 
@@ -631,11 +717,33 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
     bool cv[4];
 #pragma unroll
     for (int s = 0; s < 4; ++s) cv[s] = !kTail || p0 + 64 * wave + 16 * s + b < chunks;
+    if constexpr (kFused) {
+      // Step by step (encode the activation chunk, then its products), each
+      // step fenced from the next: one step's encode temporaries live at a
+      // time, which keeps the kernel near the code kind's register count.
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bool live = act_lane && cv[s];
+        uint32_t as[8];
+        fast_qdq16<kSrc == kActBf16>(live ? q.a[s][0] : u32x4{0, 0, 0, 0}, live ? q.a[s][1] : u32x4{0, 0, 0, 0},
+                                     fixed, rcp, qdq, as);
+#pragma unroll
+        for (int g = 0; g < kG; ++g) {
+          uint32_t p[8];
+          decode16(dec_lut, !kTail || cv[s] ? q.w[g][s] : u32x4{0, 0, 0, 0}, p);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) acc[g] = mfma4(p[2 * d], p[2 * d + 1], as[2 * d], as[2 * d + 1], acc[g]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      return;
+    }
     uint32_t ad[4][8];  // activation row j as bf16 pairs, per step s
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
-      const u32x4 a = act_lane && cv[s] ? q.a[s] : u32x4{0, 0, 0, 0};
-      decode16(dec_lut, a, ad[s]);
+      // Rows past M and chunks past k take zero codes / zero x (both give +0).
+      const bool live = act_lane && cv[s];
+      decode16(dec_lut, live ? q.a[s][0] : u32x4{0, 0, 0, 0}, ad[s]);
     }
 #pragma unroll
     for (int s = 0; s < 4; ++s)
@@ -710,7 +818,7 @@ __global__ __launch_bounds__(kThreads, 2) void gemv_mfma4_kernel(
       float sum = 0.f;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) sum += red[w][r][m];
-      float y = sum * act_scale[m] * cs[row];
+      float y = sum * (kFused ? fixed : act_scale[m]) * cs[row];
       if (bias) y += load_bias(bias, bias_dtype, row);
       store_out(out, out_dtype, size_t(m) * n + row, y);
       if (row < conv.channels) conv_epilogue(conv, m, row, y);
@@ -1027,7 +1135,7 @@ GemvPlan plan_gemv(int64_t m, int64_t n, int64_t k, int act_kind, bool vec) {
     p.kind = kGemvMfma16;
     p.rows = 16;
     p.threads = kMfmaThreads;
-  } else if (knobs.kernel != 'd' && act_kind == kActCodes &&
+  } else if (knobs.kernel != 'd' && (act_kind == kActCodes || act_kind == kActF16 || act_kind == kActBf16) &&
              ((k <= 16 * kThreads && (m == 4 || (m == 3 && wide))) || (knobs.kernel == '4' && m >= 2))) {
     // Code activations, four rows (three over wide weights), k <= 4096: the
     // MFMA does the products.  Measured on MI355X (graphs of 20 launches over
@@ -1051,8 +1159,12 @@ GemvPlan plan_gemv(int64_t m, int64_t n, int64_t k, int act_kind, bool vec) {
   p.grid = unsigned((n + p.rows - 1) / p.rows);
   // The replicated table for grids of one round, except the single-row k
   // loop (down 4096 x 12288 at M = 1: 11.07 vs 10.85 us on MI355X).
-  p.rep = knobs.lut == 'r' ||
-          (knobs.lut != 'c' && p.grid <= kRepMaxBlocks && !(m == 1 && p.kind == kGemvDot2 && !p.one_chunk));
+  // The fused static kinds of the MFMA-4 kernel hold a 16 KiB
+  // quantise-dequantise table, with which the 64 KiB replicated table would
+  // no longer leave room for two blocks per CU: they take the plain table.
+  const bool mfma4_fused = p.kind == kGemvMfma4 && act_kind != kActCodes;
+  p.rep = !mfma4_fused && (knobs.lut == 'r' || (knobs.lut != 'c' && p.grid <= kRepMaxBlocks &&
+                                                 !(m == 1 && p.kind == kGemvDot2 && !p.one_chunk)));
   return p;
 }
 
@@ -1062,12 +1174,11 @@ int mfma4_passes(int64_t k) {
   return passes <= 3 ? int(passes) : 0;
 }
 
-template <int kM, int kR, bool kRep>
+template <int kM, int kR, bool kRep, int kSrc>
 void launch_mfma4_t(const LinearArgs &a, const GemvPlan &p) {
-  const uint8_t *act = static_cast<const uint8_t *>(a.act);
 #define HIF8_MFMA4_LAUNCH(P)                                                                              \
-  gemv_mfma4_kernel<kM, kR, P, kRep><<<p.grid, kThreads, 0, a.stream>>>(                                \
-      act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.n), int(a.k), \
+  gemv_mfma4_kernel<kM, kR, P, kRep, kSrc><<<p.grid, kThreads, 0, a.stream>>>(                          \
+      a.act, a.act_scale, a.weight, a.channel_scale, a.bias, a.bias_dtype, a.out, a.out_dtype, int(a.n), int(a.k), \
       a.conv)
   // Two register sets of more than eight rows exceed the register file.
   constexpr bool kTwoSets = kR <= 8;
@@ -1080,10 +1191,20 @@ void launch_mfma4_t(const LinearArgs &a, const GemvPlan &p) {
 #undef HIF8_MFMA4_LAUNCH
 }
 
+// The fused kinds always take the plain table (see plan_gemv).
+template <int kM, int kR, int kSrc>
+void launch_mfma4_s(const LinearArgs &a, const GemvPlan &p) {
+  if (kSrc == kActCodes && p.rep) launch_mfma4_t<kM, kR, kSrc == kActCodes, kSrc>(a, p);
+  else launch_mfma4_t<kM, kR, false, kSrc>(a, p);
+}
+
 template <int kM, int kR>
 void launch_mfma4(const LinearArgs &a, const GemvPlan &p) {
-  if (p.rep) launch_mfma4_t<kM, kR, true>(a, p);
-  else launch_mfma4_t<kM, kR, false>(a, p);
+  switch (a.act_kind) {
+    case kActCodes: launch_mfma4_s<kM, kR, kActCodes>(a, p); break;
+    case kActF16: launch_mfma4_s<kM, kR, kActF16>(a, p); break;
+    default: launch_mfma4_s<kM, kR, kActBf16>(a, p); break;
+  }
 }
 
 template <int kR>
@@ -1171,8 +1292,8 @@ int describe_gemv(int64_t m, int64_t n, int64_t k, int act_kind, char *name, siz
       case kGemvSimple: snprintf(name, name_len, "gemv_simple_kernel"); break;
       case kGemvMfma16: snprintf(name, name_len, "gemv_mfma_kernel<%lld, %d>", (long long)m, act_kind); break;
       case kGemvMfma4:
-        snprintf(name, name_len, "gemv_mfma4_kernel<%lld, %d, %d, %s>", (long long)m, p.rows,
-                 p.rows > 8 && mfma4_passes(k) > 1 ? 0 : mfma4_passes(k), p.rep ? "true" : "false");
+        snprintf(name, name_len, "gemv_mfma4_kernel<%lld, %d, %d, %s, %d>", (long long)m, p.rows,
+                 p.rows > 8 && mfma4_passes(k) > 1 ? 0 : mfma4_passes(k), p.rep ? "true" : "false", act_kind);
         break;
       default: {
         const bool dyn = act_kind == kActF16Dyn || act_kind == kActBf16Dyn;

@@ -11,6 +11,7 @@
 // attention that replace the reference's quant + pack + index_copy_ and
 // gather + decode + fused-attention sequences (kv_runtime.py:1222-1563).
 #include <cstdlib>
+#include <cstring>
 #include <c10/core/DeviceGuard.h>
 #include <c10/hip/HIPStream.h>
 #include <torch/extension.h>
@@ -295,17 +296,37 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
     const char *v = getenv("HIF8_FUSED_MAX_N");
     return v && *v ? int64_t(atoll(v)) : int64_t(16383);
   }();
-  if (m >= 2 || k > 4096 || n > max_n) {
-    // Every block of the single-launch kernel encodes its whole activation
-    // chunk, which costs more than a separate quant launch once there are
-    // several rows (measured on MI355X in graphs at M = 4: q 4096x4096 14.3
-    // vs 9.9 us, gate_up 24576x4096 38.1 vs 26.6).  One row with K <= 4096
-    // and N < 16384 (one chunk per thread, loaded before the table set-up,
-    // at most 2048 blocks) is faster fused every time (q 6.5 vs 8.7-9.0 us,
-    // k/v 2048x4096 5.0-5.2 vs 7.6, o 6.6-6.7 vs 8.3-8.8, 12288x4096 12.4 vs
-    // 14.0); gate_up (N = 24576, each of 2048 blocks re-encoding: 21.5-22.9
-    // vs 21.5-21.7 us) and down (K = 12288, the chunk loop: 13.6-14.7 vs
-    // 13.7-16.0) keep two launches.
+  // Several rows run as one launch where the fused kind's plan is the MFMA-4
+  // GEMV (K <= 4096, M = 4, or M = 3 over N >= 16384) and N <= 2048 (tuning
+  // knob HIF8_FUSED_MULTI_MAX_N, read once).  Every block re-encodes all M
+  // rows (about 14 VALU operations per value), so the one launch wins only
+  // where the grid is small; measured on MI355X in graphs at M = 4 against
+  // static quant + GEMV: k/v 2048x4096 8.2 vs 8.5 us, q 4096x4096 11.5 vs
+  // 10.2, gate_up 24576x4096 31.7 vs 23.9.
+  static const int64_t multi_max_n = [] {
+    const char *v = getenv("HIF8_FUSED_MULTI_MAX_N");
+    return v && *v ? int64_t(atoll(v)) : int64_t(2048);
+  }();
+  bool multi_fused = false;
+  if (m >= 2 && n <= multi_max_n) {
+    char kernel[96] = {0};
+    int64_t grid = 0;
+    multi_fused = hif8_gemv_launch_plan(m, n, k, activation.scalar_type() == at::ScalarType::BFloat16
+                                                     ? HIF8_ACT_BF16_STATIC : HIF8_ACT_F16_STATIC,
+                                        kernel, sizeof(kernel), &grid) == HIF8_OK &&
+                  strncmp(kernel, "gemv_mfma4_kernel", 17) == 0;
+  }
+  if (m >= 2 ? !multi_fused : (k > 4096 || n > max_n)) {
+    // Every block of the dot2 kernel's fused kinds encodes its whole
+    // activation chunk, which costs more than a separate quant launch once
+    // there are several rows (measured on MI355X in graphs at M = 4: q
+    // 4096x4096 14.3 vs 9.9 us, gate_up 24576x4096 38.1 vs 26.6).  One row
+    // with K <= 4096 and N < 16384 (one chunk per thread, loaded before the
+    // table set-up, at most 2048 blocks) is faster fused every time (q 6.5
+    // vs 8.7-9.0 us, k/v 2048x4096 5.0-5.2 vs 7.6, o 6.6-6.7 vs 8.3-8.8,
+    // 12288x4096 12.4 vs 14.0); gate_up (N = 24576, each of 2048 blocks
+    // re-encoding: 21.5-22.9 vs 21.5-21.7 us) and down (K = 12288, the chunk
+    // loop: 13.6-14.7 vs 13.7-16.0) keep two launches.
     // The two launches give the same codes and the same GEMV, hence equal
     // outputs.
     auto codes = at::empty({m, k}, activation.options().dtype(at::ScalarType::Byte));

@@ -6,23 +6,24 @@ holds ``weight`` uint8 [N, K], ``weight_scale`` float32 [N, 1] and
 ``input_scale`` float32 [1]; ``apply`` statically quantises the activation and
 runs the soft HiF8 linear.
 
-Routing is the reference's by default (scheme.py:181-189): the fused
-static-quant GEMV only when ``HIF8_STATIC_FUSED_GENERATION=1``, M <= 4 and
-K < 1024, because on its hardware the fused kernel pays a global barrier.
-The MI355X fused kernel has none (every block encodes its own activation
-chunk) and its outputs equal quant -> GEMM bit for bit.  Measured on
-MI355X in HIP graphs, one token row of the q, fused k/v and o shapes is
-faster fused (q 6.5 vs 8.7-9.0 us, k/v 5.0-5.2 vs 7.6, o 6.6-6.7 vs
-8.3-8.8: the separate quant launch costs 2-3 us of launch and cold-cache
-latency), while four rows are faster separate (each block re-encodes M*K
-values: q 14.3 vs 9.9 us) and gate_up and down measured either way, so the
-fused op itself runs those (M >= 2, K > 4096 or N >= 16384) as
-quant + GEMV.
-One token row therefore goes through the fused op by default (one launch
-for K <= 4096 and N < 16384); ``HIF8_STATIC_FUSED_SINGLE_ROW=0`` restores
+The reference routes the fused static-quant GEMV only when
+``HIF8_STATIC_FUSED_GENERATION=1``, M <= 4 and K < 1024 (scheme.py:181-189),
+because on its hardware the fused kernel pays a global barrier.  The MI355X
+fused kernels have none (every block encodes its own activation chunk) and
+their outputs equal quant -> GEMM bit for bit.  Measured on MI355X in HIP
+graphs, the separate quant launch costs 2-4 us of launch and cold-cache
+latency, so decode-sized inputs go through the fused op by default: up to
+``HIF8_STATIC_FUSED_ROWS`` token rows (default 4).  The op itself picks one
+launch or quant + GEMV per shape: one row with K <= 4096 and N < 16384 runs
+the one-row fused kernel (q 6.8 vs 9.0 us, k/v 5.0 vs 7.6, o 6.8 vs 9.0);
+four rows with K <= 4096 and N <= 2048 run the MFMA-4 GEMV's fused kind (k/v
+8.2 vs 8.5 us; with more blocks the per-block re-encode of the rows costs
+more than the quant launch); other shapes run quant + GEMV.
+``HIF8_STATIC_FUSED_SINGLE_ROW=0`` or ``HIF8_STATIC_FUSED_ROWS=0`` restores
 the reference's routing (static_quant -> soft_linear unless
-``HIF8_STATIC_FUSED_GENERATION=1``, M <= 4, K < 1024, scheme.py:183-190).
-It changes which kernels run, not the outputs (equal bit for bit).
+``HIF8_STATIC_FUSED_GENERATION=1``, M <= 4, K < 1024, scheme.py:183-190);
+``HIF8_STATIC_FUSED_ROWS=1`` fuses one row only.  The routing changes which
+kernels run, not the outputs (equal bit for bit).
 
 ``HIF8_PREFILL_BF16_WEIGHTS=1`` (read in ``process_weights_after_loading``)
 keeps each weight decoded to bf16 beside its codes (2 bytes per element;
@@ -46,10 +47,26 @@ _COMPUTE_BACKEND_ENV = "HIF8_COMPUTE_BACKEND"
 _SOFT_HIF8_BACKEND = "soft_hif8"
 _STATIC_FUSED_GENERATION_ENV = "HIF8_STATIC_FUSED_GENERATION"
 _STATIC_SCALE_FACTOR_ENV = "HIF8_STATIC_SCALE_FACTOR"
-# MI355X opt-in: fuse one token row (measured; see the module text).
+# MI355X routing of decode-sized inputs through the fused op (see the module
+# text): "0" in either variable restores the reference's routing.
 _STATIC_FUSED_SINGLE_ROW_ENV = "HIF8_STATIC_FUSED_SINGLE_ROW"
+_STATIC_FUSED_ROWS_ENV = "HIF8_STATIC_FUSED_ROWS"
 # MI355X opt-in: keep each static weight decoded to bf16 for prefill GEMMs.
 _PREFILL_BF16_WEIGHTS_ENV = "HIF8_PREFILL_BF16_WEIGHTS"
+
+
+def _fused_rows() -> int:
+    """Token rows up to which apply() routes through the fused op (0..4)."""
+    if os.environ.get(_STATIC_FUSED_SINGLE_ROW_ENV, "1") == "0":
+        return 0
+    raw = os.environ.get(_STATIC_FUSED_ROWS_ENV)
+    if raw is None or raw == "":
+        return 4
+    try:
+        rows = int(raw)
+    except ValueError as exc:
+        raise ValueError(f"{_STATIC_FUSED_ROWS_ENV} must be an integer, got {raw!r}") from exc
+    return max(0, min(rows, 4))
 
 
 def _static_scale_factor() -> float:
@@ -130,14 +147,15 @@ class W8A8HiFloat8StaticLinearMethod:
         """static_quant -> soft_linear, or the fused kernel (scheme.py:174-211).
 
         Fused when the reference would fuse (``HIF8_STATIC_FUSED_GENERATION=1``,
-        M <= 4, K < 1024) and for one token row unless
-        ``HIF8_STATIC_FUSED_SINGLE_ROW=0``; the two routes give equal outputs."""
+        M <= 4, K < 1024) and for up to ``HIF8_STATIC_FUSED_ROWS`` token rows
+        (default 4; 0 or ``HIF8_STATIC_FUSED_SINGLE_ROW=0`` turns it off); the
+        routes give equal outputs."""
         del tp_rank
         token_rows = x.numel() // x.shape[-1]
         k = x.shape[-1]
         use_fused = (
             token_rows <= 4 and os.environ.get(_STATIC_FUSED_GENERATION_ENV) == "1" and k < 1024
-        ) or (token_rows == 1 and os.environ.get(_STATIC_FUSED_SINGLE_ROW_ENV, "1") != "0")
+        ) or token_rows <= _fused_rows()
         scale_factor = _static_scale_factor()
         fixed_scale = layer.input_scale
         if scale_factor != 1.0:

@@ -189,6 +189,44 @@ def test_static_fused_matches_static_quant_then_gemm(native_ops, device):
         assert torch.equal(got, want), (rows, channels, k)
 
 
+@pytest.mark.parametrize("xdtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,channels,k", [(4, 256, 4096), (4, 136, 1040), (3, 16400, 4096), (4, 40, 64),
+                                             (2, 64, 4096), (3, 96, 2048)])
+def test_static_fused_multi_row_equals_quant_then_gemm(native_ops, device, rows, channels, k, xdtype):
+    """Several rows through the fused op - one launch of the MFMA-4 kernel's
+    fused kind where it is the plan (K <= 4096 at M = 4, or M = 3 over
+    N >= 16384), quant + GEMV otherwise - give the two-stage outputs bit for
+    bit, NaN / Inf / saturating values, quotients at encode-index boundaries,
+    all-zero-code rows, partial passes and row tails included."""
+    g = torch.Generator().manual_seed(rows * 7919 + channels * 31 + k)
+    x = torch.randn(rows, k, generator=g) * 3.0
+    fixed = torch.tensor([0.75])
+    # Quotients exactly on index boundaries: (1 + (2j + 1) / 32) * 2^e * s
+    # are the midpoints between neighbouring three-bit mantissas.
+    j = torch.arange(min(k, 512))
+    x[0, : j.numel()] = (1.0 + (2 * (j % 16) + 1) / 32.0) * torch.pow(2.0, (j % 9 - 4).float()) * 0.75
+    x[rows - 1, 3] = float("nan")
+    x[rows - 1, 5] = float("inf")
+    x[rows - 1, 7] = -float("inf")
+    x[min(1, rows - 1), 9] = 1.0e5
+    if rows >= 3:
+        x[2] = torch.randn(k, generator=g) * 1.0e-9  # every code of this row is zero
+    x = x.to(xdtype).to(device)
+    w = torch.randint(0, 111, (channels, k), generator=g, dtype=torch.uint8)
+    w[:, 5] = 0  # keep Inf x 0 away from every row but one column
+    w[0, 5] = 8
+    w = w.to(device)
+    cs = (torch.rand(channels, generator=g) + 0.01).to(device)
+    bias = torch.randn(channels, generator=g).to(torch.bfloat16).to(device)
+    fixed = fixed.to(device)
+    data, row_scale = native_ops.hif8_static_quant(x, fixed)
+    for out_dtype in (torch.bfloat16, torch.float16):
+        want = native_ops.soft_hif8_gemm(data, w, row_scale.contiguous(), cs, bias, out_dtype)
+        got = native_ops.soft_hif8_static_fused_gemm(x, w, fixed, cs, bias, out_dtype)
+        torch.cuda.synchronize()
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16)), (rows, channels, k, out_dtype)
+
+
 def test_static_fused_saturates_finite_outliers(native_ops, device):
     k = 2048
     x = torch.zeros((1, k), dtype=torch.bfloat16)

@@ -224,7 +224,7 @@ def _layer(input_scale=0.25, k=8):
 def clean_env():
     with patch.dict(os.environ, {}, clear=False):
         for var in ("HIF8_COMPUTE_BACKEND", "HIF8_STATIC_FUSED_GENERATION", "HIF8_STATIC_SCALE_FACTOR",
-                    "HIF8_STATIC_FUSED_SINGLE_ROW", "HIF8_PREFILL_BF16_WEIGHTS"):
+                    "HIF8_STATIC_FUSED_SINGLE_ROW", "HIF8_STATIC_FUSED_ROWS", "HIF8_PREFILL_BF16_WEIGHTS"):
             os.environ.pop(var, None)
         yield
 
@@ -260,8 +260,8 @@ def test_apply_defaults_to_standalone_static_quant(clean_env):
     layer = _layer()
     method.process_weights_after_loading(layer)
     assert tuple(layer.weight_scale.shape) == (5,)
-    x = torch.randn((3, 8), dtype=torch.bfloat16)
-    enc, rs, out = torch.zeros_like(x, dtype=torch.uint8), torch.full((3,), 0.25), torch.randn(3, 5)
+    x = torch.randn((5, 8), dtype=torch.bfloat16)  # more rows than the decode-sized fused route takes
+    enc, rs, out = torch.zeros_like(x, dtype=torch.uint8), torch.full((5,), 0.25), torch.randn(5, 5)
     with patch("hif8_rocm.scheme.native.static_quant", return_value=(enc, rs)) as sq, \
          patch("hif8_rocm.scheme.native.soft_static_fused_linear") as fused, \
          patch("hif8_rocm.scheme.native.soft_linear", return_value=out) as lin:
@@ -300,20 +300,25 @@ def test_fused_generation_is_opt_in_and_limited_to_small_shapes(clean_env):
         fused.assert_not_called()
 
 
-def test_single_row_fusion_is_the_default_with_an_opt_out(clean_env):
-    """One token row goes through the fused op by default, whatever K, and
-    nothing else does; HIF8_STATIC_FUSED_SINGLE_ROW=0 restores the
-    reference's two-stage routing."""
+def test_decode_row_fusion_is_the_default_with_an_opt_out(clean_env):
+    """Up to four token rows go through the fused op by default, whatever K,
+    and nothing larger does; HIF8_STATIC_FUSED_SINGLE_ROW=0 or
+    HIF8_STATIC_FUSED_ROWS=0 restores the reference's two-stage routing and
+    HIF8_STATIC_FUSED_ROWS=1 fuses one row only."""
     method = W8A8HiFloat8StaticLinearMethod()
     out = torch.randn(1, 5)
-    cases = [(None, (1, 4096), True), ("1", (1, 4096), True), ("0", (1, 4096), False), (None, (1, 8), True),
-             (None, (2, 4096), False), ("1", (3, 64), False), (None, (1, 12288), True), ("0", (1, 12288), False),
-             ("0", (1, 64), False)]
-    for flag, shape, want_fused in cases:
-        if flag is None:
-            os.environ.pop("HIF8_STATIC_FUSED_SINGLE_ROW", None)
-        else:
-            os.environ["HIF8_STATIC_FUSED_SINGLE_ROW"] = flag
+    cases = [(None, None, (1, 4096), True), ("1", None, (1, 4096), True), ("0", None, (1, 4096), False),
+             (None, None, (1, 8), True), (None, None, (2, 4096), True), ("1", None, (3, 64), True),
+             (None, None, (4, 4096), True), (None, None, (5, 4096), False), (None, None, (1, 12288), True),
+             ("0", None, (1, 12288), False), ("0", None, (1, 64), False), ("0", "4", (4, 64), False),
+             (None, "0", (1, 4096), False), (None, "1", (1, 4096), True), (None, "1", (2, 4096), False),
+             (None, "3", (3, 4096), True), (None, "3", (4, 4096), False), (None, "9", (4, 64), True)]
+    for flag, rows_env, shape, want_fused in cases:
+        for var, val in (("HIF8_STATIC_FUSED_SINGLE_ROW", flag), ("HIF8_STATIC_FUSED_ROWS", rows_env)):
+            if val is None:
+                os.environ.pop(var, None)
+            else:
+                os.environ[var] = val
         layer = _layer(k=shape[1])
         method.process_weights_after_loading(layer)
         x = torch.zeros(shape, dtype=torch.bfloat16)
@@ -322,7 +327,7 @@ def test_single_row_fusion_is_the_default_with_an_opt_out(clean_env):
              patch("hif8_rocm.scheme.native.soft_linear", return_value=out), \
              patch("hif8_rocm.scheme.native.soft_static_fused_linear", return_value=out) as fused:
             method.apply(layer, x)
-        assert fused.called == want_fused and sq.called != want_fused, (flag, shape)
+        assert fused.called == want_fused and sq.called != want_fused, (flag, rows_env, shape)
         if want_fused:
             fused.assert_called_once_with(x, layer.weight, layer.input_scale, layer.weight_scale, None,
                                           output_dtype=x.dtype)
@@ -369,12 +374,12 @@ def test_scale_factor_env_multiplies_the_checkpoint_scale(clean_env):
     method = W8A8HiFloat8StaticLinearMethod()
     layer = _layer(0.25)
     method.process_weights_after_loading(layer)
-    x = torch.zeros((2, 8), dtype=torch.bfloat16)
-    with patch("hif8_rocm.scheme.native.static_quant", return_value=(x.to(torch.uint8), torch.ones(2))) as sq, \
-         patch("hif8_rocm.scheme.native.soft_linear", return_value=torch.zeros(2, 5)):
+    x = torch.zeros((6, 8), dtype=torch.bfloat16)
+    with patch("hif8_rocm.scheme.native.static_quant", return_value=(x.to(torch.uint8), torch.ones(6))) as sq, \
+         patch("hif8_rocm.scheme.native.soft_linear", return_value=torch.zeros(6, 5)):
         method.apply(layer, x)
     assert float(sq.call_args[0][1]) == 0.5
-    # One row takes the fused op, with the same scaled fixed scale.
+    # Decode-sized inputs take the fused op, with the same scaled fixed scale.
     with patch("hif8_rocm.scheme.native.soft_static_fused_linear", return_value=torch.zeros(1, 5)) as fused:
         method.apply(layer, x[:1])
     assert float(fused.call_args[0][2]) == 0.5
