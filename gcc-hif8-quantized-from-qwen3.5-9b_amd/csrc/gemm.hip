@@ -64,29 +64,35 @@ __device__ __forceinline__ void decode16(const uint16_t *lut, const u32x4 q, u32
   hi = u32x4{p[4], p[5], p[6], p[7]};
 }
 
-// Codes [rows, K] -> bf16 [rows, K], 16 codes per thread and pass.  The
-// table is computed (one entry per thread), so the first chunk's load goes
-// out before it and stays in flight across the LDS-only barrier; each pass
-// loads the next chunk before decoding the current one (a chunk past the end
-// re-reads the last one, unused).
+// Codes [rows, K] -> bf16 [rows, K], 16 codes per thread and pass, over one
+// or two independent ranges (a: `chunks` 16-code chunks into out, then b:
+// `chunks_b` chunks into out_b), walked as one index space so that one launch
+// decodes both GEMM operands.  The table is computed (one entry per thread),
+// so the first chunk's load goes out before it and stays in flight across the
+// LDS-only barrier; each pass loads the next chunk before decoding the
+// current one (a chunk past the end re-reads the last one, unused).
 __global__ __launch_bounds__(256) void decode_rows_kernel(const uint8_t *__restrict__ a,
-                                                          uint16_t *__restrict__ out, size_t chunks) {
+                                                          uint16_t *__restrict__ out, size_t chunks,
+                                                          const uint8_t *__restrict__ b,
+                                                          uint16_t *__restrict__ out_b, size_t chunks_b) {
   __shared__ __attribute__((aligned(16))) uint16_t lut[256];
-  if (chunks == 0) return;
+  const size_t total = chunks + chunks_b;
+  if (total == 0) return;
   const size_t stride = size_t(gridDim.x) * 256;
   size_t c = size_t(blockIdx.x) * 256 + threadIdx.x;
   auto fetch = [&](size_t ch) {
-    return *reinterpret_cast<const u32x4 *>(a + (ch < chunks ? ch : chunks - 1) * 16);
+    ch = ch < total ? ch : total - 1;
+    return *reinterpret_cast<const u32x4 *>(ch < chunks ? a + ch * 16 : b + (ch - chunks) * 16);
   };
   u32x4 q = fetch(c);
   lut[threadIdx.x] = uint16_t(decode_bits(threadIdx.x) >> 16);
   lds_barrier();
-  for (; c < chunks; c += stride) {
+  for (; c < total; c += stride) {
     const u32x4 cur = q;
     q = fetch(c + stride);
     u32x4 lo, hi;
     decode16(lut, cur, lo, hi);
-    u32x4 *o = reinterpret_cast<u32x4 *>(out + c * 16);
+    u32x4 *o = reinterpret_cast<u32x4 *>(c < chunks ? out + c * 16 : out_b + (c - chunks) * 16);
     o[0] = lo;
     o[1] = hi;
   }
@@ -862,7 +868,14 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k, bool decoded_weight = false)
   const bool long_k_fill = m >= 256 && tiles256 * s256 == 256;
   p.tile = tile_env == 128 || tile_env == 256 ? tile_env
                                               : (m >= 256 && (tiles256 >= 128 || long_k_fill) ? 256 : 128);
-  if (decoded_weight && tile_env == 0 && m >= 2048 && tiles256 <= 128) p.tile = 128;
+  // ... unless 256 x 128 blocks fill the CUs in one wave without a split:
+  // 8 waves per CU either way, but one block shares its A panel over 128
+  // columns instead of two 128 x 128 blocks each copying their own.
+  static const int bn128_env = env_int("HIF8_GEMM_BN128", 1);
+  const int64_t tiles256x128 = ((m + 255) / 256) * ((n + 127) / 128);
+  const bool bn128 = decoded_weight && tile_env == 0 && m >= 2048 && tiles256 <= 128 && bn128_env &&
+                     tiles256x128 > 128 && tiles256x128 <= 256;
+  if (decoded_weight && tile_env == 0 && m >= 2048 && tiles256 <= 128 && !bn128) p.tile = 128;
   const int64_t tiles = ((m + p.tile - 1) / p.tile) * ((n + p.tile - 1) / p.tile);
   const int64_t slots = p.tile == 256 ? 256 : 512;  // resident blocks on 256 CUs
   p.splits = 1;
@@ -881,9 +894,32 @@ GemmPlan plan_gemm(int64_t m, int64_t n, int64_t k, bool decoded_weight = false)
   // at M = 512: 192 -> 256 blocks).  The in-kernel weight decode does not
   // divide over 192 rows, so the code path keeps 256 x 256.
   p.bn = p.tile;
-  if (decoded_weight && p.tile == 256 && p.splits == 1 && tile_env == 0) {
+  if (bn128) {
+    p.splits = 1;
+    p.bn = 128;
+  }
+  if (decoded_weight && p.tile == 256 && p.splits == 1 && tile_env == 0 && !bn128) {
     const int64_t tiles192 = ((m + 255) / 256) * ((n + 191) / 192);
     if (tiles256 < 256 && tiles192 > tiles256 && tiles192 <= 256) p.bn = 192;
+  }
+  // Codes path below M = 2048: 256 x 128 blocks of the DMA kernel with the
+  // weight decoded in it, K split in powers of two (>= 16 steps each) until
+  // the grid is one block per CU, where that fills all 256 CUs (knob
+  // HIF8_GEMM_WDEC128=0 turns it off).  Measured on MI355X at M = 512
+  // against the 128 x 128 / 256 x 256 plans above: q and o 4096 x 4096 41
+  // vs 43-44 us, down 4096 x 12288 78.7 vs 80.4-81.5; k/v (128 blocks)
+  // 35.2 vs 31.6, so it keeps the plan above.
+  static const int wdec128_env = env_int("HIF8_GEMM_WDEC128", 1);
+  if (!decoded_weight && wdec128_env && tile_env == 0 && split_env == 0 && splittable && m >= 256 &&
+      k < kMaxDmaK && (tiles256 < 128 || long_k_fill)) {
+    const int64_t t128 = ((m + 255) / 256) * ((n + 127) / 128);
+    int s128 = 1;
+    while (t128 * s128 * 2 <= 256 && ksteps % (s128 * 2) == 0 && ksteps / (s128 * 2) >= 16) s128 *= 2;
+    if (t128 * s128 == 256) {
+      p.tile = 256;
+      p.bn = 128;
+      p.splits = s128;
+    }
   }
   p.w_pre = false;
   p.a_bytes = (size_t(m) * size_t(k) * 2 + 255) / 256 * 256;
@@ -942,6 +978,7 @@ int launch_bf16_operands(const LinearArgs &a, const GemmPlan &p, const uint16_t 
                          float *partial) {
   if (a.k >= kMaxDmaK) return fail(HIF8_ERR_UNSUPPORTED, "soft_hif8 GEMM: K >= %d", kMaxDmaK);
   if (p.tile == 256 && p.bn == 192) return launch_dma<256, 192, 4, 2>(a, act, wt, splits, partial);
+  if (p.tile == 256 && p.bn == 128) return launch_dma<256, 128, 4, 2>(a, act, wt, splits, partial);
   if (p.tile == 256) return launch_dma<256, 256, 4, 2>(a, act, wt, splits, partial);
   return launch_dma<128, 128, 2, 2>(a, act, wt, splits, partial);
 }
@@ -953,6 +990,8 @@ int launch_plan(const LinearArgs &a, const GemmPlan &p, const void *act, int spl
   // fill in one wave (gate_up at M = 512: 192 -> 256 blocks) runs the DMA
   // kernel with the weight decoded in it (142 -> 111 us there; at 256 x 256
   // it measured no faster than the ping-pong kernel).
+  if (kAPre && p.tile == 256 && p.bn == 128)
+    return launch_dma<256, 128, 4, 2, true>(a, static_cast<const uint16_t *>(act), a.weight, splits, partial);
   const int64_t tiles_m = (a.m + 255) / 256, t256 = tiles_m * ((a.n + 255) / 256), t192 = tiles_m * ((a.n + 191) / 192);
   if (kAPre && p.tile == 256 && splits == 1 && a.k < kMaxDmaK && t256 < 256 && t192 > t256 && t192 <= 256)
     return launch_dma<256, 192, 4, 2, true>(a, static_cast<const uint16_t *>(act), a.weight, splits, partial);
@@ -989,18 +1028,15 @@ int launch_gemm(const LinearArgs &a) {
   uint8_t *ws = static_cast<uint8_t *>(a.workspace);
   uint16_t *abf = reinterpret_cast<uint16_t *>(ws);
   const size_t chunks = size_t(a.m) * size_t(a.k) / 16;
-  const unsigned blocks = unsigned(std::min<size_t>((chunks + 255) / 256, 2048));
-  decode_rows_kernel<<<blocks, 256, 0, a.stream>>>(static_cast<const uint8_t *>(a.act), abf, chunks);
-  int st = check_launch("soft_hif8 GEMM (activation decode)");
+  // The activation, and with w_pre the weight too, in one launch.
+  uint16_t *wbf = p.w_pre ? reinterpret_cast<uint16_t *>(ws + p.a_bytes) : nullptr;
+  const size_t wchunks = p.w_pre ? size_t(a.n) * size_t(a.k) / 16 : 0;
+  const unsigned blocks = unsigned(std::min<size_t>((chunks + wchunks + 255) / 256, p.w_pre ? 4096 : 2048));
+  decode_rows_kernel<<<blocks, 256, 0, a.stream>>>(static_cast<const uint8_t *>(a.act), abf, chunks, a.weight, wbf,
+                                                   wchunks);
+  const int st = check_launch(p.w_pre ? "soft_hif8 GEMM (activation and weight decode)"
+                                      : "soft_hif8 GEMM (activation decode)");
   if (st) return st;
-  if (p.w_pre) {
-    uint16_t *wbf = reinterpret_cast<uint16_t *>(ws + p.a_bytes);
-    const size_t wchunks = size_t(a.n) * size_t(a.k) / 16;
-    decode_rows_kernel<<<unsigned(std::min<size_t>((wchunks + 255) / 256, 4096)), 256, 0, a.stream>>>(
-        a.weight, wbf, wchunks);
-    st = check_launch("soft_hif8 GEMM (weight decode)");
-    if (st) return st;
-  }
   float *partial = p.part_bytes ? reinterpret_cast<float *>(ws + p.a_bytes + p.w_bytes) : nullptr;
   if (p.w_pre) {
     const uint16_t *wbf = reinterpret_cast<const uint16_t *>(ws + p.a_bytes);
@@ -1022,7 +1058,7 @@ int launch_gemm_decoded_weight(const LinearArgs &a) {
   uint16_t *abf = reinterpret_cast<uint16_t *>(ws);
   const size_t chunks = size_t(a.m) * size_t(a.k) / 16;
   decode_rows_kernel<<<unsigned(std::min<size_t>((chunks + 255) / 256, 2048)), 256, 0, a.stream>>>(
-      static_cast<const uint8_t *>(a.act), abf, chunks);
+      static_cast<const uint8_t *>(a.act), abf, chunks, nullptr, nullptr, 0);
   const int st = check_launch("soft_hif8 GEMM (activation decode)");
   if (st) return st;
   float *partial = p.part_bytes ? reinterpret_cast<float *>(ws + p.a_bytes) : nullptr;
@@ -1031,8 +1067,8 @@ int launch_gemm_decoded_weight(const LinearArgs &a) {
 
 int launch_decode_bf16(const uint8_t *codes, uint16_t *out, size_t elements, hipStream_t stream) {
   const size_t chunks = elements / 16;
-  decode_rows_kernel<<<unsigned(std::min<size_t>((chunks + 255) / 256, 4096)), 256, 0, stream>>>(codes, out,
-                                                                                                  chunks);
+  decode_rows_kernel<<<unsigned(std::min<size_t>((chunks + 255) / 256, 4096)), 256, 0, stream>>>(
+      codes, out, chunks, nullptr, nullptr, 0);
   return check_launch("hif8_decode_bf16");
 }
 
