@@ -322,11 +322,13 @@ def gemv_plan(m: int, n: int, k: int, kind: int = 0):
 
 def fused_one_launch(m: int, n: int, k: int) -> bool:
     """Whether soft_static_fused_linear runs one launch for these sizes (the
-    torch op's rule): one row with K <= 4096 and N < 16384, or several rows
-    whose fused-kind plan is the MFMA-4 GEMV; otherwise static quant + GEMV."""
+    torch op's rule, with its knobs HIF8_FUSED_MAX_N / HIF8_FUSED_MULTI_MAX_N):
+    one row with K <= 4096 and N < 16384, or several rows with N <= 2048 whose
+    fused-kind plan is the MFMA-4 GEMV; otherwise static quant + GEMV."""
     if m == 1:
-        return k <= 4096 and n < 16384
-    return gemv_plan(m, n, k, 2)[0].startswith("gemv_mfma4_kernel")
+        return k <= 4096 and n <= int(os.environ.get("HIF8_FUSED_MAX_N") or 16383)
+    return (n <= int(os.environ.get("HIF8_FUSED_MULTI_MAX_N") or 2048)
+            and gemv_plan(m, n, k, 2)[0].startswith("gemv_mfma4_kernel"))
 
 
 def decode_step_fn(st: Setup, copy: int, fused: bool = False):
@@ -691,8 +693,8 @@ def profile_pass(st: Setup, reps: int = 3) -> None:
     Known-size calibration kernels first: a torch copy of 64 MiB (read + write)
     and an fp32 sum over the same 64 MiB (a plain streaming read with 16-byte
     vector loads, the load width of the GEMV).  Then every decode GEMV, static
-    quant and prefill GEMM launch `reps` times, and the one-row fused op per
-    shape `reps` times."""
+    quant and prefill GEMM launch `reps` times, and the fused op per decode
+    (M, shape) `reps` times."""
     torch, native = st.torch, st.native
     src = torch.empty(64 << 20, dtype=torch.uint8, device=st.device).fill_(3)
     dst = torch.empty_like(src)
@@ -710,12 +712,13 @@ def profile_pass(st: Setup, reps: int = 3) -> None:
                 w, ws = st.weights[i % N_COPIES][name]
                 native.soft_linear(q, w, rs, ws, None, output_dtype=torch.bfloat16)
     torch.cuda.synchronize()
-    # The one-row fused op (the scheme's default for one token row), `reps` times per shape.
-    for name, n, k in LAYER:
-        x, s = st.x[(1, k)]
-        for i in range(reps):
-            w, ws = st.weights[i % N_COPIES][name]
-            native.soft_static_fused_linear(x, w, s, ws, None, output_dtype=torch.bfloat16)
+    # The fused op (the scheme's default for decode-sized inputs), `reps` times per (M, shape).
+    for m in DECODE_M:
+        for name, n, k in LAYER:
+            x, s = st.x[(m, k)]
+            for i in range(reps):
+                w, ws = st.weights[i % N_COPIES][name]
+                native.soft_static_fused_linear(x, w, s, ws, None, output_dtype=torch.bfloat16)
     torch.cuda.synchronize()
     log("profile pass: linear done")
     # KV path: decode attention (b4 ctx16384, b1 ctx512), the fused cache write
