@@ -113,17 +113,17 @@ def test_gemm_workspace_query_follows_the_split_plan(lib):
     # Enough 256 x 256 tiles to fill the GPU: no split.  GEMV-sized M: no workspace.
     assert size(4096, 24576, 4096) == 4096 * 4096 * 2 + 24576 * 4096 * 2
     # From M = 2048 the plan is the decoded-weight one: k+v at M = 4096 runs
-    # 512 unsplit 128 x 128 tiles instead of 128 256-tiles split in two.
+    # 256 unsplit 256 x 128 tiles instead of 128 256-tiles split in two.
     assert size(4096, 2048, 4096) == 4096 * 4096 * 2 + 2048 * 4096 * 2
     assert size(1024, 24576, 4096) == 1024 * 4096 * 2
     assert size(4, 4096, 4096) == 0
-    # Prefill M=512 over a 4096 x 4096 projection: 128 tiles of 128 x 128, K split in 4.
+    # Prefill M=512 over a 4096 x 4096 projection: 64 tiles of 256 x 128, K split in 4.
     assert size(512, 4096, 4096) == 512 * 4096 * 2 + 4 * 512 * 4096 * 4
     # Splits keep >= 16 K steps of 64 and need N % 4 == 0; K must be a multiple of 64.
     assert size(512, 4096, 1024) == 512 * 1024 * 2
     assert size(512, 4096, 2048) == 512 * 2048 * 2 + 2 * 512 * 4096 * 4
-    # Long K: 32 tiles of 256 x 256 split 8 ways (24 steps each) fill the 256 CUs.
-    assert size(512, 4096, 12288) == 512 * 12288 * 2 + 8 * 512 * 4096 * 4
+    # Long K: 64 tiles of 256 x 128 split 4 ways (48 steps each) fill the 256 CUs.
+    assert size(512, 4096, 12288) == 512 * 12288 * 2 + 4 * 512 * 4096 * 4
     assert size(512, 4094, 4096) == 512 * 4096 * 2
     assert size(300, 16, 100) == 0
     assert size(0, 16, 16) == 0
