@@ -236,11 +236,13 @@ __device__ __forceinline__ void decode_tile(const float *dec, const u32x4 (&kraw
 // per-key bias, the online softmax update of (m, l) in base 2, and
 // O^T += V^T P^T with P rounded to the query dtype.  Each K or V^T fragment
 // read from LDS feeds the MFMAs of all kRB row blocks.
+// full (wave-uniform): every row of the wavefront sees every key of the tile
+// (keys k0 .. k0 + 63 below each lim), so the per-key mask is skipped.
 template <int kD, bool kBf16, int kRB>
 __device__ __forceinline__ void tile_math(const uint16_t *ks, const uint16_t *vt, const float *kbias,
                                           const u32x4 (&qf)[kRB][kD / 32], int k0, const int (&lim)[kRB],
                                           float scale_log2, int n, int g, float (&m)[kRB], float (&l)[kRB],
-                                          f32x4_t (&oacc)[kRB][kD / 16]) {
+                                          f32x4_t (&oacc)[kRB][kD / 16], bool full = false) {
   constexpr int kQSteps = kD / 32;
   constexpr int kDB = kD / 16;
   constexpr int kKGran = kD / 8;
@@ -267,15 +269,27 @@ __device__ __forceinline__ void tile_math(const uint16_t *ks, const uint16_t *vt
   for (int rb = 0; rb < kRB; ++rb) {
     float x[16];
     float tmax = -__builtin_inff();
+    if (full) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const f32x4_t bias = *reinterpret_cast<const f32x4_t *>(kbias + 16 * kb + 4 * g);
+      for (int kb = 0; kb < 4; ++kb) {
+        const f32x4_t bias = *reinterpret_cast<const f32x4_t *>(kbias + 16 * kb + 4 * g);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int key = k0 + 16 * kb + 4 * g + e;
-        const float v = sacc[rb][kb][e] * scale_log2 + bias[e];
-        x[4 * kb + e] = key < lim[rb] ? v : -__builtin_inff();
-        tmax = fmaxf(tmax, x[4 * kb + e]);
+        for (int e = 0; e < 4; ++e) {
+          x[4 * kb + e] = sacc[rb][kb][e] * scale_log2 + bias[e];
+          tmax = fmaxf(tmax, x[4 * kb + e]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const f32x4_t bias = *reinterpret_cast<const f32x4_t *>(kbias + 16 * kb + 4 * g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int key = k0 + 16 * kb + 4 * g + e;
+          const float v = sacc[rb][kb][e] * scale_log2 + bias[e];
+          x[4 * kb + e] = key < lim[rb] ? v : -__builtin_inff();
+          tmax = fmaxf(tmax, x[4 * kb + e]);
+        }
       }
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
@@ -601,14 +615,23 @@ __global__ __launch_bounds__(kWaves * 64) void paged_prefill_attention_img_kerne
 #pragma unroll
     for (int db = 0; db < kDB; ++db) oacc[rb][db] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
+  // The smallest key limit of the wavefront's rows: tiles wholly below it
+  // need no mask.
+  int lim_lo = lim[0];
+#pragma unroll
+  for (int rb = 1; rb < kRB; ++rb) lim_lo = min(lim_lo, lim[rb]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) lim_lo = min(lim_lo, __shfl_xor(lim_lo, off, kWave));
+  lim_lo = __builtin_amdgcn_readfirstlane(lim_lo);
   for (int it = 0; it < ntiles; ++it) {
     wait_vmcnt<0>();  // this wavefront's copies of tile it (the only ones in flight)
     lds_barrier();
     if (it + 1 < ntiles) copy(t0 + it + 1, (it + 1) & 1);
     const uint8_t *st = smem_raw + (it & 1) * kImg;
     const uint16_t *ks = reinterpret_cast<const uint16_t *>(st);
-    tile_math<kD, kBf16, kRB>(ks, ks + kKT * kD, reinterpret_cast<const float *>(st + 4 * kKT * kD), qf,
-                              s_k0 + it * kKT, lim, p.scale_log2, n, g, m, l, oacc);
+    const int k0 = s_k0 + it * kKT;
+    tile_math<kD, kBf16, kRB>(ks, ks + kKT * kD, reinterpret_cast<const float *>(st + 4 * kKT * kD), qf, k0,
+                              lim, p.scale_log2, n, g, m, l, oacc, k0 + kKT <= lim_lo);
   }
 
 #pragma unroll
