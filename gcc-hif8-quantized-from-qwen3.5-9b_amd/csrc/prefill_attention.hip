@@ -236,6 +236,9 @@ __device__ __forceinline__ void decode_tile(const float *dec, const u32x4 (&kraw
 // per-key bias, the online softmax update of (m, l) in base 2, and
 // O^T += V^T P^T with P rounded to the query dtype.  Each K or V^T fragment
 // read from LDS feeds the MFMAs of all kRB row blocks.
+// Log2 headroom of the lazily updated softmax reference (see tile_math).
+constexpr float kLazyMax = 8.f;
+
 // full (wave-uniform): every row of the wavefront sees every key of the tile
 // (keys k0 .. k0 + 63 below each lim), so the per-key mask is skipped.
 template <int kD, bool kBf16, int kRB>
@@ -294,21 +297,29 @@ __device__ __forceinline__ void tile_math(const uint16_t *ks, const uint16_t *vt
     }
     tmax = fmaxf(tmax, __shfl_xor(tmax, 16, kWave));
     tmax = fmaxf(tmax, __shfl_xor(tmax, 32, kWave));
-    const float m_new = fmaxf(m[rb], tmax);
-    const float m_use = m_new == -__builtin_inff() ? 0.f : m_new;
-    const float alpha = __builtin_amdgcn_exp2f(m[rb] - m_use);
+    // m is the reference the row's weights, l and O are taken against; it
+    // moves (and l, O are rescaled) only when the row's max exceeds it by
+    // more than kLazyMax, so every weight stays below 2^kLazyMax and most
+    // tiles skip the rescale (rows start at -inf, where O and l are still 0).
+    const bool grow = tmax > m[rb] + kLazyMax;
+    if (__any(grow)) {
+      const float m_next = grow ? fmaxf(m[rb], tmax) : m[rb];
+      if (!__all(!grow || m[rb] == -__builtin_inff())) {
+        const float alpha = __builtin_amdgcn_exp2f(m[rb] - (m_next == -__builtin_inff() ? 0.f : m_next));
+        l[rb] *= alpha;
+#pragma unroll
+        for (int db = 0; db < kDB; ++db) oacc[rb][db] *= alpha;
+      }
+      m[rb] = m_next;
+    }
+    const float m_use = m[rb] == -__builtin_inff() ? 0.f : m[rb];
     float pw[16], psum = 0.f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
       pw[e] = __builtin_amdgcn_exp2f(x[e] - m_use);
       psum += pw[e];
     }
-    l[rb] = l[rb] * alpha + psum;
-    if (!__all(m_new == m[rb] || m[rb] == -__builtin_inff())) {
-#pragma unroll
-      for (int db = 0; db < kDB; ++db) oacc[rb][db] *= alpha;
-    }
-    m[rb] = m_new;
+    l[rb] += psum;
     // P^T operands of the two 32-key steps.
 #pragma unroll
     for (int s = 0; s < 2; ++s) {
