@@ -648,8 +648,9 @@ def c1_gpu(torch, native, device) -> dict:
            "quant_plus_gemv_us": round(ms_both * 1e3, 3),
            "quant_plus_gemv_GBps": round((gb + qb) / (ms_both * 1e-3) / 1e9, 1),
            "scheme_route_us": round(ms_fused * 1e3, 3),
-           "scheme_route": "the scheme's default for one token row: the fused static-quant op (static quant + "
-                           "GEMV inside it at N >= 12288)"}
+           "scheme_route": "the scheme's default for one token row: the fused static-quant op, "
+                           + ("one launch of " + gemv_plan(1, C1_N, C1_K, 2)[0] if fused_one_launch(1, C1_N, C1_K)
+                              else "static quant + the code GEMV inside it")}
     del copies
     return res
 
