@@ -138,6 +138,49 @@ def test_prefill_peaked_softmax(native_ops, device):
     _check(device, [1000, 300], [200, 31], 16, 4, 256, 128, seed=19, q_mul=8.0, bound=1e-2)
 
 
+@pytest.mark.parametrize("qlen", [17, 200])
+@pytest.mark.parametrize("order", ["rising", "falling"])
+def test_prefill_scores_whose_max_keeps_growing(native_ops, device, qlen, order):
+    """Scores that rise (or fall) along the keys by ~16 log2 units per 64-key
+    tile: rising, every tile moves the softmax's running max by more than
+    2^8, so the lazily updated reference and the rescale of O and l run at
+    every tile; falling, the first tile holds the max and no rescale runs.
+    Both the in-kernel path (17 tokens) and the tile-image path (200) take the
+    same tile math; checked against the float64 oracle."""
+    from hif8_rocm import kv_cache
+
+    hq, hkv, d, bs = 16, 4, 256, 128
+    ctx = 1000
+    g = torch.Generator().manual_seed(77)
+    u = torch.randn(hkv, d, generator=g)
+    u = u / u.norm(dim=-1, keepdim=True)
+    ramp = torch.arange(ctx, dtype=torch.float32) / 64.0
+    if order == "falling":
+        ramp = ramp.flip(0)
+    nb = math.ceil(ctx / bs) + 2
+    key = torch.zeros(nb * bs, hkv, d)
+    key[:ctx] = ramp[:, None, None] * u[None] + 0.05 * torch.randn(ctx, hkv, d, generator=g)
+    value = torch.randn(nb * bs, hkv, d, generator=g)
+    key, value = key.to(torch.bfloat16), value.to(torch.bfloat16)
+    ks = (key.float().abs().amax(dim=(0, 2)) / o.MAX_FINITE).to(device)
+    vs = (value.float().abs().amax(dim=(0, 2)) / o.MAX_FINITE).to(device)
+    kc = torch.zeros((nb, bs, hkv, d + 4), dtype=torch.uint8, device=device)
+    vc = torch.zeros((nb, bs, hkv, d + 4), dtype=torch.uint8, device=device)
+    kv_cache.write_kv_cache(key.to(device), value.to(device), kc, vc, torch.arange(nb * bs, device=device), ks, vs)
+    table = torch.randperm(nb, generator=g)[None, :].to(torch.int32)
+    # q along u with |q| so that one tile (64 keys, ramp + 1) adds ~16 log2 units to the logit.
+    q = (u.repeat_interleave(hq // hkv, dim=0)[None] * (16.0 / math.log2(math.e)) * math.sqrt(d)
+         + 0.1 * torch.randn(qlen, hq, d, generator=g)).to(torch.bfloat16)
+    scale = 1.0 / math.sqrt(d)
+    print(f"case growing max order={order} qlen={qlen}", flush=True)
+    out = _run_op(device, q, kc, vc, table, [ctx], [qlen], scale, True)
+    got = out.float().cpu().numpy()
+    ref = o.paged_attention_reference(q.float().numpy(), kc.cpu().numpy(), vc.cpu().numpy(), table.numpy(), [ctx],
+                                      bs, scale, rounding="f64", query_lens=[qlen], causal=True, dtype="bf16")
+    assert np.isfinite(got).all()
+    np.testing.assert_allclose(got, ref, rtol=1e-2, atol=1e-2)
+
+
 def test_prefill_fp16_query(native_ops, device):
     _check(device, [600, 130], [70, 130], 16, 4, 256, 128, dtype=torch.float16, seed=20)
 
