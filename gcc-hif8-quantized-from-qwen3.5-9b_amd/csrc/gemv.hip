@@ -1151,9 +1151,11 @@ GemvPlan plan_gemv(int64_t m, int64_t n, int64_t k, int act_kind, bool vec) {
     // 8 rows per block; over wide weights (N >= 16384) M = 4 streams faster
     // with 16 (gate_up 24576 x 4096: 24.8 vs 25.7-26.5 us on MI355X) and
     // M = 1 with 12, 2048 blocks (17.4-17.6 vs 17.8 us; 6 rows 17.6-18.3).
+    // M = 1 takes 12 rows from N = 8192 on: the one-launch fused static kind
+    // over 12288 x 4096 runs 12.3 vs 13.9 us (the code GEMV 11.09 vs 11.07).
     // q/o/k-v and down are fastest with 8.
     p.kind = kGemvDot2;
-    const int r = knobs.rows ? knobs.rows : (wide && m == 4 ? 16 : wide && m == 1 ? 12 : 8);
+    const int r = knobs.rows ? knobs.rows : (wide && m == 4 ? 16 : m == 1 && n >= 8192 ? 12 : 8);
     p.rows = r >= 16 ? 16 : r == 12 && m == 1 ? 12 : r >= 8 ? 8 : 4;
   }
   p.grid = unsigned((n + p.rows - 1) / p.rows);
