@@ -145,9 +145,28 @@ __device__ __forceinline__ f32x4_t mfma16(u32x4 a, u32x4 b, f32x4_t c) {
   }
 }
 
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+// Two fp32 values rounded to nearest-even into the MFMA operand dtype, lo in
+// the low half (bf16: one v_cvt_pk_bf16_f32 for the pair).
 template <bool kBf16>
 __device__ __forceinline__ uint32_t pack2(float lo, float hi) {
-  return uint32_t(float_to_half_bits<kBf16>(lo)) | (uint32_t(float_to_half_bits<kBf16>(hi)) << 16);
+  if constexpr (kBf16) return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
+  return uint32_t(float_to_f16_bits(lo)) | (uint32_t(float_to_f16_bits(hi)) << 16);
+}
+
+// Granule swizzle of K row `key` (16-byte granules of kD bf16 values).  The
+// in-kernel path, whose threads write four keys 4 kq + j of a column
+// together, folds key >> 4 in so those 16 rows hit 16 bank groups; tile
+// images (written to global memory, copied into LDS verbatim) use key & 15
+// alone, which leaves the 16 rows one fragment read touches conflict-free
+// and makes the swizzle the same for the four 16-key blocks, so a fragment
+// address is one of four per-lane bases plus an immediate.
+template <int kD, bool kImg>
+__device__ __forceinline__ int k_swizzle(int key) {
+  constexpr int kKGran = kD / 8;
+  constexpr int kKSwz = (kKGran < 16 ? kKGran : 16) - 1;
+  return kImg ? key & kKSwz : (key ^ (key >> 4)) & kKSwz;
 }
 
 __device__ __forceinline__ int clamp_len(int len, int max_len) {
@@ -167,14 +186,12 @@ __device__ __forceinline__ int vt_pos(int k) {
 // granule-swizzled, and a per-key logit bias; absent keys become zeros and a
 // -inf bias.  The destinations are LDS or a tile image in global memory with
 // the same layout.
-template <int kD, bool kBf16>
+template <int kD, bool kBf16, bool kImg>
 __device__ __forceinline__ void decode_tile(const float *dec, const u32x4 (&kraw)[kD / 64],
                                             const u32x4 (&vraw)[kD / 64], const float (&kscl)[kD / 64],
                                             const float (&vscl)[kD / 64], uint32_t ok, int kq, int dc,
                                             uint16_t *ks, uint16_t *vt, float *kbias) {
   constexpr int kKPT = kD / 64;
-  constexpr int kKGran = kD / 8;
-  constexpr int kKSwz = (kKGran < 16 ? kKGran : 16) - 1;
 #pragma unroll
   for (int j = 0; j < kKPT; ++j) {
     const int kt = kq * kKPT + j;  // key within the tile
@@ -189,7 +206,7 @@ __device__ __forceinline__ void decode_tile(const float *dec, const u32x4 (&kraw
       kp[2 * w] = pack2<kBf16>(dec[kw[w] & 0xFFu] * ksc, dec[(kw[w] >> 8) & 0xFFu] * ksc);
       kp[2 * w + 1] = pack2<kBf16>(dec[(kw[w] >> 16) & 0xFFu] * ksc, dec[kw[w] >> 24] * ksc);
     }
-    const int sw = (kt ^ (kt >> 4)) & kKSwz;
+    const int sw = k_swizzle<kD, kImg>(kt);
     uint16_t *krow = ks + kt * kD;
     *reinterpret_cast<u32x4 *>(krow + 8 * ((2 * dc) ^ sw)) = u32x4{kp[0], kp[1], kp[2], kp[3]};
     *reinterpret_cast<u32x4 *>(krow + 8 * ((2 * dc + 1) ^ sw)) = u32x4{kp[4], kp[5], kp[6], kp[7]};
@@ -241,27 +258,33 @@ constexpr float kLazyMax = 8.f;
 
 // full (wave-uniform): every row of the wavefront sees every key of the tile
 // (keys k0 .. k0 + 63 below each lim), so the per-key mask is skipped.
-template <int kD, bool kBf16, int kRB>
+template <int kD, bool kBf16, int kRB, bool kImg>
 __device__ __forceinline__ void tile_math(const uint16_t *ks, const uint16_t *vt, const float *kbias,
                                           const u32x4 (&qf)[kRB][kD / 32], int k0, const int (&lim)[kRB],
                                           float scale_log2, int n, int g, float (&m)[kRB], float (&l)[kRB],
                                           f32x4_t (&oacc)[kRB][kD / 16], bool full = false) {
   constexpr int kQSteps = kD / 32;
   constexpr int kDB = kD / 16;
-  constexpr int kKGran = kD / 8;
-  constexpr int kKSwz = (kKGran < 16 ? kKGran : 16) - 1;
-  // S^T = K Q^T: four 16-key blocks.
+  // S^T = K Q^T: four 16-key blocks.  Lane (g, n) reads granule 4 i + g of
+  // key 16 kb + n.  Image layout: the swizzle n' = n & 15 (or & 7) touches
+  // granule bits 0-3 only, so granule (4 i + g) ^ n' = 16 (i >> 2) +
+  // ((4 (i & 3) + g) ^ n'): four per-lane bases, the rest immediates.
+  constexpr int kBases = kQSteps < 4 ? kQSteps : 4;
+  const uint16_t *kbase[kBases];
+#pragma unroll
+  for (int j = 0; j < kBases; ++j) kbase[j] = ks + n * kD + 8 * ((4 * j + g) ^ k_swizzle<kD, true>(n));
   f32x4_t sacc[kRB][4];
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
 #pragma unroll
     for (int rb = 0; rb < kRB; ++rb) sacc[rb][kb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     const int key = 16 * kb + n;
-    const int sw = (key ^ (key >> 4)) & kKSwz;
+    const int sw = k_swizzle<kD, kImg>(key);
     const uint16_t *krow = ks + key * kD;
 #pragma unroll
     for (int i = 0; i < kQSteps; ++i) {
-      const u32x4 a = *reinterpret_cast<const u32x4 *>(krow + 8 * ((4 * i + g) ^ sw));
+      const uint16_t *src = kImg ? kbase[i & 3] + 16 * kb * kD + 128 * (i >> 2) : krow + 8 * ((4 * i + g) ^ sw);
+      const u32x4 a = *reinterpret_cast<const u32x4 *>(src);
 #pragma unroll
       for (int rb = 0; rb < kRB; ++rb) sacc[rb][kb] = mfma16<kBf16>(a, qf[rb][i], sacc[rb][kb]);
     }
@@ -313,12 +336,12 @@ __device__ __forceinline__ void tile_math(const uint16_t *ks, const uint16_t *vt
       m[rb] = m_next;
     }
     const float m_use = m[rb] == -__builtin_inff() ? 0.f : m[rb];
-    float pw[16], psum = 0.f;
+    float pw[16];
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      pw[e] = __builtin_amdgcn_exp2f(x[e] - m_use);
-      psum += pw[e];
-    }
+    for (int e = 0; e < 16; ++e) pw[e] = __builtin_amdgcn_exp2f(x[e] - m_use);
+    float psum = pw[0];
+#pragma unroll
+    for (int e = 1; e < 16; ++e) psum += pw[e];
     l[rb] += psum;
     // P^T operands of the two 32-key steps.
 #pragma unroll
@@ -351,8 +374,6 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
   constexpr int kChunks = kD / 16;     // 16-byte code chunks per row
   constexpr int kQSteps = kD / 32;     // MFMA steps over the head dims
   constexpr int kDB = kD / 16;         // 16-dim blocks of O^T
-  constexpr int kKGran = kD / 8;       // 16-byte bf16 granules per K row
-  constexpr int kKSwz = (kKGran < 16 ? kKGran : 16) - 1;
   static_assert(kKPT >= 1 && kKT * kChunks == kPThreads * kKPT, "thread map covers the tile");
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem_raw[];
@@ -459,14 +480,14 @@ __global__ __launch_bounds__(kPThreads, 2) void paged_prefill_attention_kernel(c
 
   for (int it = 0; it < ntiles; ++it) {
     const int k0 = s_k0 + it * kKT;
-    decode_tile<kD, kBf16>(dec, kraw, vraw, kscl, vscl, ok, kq, dc, ks, vt, kbias);
+    decode_tile<kD, kBf16, false>(dec, kraw, vraw, kscl, vscl, ok, kq, dc, ks, vt, kbias);
     lds_barrier();
     if (it + 1 < ntiles) {  // in flight during this tile's math
       issue(k0 + kKT, blk_next);
       if (it + 2 < ntiles) blk_next = block_of(k0 + 2 * kKT);
     }
 
-    tile_math<kD, kBf16, 1>(ks, vt, kbias, qf, k0, limv, p.scale_log2, n, g, m, l, oacc);
+    tile_math<kD, kBf16, 1, false>(ks, vt, kbias, qf, k0, limv, p.scale_log2, n, g, m, l, oacc);
     lds_barrier();  // the tile's LDS is rewritten by the next iteration
   }
 
@@ -543,7 +564,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_decode_tiles_kernel(const P
   lds_barrier();
   uint8_t *im = p.img + ((size_t(slot) * p.hkv + h) * p.img_tiles + tile) * kImg;
   uint16_t *ks = reinterpret_cast<uint16_t *>(im);
-  decode_tile<kD, kBf16>(dec, kraw, vraw, kscl, vscl, ok, kq, dc, ks, ks + kKT * kD,
+  decode_tile<kD, kBf16, true>(dec, kraw, vraw, kscl, vscl, ok, kq, dc, ks, ks + kKT * kD,
                          reinterpret_cast<float *>(im + 4 * kKT * kD));
 }
 
@@ -641,7 +662,7 @@ __global__ __launch_bounds__(kWaves * 64) void paged_prefill_attention_img_kerne
     const uint8_t *st = smem_raw + (it & 1) * kImg;
     const uint16_t *ks = reinterpret_cast<const uint16_t *>(st);
     const int k0 = s_k0 + it * kKT;
-    tile_math<kD, kBf16, kRB>(ks, ks + kKT * kD, reinterpret_cast<const float *>(st + 4 * kKT * kD), qf, k0,
+    tile_math<kD, kBf16, kRB, true>(ks, ks + kKT * kD, reinterpret_cast<const float *>(st + 4 * kKT * kD), qf, k0,
                               lim, p.scale_log2, n, g, m, l, oacc, k0 + kKT <= lim_lo);
   }
 
