@@ -159,7 +159,8 @@ def test_cpu_reference_gemv_config(native_ops, device):
 @pytest.mark.parametrize("n,k", [(4096, 4096), (2048, 4096), (4096, 12288), (24576, 4096)])
 @pytest.mark.parametrize("heavy", [False, True])
 def test_prefill_gemm_config_shapes(native_ops, device, m, n, k, heavy):
-    """BASELINE config 3 (sampled rows checked against the oracle at full size)."""
+    """BASELINE configs[2] shapes at full size: 48 sampled rows against the float64
+    oracle, and every output against an FP32 product of the decoded operands."""
     from hif8_rocm import native as api
 
     x = bf16_activation(m, k, seed=m + n + k, heavy_tail=heavy)
@@ -171,6 +172,19 @@ def test_prefill_gemm_config_shapes(native_ops, device, m, n, k, heavy):
     xq = data.cpu().numpy()[rows]
     want = o.linear_u8_u8(xq, np.repeat(s.numpy(), rows.size), w, ws)
     _check(y[torch.from_numpy(rows).to(device)], want)
+    # Every output against an FP32 product of the decoded operands on the GPU
+    # (the oracle's decode table; pinned to the float64 oracle by the rows
+    # above), so a wrong tile or split anywhere in the M x N output fails.
+    table = torch.from_numpy(o.DECODE_F32).to(device)
+    allow = torch.backends.cuda.matmul.allow_tf32
+    torch.backends.cuda.matmul.allow_tf32 = False
+    try:
+        a32 = table[data.long()] * rs.reshape(-1, 1)
+        w32 = table[_t(w, device).long()] * _t(ws, device).reshape(-1, 1)
+        ref = a32 @ w32.T
+    finally:
+        torch.backends.cuda.matmul.allow_tf32 = allow
+    torch.testing.assert_close(y.float(), ref, **TOL, equal_nan=True)
 
 
 def test_static_fused_matches_static_quant_then_gemm(native_ops, device):
