@@ -10,6 +10,7 @@
 // Two operators are new: the fused KV-cache write and the paged decode
 // attention that replace the reference's quant + pack + index_copy_ and
 // gather + decode + fused-attention sequences (kv_runtime.py:1222-1563).
+#include <cstdint>
 #include <cstdlib>
 #include <cstring>
 #include <c10/core/DeviceGuard.h>
@@ -291,10 +292,11 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
   const void *bias_ptr = bias.has_value() ? bias->data_ptr() : nullptr;
   const int bias_dtype = bias.has_value() ? DtypeCode(bias->scalar_type()) : HIF8_DTYPE_NONE;
   const int64_t m = activation.size(0), n = weight.size(0), k = activation.size(1);
-  // Widest N fused into one launch (tuning knob HIF8_FUSED_MAX_N, read once).
+  // Widest N fused into one launch at M = 1 (tuning knob HIF8_FUSED_MAX_N,
+  // read once; no limit by default).
   static const int64_t max_n = [] {
     const char *v = getenv("HIF8_FUSED_MAX_N");
-    return v && *v ? int64_t(atoll(v)) : int64_t(16383);
+    return v && *v ? int64_t(atoll(v)) : INT64_MAX;
   }();
   // Several rows run as one launch where the fused kind's plan is the MFMA-4
   // GEMV (K <= 4096, M = 4, or M = 3 over N >= 16384) and N <= 2048 (tuning
@@ -321,12 +323,12 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
     // activation chunk, which costs more than a separate quant launch once
     // there are several rows (measured on MI355X in graphs at M = 4: q
     // 4096x4096 14.3 vs 9.9 us, gate_up 24576x4096 38.1 vs 26.6).  One row
-    // with K <= 4096 and N < 16384 (one chunk per thread, loaded before the
-    // table set-up, at most 2048 blocks) is faster fused every time (q 6.5
-    // vs 8.7-9.0 us, k/v 2048x4096 5.0-5.2 vs 7.6, o 6.6-6.7 vs 8.3-8.8,
-    // 12288x4096 12.4 vs 14.0); gate_up (N = 24576, each of 2048 blocks
-    // re-encoding: 21.5-22.9 vs 21.5-21.7 us) and down (K = 12288, the chunk
-    // loop: 13.6-14.7 vs 13.7-16.0) keep two launches.
+    // with K <= 4096 (one chunk per thread, loaded before the table set-up)
+    // is faster fused (q 6.5 vs 8.7-9.0 us, k/v 2048x4096 5.0-5.2 vs 7.6, o
+    // 6.6-6.7 vs 8.3-8.8, 12288x4096 12.1-12.3 vs 13.7-14.0, gate_up
+    // 24576x4096 20.6 vs 21.2-21.4 since the encode takes one slow-path
+    // branch per 16 values); down (K = 12288, the chunk loop: 13.6-14.7 vs
+    // 13.7-16.0) keeps two launches.
     // The two launches give the same codes and the same GEMV, hence equal
     // outputs.
     auto codes = at::empty({m, k}, activation.options().dtype(at::ScalarType::Byte));
