@@ -6,9 +6,9 @@ M in {1, 4}, every projection of one 9B-class decoder layer (q 4096x4096,
 fused k+v 2048x4096, o 4096x4096, fused gate+up 24576x4096, down 4096x12288)
 runs the static W8A8 linear method (hif8_rocm.scheme) with its default
 routing: decode-sized inputs through the fused op soft_hif8_static_fused_gemm
-(one launch for one row with K <= 4096, and for four rows with K <= 4096
-and N <= 2048 on the MFMA-4 GEMV; hif8_static_quant then the code GEMV
-inside the op otherwise; outputs equal to the two-stage route).  The reference's
+(one launch for one row, and for four rows with K <= 4096 and N <= 2048 on
+the MFMA-4 GEMV; hif8_static_quant then the code GEMV inside the op
+otherwise; outputs equal to the two-stage route).  The reference's
 routing (every projection as static quant + soft_hif8_gemm,
 HIF8_STATIC_FUSED_SINGLE_ROW=0) is reported beside it.  One step = that sweep over one layer's weights; five
 distinct weight copies (966 MB) are rotated so the 256 MB Infinity Cache
@@ -322,13 +322,13 @@ def gemv_plan(m: int, n: int, k: int, kind: int = 0):
 
 def fused_one_launch(m: int, n: int, k: int) -> bool:
     """Whether soft_static_fused_linear runs one launch for these sizes (the
-    torch op's rule, with its knobs HIF8_FUSED_MAX_N / HIF8_FUSED_MULTI_MAX_N):
-    one row with K <= 4096 (any N unless HIF8_FUSED_MAX_N caps it), or several
-    rows with N <= 2048 whose fused-kind plan is the MFMA-4 GEMV; otherwise
-    static quant + GEMV."""
+    torch op's rule, with its knobs HIF8_FUSED_MAX_N / HIF8_FUSED_MAX_K /
+    HIF8_FUSED_MULTI_MAX_N): every one-row call (unless the first two cap N
+    or K), or several rows with N <= 2048 whose fused-kind plan is the MFMA-4
+    GEMV; otherwise static quant + GEMV."""
     if m == 1:
-        cap = os.environ.get("HIF8_FUSED_MAX_N")
-        return k <= 4096 and (not cap or n <= int(cap))
+        cap_n, cap_k = os.environ.get("HIF8_FUSED_MAX_N"), os.environ.get("HIF8_FUSED_MAX_K")
+        return (not cap_n or n <= int(cap_n)) and (not cap_k or k <= int(cap_k))
     return (n <= int(os.environ.get("HIF8_FUSED_MULTI_MAX_N") or 2048)
             and gemv_plan(m, n, k, 2)[0].startswith("gemv_mfma4_kernel"))
 

@@ -292,10 +292,14 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
   const void *bias_ptr = bias.has_value() ? bias->data_ptr() : nullptr;
   const int bias_dtype = bias.has_value() ? DtypeCode(bias->scalar_type()) : HIF8_DTYPE_NONE;
   const int64_t m = activation.size(0), n = weight.size(0), k = activation.size(1);
-  // Widest N fused into one launch at M = 1 (tuning knob HIF8_FUSED_MAX_N,
-  // read once; no limit by default).
+  // Widest N and K fused into one launch at M = 1 (tuning knobs
+  // HIF8_FUSED_MAX_N / HIF8_FUSED_MAX_K, read once; no limit by default).
   static const int64_t max_n = [] {
     const char *v = getenv("HIF8_FUSED_MAX_N");
+    return v && *v ? int64_t(atoll(v)) : INT64_MAX;
+  }();
+  static const int64_t max_k = [] {
+    const char *v = getenv("HIF8_FUSED_MAX_K");
     return v && *v ? int64_t(atoll(v)) : INT64_MAX;
   }();
   // Several rows run as one launch where the fused kind's plan is the MFMA-4
@@ -318,17 +322,16 @@ at::Tensor SoftHif8StaticFusedGemm(const at::Tensor &activation, const at::Tenso
                                         kernel, sizeof(kernel), &grid) == HIF8_OK &&
                   strncmp(kernel, "gemv_mfma4_kernel", 17) == 0;
   }
-  if (m >= 2 ? !multi_fused : (k > 4096 || n > max_n)) {
+  if (m >= 2 ? !multi_fused : (k > max_k || n > max_n)) {
     // Every block of the dot2 kernel's fused kinds encodes its whole
     // activation chunk, which costs more than a separate quant launch once
     // there are several rows (measured on MI355X in graphs at M = 4: q
     // 4096x4096 14.3 vs 9.9 us, gate_up 24576x4096 38.1 vs 26.6).  One row
-    // with K <= 4096 (one chunk per thread, loaded before the table set-up)
     // is faster fused (q 6.5 vs 8.7-9.0 us, k/v 2048x4096 5.0-5.2 vs 7.6, o
-    // 6.6-6.7 vs 8.3-8.8, 12288x4096 12.1-12.3 vs 13.7-14.0, gate_up
-    // 24576x4096 20.6 vs 21.2-21.4 since the encode takes one slow-path
-    // branch per 16 values); down (K = 12288, the chunk loop: 13.6-14.7 vs
-    // 13.7-16.0) keeps two launches.
+    // 6.6-6.7 vs 8.3-8.8, 12288x4096 12.1-12.3 vs 13.7-14.0; since the
+    // encode takes one slow-path branch per 16 values also gate_up
+    // 24576x4096, 19.9-20.6 vs 21.2-21.7, and down 4096x12288 with its
+    // chunk loop, 13.6-13.7 vs 14.1-14.2).
     // The two launches give the same codes and the same GEMV, hence equal
     // outputs.
     auto codes = at::empty({m, k}, activation.options().dtype(at::ScalarType::Byte));

@@ -14,9 +14,9 @@ their outputs equal quant -> GEMM bit for bit.  Measured on MI355X in HIP
 graphs, the separate quant launch costs 2-4 us of launch and cold-cache
 latency, so decode-sized inputs go through the fused op by default: up to
 ``HIF8_STATIC_FUSED_ROWS`` token rows (default 4).  The op itself picks one
-launch or quant + GEMV per shape: one row with K <= 4096 runs the one-row
-fused kernel (q 6.8 vs 9.0 us, k/v 5.0 vs 7.6, o 6.8 vs 9.0, gate_up 20.6
-vs 21.3);
+launch or quant + GEMV per shape: one row runs the one-row fused kernel (q
+6.8 vs 9.0 us, k/v 5.0 vs 7.6, o 6.8 vs 9.0, gate_up 20.6 vs 21.3, down 13.6
+vs 14.1);
 four rows with K <= 4096 and N <= 2048 run the MFMA-4 GEMV's fused kind (k/v
 8.2 vs 8.5 us; with more blocks the per-block re-encode of the rows costs
 more than the quant launch); other shapes run quant + GEMV.
