@@ -394,7 +394,8 @@ def per_kernel_table(st: Setup) -> dict:
                 fb = gemv_bytes(m, n, k) + m * k  # bf16 x instead of u8 codes
                 gbs = fb / (med * 1e-3) / 1e9
                 kern, grid = gemv_plan(m, n, k, 2)
-                table[f"{name}_m{m}_fused"] = {"kernel": "fused_quant_gemv", "us": round(med * 1e3, 3), "bytes": fb,
+                table[f"{name}_m{m}_fused"] = {"kernel": "fused_quant_gemv", "us": round(med * 1e3, 3),
+                                               "copies": len(rot), "bytes": fb,
                                                "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4),
                                                "quant_then_gemv_us": round(med2 * 1e3, 3),
                                                "launch": kern if fused_one_launch(m, n, k)
