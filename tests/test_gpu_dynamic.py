@@ -62,7 +62,8 @@ def test_dynamic_quant_rejects_bad_input(native_ops, device):
         native.dynamic_quant(torch.zeros(2, 16, device=device))
 
 
-@pytest.mark.parametrize("m,n,k", [(1, 128, 4096), (2, 128, 4096), (1, 128, 12288), (2, 300, 1024), (2, 37, 100)])
+@pytest.mark.parametrize("m,n,k", [(1, 128, 4096), (2, 128, 4096), (1, 128, 12288), (2, 300, 1024), (2, 37, 100),
+                                   (1, 12288, 4096), (1, 8200, 12288)])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 def test_dynamic_fused_gemv_matches_oracle(native_ops, device, m, n, k, dtype):
     from hif8_rocm import native
