@@ -190,7 +190,9 @@ def test_prefill_gemm_config_shapes(native_ops, device, m, n, k, heavy):
 def test_static_fused_matches_static_quant_then_gemm(native_ops, device):
     g = torch.Generator().manual_seed(20260821)
     for rows, channels, k, with_bias in ((1, 128, 2048, False), (2, 256, 4096, True), (4, 256, 4096, True),
-                                         (1, 128, 12288, True), (3, 77, 48, True), (1, 12288, 512, True)):
+                                         (1, 128, 12288, True), (3, 77, 48, True), (1, 12288, 512, True),
+                                         (1, 200, 5000, True), (1, 16400, 8192, False), (1, 300, 4100, True),
+                                         (1, 64, 1000, False)):
         x = (torch.randn(rows, k, generator=g) * 3.0).to(torch.bfloat16).to(device)
         w = torch.randint(0, 111, (channels, k), generator=g, dtype=torch.uint8).to(device)
         fixed = torch.tensor([0.75], device=device)
